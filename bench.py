@@ -1,0 +1,307 @@
+"""Benchmark of the fused normalization hot path on one MI355X.
+
+Default workload (BASELINE metric): LayerNorm forward + backward, bf16, 8192 x 4096 -- one
+"step" is the forward (y, mean, rstd) plus the backward (dx, dgamma, dbeta) over one batch, with
+inputs already resident in HBM.  The RMSNorm forward + backward at the same shape is timed the
+same way and reported under "rms_fwd_bwd".
+
+The kernels are called through the C ABI (libfln.so) on torch's current HIP stream, with every
+output preallocated; inputs and outputs rotate over enough buffer sets (> 512 MiB) that the
+256 MiB Infinity Cache cannot serve a step from the previous one.
+
+Prints ONE JSON line (rank 0).  `value` = algorithmic bytes of one step / measured step time, in
+GB/s.  `roofline` covers the backward launch group (stage-1 kernel + column reduction), timed
+with HIP events on the launch stream; `cpu_baseline` times the C oracle (oracle/fln_oracle.c,
+the "port") on a bounded row sample on the host, single thread.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "fused-layernorm-cuda-operator_amd")
+sys.path.insert(0, PKG)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+METRIC = "HBM GB/s (% of peak) + µs/call, LN/RMSNorm fwd+bwd bf16 8192×4096"
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 640 * 2 ** 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="approximate host time budget of the CPU baseline")
+    ap.add_argument("--all", action="store_true",
+                    help="also time every BASELINE config (C1..C5) and report them")
+    return ap.parse_args()
+
+
+class Runner:
+    """Preallocated buffers + C-ABI launches for one workload."""
+
+    def __init__(self, lib, capi, torch, w, inputs):
+        self.lib, self.capi, self.torch, self.w = lib, capi, torch, w
+        dev = "cuda"
+        x = inputs["x"]
+        set_bytes = x.numel() * x.element_size() * (4 if "dy" in inputs else 2)
+        self.nsets = max(1, -(-ROTATE_BYTES // set_bytes))
+        self.sets = []
+        for k in range(self.nsets):
+            s = {n: t.to(dev) for n, t in inputs.items()}
+            if k > 0:  # distinct buffers, same values
+                s = {n: t.clone() for n, t in s.items()}
+            s["y"] = torch.empty_like(s["x"])
+            s["mean"] = torch.empty(w.rows, device=dev)
+            s["rstd"] = torch.empty(w.rows, device=dev)
+            if "dy" in s:
+                s["dx"] = torch.empty_like(s["x"])
+            self.sets.append(s)
+        self.rows, self.cols = w.rows, w.cols
+        self.code = capi.dtype_code(self.sets[0]["x"])
+        self.ws_bytes = lib.fln_backward_workspace_bytes(self.rows, self.cols, self.code)
+        self.ws = torch.empty(max(1, self.ws_bytes // 4), device=dev)
+        self.dg = torch.empty(self.cols, device=dev)
+        self.db = torch.empty(self.cols, device=dev)
+        self.i = 0
+
+    def fwd(self, s, stream):
+        c, p = self.capi, self.capi.ptr
+        if self.w.op.startswith("rms"):
+            rc = self.lib.fln_rmsnorm_forward(p(s["x"]), p(s.get("gamma")), p(s["y"]),
+                                              p(s["rstd"]), self.rows, self.cols, self.code,
+                                              self.w.eps, stream)
+        else:
+            rc = self.lib.fln_layernorm_forward(p(s["x"]), p(s.get("gamma")), p(s.get("beta")),
+                                                p(s["y"]), p(s["mean"]), p(s["rstd"]),
+                                                self.rows, self.cols, self.code, self.w.eps,
+                                                stream)
+        c.check(rc)
+
+    def bwd(self, s, stream):
+        c, p = self.capi, self.capi.ptr
+        if self.w.op.startswith("rms"):
+            rc = self.lib.fln_rmsnorm_backward(p(s["dy"]), p(s["x"]), p(s["rstd"]),
+                                               p(s.get("gamma")), None, p(s["dx"]), p(self.dg),
+                                               self.rows, self.cols, self.code, c.F32,
+                                               p(self.ws), self.ws_bytes, stream)
+        else:
+            rc = self.lib.fln_layernorm_backward(p(s["dy"]), p(s["x"]), p(s["mean"]),
+                                                 p(s["rstd"]), p(s.get("gamma")), None,
+                                                 p(s["dx"]), p(self.dg), p(self.db), self.rows,
+                                                 self.cols, self.code, c.F32, p(self.ws),
+                                                 self.ws_bytes, stream)
+        c.check(rc)
+
+    def step(self, stream):
+        s = self.sets[self.i % self.nsets]
+        self.i += 1
+        self.fwd(s, stream)
+        self.bwd(s, stream)
+
+    def time_region(self, fn, n, stream_obj):
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream_obj)
+        for _ in range(n):
+            fn()
+        e1.record(stream_obj)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+
+def time_launch_group(runner, which, n, stream, stream_obj):
+    """Average duration (ms) of one forward or backward launch group, rotating buffer sets."""
+    it = [0]
+
+    def one():
+        s = runner.sets[it[0] % runner.nsets]
+        it[0] += 1
+        (runner.fwd if which == "fwd" else runner.bwd)(s, stream)
+
+    for _ in range(3):
+        one()
+    return runner.time_region(one, n, stream_obj)
+
+
+def cpu_baseline(w, seconds):
+    """Time the C oracle (scalar C port, one thread) on a bounded row sample of the workload."""
+    import numpy as np
+    from oracle import c_oracle
+    from fused_layernorm.testing import algorithmic_bytes, make_inputs
+
+    c_oracle.load()
+    rows = 256
+    inp = make_inputs(w, rows)
+    f = {k: v.float().numpy() for k, v in inp.items()}
+    rms = w.op.startswith("rms")
+
+    def run():
+        if rms:
+            c_oracle.rmsnorm_fwd(f["x"], f.get("gamma"), w.eps)
+            c_oracle.rmsnorm_bwd(f["dy"], f["x"], f.get("gamma"), w.eps)
+        else:
+            c_oracle.layernorm_fwd(f["x"], f.get("gamma"), f.get("beta"), w.eps)
+            c_oracle.layernorm_bwd(f["dy"], f["x"], f.get("gamma"), w.eps)
+
+    run()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    nbytes = algorithmic_bytes(w, rows)["total"]
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": (f"{rows} of {w.rows} rows of the same seeded workload ({w.name}), "
+                   f"C oracle fwd+bwd (fp64 accumulation), median of {len(times)} runs "
+                   f"({med * 1e3:.1f} ms per {rows}-row fwd+bwd)"),
+        "ms_per_step_full_size_extrapolated": round(med * (w.rows / rows) * 1e3, 1),
+        "cpu_model": cpu, "host_cpus": os.cpu_count(),
+    }
+
+
+def torch_cpu_baseline(w, seconds):
+    """The reference's CPU path (torch-CPU F.layer_norm / F.rms_norm + autograd backward) on the
+    same row sample, all host threads."""
+    import torch
+    from fused_layernorm.testing import algorithmic_bytes, make_inputs
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    rows = 256
+    inp = make_inputs(w, rows)
+    x = inp["x"].requires_grad_(True)
+    g = inp.get("gamma")
+    b = inp.get("beta")
+    dy = inp["dy"]
+    rms = w.op.startswith("rms")
+
+    def run():
+        x.grad = None
+        if rms:
+            y = torch.nn.functional.rms_norm(x, (w.cols,), g, w.eps)
+        else:
+            y = torch.nn.functional.layer_norm(x, (w.cols,), g, b, w.eps)
+        y.backward(dy)
+
+    run()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(algorithmic_bytes(w, rows)["total"] / med / 1e9, 3), "unit": "GB/s",
+            "threads": torch.get_num_threads(), "kind": "torch-cpu (reference CPU path)",
+            "sample": f"{rows} rows of {w.name}, median of {len(times)}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU layout is described in DESIGN.md and not measured here.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import capi
+    from fused_layernorm.testing import WORKLOADS, algorithmic_bytes, make_inputs
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    lib = capi.load()
+    stream_obj = torch.cuda.current_stream()
+    stream = capi.stream()
+
+    results = {}
+    for name in ("ln_fwd_bwd_bf16_8192x4096", "rms_fwd_bwd_bf16_8192x4096"):
+        w = WORKLOADS[name]
+        r = Runner(lib, capi, torch, w, make_inputs(w))
+        for _ in range(args.warmup):
+            r.step(stream)
+        ms = r.time_region(lambda: r.step(stream), args.steps, stream_obj)
+        nb = algorithmic_bytes(w)
+        ms_f = time_launch_group(r, "fwd", max(20, args.steps // 2), stream, stream_obj)
+        ms_b = time_launch_group(r, "bwd", max(20, args.steps // 2), stream, stream_obj)
+        results[name] = dict(ms=ms, bytes=nb, ms_fwd=ms_f, ms_bwd=ms_b, nsets=r.nsets)
+        del r
+        torch.cuda.empty_cache()
+
+    head = results["ln_fwd_bwd_bf16_8192x4096"]
+    gbs = head["bytes"]["total"] / (head["ms"] * 1e-3) / 1e9
+    bwd_gbs = head["bytes"]["bwd"] / (head["ms_bwd"] * 1e-3) / 1e9
+    rms = results["rms_fwd_bwd_bf16_8192x4096"]
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded torch.randn inputs (x seed 3, gamma 103, beta 203, dy 303)",
+        "config": {"workload": "ln_fwd_bwd_bf16_8192x4096", "rows": 8192, "cols": 4096,
+                   "step": "LayerNorm fwd (y, mean, rstd) + bwd (dx, dgamma, dbeta fp32)",
+                   "algorithmic_bytes_per_step": head["bytes"]["total"],
+                   "rotating_buffer_sets": head["nsets"]},
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "us_per_call": {"fwd": round(head["ms_fwd"] * 1e3, 2),
+                        "bwd": round(head["ms_bwd"] * 1e3, 2),
+                        "fwd_bwd": round(head["ms"] * 1e3, 2)},
+        "roofline": {
+            "kernel": "layernorm backward launch group (bwd_reg_kernel + col_reduce_kernel)",
+            "bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(bwd_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "algorithmic_bytes_per_launch": head["bytes"]["bwd"],
+            "avg_launch_us": round(head["ms_bwd"] * 1e3, 2),
+        },
+        "forward_kernel": {
+            "kernel": "fwd_reg_kernel", "algorithmic_bytes_per_launch": head["bytes"]["fwd"],
+            "avg_launch_us": round(head["ms_fwd"] * 1e3, 2),
+            "achieved_gbs": round(head["bytes"]["fwd"] / (head["ms_fwd"] * 1e-3) / 1e9, 1),
+        },
+        "rms_fwd_bwd": {
+            "workload": "rms_fwd_bwd_bf16_8192x4096",
+            "value": round(rms["bytes"]["total"] / (rms["ms"] * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "us_per_call": {"fwd": round(rms["ms_fwd"] * 1e3, 2),
+                            "bwd": round(rms["ms_bwd"] * 1e3, 2),
+                            "fwd_bwd": round(rms["ms"] * 1e3, 2)},
+        },
+    }
+    if not args.no_cpu_baseline:
+        w = WORKLOADS["ln_fwd_bwd_bf16_8192x4096"]
+        out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        out["cpu_baseline"]["torch_cpu"] = torch_cpu_baseline(w, max(2.0, args.cpu_seconds / 2))
+    out["host"] = platform.node()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,462 @@
+// fln_backward.hip -- LayerNorm / RMSNorm backward for gfx950 and its C-ABI entry points.
+//
+// The reference declares `layernorm_backward_cuda` (csrc/layernorm.h:24-32) and calls it from
+// `layernorm_backward` (csrc/layernorm_cuda.cpp:97-141), but never defines it: this file is the
+// first implementation of that contract.
+//
+// Stage 1 (bwd_reg_kernel): each block owns a contiguous chunk of rows, processed by row groups
+// of `wpr` waves.  Per row it computes
+//     LayerNorm: xhat = (x - mean) rstd, g = dy gamma,
+//                dx = rstd (g - sum(g)/N - xhat sum(g xhat)/N)
+//     RMSNorm:   xhat = x rstd,          dx = rstd (g - xhat sum(g xhat)/N)
+// and accumulates the column sums dy*xhat (dgamma) and dy (dbeta) for the columns each lane
+// owns in fp32 registers.  At the end the block's row groups are combined through LDS in a
+// fixed order and written as one fp32 partial row per block.
+// Stage 2 (col_reduce_kernel): sums the partial rows per column in a fixed order.  Nothing uses
+// atomics, so dgamma/dbeta are bitwise reproducible run to run.
+#include <stdlib.h>
+
+#include "fln_device.h"
+#include "fln_internal.h"
+
+namespace fln {
+
+template <class T, int VEC, int VPL, int MAXT>
+__global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
+  __shared__ float red[2][2][MAXT / kWave];  // [double buffer][sum g, sum g*xhat][wave]
+  __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
+  using P = Pack<T, VEC>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int wpr = p.wpr;
+  const int rg = wave / wpr;
+  const int t = (wave - rg * wpr) * kWave + lane;
+  const int tpr = kWave * wpr;
+  const int rgs = p.rgs;
+  const int64_t N = p.cols;
+  const int nvec = static_cast<int>(N / VEC);
+  const float inv_n = 1.0f / static_cast<float>(N);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * p.rows_per_block;
+  const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
+  const int iters = static_cast<int>((p.rows_per_block + rgs - 1) / rgs);
+
+  // gamma stays packed in the I/O type (half the VGPRs of an fp32 copy for 16-bit types).
+  P gam[VPL];
+  {
+    const P* gr = static_cast<const P*>(p.gamma);
+    P ones;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ones.v[e] = static_cast<T>(1.0f);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = t + i * tpr;
+      gam[i] = gr ? (v < nvec ? gr[v] : zero_pack<T, VEC>()) : ones;
+    }
+  }
+  float acc_g[VPL][VEC], acc_b[VPL][VEC];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc_g[i][e] = acc_b[i][e] = 0.0f;
+
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row = r0 + static_cast<int64_t>(it) * rgs + rg;
+    const bool row_ok = row < r1;
+    const P* xr = reinterpret_cast<const P*>(static_cast<const T*>(p.x) + row * N);
+    const P* dr = reinterpret_cast<const P*>(static_cast<const T*>(p.dy) + row * N);
+    P xv[VPL], dv[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = t + i * tpr;
+      const bool ok = row_ok && v < nvec;
+      xv[i] = ok ? xr[v] : zero_pack<T, VEC>();
+      dv[i] = ok ? dr[v] : zero_pack<T, VEC>();
+    }
+    const float mu = (row_ok && !p.rms) ? p.mean[row] : 0.0f;
+    const float rs = row_ok ? p.rstd[row] : 0.0f;
+
+    // Pass 1 over registers: the two row sums.  xhat and g are recomputed in pass 2 instead of
+    // being kept, which keeps the kernel within 128 VGPRs at 16 elements per lane.
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xh = (to_f32(xv[i].v[e]) - mu) * rs;
+        const float g = to_f32(dv[i].v[e]) * to_f32(gam[i].v[e]);
+        s1 += g;
+        s2 += g * xh;
+      }
+    s1 = wave_allreduce<SumOp>(s1);
+    s2 = wave_allreduce<SumOp>(s2);
+    if (wpr > 1) {
+      float(*slot)[MAXT / kWave] = red[it & 1];
+      if (lane == 0) {
+        slot[0][wave] = s1;
+        slot[1][wave] = s2;
+      }
+      __syncthreads();
+      s1 = slot[0][rg * wpr];
+      s2 = slot[1][rg * wpr];
+      for (int k = 1; k < wpr; ++k) {
+        s1 += slot[0][rg * wpr + k];
+        s2 += slot[1][rg * wpr + k];
+      }
+    }
+    const float c1 = p.rms ? 0.0f : s1 * inv_n;
+    const float c2 = s2 * inv_n;
+
+    P* xo = reinterpret_cast<P*>(static_cast<T*>(p.dx) + row * N);
+    const P* rr = reinterpret_cast<const P*>(static_cast<const T*>(p.dres) + row * N);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = t + i * tpr;
+      const bool ok = row_ok && v < nvec;
+      P rv, o;
+      if (p.dres && ok) rv = rr[v];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = to_f32(dv[i].v[e]);  // zero outside the row / tensor
+        const float xh = (to_f32(xv[i].v[e]) - mu) * rs;
+        float dxv = rs * (d * to_f32(gam[i].v[e]) - c1 - xh * c2);
+        if (p.dres) dxv += ok ? to_f32(rv.v[e]) : 0.0f;
+        o.v[e] = from_f32<T>(dxv);
+        acc_g[i][e] += d * xh;
+        acc_b[i][e] += d;
+      }
+      if (p.dx && ok) xo[v] = o;
+    }
+  }
+
+  // Stage-1 output: one fp32 partial row per block (row stride ld_part, a multiple of 4).
+  const int64_t ld = (N + 3) & ~int64_t(3);
+  float* outs[2] = {p.part_g, p.part_b};
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    float* out = outs[a];
+    if (!out) continue;
+    out += static_cast<int64_t>(blockIdx.x) * ld;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = t + i * tpr;
+      float vals[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) vals[e] = a == 0 ? acc_g[i][e] : acc_b[i][e];
+      if (rgs > 1) {
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) comb[(rg * tpr + t) * VEC + e] = vals[e];
+        __syncthreads();
+        if (rg == 0) {
+          for (int k = 1; k < rgs; ++k)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) vals[e] += comb[(k * tpr + t) * VEC + e];
+        }
+      }
+      if (rg == 0 && v < nvec) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) out[static_cast<int64_t>(v) * VEC + e] = vals[e];
+      }
+    }
+  }
+}
+
+// Rows too long for the register path: one block per row chunk, three strided passes per row,
+// column partials accumulated in place in the block's partial row (each column is owned by one
+// thread of the block, so the read-modify-write is race free).
+template <class T>
+__global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
+  __shared__ float red[2][2][16];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int64_t N = p.cols;
+  const int64_t ld = (N + 3) & ~int64_t(3);
+  const T* gm = static_cast<const T*>(p.gamma);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * p.rows_per_block;
+  const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
+  float* pg = p.part_g ? p.part_g + static_cast<int64_t>(blockIdx.x) * ld : nullptr;
+  float* pb = p.part_b ? p.part_b + static_cast<int64_t>(blockIdx.x) * ld : nullptr;
+  for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+    if (pg) pg[j] = 0.0f;
+    if (pb) pb[j] = 0.0f;
+  }
+  const float inv_n = 1.0f / static_cast<float>(N);
+  int buf = 0;
+  for (int64_t row = r0; row < r1; ++row, buf ^= 1) {
+    const T* x = static_cast<const T*>(p.x) + row * N;
+    const T* dy = static_cast<const T*>(p.dy) + row * N;
+    const float mu = p.rms ? 0.0f : p.mean[row];
+    const float rs = p.rstd[row];
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+      const float xh = (to_f32(x[j]) - mu) * rs;
+      const float g = to_f32(dy[j]) * (gm ? to_f32(gm[j]) : 1.0f);
+      s1 += g;
+      s2 += g * xh;
+    }
+    s1 = wave_allreduce<SumOp>(s1);
+    s2 = wave_allreduce<SumOp>(s2);
+    if (lane == 0) {
+      red[buf][0][wave] = s1;
+      red[buf][1][wave] = s2;
+    }
+    __syncthreads();
+    s1 = red[buf][0][0];
+    s2 = red[buf][1][0];
+    for (int k = 1; k < nw; ++k) {
+      s1 += red[buf][0][k];
+      s2 += red[buf][1][k];
+    }
+    const float c1 = p.rms ? 0.0f : s1 * inv_n, c2 = s2 * inv_n;
+    T* dx = p.dx ? static_cast<T*>(p.dx) + row * N : nullptr;
+    const T* dres = p.dres ? static_cast<const T*>(p.dres) + row * N : nullptr;
+    for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+      const float xh = (to_f32(x[j]) - mu) * rs;
+      const float d = to_f32(dy[j]);
+      const float g = d * (gm ? to_f32(gm[j]) : 1.0f);
+      if (dx) {
+        float v = rs * (g - c1 - xh * c2);
+        if (dres) v += to_f32(dres[j]);
+        dx[j] = from_f32<T>(v);
+      }
+      if (pg) pg[j] += d * xh;
+      if (pb) pb[j] += d;
+    }
+  }
+}
+
+// Stage 2: out[c] = sum over partial rows k (in order) of part[k][c].  Block = 16 waves over
+// 256 columns: lane l owns 4 columns, wave w sums rows w, w+16, ...; the 16 wave sums are then
+// added in wave order through LDS.  A y-block index selects the array (dgamma or dbeta).
+struct ColReduceArgs {
+  const float* part[2];
+  void* out[2];
+  int64_t G;
+  int64_t N;
+};
+
+template <class TO>
+__global__ __launch_bounds__(1024) void col_reduce_kernel(const ColReduceArgs a) {
+  __shared__ float4 comb[16][64];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const float* part = a.part[blockIdx.y];
+  TO* out = static_cast<TO*>(a.out[blockIdx.y]);
+  const int64_t ld = (a.N + 3) & ~int64_t(3);
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + lane * 4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < ld) {
+#pragma unroll 8
+    for (int64_t k = wave; k < a.G; k += 16) {
+      const float4 v = *reinterpret_cast<const float4*>(part + k * ld + c);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+  }
+  comb[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0) {
+    float4 r = comb[0][lane];
+    for (int k = 1; k < 16; ++k) {
+      const float4 v = comb[k][lane];
+      r.x += v.x;
+      r.y += v.y;
+      r.z += v.z;
+      r.w += v.w;
+    }
+    const float rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (c + e < a.N) out[c + e] = from_f32<TO>(rr[e]);
+  }
+}
+
+namespace {
+
+// Vectors per lane of the backward register path: 16 elements per lane for 16-byte vectors of
+// 16-bit types, 8 for fp32 and for the scalar path.
+constexpr int bwd_max_vpl(int vec, int es) { return vec == 1 ? 8 : (es == 2 ? 2 : 2); }
+
+int next_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+template <class T, int VEC, int VPL>
+int launch_stage1(const BwdParams& p, int64_t blocks, hipStream_t s) {
+  hipLaunchKernelGGL((bwd_reg_kernel<T, VEC, VPL, 1024>), dim3(blocks), dim3(1024), 0, s, p);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <class T, int VEC>
+int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, hipStream_t s) {
+  constexpr int CAP = bwd_max_vpl(VEC, sizeof(T));
+  switch (vpl) {
+    case 1: return launch_stage1<T, VEC, 1>(p, blocks, s);
+    case 2:
+      if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, s);
+      return FLN_ERR_INVALID;
+    case 4:
+      if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, s);
+      return FLN_ERR_INVALID;
+    case 8:
+      if constexpr (CAP >= 8) return launch_stage1<T, VEC, 8>(p, blocks, s);
+      return FLN_ERR_INVALID;
+    case 16:
+      if constexpr (CAP >= 16) return launch_stage1<T, VEC, 16>(p, blocks, s);
+      return FLN_ERR_INVALID;
+    default: return FLN_ERR_INVALID;
+  }
+}
+
+template <class T>
+int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s) {
+  p.wpr = geo.wpr;
+  p.rgs = geo.rgs;
+  p.rows_per_block = geo.rows_per_block;
+  if (!geo.reg_path) {
+    hipLaunchKernelGGL((bwd_loop_kernel<T>), dim3(geo.blocks), dim3(1024), 0, s, p);
+    return static_cast<int>(hipGetLastError());
+  }
+  constexpr int VV = 16 / sizeof(T);
+  if (geo.vec == VV) return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, s);
+  return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, s);
+}
+
+}  // namespace
+
+BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok) {
+  BwdGeometry g{};
+  const int es = element_size(dtype);
+  const int vv = es > 0 ? 16 / es : 1;
+  g.vec = (vec_ok && cols % vv == 0) ? vv : 1;
+  const int64_t nvec = cols / g.vec;
+  auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
+  // At most 16 (16-bit types) or 8 (fp32, scalar path) elements per lane keeps dy, x, gamma and
+  // both fp32 column accumulators of a lane's columns in VGPRs (<= 128, the budget of a
+  // 1024-thread block).
+  const int cap = bwd_max_vpl(g.vec, es);
+  int wpr = 1;
+  while (per_lane(wpr) > cap && wpr < 16) wpr *= 2;
+  const int forced = getenv("FLN_BWD_WPR") ? atoi(getenv("FLN_BWD_WPR")) : 0;
+  if (forced >= 1 && forced <= 16 && (forced & (forced - 1)) == 0 && per_lane(forced) <= cap)
+    wpr = forced;
+  g.reg_path = per_lane(wpr) <= cap;
+  g.wpr = wpr;
+  g.vpl = g.reg_path ? next_pow2(static_cast<int>(per_lane(wpr))) : 0;
+  g.threads = 1024;
+  g.rgs = g.reg_path ? 1024 / (kWave * wpr) : 1;
+  const int64_t cus = device_cu_count();
+  int64_t blocks = (rows + g.rgs - 1) / g.rgs;
+  if (blocks > cus) blocks = cus;
+  if (blocks < 1) blocks = 1;
+  g.rows_per_block = (rows + blocks - 1) / blocks;
+  g.blocks = (rows + g.rows_per_block - 1) / g.rows_per_block;
+  return g;
+}
+
+int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
+                    hipStream_t s) {
+  // p0.part_g / p0.part_b carry the workspace base (validated by the caller).
+  BwdParams p = p0;
+  const bool vec_ok = aligned16(p.x) && aligned16(p.dy) && aligned16(p.dx) &&
+                      aligned16(p.gamma) && aligned16(p.dres);
+  const BwdGeometry geo = backward_geometry(p.rows, p.cols, dtype, vec_ok);
+  const int64_t ld = (p.cols + 3) & ~int64_t(3);
+  float* ws = p0.part_g;
+  p.part_g = dgamma ? ws : nullptr;
+  p.part_b = dbeta ? ws + geo.blocks * ld : nullptr;
+  int rc;
+  switch (dtype) {
+    case FLN_F32: rc = dispatch_backward<float>(p, geo, s); break;
+    case FLN_BF16: rc = dispatch_backward<__bf16>(p, geo, s); break;
+    case FLN_F16: rc = dispatch_backward<_Float16>(p, geo, s); break;
+    default: return FLN_ERR_INVALID;
+  }
+  if (rc != 0 || (!dgamma && !dbeta)) return rc;
+
+  ColReduceArgs a{};
+  int ny = 0;
+  if (dgamma) { a.part[ny] = p.part_g; a.out[ny] = dgamma; ++ny; }
+  if (dbeta) { a.part[ny] = p.part_b; a.out[ny] = dbeta; ++ny; }
+  a.G = geo.blocks;
+  a.N = p.cols;
+  const dim3 grid(static_cast<unsigned>((p.cols + 255) / 256), ny);
+  const int od = dparam_dtype;
+  if (od == FLN_F32)
+    hipLaunchKernelGGL((col_reduce_kernel<float>), grid, dim3(1024), 0, s, a);
+  else if (od == FLN_BF16)
+    hipLaunchKernelGGL((col_reduce_kernel<__bf16>), grid, dim3(1024), 0, s, a);
+  else if (od == FLN_F16)
+    hipLaunchKernelGGL((col_reduce_kernel<_Float16>), grid, dim3(1024), 0, s, a);
+  else
+    return FLN_ERR_INVALID;
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace fln
+
+namespace {
+
+int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (p.rows < 0 || p.cols < 0 || p.rows > INT32_MAX || p.cols > INT32_MAX) return FLN_ERR_INVALID;
+  if (dtype != FLN_F32 && dtype != FLN_BF16 && dtype != FLN_F16) return FLN_ERR_INVALID;
+  if ((dgamma || dbeta) && dparam_dtype != FLN_F32 && dparam_dtype != dtype) return FLN_ERR_INVALID;
+  if (p.rows == 0 || p.cols == 0) {
+    // Nothing to reduce: parameter gradients of an empty batch are zero.
+    if (p.cols > 0 && (dgamma || dbeta)) {
+      const size_t bytes = static_cast<size_t>(p.cols) * fln::element_size(dparam_dtype);
+      hipStream_t s = static_cast<hipStream_t>(stream);
+      if (dgamma && hipMemsetAsync(dgamma, 0, bytes, s) != hipSuccess) return FLN_ERR_INVALID;
+      if (dbeta && hipMemsetAsync(dbeta, 0, bytes, s) != hipSuccess) return FLN_ERR_INVALID;
+    }
+    return FLN_OK;
+  }
+  if (!p.dy || !p.x || !p.rstd || (!p.rms && !p.mean)) return FLN_ERR_INVALID;
+  if (!p.dx && !dgamma && !dbeta) return FLN_OK;
+  if (dgamma || dbeta) {
+    if (!workspace || !fln::aligned16(workspace) ||
+        workspace_bytes < fln_backward_workspace_bytes(p.rows, p.cols, dtype))
+      return FLN_ERR_INVALID;
+  }
+  p.part_g = static_cast<float*>(workspace);
+  return fln::launch_backward(p, dtype, dgamma, dbeta, dparam_dtype,
+                              static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" size_t fln_backward_workspace_bytes(int64_t rows, int64_t cols, int dtype) {
+  (void)dtype;
+  if (rows <= 0 || cols <= 0) return 0;
+  int64_t g = fln::device_cu_count();
+  if (rows < g) g = rows;
+  const int64_t ld = (cols + 3) & ~int64_t(3);
+  return static_cast<size_t>(2 * g * ld) * sizeof(float);
+}
+
+extern "C" int fln_layernorm_backward(const void* dy, const void* x, const float* mean,
+                                      const float* rstd, const void* gamma, const void* dres,
+                                      void* dx, void* dgamma, void* dbeta, int64_t rows,
+                                      int64_t cols, int dtype, int dparam_dtype, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  fln::BwdParams p{};
+  p.dy = dy; p.x = x; p.mean = mean; p.rstd = rstd; p.gamma = gamma; p.dres = dres; p.dx = dx;
+  p.rows = rows; p.cols = cols; p.rms = 0;
+  return backward_common(p, dtype, dgamma, dbeta, dparam_dtype, workspace, workspace_bytes,
+                         stream);
+}
+
+extern "C" int fln_rmsnorm_backward(const void* dy, const void* x, const float* rstd,
+                                    const void* weight, const void* dres, void* dx, void* dweight,
+                                    int64_t rows, int64_t cols, int dtype, int dweight_dtype,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  fln::BwdParams p{};
+  p.dy = dy; p.x = x; p.rstd = rstd; p.gamma = weight; p.dres = dres; p.dx = dx;
+  p.rows = rows; p.cols = cols; p.rms = 1;
+  return backward_common(p, dtype, dweight, nullptr, dweight_dtype, workspace, workspace_bytes,
+                         stream);
+}

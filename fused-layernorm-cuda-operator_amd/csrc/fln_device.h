@@ -1,0 +1,117 @@
+// fln_device.h -- device-side building blocks shared by the forward and backward kernels.
+//
+// Everything here is written for CDNA4 (gfx950) wave64: cross-lane sums use DPP row
+// permutations inside each 16-lane row, ds_swizzle across the two rows of a 32-lane half, and
+// v_readlane across the halves, so a reduction never touches LDS unless a row of the tensor is
+// spread over several waves.  The reference's warp32 shuffle tree and its shared-memory block
+// step (csrc/layernorm_cuda_kernel.cu:7-28) play the same role there.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fln {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------------------
+// Element types.  __bf16 / _Float16 are clang's native storage types: widening is exact and the
+// narrowing cast lowers to v_cvt_pk_bf16_f32 (round-to-nearest-even) on gfx950.
+// ---------------------------------------------------------------------------------------------
+template <class T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }
+template <class T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+template <class T, int N> struct alignas(sizeof(T) * N) Pack {
+  T v[N];
+};
+
+template <class T, int N> __device__ __forceinline__ Pack<T, N> zero_pack() {
+  Pack<T, N> p;
+#pragma unroll
+  for (int e = 0; e < N; ++e) p.v[e] = static_cast<T>(0.0f);
+  return p;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wave64 all-reduce.  After the four DPP steps every lane of a 16-lane row holds that row's
+// total; ds_swizzle (xor 16) combines the two rows of each 32-lane half; two readlanes combine
+// the halves into a wave-uniform value.  Every combining step adds a value to its mirror image,
+// so all lanes end with the bitwise-identical result (fp add is commutative).
+// All 64 lanes must be active when these are called.
+// ---------------------------------------------------------------------------------------------
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float readlane(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+struct SumOp {
+  __device__ __forceinline__ static float apply(float a, float b) { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
+};
+
+template <class Op> __device__ __forceinline__ float wave_allreduce(float v) {
+  v = Op::apply(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]: lane ^ 1
+  v = Op::apply(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]: lane ^ 2
+  v = Op::apply(v, dpp<0x141>(v));  // row_half_mirror: 4-lane groups within 8
+  v = Op::apply(v, dpp<0x140>(v));  // row_mirror: 8-lane groups within 16
+  v = Op::apply(v, swz_xor16(v));   // 16-lane rows within 32
+  return Op::apply(readlane(v, 0), readlane(v, 32));
+}
+
+// Generic-type wave sum through ds_bpermute (used by the looped fallback kernels, which also
+// handle fp64 accumulation).
+template <class A> __device__ __forceinline__ A wave_sum_generic(A v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// GELU.  mode 1: exact erf form (torch approximate='none'); mode 2: tanh form, the one fused by
+// the reference (csrc/layernorm_cuda_kernel.cu:31-36).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float gelu_erf(float v) {
+  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float k0 = 0.79788456080286535588f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  return 0.5f * v * (1.0f + tanhf(k0 * (v + k1 * v * v * v)));
+}
+template <class A> __device__ __forceinline__ A apply_gelu(A v, int mode) {
+  if (mode == 1) return gelu_erf(static_cast<float>(v));
+  if (mode == 2) return gelu_tanh(static_cast<float>(v));
+  return v;
+}
+__device__ __forceinline__ double apply_gelu(double v, int mode) {
+  if (mode == 1) return 0.5 * v * (1.0 + erf(v * 0.70710678118654752440));
+  if (mode == 2) return 0.5 * v * (1.0 + tanh(0.79788456080286535588 * (v + 0.044715 * v * v * v)));
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// OCP fp8 e4m3fn.  v_cvt_pk_fp8_f32 (gfx950: OCP encoding, round-to-nearest-even) converts two
+// fp32 values into two bytes of a dword half.  Values are clamped to +-448 first, so the
+// conversion never sees an out-of-range input (saturating semantics).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float sat448(float v) { return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f); }
+
+__device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), w, true);
+  return static_cast<uint32_t>(w);
+}
+__device__ __forceinline__ uint8_t fp8x1(float a) {
+  return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), 0.0f, 0, false) & 0xFF);
+}
+
+}  // namespace fln

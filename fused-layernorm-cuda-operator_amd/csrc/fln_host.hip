@@ -1,0 +1,87 @@
+// fln_host.hip -- host-only helpers of libfln: device queries, the reference's utility
+// functions (csrc/layernorm_cuda.cpp:144-195) and version / error strings.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "fln_internal.h"
+
+namespace fln {
+
+int element_size(int dtype) {
+  switch (dtype) {
+    case FLN_F32: return 4;
+    case FLN_BF16: return 2;
+    case FLN_F16: return 2;
+    case FLN_F64: return 8;
+    case FLN_F8E4M3FN: return 1;
+    default: return 0;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// CU count of the current device, cached per device index.
+int device_cu_count() {
+  static std::mutex mu;
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+}  // namespace fln
+
+// Same estimate as the reference's get_memory_usage (csrc/layernorm_cuda.cpp:144-164):
+// forward in/out + fp32 mean/rstd, backward grad_input + grad_gamma/beta, plus a per-row
+// workspace term.
+extern "C" int64_t fln_get_memory_usage(int batch_size, int hidden_size,
+                                        int use_mixed_precision) {
+  const int64_t es = use_mixed_precision ? 2 : 4;
+  const int64_t b = batch_size, h = hidden_size;
+  const int64_t forward_memory = 2 * b * h * es + 2 * b * static_cast<int64_t>(sizeof(float));
+  const int64_t backward_memory = b * h * es + 2 * h * es;
+  const int64_t workspace = b * 32 * static_cast<int64_t>(sizeof(float));
+  return forward_memory + backward_memory + workspace;
+}
+
+// Hints with the reference's wording and thresholds (csrc/layernorm_cuda.cpp:167-195), except
+// that the occupancy check uses this device's CU count instead of an assumed 80 SMs.
+extern "C" int fln_get_performance_hints(int batch_size, int hidden_size, char* buf,
+                                         size_t buflen) {
+  std::string hints;
+  if (hidden_size % 32 != 0)
+    hints += "Warning: hidden_size is not divisible by 32, may impact performance.\n";
+  if (hidden_size > 8192)
+    hints += "Info: Large hidden dimension detected. Consider using mixed precision.\n";
+  if (batch_size < 8) hints += "Info: Small batch size may not fully utilize GPU.\n";
+  const int cus = fln::device_cu_count();
+  if (batch_size < cus) hints += "Info: Not enough blocks to saturate GPU. Consider batching.\n";
+  if (buf && buflen > 0) {
+    const size_t n = hints.size() < buflen - 1 ? hints.size() : buflen - 1;
+    memcpy(buf, hints.data(), n);
+    buf[n] = '\0';
+  }
+  return static_cast<int>(hints.size());
+}
+
+extern "C" const char* fln_version(void) { return "1.0.0"; }
+
+extern "C" int fln_hip_version(void) { return HIP_VERSION; }
+
+extern "C" const char* fln_error_string(int code) {
+  if (code == FLN_OK) return "success";
+  if (code == FLN_ERR_INVALID) return "invalid argument (shape, dtype, pointer or workspace)";
+  return hipGetErrorString(static_cast<hipError_t>(code));
+}

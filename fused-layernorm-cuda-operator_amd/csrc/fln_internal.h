@@ -1,0 +1,71 @@
+// fln_internal.h -- parameter blocks and host helpers shared by the libfln translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/fused_layernorm.h"
+
+namespace fln {
+
+// Forward launch description (one struct for every forward flavour).
+struct FwdParams {
+  const void* x;
+  const void* res;    // residual, or nullptr
+  const void* gamma;  // [cols] or nullptr
+  const void* beta;   // [cols] or nullptr (LayerNorm only)
+  void* y;            // [rows, cols] of dtype, or fp8 bytes when out_fp8
+  void* h;            // residual sum output, or nullptr
+  float* mean;        // [rows] or nullptr
+  float* rstd;        // [rows] or nullptr
+  float* scale;       // [rows] fp8 row scales (out_fp8 only)
+  int64_t rows;
+  int64_t cols;
+  float eps;
+  int rms;   // 1: RMSNorm (no centring, no beta)
+  int gelu;  // FLN_GELU_*
+  int wpr;   // waves per row (register path)
+};
+
+// Backward launch description.
+struct BwdParams {
+  const void* dy;
+  const void* x;
+  const float* mean;  // LayerNorm only
+  const float* rstd;
+  const void* gamma;  // or nullptr (treated as ones)
+  const void* dres;   // gradient added into dx, or nullptr
+  void* dx;           // or nullptr
+  float* part_g;      // [blocks, cols] stage-1 partial of sum(dy * xhat), or nullptr
+  float* part_b;      // [blocks, cols] stage-1 partial of sum(dy), or nullptr
+  int64_t rows;
+  int64_t cols;
+  int64_t rows_per_block;
+  int rms;
+  int wpr;  // waves per row
+  int rgs;  // row groups per block
+};
+
+int element_size(int dtype);
+int device_cu_count();
+bool aligned16(const void* p);
+
+int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s);
+int launch_backward(const BwdParams& p, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
+                    hipStream_t s);
+
+// Stage-1 geometry of the backward (shared by workspace sizing and the launch).
+struct BwdGeometry {
+  bool reg_path;  // register-resident rows
+  int vec;        // elements per vector access
+  int vpl;        // vectors per lane (power of two, <= 16)
+  int wpr;        // waves per row
+  int threads;    // block size
+  int rgs;        // row groups per block
+  int64_t blocks; // stage-1 blocks == partial rows
+  int64_t rows_per_block;
+};
+BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok);
+
+}  // namespace fln

@@ -1,0 +1,132 @@
+/*
+ * fused_layernorm.h -- C ABI of the MI355X (gfx950) fused normalization library (libfln.so).
+ *
+ * Plain pointers and sizes only: no torch types cross this boundary.  Every tensor is a dense
+ * row-major [rows, cols] array (row stride == cols); per-column parameters are [cols]; per-row
+ * statistics are fp32 [rows].  `stream` is a hipStream_t (NULL = the null stream).  All calls
+ * are asynchronous with respect to the host and return 0 on success, FLN_ERR_INVALID for bad
+ * arguments (detected before anything is launched), or a nonzero hipError_t value from the
+ * launch.  fln_error_string() turns a code into text.
+ *
+ * Each entry point names the reference interface it replaces (paths relative to the
+ * JonSnow1807/Fused-LayerNorm-CUDA-Operator tree).
+ */
+#ifndef FUSED_LAYERNORM_H
+#define FUSED_LAYERNORM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+#define FLN_F32 0
+#define FLN_BF16 1
+#define FLN_F16 2
+#define FLN_F64 3 /* forward only (the reference dispatches fp32/fp64 in its built kernels) */
+#define FLN_F8E4M3FN 4 /* OCP fp8 e4m3fn, output of fln_layernorm_fp8_forward only */
+
+/* GELU flavours for fln_layernorm_gelu. */
+#define FLN_GELU_NONE 0
+#define FLN_GELU_ERF 1  /* 0.5 v (1 + erf(v / sqrt 2)) -- torch approximate='none' */
+#define FLN_GELU_TANH 2 /* 0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3))) -- the reference's gelu() */
+
+#define FLN_OK 0
+#define FLN_ERR_INVALID 1 /* == hipErrorInvalidValue */
+
+/* y = LN(x) [* gamma + beta].  gamma and beta may each be NULL (then that term is skipped).
+ * Replaces `layernorm_cuda` (csrc/layernorm_cuda_kernel.cu:152-178) behind
+ * `layernorm` (csrc/bindings.cpp:19-28). */
+int fln_layernorm(const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
+                  int64_t cols, int dtype, float eps, void* stream);
+
+/* y = GELU(LN(x) [* gamma + beta]), gelu_mode = FLN_GELU_ERF or FLN_GELU_TANH.
+ * Replaces `layernorm_gelu_cuda` (csrc/layernorm_cuda_kernel.cu:180-206) behind
+ * `layernorm_gelu` (csrc/bindings.cpp:30-39). */
+int fln_layernorm_gelu(const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
+                       int64_t cols, int dtype, float eps, int gelu_mode, void* stream);
+
+/* Training forward: y plus fp32 mean[rows] and rstd[rows] (either may be NULL).
+ * Replaces `layernorm_forward_cuda` (csrc/layernorm.h:15-22, csrc/layernorm_cuda.cpp:14-21) and
+ * `layernorm_forward_cuda_optimized` (csrc/layernorm_cuda_kernel_optimized.cu:171-212), called
+ * from `layernorm_forward` (csrc/layernorm_cuda.cpp:49-94). */
+int fln_layernorm_forward(const void* x, const void* gamma, const void* beta, void* y, float* mean,
+                          float* rstd, int64_t rows, int64_t cols, int dtype, float eps,
+                          void* stream);
+
+/* Workspace (bytes) the backward entry points need for the two-stage column reduction. */
+size_t fln_backward_workspace_bytes(int64_t rows, int64_t cols, int dtype);
+
+/* LayerNorm backward.  dx = rstd (g - mean(g) - xhat mean(g xhat)), g = dy * gamma,
+ * xhat = (x - mean) rstd; dgamma = sum_rows dy xhat; dbeta = sum_rows dy.
+ * dx, dgamma, dbeta may each be NULL (the reference's output_mask).  dres, if not NULL, is an
+ * incoming gradient [rows, cols] added into dx (backward of a fused residual add).
+ * dparam_dtype is the element type of dgamma/dbeta (FLN_F32 or `dtype`).  workspace must hold
+ * fln_backward_workspace_bytes(rows, cols, dtype) bytes whenever dgamma or dbeta is requested.
+ * Replaces `layernorm_backward_cuda` (csrc/layernorm.h:24-32, csrc/layernorm_cuda.cpp:33-41),
+ * declared but never defined in the reference; called from `layernorm_backward`
+ * (csrc/layernorm_cuda.cpp:97-141). */
+int fln_layernorm_backward(const void* dy, const void* x, const float* mean, const float* rstd,
+                           const void* gamma, const void* dres, void* dx, void* dgamma,
+                           void* dbeta, int64_t rows, int64_t cols, int dtype, int dparam_dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* RMSNorm forward: y = x rstd [* weight], rstd = 1/sqrt(mean(x^2) + eps); rstd[rows] optional.
+ * No counterpart in the reference (new capability on the same path). */
+int fln_rmsnorm_forward(const void* x, const void* weight, void* y, float* rstd, int64_t rows,
+                        int64_t cols, int dtype, float eps, void* stream);
+
+/* RMSNorm backward: dx = rstd (g - xhat mean(g xhat)), g = dy * weight, xhat = x rstd;
+ * dweight = sum_rows dy xhat.  Same optional-output and workspace rules as
+ * fln_layernorm_backward.  No counterpart in the reference. */
+int fln_rmsnorm_backward(const void* dy, const void* x, const float* rstd, const void* weight,
+                         const void* dres, void* dx, void* dweight, int64_t rows, int64_t cols,
+                         int dtype, int dweight_dtype, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* Residual add + LayerNorm: h = x + residual (rounded to dtype), y = LN(h) [* gamma + beta];
+ * statistics are taken over the rounded h.  h, mean, rstd may be NULL.
+ * No counterpart in the reference. */
+int fln_add_layernorm_forward(const void* x, const void* residual, const void* gamma,
+                              const void* beta, void* h, void* y, float* mean, float* rstd,
+                              int64_t rows, int64_t cols, int dtype, float eps, void* stream);
+
+/* Residual add + RMSNorm: h = x + residual (rounded), y = h rstd [* weight].
+ * No counterpart in the reference. */
+int fln_add_rmsnorm_forward(const void* x, const void* residual, const void* weight, void* h,
+                            void* y, float* rstd, int64_t rows, int64_t cols, int dtype, float eps,
+                            void* stream);
+
+/* LayerNorm with OCP fp8 e4m3fn output: v = LN(x) [* gamma + beta] in fp32,
+ * scale[r] = max_j |v_rj| / 448, q = sat_rne_e4m3fn(v / scale[r]) (one byte per element);
+ * a row whose max is 0 gets scale 0 and all-zero codes.  mean and rstd may be NULL.
+ * No counterpart in the reference. */
+int fln_layernorm_fp8_forward(const void* x, const void* gamma, const void* beta, uint8_t* q,
+                              float* scale, float* mean, float* rstd, int64_t rows, int64_t cols,
+                              int dtype, float eps, void* stream);
+
+/* Elementwise fp32 -> OCP fp8 e4m3fn (saturating, round-to-nearest-even) with the same device
+ * conversion the fp8 forward uses; n elements, any alignment.  A standalone quantizer for
+ * callers that scale themselves (and a direct check of the conversion).
+ * No counterpart in the reference. */
+int fln_fp8_e4m3fn_encode(const float* x, uint8_t* q, int64_t n, void* stream);
+
+/* Host utilities with the reference's meaning (csrc/layernorm_cuda.cpp:144-164 and :167-195).
+ * fln_get_performance_hints writes a NUL-terminated string into buf (truncated to buflen) and
+ * returns the full length; it reads the CU count of the current device. */
+int64_t fln_get_memory_usage(int batch_size, int hidden_size, int use_mixed_precision);
+int fln_get_performance_hints(int batch_size, int hidden_size, char* buf, size_t buflen);
+
+/* Library version ("1.0.0", as the reference's __version__, csrc/layernorm_cuda.cpp:230). */
+const char* fln_version(void);
+/* HIP runtime version the library was built against (the reference's __cuda_version__). */
+int fln_hip_version(void);
+const char* fln_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSED_LAYERNORM_H */

@@ -1,0 +1,473 @@
+"""GPU parity of the HIP kernels, called through the C ABI (libfln.so via ctypes).
+
+Every check compares against the CPU oracle (oracle/norms.py in numpy fp64, oracle/fln_oracle.c
+for full BASELINE sizes) on the same seeded inputs (fused_layernorm.testing).  Tolerances, from
+the BASELINE contract:
+  * fp32 outputs: max-abs <= 1e-5;
+  * bf16 outputs (y, h): within 1 bf16 ulp of the fp64 reference; h = x + r is bit-exact;
+  * bf16 dx: within 1 bf16 ulp + 2^-12 * max|dx_ref| (dx = rstd (g - c1 - xhat c2) cancels, so
+    elements near zero carry an absolute fp32 error relative to the row scale);
+  * dgamma / dbeta / dweight (fp32 column sums): max|err| <= 1e-4 * max|ref|;
+  * fp8 codes: identical except +-1 code on <= 0.1% of elements; per-row scales within 1e-6
+    relative.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import capi
+from helpers import assert_close_rel, assert_within_ulp, to_np
+from oracle import c_oracle, norms
+from fused_layernorm.testing import WORKLOADS, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+DX_ATOL_REL = 2.0 ** -12
+
+
+@pytest.fixture(scope="module")
+def lib(gpu_available):
+    return capi.load()
+
+
+def cuda(t):
+    return None if t is None else t.to("cuda")
+
+
+def f32(t):
+    return None if t is None else to_np(t).astype(np.float32)
+
+
+# ------------------------------------------------------------------------------------------------
+# C-ABI call wrappers.
+# ------------------------------------------------------------------------------------------------
+def ln_forward(lib, x, g, b, eps, stats=True):
+    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, device=x.device, dtype=torch.float32) if stats else None
+    rstd = torch.empty(rows, device=x.device, dtype=torch.float32) if stats else None
+    capi.check(lib.fln_layernorm_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y),
+                                         capi.ptr(mean), capi.ptr(rstd), rows, cols,
+                                         capi.dtype_code(x), eps, capi.stream()))
+    return y, mean, rstd
+
+
+def rms_forward(lib, x, w, eps):
+    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+    capi.check(lib.fln_rmsnorm_forward(capi.ptr(x), capi.ptr(w), capi.ptr(y), capi.ptr(rstd),
+                                       rows, cols, capi.dtype_code(x), eps, capi.stream()))
+    return y, rstd
+
+
+def workspace(lib, rows, cols, x):
+    n = lib.fln_backward_workspace_bytes(rows, cols, capi.dtype_code(x))
+    return torch.empty(max(1, (n + 3) // 4), device=x.device, dtype=torch.float32), n
+
+
+def ln_backward(lib, dy, x, mean, rstd, g, want_params=True, dres=None, dparam_f32=True):
+    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+    dx = torch.empty_like(x)
+    pdt = torch.float32 if dparam_f32 else x.dtype
+    dg = torch.empty(cols, device=x.device, dtype=pdt) if want_params else None
+    db = torch.empty(cols, device=x.device, dtype=pdt) if want_params else None
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_layernorm_backward(
+        capi.ptr(dy), capi.ptr(x), capi.ptr(mean), capi.ptr(rstd), capi.ptr(g), capi.ptr(dres),
+        capi.ptr(dx), capi.ptr(dg), capi.ptr(db), rows, cols, capi.dtype_code(x),
+        capi.F32 if dparam_f32 else capi.dtype_code(x), capi.ptr(ws), n, capi.stream()))
+    return dx, dg, db
+
+
+def rms_backward(lib, dy, x, rstd, w, dres=None):
+    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+    dx = torch.empty_like(x)
+    dw = torch.empty(cols, device=x.device, dtype=torch.float32) if w is not None else None
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_rmsnorm_backward(
+        capi.ptr(dy), capi.ptr(x), capi.ptr(rstd), capi.ptr(w), capi.ptr(dres), capi.ptr(dx),
+        capi.ptr(dw), rows, cols, capi.dtype_code(x), capi.F32, capi.ptr(ws), n, capi.stream()))
+    return dx, dw
+
+
+# ------------------------------------------------------------------------------------------------
+# BASELINE configurations.
+# ------------------------------------------------------------------------------------------------
+def test_library_exports_every_declared_symbol(lib):
+    for name in capi.declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_c1_layernorm_fp32_32x768(lib):
+    w = WORKLOADS["c1_ln_fwd_fp32_32x768"]
+    inp = make_inputs(w)
+    x, g, b = (cuda(inp[k]) for k in ("x", "gamma", "beta"))
+    y = torch.empty_like(x)
+    capi.check(lib.fln_layernorm(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y), 32, 768,
+                                 capi.F32, w.eps, capi.stream()))
+    ref, _, _ = norms.layer_norm_fwd(to_np(inp["x"]), to_np(inp["gamma"]), to_np(inp["beta"]),
+                                     w.eps)
+    assert np.abs(to_np(y) - ref).max() <= 1e-5
+    ref_t = torch.nn.functional.layer_norm(inp["x"], (768,), inp["gamma"], inp["beta"], w.eps)
+    assert (y.cpu() - ref_t).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("name", ["c2_ln_gelu_fp32_17x1023", "c2_ln_gelu_fp32_64x4096"])
+@pytest.mark.parametrize("mode", ["none", "tanh"])
+def test_c2_layernorm_gelu_fp32(lib, name, mode):
+    w = WORKLOADS[name]
+    inp = make_inputs(w)
+    x, g, b = (cuda(inp[k]) for k in ("x", "gamma", "beta"))
+    y = torch.empty_like(x)
+    capi.check(lib.fln_layernorm_gelu(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y),
+                                      w.rows, w.cols, capi.F32, w.eps,
+                                      capi.GELU_ERF if mode == "none" else capi.GELU_TANH,
+                                      capi.stream()))
+    ref = norms.layer_norm_gelu_fwd(to_np(inp["x"]), to_np(inp["gamma"]), to_np(inp["beta"]),
+                                    w.eps, mode)
+    assert np.abs(to_np(y) - ref).max() <= 1e-5
+
+
+def test_c3_add_layernorm_bf16_8192x4096(lib):
+    w = WORKLOADS["c3_add_ln_fwd_bf16_8192x4096"]
+    inp = make_inputs(w)
+    x, r, g, b = (cuda(inp[k]) for k in ("x", "residual", "gamma", "beta"))
+    y, h = torch.empty_like(x), torch.empty_like(x)
+    mean = torch.empty(w.rows, device="cuda")
+    rstd = torch.empty(w.rows, device="cuda")
+    capi.check(lib.fln_add_layernorm_forward(
+        capi.ptr(x), capi.ptr(r), capi.ptr(g), capi.ptr(b), capi.ptr(h), capi.ptr(y),
+        capi.ptr(mean), capi.ptr(rstd), w.rows, w.cols, capi.BF16, w.eps, capi.stream()))
+    h_ref = (inp["x"] + inp["residual"])  # torch CPU bf16 add: fp32 sum rounded to bf16
+    assert torch.equal(h.cpu(), h_ref), "h must be bit-exact"
+    h_np = norms.round_to_bf16(to_np(inp["x"]) + to_np(inp["residual"]))
+    assert np.array_equal(h_np, to_np(h_ref))
+    y_ref, m_ref, r_ref = c_oracle.layernorm_fwd(h_np, f32(inp["gamma"]), f32(inp["beta"]), w.eps)
+    assert_within_ulp(to_np(y), y_ref, 1.0, what="c3 y")
+    assert np.abs(to_np(mean) - m_ref).max() <= 1e-5 * max(1.0, np.abs(m_ref).max())
+    assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+
+
+def _ln_fwd_bwd_check(lib, name, rows=None):
+    w = WORKLOADS[name]
+    inp = make_inputs(w, rows)
+    x, g, b, dy = (cuda(inp[k]) for k in ("x", "gamma", "beta", "dy"))
+    y, mean, rstd = ln_forward(lib, x, g, b, w.eps)
+    dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+    xs, gs, bs, dys = f32(inp["x"]), f32(inp["gamma"]), f32(inp["beta"]), f32(inp["dy"])
+    y_ref, m_ref, r_ref = c_oracle.layernorm_fwd(xs, gs, bs, w.eps)
+    assert_within_ulp(to_np(y), y_ref, 1.0, what=f"{name} y")
+    assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+    dx_ref, dg_ref, db_ref = c_oracle.layernorm_bwd(dys, xs, gs, w.eps)
+    assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                      what=f"{name} dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, f"{name} dgamma")
+    assert_close_rel(to_np(db), db_ref, 1e-4, f"{name} dbeta")
+
+
+def _rms_fwd_bwd_check(lib, name, rows=None):
+    w = WORKLOADS[name]
+    inp = make_inputs(w, rows)
+    x, g, dy = (cuda(inp[k]) for k in ("x", "gamma", "dy"))
+    y, rstd = rms_forward(lib, x, g, w.eps)
+    dx, dw = rms_backward(lib, dy, x, rstd, g)
+    xs, gs, dys = f32(inp["x"]), f32(inp["gamma"]), f32(inp["dy"])
+    y_ref, r_ref = c_oracle.rmsnorm_fwd(xs, gs, w.eps)
+    assert_within_ulp(to_np(y), y_ref, 1.0, what=f"{name} y")
+    assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+    dx_ref, dw_ref = c_oracle.rmsnorm_bwd(dys, xs, gs, w.eps)
+    assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                      what=f"{name} dx")
+    assert_close_rel(to_np(dw), dw_ref, 1e-4, f"{name} dweight")
+
+
+def test_headline_layernorm_fwd_bwd_bf16_8192x4096(lib):
+    _ln_fwd_bwd_check(lib, "ln_fwd_bwd_bf16_8192x4096")
+
+
+def test_headline_rmsnorm_fwd_bwd_bf16_8192x4096(lib):
+    _rms_fwd_bwd_check(lib, "rms_fwd_bwd_bf16_8192x4096")
+
+
+def test_c4_rmsnorm_fwd_bwd_bf16_16384x8192(lib):
+    _rms_fwd_bwd_check(lib, "c4_rms_fwd_bwd_bf16_16384x8192")
+
+
+def _ordinal(codes):
+    """Signed position of an e4m3fn code on the number line (+0 and -0 both map to 0), so that
+    adjacent representable values differ by exactly 1."""
+    c = codes.astype(np.int32)
+    mag = c & 0x7F
+    return np.where(c & 0x80, -mag, mag)
+
+
+def _fp8_check(q_gpu, s_gpu, q_ref, s_ref, what):
+    s_gpu = s_gpu.astype(np.float64)
+    s_ref = s_ref.astype(np.float64)
+    rel = np.abs(s_gpu - s_ref) / np.where(s_ref > 0, s_ref, 1.0)
+    assert rel.max() <= 1e-6, f"{what}: scale rel err {rel.max():.3g}"
+    diff = np.abs(_ordinal(q_gpu) - _ordinal(q_ref))
+    n_diff = int((diff != 0).sum())
+    assert int(diff.max()) <= 1, f"{what}: a code differs by {int(diff.max())} steps"
+    assert n_diff <= 1e-3 * diff.size, f"{what}: {n_diff} of {diff.size} codes differ"
+
+
+def test_c5_layernorm_fp8_bf16_32768x7168(lib):
+    w = WORKLOADS["c5_ln_fp8_bf16_32768x7168"]
+    inp = make_inputs(w)
+    x, g, b = (cuda(inp[k]) for k in ("x", "gamma", "beta"))
+    q = torch.empty(x.shape, device="cuda", dtype=torch.uint8)
+    scale = torch.empty(w.rows, device="cuda", dtype=torch.float32)
+    capi.check(lib.fln_layernorm_fp8_forward(
+        capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(q), capi.ptr(scale), None, None,
+        w.rows, w.cols, capi.BF16, w.eps, capi.stream()))
+    del x
+    q_ref, s_ref = c_oracle.layernorm_fp8(f32(inp["x"]), f32(inp["gamma"]), f32(inp["beta"]),
+                                          w.eps)
+    _fp8_check(q.cpu().numpy(), to_np(scale), q_ref, s_ref, "c5")
+    # The outlier channels must reach the top of the fp8 range in every row.
+    assert (np.abs(norms.fp8_e4m3fn_decode(q_ref)).max(axis=1) == 448).all()
+
+
+def test_fp8_encoder_bit_exact(lib):
+    """The device conversion (v_cvt_pk_fp8_f32 after a +-448 clamp) against the oracle's
+    format-level encoder, over every exponent of the e4m3fn range and beyond, all 8 mantissa
+    codes, the midpoints between codes (ties to even) and +-1 float32 ulp around them."""
+    vals = [0.0, -0.0, 448.0, -448.0, 449.0, 464.0, 480.0, 1e30, -1e30, 2.0 ** -9, 2.0 ** -10,
+            3 * 2.0 ** -11, 2.0 ** -6, 2.0 ** -7 * 1.0625]
+    for e in range(-12, 10):
+        for m in range(16):  # codes and midpoints (m odd)
+            v = (1.0 + m / 16.0) * 2.0 ** e
+            for d in (-1, 0, 1):
+                f = np.nextafter(np.float32(v), np.float32(np.inf if d > 0 else -np.inf)) \
+                    if d else np.float32(v)
+                vals += [float(f), -float(f)]
+    rng = np.random.RandomState(0)
+    vals += list(rng.randn(20000) * 50)
+    a = np.asarray(vals, np.float32)
+    xg = torch.from_numpy(a).cuda()
+    qg = torch.empty(a.shape, dtype=torch.uint8, device="cuda")
+    capi.check(lib.fln_fp8_e4m3fn_encode(capi.ptr(xg), capi.ptr(qg), a.size, capi.stream()))
+    ref = norms.fp8_e4m3fn_encode(a.astype(np.float64))
+    got = qg.cpu().numpy()
+    bad = np.nonzero(got != ref)[0]
+    assert bad.size == 0, [(float(a[i]), hex(got[i]), hex(ref[i])) for i in bad[:10]]
+
+
+# ------------------------------------------------------------------------------------------------
+# Shapes, dtypes and paths beyond the BASELINE configurations.
+# ------------------------------------------------------------------------------------------------
+EDGE_SHAPES = [(1, 1), (1, 17), (1000, 1), (1, 100000), (512, 512), (1, 32767), (1, 65536),
+               (13, 13), (1, 4095), (1, 4097), (2, 16384), (32, 1)]
+
+
+@pytest.mark.parametrize("rows,cols", EDGE_SHAPES)
+def test_edge_shapes_fp32(lib, rows, cols):
+    """The reference's edge list (tests/edge_cases.py:12-23, test_layernorm.py:340-358) with its
+    tolerance allclose(rtol=1e-4, atol=1e-5) (edge_cases.py:37), against the oracle."""
+    gen = torch.Generator().manual_seed(rows * 100003 + cols)
+    xc = torch.randn(rows, cols, generator=gen)
+    gc = 1 + 0.1 * torch.randn(cols, generator=gen)
+    bc = 0.1 * torch.randn(cols, generator=gen)
+    y, mean, rstd = ln_forward(lib, cuda(xc), cuda(gc), cuda(bc), 1e-5)
+    ref, m_ref, r_ref = norms.layer_norm_fwd(xc.numpy(), gc.numpy(), bc.numpy(), 1e-5)
+    np.testing.assert_allclose(to_np(y), ref, rtol=1e-4, atol=1e-5)
+    if cols == 1:
+        np.testing.assert_array_equal(to_np(y), np.broadcast_to(bc.numpy(), (rows, 1)))
+
+
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+SHAPES = [(1, 768), (8, 768), (32, 1024), (64, 2048), (128, 4096), (3, 1023), (5, 5120),
+          (4, 16384), (2, 32768), (33, 7168), (7, 96)]
+
+
+def _tol_fwd(dtype):
+    return dict(kind="bf16" if dtype == torch.bfloat16 else "f16")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_layernorm_fwd_bwd_matrix(lib, dtype, rows, cols):
+    gen = torch.Generator().manual_seed(rows * 7919 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, b, dy = cuda(xc), cuda(gc), cuda(bc), cuda(dyc)
+    y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+    dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+    xs, gs, bs, dys = f32(xc), f32(gc), f32(bc), f32(dyc)
+    y_ref, _, _ = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
+    dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(y), y_ref, 1.0, **_tol_fwd(dtype), what="y")
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          **_tol_fwd(dtype), what="dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_rmsnorm_fwd_bwd_matrix(lib, dtype, rows, cols):
+    gen = torch.Generator().manual_seed(rows * 104729 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    wc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, wt, dy = cuda(xc), cuda(wc), cuda(dyc)
+    y, rstd = rms_forward(lib, x, wt, 1e-6)
+    dx, dw = rms_backward(lib, dy, x, rstd, wt)
+    xs, ws, dys = f32(xc), f32(wc), f32(dyc)
+    y_ref, _ = norms.rms_norm_fwd(xs, ws, 1e-6)
+    dx_ref, dw_ref = norms.rms_norm_bwd(dys, xs, ws, 1e-6)
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(y), y_ref, 1.0, **_tol_fwd(dtype), what="y")
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          **_tol_fwd(dtype), what="dx")
+    assert_close_rel(to_np(dw), dw_ref, 1e-4, "dweight")
+
+
+def test_unaligned_rows_take_scalar_path(lib):
+    """Input offset by one element (not 16-byte aligned): the scalar path must agree."""
+    gen = torch.Generator().manual_seed(11)
+    base = torch.randn(64 * 1024 + 1, generator=gen).to(torch.bfloat16).cuda()
+    x = base[1:].view(64, 1024)
+    gc = (1 + 0.1 * torch.randn(1024, generator=gen)).to(torch.bfloat16)
+    bc = (0.1 * torch.randn(1024, generator=gen)).to(torch.bfloat16)
+    y, mean, rstd = ln_forward(lib, x, cuda(gc), cuda(bc), 1e-5)
+    ref, _, _ = norms.layer_norm_fwd(f32(x.cpu()), f32(gc), f32(bc), 1e-5)
+    assert_within_ulp(to_np(y), ref, 1.0, what="unaligned y")
+
+
+def test_output_canaries_untouched(lib):
+    """Outputs carved out of larger buffers: the guard bytes after them must survive."""
+    rows, cols, pad = 37, 1000, 4096
+    gen = torch.Generator().manual_seed(5)
+    xc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16)
+    x, g, b = cuda(xc), cuda(gc), cuda(gc * 0.1)
+    ybuf = torch.full((rows * cols + pad,), 7.0, device="cuda", dtype=torch.bfloat16)
+    y = ybuf[: rows * cols].view(rows, cols)
+    mbuf = torch.full((rows + pad,), 7.0, device="cuda")
+    capi.check(lib.fln_layernorm_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y),
+                                         capi.ptr(mbuf), None, rows, cols, capi.BF16, 1e-5,
+                                         capi.stream()))
+    dxbuf = torch.full((rows * cols + pad,), 7.0, device="cuda", dtype=torch.bfloat16)
+    dgbuf = torch.full((cols + pad,), 7.0, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    ln_forward(lib, x, g, b, 1e-5)
+    _, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_layernorm_backward(
+        capi.ptr(x), capi.ptr(x), capi.ptr(mean), capi.ptr(rstd), capi.ptr(g), None,
+        capi.ptr(dxbuf), capi.ptr(dgbuf), None, rows, cols, capi.BF16, capi.F32, capi.ptr(ws), n,
+        capi.stream()))
+    torch.cuda.synchronize()
+    assert (ybuf[rows * cols:] == 7).all()
+    assert (mbuf[rows:] == 7).all()
+    assert (dxbuf[rows * cols:] == 7).all()
+    assert (dgbuf[cols:] == 7).all()
+
+
+def test_backward_is_deterministic(lib):
+    w = WORKLOADS["ln_fwd_bwd_bf16_8192x4096"]
+    inp = make_inputs(w, 2048)
+    x, g, b, dy = (cuda(inp[k]) for k in ("x", "gamma", "beta", "dy"))
+    _, mean, rstd = ln_forward(lib, x, g, b, w.eps)
+    first = ln_backward(lib, dy, x, mean, rstd, g)
+    for _ in range(3):
+        again = ln_backward(lib, dy, x, mean, rstd, g)
+        for a, c in zip(first, again):
+            assert torch.equal(a, c)
+
+
+def test_residual_gradient_is_added(lib):
+    gen = torch.Generator().manual_seed(9)
+    xc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
+    dyc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
+    drc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
+    gc = (1 + 0.1 * torch.randn(2048, generator=gen)).to(torch.bfloat16)
+    x, dy, dr, g = cuda(xc), cuda(dyc), cuda(drc), cuda(gc)
+    _, mean, rstd = ln_forward(lib, x, g, g, 1e-5)
+    dx, _, _ = ln_backward(lib, dy, x, mean, rstd, g, want_params=False, dres=dr)
+    dx_ref, _, _ = norms.layer_norm_bwd(f32(dyc), f32(xc), f32(gc), 1e-5)
+    dx_ref = dx_ref + f32(drc)
+    assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                      what="dx + dres")
+    _, rs = rms_forward(lib, x, g, 1e-6)
+    dxr, _ = rms_backward(lib, dy, x, rs, g, dres=dr)
+    dxr_ref, _ = norms.rms_norm_bwd(f32(dyc), f32(xc), f32(gc), 1e-6)
+    dxr_ref = dxr_ref + f32(drc)
+    assert_within_ulp(to_np(dxr), dxr_ref, 1.0, atol=DX_ATOL_REL * np.abs(dxr_ref).max(),
+                      what="rms dx + dres")
+
+
+def test_add_rmsnorm_bf16(lib):
+    gen = torch.Generator().manual_seed(21)
+    xc = torch.randn(300, 4096, generator=gen).to(torch.bfloat16)
+    rc = torch.randn(300, 4096, generator=gen).to(torch.bfloat16)
+    wc = (1 + 0.02 * torch.randn(4096, generator=gen)).to(torch.bfloat16)
+    x, r, wt = cuda(xc), cuda(rc), cuda(wc)
+    y, h = torch.empty_like(x), torch.empty_like(x)
+    rstd = torch.empty(300, device="cuda")
+    capi.check(lib.fln_add_rmsnorm_forward(capi.ptr(x), capi.ptr(r), capi.ptr(wt), capi.ptr(h),
+                                           capi.ptr(y), capi.ptr(rstd), 300, 4096, capi.BF16,
+                                           1e-6, capi.stream()))
+    assert torch.equal(h.cpu(), xc + rc)
+    y_ref, h_ref, _ = norms.add_rms_norm_fwd(f32(xc), f32(rc), f32(wc), 1e-6, "bf16")
+    assert_within_ulp(to_np(y), y_ref, 1.0, what="add_rms y")
+
+
+def test_looped_fallback_matches_register_path(lib, monkeypatch):
+    gen = torch.Generator().manual_seed(3)
+    xc = torch.randn(40, 3072, generator=gen)
+    gc = 1 + 0.1 * torch.randn(3072, generator=gen)
+    x, g = cuda(xc), cuda(gc)
+    y_reg, m_reg, r_reg = ln_forward(lib, x, g, g, 1e-5)
+    monkeypatch.setenv("FLN_FORCE_LOOP", "1")
+    y_loop, m_loop, r_loop = ln_forward(lib, x, g, g, 1e-5)
+    monkeypatch.delenv("FLN_FORCE_LOOP")
+    ref, _, _ = norms.layer_norm_fwd(xc.numpy(), gc.numpy(), gc.numpy(), 1e-5)
+    assert np.abs(to_np(y_loop) - ref).max() <= 1e-5 * np.abs(ref).max()
+    assert np.abs(to_np(y_reg) - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_float64_forward(lib):
+    gen = torch.Generator().manual_seed(4)
+    xc = torch.randn(10, 777, generator=gen, dtype=torch.float64)
+    gc = 1 + 0.1 * torch.randn(777, generator=gen, dtype=torch.float64)
+    y = torch.empty(10, 777, device="cuda", dtype=torch.float64)
+    capi.check(lib.fln_layernorm(capi.ptr(cuda(xc)), capi.ptr(cuda(gc)), capi.ptr(cuda(gc)),
+                                 capi.ptr(y), 10, 777, capi.F64, 1e-5, capi.stream()))
+    ref, _, _ = norms.layer_norm_fwd(xc.numpy(), gc.numpy(), gc.numpy(), 1e-5)
+    assert np.abs(y.cpu().numpy() - ref).max() <= 1e-12
+
+
+def test_invalid_arguments_are_rejected_before_launch(lib):
+    x = torch.zeros(4, 8, device="cuda")
+    y = torch.empty_like(x)
+    s = capi.stream()
+    assert lib.fln_layernorm(capi.ptr(x), None, None, capi.ptr(y), -1, 8, capi.F32, 1e-5, s) == 1
+    assert lib.fln_layernorm(None, None, None, capi.ptr(y), 4, 8, capi.F32, 1e-5, s) == 1
+    assert lib.fln_layernorm(capi.ptr(x), None, None, capi.ptr(y), 4, 8, 99, 1e-5, s) == 1
+    assert lib.fln_layernorm_gelu(capi.ptr(x), None, None, capi.ptr(y), 4, 8, capi.F32, 1e-5, 7,
+                                  s) == 1
+    mean = torch.zeros(4, device="cuda")
+    dg = torch.empty(8, device="cuda")
+    # dgamma requested without a workspace
+    assert lib.fln_layernorm_backward(capi.ptr(x), capi.ptr(x), capi.ptr(mean), capi.ptr(mean),
+                                      None, None, None, capi.ptr(dg), None, 4, 8, capi.F32,
+                                      capi.F32, None, 0, s) == 1
+    assert lib.fln_layernorm(capi.ptr(x), None, None, capi.ptr(y), 0, 8, capi.F32, 1e-5, s) == 0
