@@ -1,6 +1,6 @@
 """Benchmark of the fused normalization hot path on one MI355X.
 
-Default workload (BASELINE metric): LayerNorm forward + backward, bf16, 8192 x 4096 -- one
+Default workload (the headline metric): LayerNorm forward + backward, bf16, 8192 x 4096 -- one
 "step" is the forward (y, mean, rstd) plus the backward (dx, dgamma, dbeta) over one batch, with
 inputs already resident in HBM.  The RMSNorm forward + backward at the same shape is timed the
 same way and reported under "rms_fwd_bwd".
@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate host time budget of the CPU baseline")
     ap.add_argument("--all", action="store_true",
-                    help="also time every BASELINE config (C1..C5) and report them")
+                    help="also time every benchmark config (C1..C5) and report them")
     return ap.parse_args()
 
 
@@ -223,7 +223,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
-              "multi-GPU layout is described in DESIGN.md and not measured here.",
+              "row-sharded multi-GPU layout is not built or measured here.",
               file=sys.stderr)
         sys.exit(2)
 

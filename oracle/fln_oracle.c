@@ -1,6 +1,6 @@
 /*
  * fln_oracle.c -- plain-C restatement of the fused normalization path (TEST INFRASTRUCTURE ONLY:
- * used by tests/ as a checker at full BASELINE sizes and by bench.py's cpu_baseline leg as the
+ * used by tests/ as a checker at the full benchmark sizes and by bench.py's cpu_baseline leg as the
  * CPU port that is timed; never linked into the product library).
  *
  * Scalar, single-threaded, float64 accumulation.  Inputs are float32 arrays (bf16/f16 values

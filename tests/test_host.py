@@ -1,0 +1,171 @@
+"""Host-side tests (CPU only): the C-ABI library loads and exports every declared symbol, the
+binding validates arguments before anything is launched, the operator schemas trace with fake
+tensors, and the host utilities keep the reference's formulas."""
+import ctypes
+
+import pytest
+import torch
+
+import capi
+import fused_layernorm as fl
+import fused_layernorm_cuda as ext
+from fused_layernorm.testing import WORKLOADS, algorithmic_bytes
+
+
+def test_c_abi_library_exports_every_declared_symbol():
+    lib = capi.load()
+    declared = capi.declared_functions()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/fused_layernorm.h but not exported"
+    assert set(declared) <= set(capi.SIGNATURES), "tests/capi.py lacks a signature"
+
+
+def test_c_abi_rejects_bad_arguments_without_a_device():
+    lib = capi.load()
+    # Every one of these fails validation before any HIP call is made.
+    assert lib.fln_layernorm(None, None, None, None, -1, 8, capi.F32, 1e-5, None) == 1
+    assert lib.fln_layernorm(None, None, None, None, 4, 8, capi.F32, 1e-5, None) == 1
+    assert lib.fln_layernorm(ctypes.c_void_p(16), None, None, ctypes.c_void_p(16), 4, 8, 77,
+                             1e-5, None) == 1
+    assert lib.fln_layernorm(ctypes.c_void_p(16), None, None, ctypes.c_void_p(16), 4, 8,
+                             capi.F32, -1.0, None) == 1
+    assert lib.fln_layernorm_gelu(ctypes.c_void_p(16), None, None, ctypes.c_void_p(16), 4, 8,
+                                  capi.F32, 1e-5, 0, None) == 1
+    assert lib.fln_layernorm_fp8_forward(ctypes.c_void_p(16), None, None, ctypes.c_void_p(16),
+                                         None, None, None, 4, 8, capi.F64, 1e-5, None) == 1
+    assert lib.fln_rmsnorm_backward(None, None, None, None, None, None, None, 4, 8, capi.F64,
+                                    capi.F32, None, 0, None) == 1
+    # empty problems are a successful no-op
+    assert lib.fln_layernorm(None, None, None, None, 0, 8, capi.F32, 1e-5, None) == 0
+    assert lib.fln_error_string(1).decode().startswith("invalid argument")
+
+
+def test_version_attributes():
+    assert ext.__version__ == "1.0.0" == capi.load().fln_version().decode()
+    assert ext.__cuda_version__ == ext.__hip_version__ == capi.load().fln_hip_version()
+    assert fl.__version__ == "1.0.0"
+
+
+def test_get_memory_usage_matches_reference_formula():
+    # csrc/layernorm_cuda.cpp:144-164
+    for b, h, mp in [(32, 768, False), (8, 4096, True), (1, 1, False)]:
+        es = 2 if mp else 4
+        expect = 2 * b * h * es + 2 * b * 4 + b * h * es + 2 * h * es + b * 32 * 4
+        assert ext.get_memory_usage(b, h, mp) == expect
+        assert ext.get_memory_usage(batch_size=b, hidden_size=h, use_mixed_precision=mp) == expect
+
+
+def test_performance_hints_wording():
+    s = ext.get_performance_hints(4, 100)
+    assert "hidden_size is not divisible by 32" in s
+    assert "Small batch size" in s
+    assert "Not enough blocks" in s
+    assert "Large hidden dimension" in ext.get_performance_hints(100000, 16384)
+
+
+def _cpu(*shape, dtype=torch.float32):
+    return torch.randn(*shape).to(dtype)
+
+
+@pytest.mark.parametrize("call", [
+    lambda: ext.layernorm(_cpu(4, 8), _cpu(8), _cpu(8), 1e-5),
+    lambda: ext.layernorm_gelu(_cpu(4, 8), _cpu(8), _cpu(8)),
+    lambda: ext.forward(_cpu(4, 8)),
+    lambda: ext.rms_norm_forward(_cpu(4, 8)),
+    lambda: ext.layernorm_fp8_forward(_cpu(4, 8)),
+    lambda: ext.backward(_cpu(4, 8), _cpu(4, 8), _cpu(4), _cpu(4)),
+])
+def test_binding_rejects_cpu_tensors(call):
+    with pytest.raises(RuntimeError, match="GPU"):
+        call()
+
+
+def test_binding_reports_bad_shapes_and_dtypes_before_launch():
+    # The device check comes first on CPU tensors; shape and dtype checks are exercised on
+    # fake GPU tensors through the dispatcher-free Python checks of the module API.
+    with pytest.raises(ValueError):
+        fl.FusedLayerNormFunction.apply(_cpu(2, 3, 4), (4,), None, None, 1e-5)
+    with pytest.raises(ValueError):
+        fl.FusedLayerNormFunction.apply(_cpu(2, 4), (5,), None, None, 1e-5)
+    with pytest.raises(RuntimeError, match="normalized_shape"):
+        fl.layer_norm(_cpu(2, 4), (5,))
+
+
+def test_fake_tensor_shapes_of_every_op():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(3, 5, 64, device="cuda", dtype=torch.bfloat16)
+        w = torch.empty(64, device="cuda", dtype=torch.bfloat16)
+        y, m, r = torch.ops.fused_layernorm.layer_norm_fwd(x, w, w, 1e-5)
+        assert y.shape == x.shape and m.shape == (3, 5) and m.dtype == torch.float32
+        dx, dw, db = torch.ops.fused_layernorm.layer_norm_bwd(x, x, m, r, w, w,
+                                                              [True, True, False], None)
+        assert dx.shape == x.shape and dw.shape == (64,) and db.numel() == 0
+        y, r = torch.ops.fused_layernorm.rms_norm_fwd(x, w, 1e-6)
+        assert r.shape == (3, 5)
+        y, h, m, r = torch.ops.fused_layernorm.add_layer_norm_fwd(x, x, w, None, 1e-5)
+        assert h.shape == x.shape
+        q, s = torch.ops.fused_layernorm.layer_norm_fp8_fwd(x, None, None, 1e-5)
+        assert q.dtype == torch.float8_e4m3fn and s.shape == (3, 5)
+        assert fl.layer_norm_gelu(x, 64, w, w, approximate="none").shape == x.shape
+        y2, h2 = fl.add_rms_norm(x, x, (64,), w)
+        assert y2.shape == x.shape == h2.shape
+
+
+def test_module_state_dict_keys_match_nn_layernorm():
+    a = fl.FusedLayerNorm(768)
+    b = torch.nn.LayerNorm(768)
+    assert a.state_dict().keys() == b.state_dict().keys()
+    assert torch.equal(a.weight, b.weight) and torch.equal(a.bias, b.bias)
+    a.load_state_dict(b.state_dict())
+    assert repr(a) == "FusedLayerNorm((768,), eps=1e-05, elementwise_affine=True)"
+    assert fl.FusedLayerNorm(16, elementwise_affine=False).weight is None
+    assert fl.FusedRMSNorm(16).state_dict().keys() == torch.nn.RMSNorm(16).state_dict().keys()
+
+
+def test_replace_and_restore_torch_layernorm(capsys):
+    orig = torch.nn.LayerNorm
+    fl.replace_torch_layernorm()
+    try:
+        assert torch.nn.LayerNorm is fl.FusedLayerNorm
+    finally:
+        fl.restore_torch_layernorm()
+    assert torch.nn.LayerNorm is orig
+    out = capsys.readouterr().out
+    assert "Successfully replaced torch.nn.LayerNorm with FusedLayerNorm" in out
+    assert "Restored original torch.nn.LayerNorm" in out
+
+
+def test_profiler_utilities():
+    p = fl.functional.get_profiler()
+    fl.functional.enable_profiling()
+    p.record(32, 768, 0.01, 0.02)
+    p.record(32, 768, 0.03, 0.04)
+    res = fl.functional.disable_profiling()
+    assert res["num_calls"] == 2 and res["total"]["max_ms"] == pytest.approx(0.07)
+    with pytest.raises(RuntimeError):
+        fl.functional.check_input_dtype_and_device(_cpu(2, 4))
+
+
+def test_optimal_config_reports_dispatch_geometry():
+    c = fl.functional.get_optimal_config(8192, 4096, torch.bfloat16)
+    assert c["register_resident"] and c["vector_elems"] == 8
+    assert c["waves_per_row"] * 64 * c["vectors_per_lane"] * c["vector_elems"] >= 4096
+    c2 = fl.functional.get_optimal_config(1, 100000, torch.float32)
+    assert not c2["register_resident"]
+
+
+def test_byte_model_matches_baseline_figures():
+    expect = {
+        "c1_ln_fwd_fp32_32x768": 202752,
+        "c2_ln_gelu_fp32_17x1023": 147312,
+        "c2_ln_gelu_fp32_64x4096": 2129920,
+        "c3_add_ln_fwd_bf16_8192x4096": 268451840,
+        "c4_rms_fwd_bwd_bf16_16384x8192": 1342373888,
+        "c5_ln_fp8_bf16_32768x7168": 704802816,
+        "ln_fwd_bwd_bf16_8192x4096": 335732736,
+        "rms_fwd_bwd_bf16_8192x4096": 335642624,
+    }
+    for name, nbytes in expect.items():
+        assert algorithmic_bytes(WORKLOADS[name])["total"] == nbytes, name

@@ -1,0 +1,259 @@
+"""Pins the CPU oracle (oracle/norms.py, oracle/fln_oracle.c) -- CPU only.
+
+The reference ships no golden vectors or known-answer files (its tests compare live against
+PyTorch on the GPU), so each oracle function is pinned by checks chosen so that a plausible
+mistake (dropped term, wrong sign, wrong reduction axis, biased/unbiased mix-up, transposed
+operand, wrong rounding) fails at least one of them:
+  * library routines: torch-CPU F.layer_norm / F.rms_norm / F.gelu and autograd in float64;
+  * closed forms and invariants (hand-computed rows, mean 0 / variance 1, N = 1, constant rows);
+  * finite differences (torch.autograd.gradcheck on the oracle's closed-form backward);
+  * a known-answer table and an exhaustive decode/encode round trip for fp8 e4m3fn, plus
+    torch's own float8_e4m3fn cast after clamping;
+  * the C oracle against the numpy oracle.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import c_oracle, norms
+
+
+def t64(a):
+    return torch.tensor(np.asarray(a), dtype=torch.float64)
+
+
+@pytest.fixture(scope="module")
+def rng():
+    return np.random.RandomState(1234)
+
+
+# ---------------------------------------------------------------- LayerNorm forward
+def test_layer_norm_hand_computed_row():
+    # x = [1, 2, 3, 4]: mean 2.5, biased variance 1.25 (reference kernel.cu:69-80 divides by N).
+    y, mean, rstd = norms.layer_norm_fwd(np.array([[1.0, 2.0, 3.0, 4.0]]), eps=0.0)
+    assert mean[0] == 2.5
+    assert rstd[0] == pytest.approx(1 / math.sqrt(1.25), rel=1e-15)
+    np.testing.assert_allclose(y[0], (np.array([1, 2, 3, 4]) - 2.5) / math.sqrt(1.25),
+                               rtol=1e-15)
+
+
+@pytest.mark.parametrize("shape", [(3, 5), (7, 768), (2, 3, 1023), (4, 4096)])
+def test_layer_norm_matches_torch(rng, shape):
+    x = rng.randn(*shape) * 3 + 0.5
+    g = 1 + 0.1 * rng.randn(shape[-1])
+    b = 0.1 * rng.randn(shape[-1])
+    for gg, bb in ((g, b), (None, None), (g, None), (None, b)):
+        y, _, _ = norms.layer_norm_fwd(x, gg, bb, 1e-5)
+        yt = F.layer_norm(t64(x), (shape[-1],), None if gg is None else t64(gg),
+                          None if bb is None else t64(bb), 1e-5)
+        np.testing.assert_allclose(y, yt.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_layer_norm_invariants(rng):
+    x = rng.randn(16, 513) * 1000 + 7
+    y, _, _ = norms.layer_norm_fwd(x, eps=0.0)
+    np.testing.assert_allclose(y.mean(-1), 0, atol=1e-12)
+    np.testing.assert_allclose(y.var(-1), 1, rtol=1e-12)  # biased variance == 1
+    # N = 1 and constant rows -> the output is beta exactly
+    b = np.array([0.25])
+    y1, _, _ = norms.layer_norm_fwd(rng.randn(9, 1), np.array([3.0]), b)
+    assert (y1 == 0.25).all()
+    yc, _, _ = norms.layer_norm_fwd(np.full((2, 768), 1e8), None, np.full(768, -0.5))
+    assert (yc == -0.5).all()
+
+
+def test_gelu_matches_torch_and_reference_formula(rng):
+    v = rng.randn(10000) * 4
+    np.testing.assert_allclose(norms.gelu(v, "none"), F.gelu(t64(v)).numpy(), rtol=1e-12,
+                               atol=1e-14)
+    np.testing.assert_allclose(norms.gelu(v, "tanh"),
+                               F.gelu(t64(v), approximate="tanh").numpy(), rtol=1e-12,
+                               atol=1e-14)
+    # reference formula, csrc/layernorm_cuda_kernel.cu:31-36
+    s = math.sqrt(2 / math.pi)
+    ref = [0.5 * a * (1 + math.tanh(s * (a + 0.044715 * a ** 3))) for a in v[:50]]
+    np.testing.assert_allclose(norms.gelu(v[:50], "tanh"), ref, rtol=1e-13, atol=1e-15)
+    assert norms.gelu(np.array([0.0]), "none")[0] == 0.0
+    np.testing.assert_allclose(norms.gelu(np.array([40.0, -40.0]), "none"), [40.0, 0.0])
+
+
+def test_layer_norm_gelu_composition(rng):
+    x, g, b = rng.randn(5, 64), 1 + 0.1 * rng.randn(64), 0.1 * rng.randn(64)
+    y = norms.layer_norm_gelu_fwd(x, g, b, 1e-5, "none")
+    yt = F.gelu(F.layer_norm(t64(x), (64,), t64(g), t64(b), 1e-5))
+    np.testing.assert_allclose(y, yt.numpy(), rtol=1e-12, atol=1e-14)
+
+
+# ---------------------------------------------------------------- RMSNorm, residual
+def test_rms_norm_matches_torch(rng):
+    x, w = rng.randn(6, 1000) * 2, 1 + 0.1 * rng.randn(1000)
+    y, rstd = norms.rms_norm_fwd(x, w, 1e-6)
+    yt = F.rms_norm(t64(x), (1000,), t64(w), 1e-6)
+    np.testing.assert_allclose(y, yt.numpy(), rtol=1e-12)
+    np.testing.assert_allclose(rstd, 1 / np.sqrt((x ** 2).mean(-1) + 1e-6), rtol=1e-14)
+
+
+def test_bf16_rounding_matches_torch(rng):
+    a = np.concatenate([rng.randn(100000).astype(np.float32) * 10,
+                        np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 0.0, -0.0,
+                                  np.inf, -np.inf, 3.4e38], np.float32)])
+    ours = norms.round_to_bf16(a)
+    theirs = torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+    # ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> 1
+    assert norms.round_to_bf16(np.float32(1 + 2 ** -8)) == 1.0
+
+
+def test_add_layer_norm_rounds_h_before_statistics(rng):
+    x = torch.randn(4, 256).to(torch.bfloat16)
+    r = torch.randn(4, 256).to(torch.bfloat16)
+    y, h, _, _ = norms.add_layer_norm_fwd(x.float().numpy(), r.float().numpy(), eps=1e-5)
+    h_t = (x + r).float()
+    assert np.array_equal(h, h_t.numpy())
+    yt = F.layer_norm(h_t.double(), (256,), eps=1e-5)
+    np.testing.assert_allclose(y, yt.numpy(), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- backward
+@pytest.mark.parametrize("shape", [(3, 5), (16, 768), (2, 4, 33)])
+def test_layer_norm_backward_matches_autograd(rng, shape):
+    x, dy = rng.randn(*shape), rng.randn(*shape)
+    g, b = 1 + 0.1 * rng.randn(shape[-1]), 0.1 * rng.randn(shape[-1])
+    xt, gt, bt = (t64(a).requires_grad_(True) for a in (x, g, b))
+    F.layer_norm(xt, (shape[-1],), gt, bt, 1e-5).backward(t64(dy))
+    dx, dg, db = norms.layer_norm_bwd(dy, x, g, 1e-5)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dg, gt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(db, bt.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("shape", [(3, 5), (16, 768)])
+def test_rms_norm_backward_matches_autograd(rng, shape):
+    x, dy, w = rng.randn(*shape), rng.randn(*shape), 1 + 0.1 * rng.randn(shape[-1])
+    xt, wt = t64(x).requires_grad_(True), t64(w).requires_grad_(True)
+    F.rms_norm(xt, (shape[-1],), wt, 1e-6).backward(t64(dy))
+    dx, dw = norms.rms_norm_bwd(dy, x, w, 1e-6)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, wt.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_backward_closed_forms_against_finite_differences(rng):
+    """Brute force: central differences of sum(dy * LN(x)) and sum(dy * RMS(x))."""
+    x, dy, g = rng.randn(3, 5), rng.randn(3, 5), 1 + 0.3 * rng.randn(5)
+    b = 0.2 * rng.randn(5)
+    h = 1e-6
+
+    def loss_ln(xx, gg, bb):
+        return float((dy * norms.layer_norm_fwd(xx, gg, bb, 1e-5)[0]).sum())
+
+    def loss_rms(xx, gg):
+        return float((dy * norms.rms_norm_fwd(xx, gg, 1e-6)[0]).sum())
+
+    dx, dg, db = norms.layer_norm_bwd(dy, x, g, 1e-5)
+    dxr, dgr = norms.rms_norm_bwd(dy, x, g, 1e-6)
+    for idx in np.ndindex(x.shape):
+        e = np.zeros_like(x)
+        e[idx] = h
+        fd = (loss_ln(x + e, g, b) - loss_ln(x - e, g, b)) / (2 * h)
+        assert fd == pytest.approx(dx[idx], rel=1e-5, abs=1e-7)
+        fdr = (loss_rms(x + e, g) - loss_rms(x - e, g)) / (2 * h)
+        assert fdr == pytest.approx(dxr[idx], rel=1e-5, abs=1e-7)
+    for j in range(5):
+        e = np.zeros(5)
+        e[j] = h
+        assert (loss_ln(x, g + e, b) - loss_ln(x, g - e, b)) / (2 * h) == \
+            pytest.approx(dg[j], rel=1e-6, abs=1e-8)
+        assert (loss_ln(x, g, b + e) - loss_ln(x, g, b - e)) / (2 * h) == \
+            pytest.approx(db[j], rel=1e-6, abs=1e-8)
+        assert (loss_rms(x, g + e) - loss_rms(x, g - e)) / (2 * h) == \
+            pytest.approx(dgr[j], rel=1e-6, abs=1e-8)
+
+
+# ---------------------------------------------------------------- fp8 e4m3fn
+KNOWN_FP8 = [
+    (0.0, 0x00), (-0.0, 0x80), (448.0, 0x7E), (-448.0, 0xFE), (2.0 ** -9, 0x01),
+    (2.0 ** -6, 0x08), (0.0625, 0x18), (1.0, 0x38), (-1.0, 0xB8), (1.125, 0x39), (1.75, 0x3E),
+    (2.0, 0x40), (240.0, 0x77), (256.0, 0x78), (416.0, 0x7D),
+    (1.0625, 0x38),            # tie between 1.0 (even) and 1.125 -> 1.0
+    (1.1875, 0x3A),            # tie between 1.125 and 1.25 (even) -> 1.25
+    (2.0 ** -10, 0x00),        # tie between 0 and the smallest subnormal -> 0
+    (3 * 2.0 ** -10, 0x02),    # tie between 1 and 2 subnormal steps -> 2 (even)
+    (464.0, 0x7E), (480.0, 0x7E), (1e6, 0x7E), (-1e6, 0xFE),  # saturation
+]
+
+
+def test_fp8_known_answers():
+    vals = np.array([v for v, _ in KNOWN_FP8])
+    codes = norms.fp8_e4m3fn_encode(vals)
+    assert [int(c) for c in codes] == [c for _, c in KNOWN_FP8]
+    assert [c_oracle.fp8_encode_scalar(v) for v in vals] == [c for _, c in KNOWN_FP8]
+    assert norms.fp8_e4m3fn_encode(np.array([np.nan]))[0] == 0x7F
+
+
+def test_fp8_decode_encode_round_trip_all_codes():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    vals = norms.fp8_e4m3fn_decode(codes)
+    assert np.array_equal(norms.fp8_e4m3fn_encode(vals), codes)
+    # decoded values are strictly increasing over the positive codes (no gaps, no overlaps)
+    pos = norms.fp8_e4m3fn_decode(np.arange(0, 0x7F, dtype=np.uint8))
+    assert (np.diff(pos) > 0).all() and pos[-1] == 448.0
+
+
+def test_fp8_matches_torch_cast_after_clamp(rng):
+    v = np.concatenate([rng.randn(200000) * 100, rng.randn(50000) * 0.01,
+                        np.linspace(-450, 450, 100001)]).astype(np.float32)
+    ours = norms.fp8_e4m3fn_encode(v.astype(np.float64))
+    t = torch.from_numpy(np.clip(v, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert np.array_equal(ours, t.numpy())
+
+
+def test_layer_norm_fp8_row_scale_and_codes(rng):
+    x = rng.randn(8, 300).astype(np.float32)
+    x[:, 7] *= 20
+    q, s = norms.layer_norm_fp8_fwd(x, None, None, 1e-5)
+    y, _, _ = norms.layer_norm_fwd(x, None, None, 1e-5)
+    np.testing.assert_allclose(s, np.abs(y).max(-1) / 448, rtol=1e-7)
+    assert (np.abs(norms.fp8_e4m3fn_decode(q)).max(-1) == 448).all()
+    deq = norms.fp8_e4m3fn_decode(q) * s[:, None]
+    assert np.abs(deq - y).max() <= np.abs(y).max() * 2 ** -4  # 3 mantissa bits
+    qz, sz = norms.layer_norm_fp8_fwd(np.zeros((2, 16), np.float32), None, None)
+    assert (qz == 0).all() and (sz == 0).all()
+
+
+# ---------------------------------------------------------------- C oracle vs numpy oracle
+def test_c_oracle_matches_numpy_oracle(rng):
+    x = rng.randn(9, 1023).astype(np.float32)
+    dy = rng.randn(9, 1023).astype(np.float32)
+    g = (1 + 0.1 * rng.randn(1023)).astype(np.float32)
+    b = (0.1 * rng.randn(1023)).astype(np.float32)
+    y, m, r = c_oracle.layernorm_fwd(x, g, b, 1e-5)
+    yn, mn, rn = norms.layer_norm_fwd(x, g, b, 1e-5)
+    np.testing.assert_allclose(y, yn, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(m, mn, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(r, rn, rtol=1e-13)
+    dx, dg, db = c_oracle.layernorm_bwd(dy, x, g, 1e-5)
+    dxn, dgn, dbn = norms.layer_norm_bwd(dy, x, g, 1e-5)
+    np.testing.assert_allclose(dx, dxn, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(dg, dgn, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(db, dbn, rtol=1e-12, atol=1e-12)
+    yr, rr = c_oracle.rmsnorm_fwd(x, g, 1e-6)
+    yrn, rrn = norms.rms_norm_fwd(x, g, 1e-6)
+    np.testing.assert_allclose(yr, yrn, rtol=1e-6, atol=1e-6)
+    dxr, dwr = c_oracle.rmsnorm_bwd(dy, x, g, 1e-6)
+    dxrn, dwrn = norms.rms_norm_bwd(dy, x, g, 1e-6)
+    np.testing.assert_allclose(dxr, dxrn, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(dwr, dwrn, rtol=1e-12, atol=1e-12)
+    q, s = c_oracle.layernorm_fp8(x, g, b, 1e-5)
+    qn, sn = norms.layer_norm_fp8_fwd(x, g, b, 1e-5)
+    assert np.array_equal(q, qn)
+    np.testing.assert_allclose(s, sn, rtol=1e-7)
+
+
+def test_c_fp8_encoder_matches_numpy_on_a_sweep(rng):
+    v = np.concatenate([rng.randn(3000) * 100, rng.randn(1000) * 1e-3,
+                        [(1 + m / 16) * 2.0 ** e for e in range(-11, 10) for m in range(16)]])
+    ours = norms.fp8_e4m3fn_encode(v)
+    assert [c_oracle.fp8_encode_scalar(a) for a in v] == [int(c) for c in ours]
