@@ -54,7 +54,8 @@ class Runner:
         self.lib, self.capi, self.torch, self.w = lib, capi, torch, w
         dev = "cuda"
         x = inputs["x"]
-        set_bytes = x.numel() * x.element_size() * (4 if "dy" in inputs else 2)
+        set_bytes = x.numel() * x.element_size() * (4 if ("dy" in inputs or
+                                                         "residual" in inputs) else 2)
         self.nsets = max(1, -(-ROTATE_BYTES // set_bytes))
         self.sets = []
         for k in range(self.nsets):
@@ -62,6 +63,11 @@ class Runner:
             if k > 0:  # distinct buffers, same values
                 s = {n: t.clone() for n, t in s.items()}
             s["y"] = torch.empty_like(s["x"])
+            if w.op == "add_layer_norm":
+                s["h"] = torch.empty_like(s["x"])
+            if w.op == "layer_norm_fp8":
+                s["q"] = torch.empty(s["x"].shape, device=dev, dtype=torch.uint8)
+                s["scale"] = torch.empty(w.rows, device=dev)
             s["mean"] = torch.empty(w.rows, device=dev)
             s["rstd"] = torch.empty(w.rows, device=dev)
             if "dy" in s:
@@ -77,7 +83,25 @@ class Runner:
 
     def fwd(self, s, stream):
         c, p = self.capi, self.capi.ptr
-        if self.w.op.startswith("rms"):
+        if self.w.op == "add_layer_norm":
+            rc = self.lib.fln_add_layernorm_forward(
+                p(s["x"]), p(s["residual"]), p(s.get("gamma")), p(s.get("beta")), p(s["h"]),
+                p(s["y"]), None, None, self.rows, self.cols, self.code, self.w.eps, stream)
+        elif self.w.op == "layer_norm_fp8":
+            rc = self.lib.fln_layernorm_fp8_forward(
+                p(s["x"]), p(s.get("gamma")), p(s.get("beta")), p(s["q"]), p(s["scale"]), None,
+                None, self.rows, self.cols, self.code, self.w.eps, stream)
+        elif self.w.op in ("layer_norm", "layer_norm_gelu"):
+            gelu = {"none": c.GELU_ERF, "tanh": c.GELU_TANH}[self.w.approximate]
+            if self.w.op == "layer_norm":
+                rc = self.lib.fln_layernorm(p(s["x"]), p(s.get("gamma")), p(s.get("beta")),
+                                            p(s["y"]), self.rows, self.cols, self.code,
+                                            self.w.eps, stream)
+            else:
+                rc = self.lib.fln_layernorm_gelu(p(s["x"]), p(s.get("gamma")), p(s.get("beta")),
+                                                 p(s["y"]), self.rows, self.cols, self.code,
+                                                 self.w.eps, gelu, stream)
+        elif self.w.op.startswith("rms"):
             rc = self.lib.fln_rmsnorm_forward(p(s["x"]), p(s.get("gamma")), p(s["y"]),
                                               p(s["rstd"]), self.rows, self.cols, self.code,
                                               self.w.eps, stream)

@@ -21,36 +21,39 @@
 
 namespace fln {
 
-template <class T, int VEC, int VPL, int MAXT>
+template <class T, bool DRES, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   __shared__ float red[2][2][MAXT / kWave];  // [double buffer][sum g, sum g*xhat][wave]
   __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
   using P = Pack<T, VEC>;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wpr = p.wpr;
   const int rg = wave / wpr;
   const int t = (wave - rg * wpr) * kWave + lane;
   const int tpr = kWave * wpr;
   const int rgs = p.rgs;
   const int64_t N = p.cols;
-  const int nvec = static_cast<int>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
   const float inv_n = 1.0f / static_cast<float>(N);
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * p.rows_per_block;
   const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
   const int iters = static_cast<int>((p.rows_per_block + rgs - 1) / rgs);
+  const T* X = static_cast<const T*>(p.x);
+  const T* DY = static_cast<const T*>(p.dy);
+  const T* DR = static_cast<const T*>(p.dres);
+  T* DX = static_cast<T*>(p.dx);
 
-  // gamma stays packed in the I/O type (half the VGPRs of an fp32 copy for 16-bit types).
-  P gam[VPL];
+  // gamma in fp32 registers (ones when absent; zeros past the row).
+  float gam[VPL][VEC];
   {
-    const P* gr = static_cast<const P*>(p.gamma);
-    P ones;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) ones.v[e] = static_cast<T>(1.0f);
+    const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
+    const bool has_g = p.gamma != nullptr;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int v = t + i * tpr;
-      gam[i] = gr ? (v < nvec ? gr[v] : zero_pack<T, VEC>()) : ones;
+      const P gv = buf_load<P>(gr, t + i * tpr);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) gam[i][e] = has_g ? to_f32(gv.v[e]) : 1.0f;
     }
   }
   float acc_g[VPL][VEC], acc_b[VPL][VEC];
@@ -59,33 +62,67 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc_g[i][e] = acc_b[i][e] = 0.0f;
 
-  for (int it = 0; it < iters; ++it) {
-    const int64_t row = r0 + static_cast<int64_t>(it) * rgs + rg;
-    const bool row_ok = row < r1;
-    const P* xr = reinterpret_cast<const P*>(static_cast<const T*>(p.x) + row * N);
-    const P* dr = reinterpret_cast<const P*>(static_cast<const T*>(p.dy) + row * N);
-    P xv[VPL], dv[VPL];
+  auto row_of = [&](int it) { return r0 + static_cast<int64_t>(it) * rgs + rg; };
+  auto bytes_of = [&](int it) -> uint32_t { return row_of(it) < r1 ? row_bytes : 0u; };
+
+  // Raw loads of the row in flight (x, dy, dres, mean, rstd); rows past the block's range have
+  // zero-byte resources and read as zeros.
+  P xn[VPL], dn[VPL], rn[VPL];
+  float mun = 0.0f, rsn = 0.0f;
+  auto load_row = [&](int it) {
+    const int64_t row = row_of(it);
+    const uint32_t nb = bytes_of(it);
+    const rsrc_t xr = make_rsrc(X + row * N, nb);
+    const rsrc_t dr = make_rsrc(DY + row * N, nb);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int v = t + i * tpr;
-      const bool ok = row_ok && v < nvec;
-      xv[i] = ok ? xr[v] : zero_pack<T, VEC>();
-      dv[i] = ok ? dr[v] : zero_pack<T, VEC>();
+      xn[i] = buf_load<P>(xr, t + i * tpr);
+      dn[i] = buf_load<P>(dr, t + i * tpr);
     }
-    const float mu = (row_ok && !p.rms) ? p.mean[row] : 0.0f;
-    const float rs = row_ok ? p.rstd[row] : 0.0f;
+    if constexpr (DRES) {
+      const rsrc_t rr = make_rsrc(DR + row * N, nb);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) rn[i] = buf_load<P>(rr, t + i * tpr);
+    }
+    const uint32_t sb = nb ? 4u : 0u;
+    mun = __builtin_bit_cast(float,
+                             BufIO<4>::load(make_rsrc(p.rms ? nullptr : p.mean + row, sb), 0));
+    rsn = __builtin_bit_cast(float, BufIO<4>::load(make_rsrc(p.rstd + row, sb), 0));
+  };
 
-    // Pass 1 over registers: the two row sums.  xhat and g are recomputed in pass 2 instead of
-    // being kept, which keeps the kernel within 128 VGPRs at 16 elements per lane.
+  // The row being processed, widened once: xhat, dy and g = dy * gamma in fp32.
+  float xh[VPL][VEC], dd[VPL][VEC], gg[VPL][VEC];
+  P rv[VPL];
+  float rs = 0.0f;
+  auto widen = [&]() {
+    rs = rsn;
+    const float mu = mun;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        xh[i][e] = (to_f32(xn[i].v[e]) - mu) * rs;
+        dd[i][e] = to_f32(dn[i].v[e]);
+        gg[i][e] = dd[i][e] * gam[i][e];
+      }
+      if constexpr (DRES) rv[i] = rn[i];
+    }
+  };
+
+  load_row(0);
+  widen();
+  load_row(1);
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row = row_of(it);
+    const uint32_t nb = bytes_of(it);
+    // Row sums (elements past the row are zero in dy, hence in g).
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const float xh = (to_f32(xv[i].v[e]) - mu) * rs;
-        const float g = to_f32(dv[i].v[e]) * to_f32(gam[i].v[e]);
-        s1 += g;
-        s2 += g * xh;
+        s1 += gg[i][e];
+        s2 = fmaf(gg[i][e], xh[i][e], s2);
       }
     s1 = wave_allreduce<SumOp>(s1);
     s2 = wave_allreduce<SumOp>(s2);
@@ -103,33 +140,33 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
         s2 += slot[1][rg * wpr + k];
       }
     }
-    const float c1 = p.rms ? 0.0f : s1 * inv_n;
-    const float c2 = s2 * inv_n;
-
-    P* xo = reinterpret_cast<P*>(static_cast<T*>(p.dx) + row * N);
-    const P* rr = reinterpret_cast<const P*>(static_cast<const T*>(p.dres) + row * N);
+    // dx = rstd (g - sum(g)/N - xhat sum(g xhat)/N) = rstd g + cb + cx xhat.
+    const float cb = p.rms ? 0.0f : -rs * (s1 * inv_n);
+    const float cx = -rs * (s2 * inv_n);
+    P o[VPL];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int v = t + i * tpr;
-      const bool ok = row_ok && v < nvec;
-      P rv, o;
-      if (p.dres && ok) rv = rr[v];
+    for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const float d = to_f32(dv[i].v[e]);  // zero outside the row / tensor
-        const float xh = (to_f32(xv[i].v[e]) - mu) * rs;
-        float dxv = rs * (d * to_f32(gam[i].v[e]) - c1 - xh * c2);
-        if (p.dres) dxv += ok ? to_f32(rv.v[e]) : 0.0f;
-        o.v[e] = from_f32<T>(dxv);
-        acc_g[i][e] += d * xh;
-        acc_b[i][e] += d;
+        float dxv = fmaf(rs, gg[i][e], fmaf(cx, xh[i][e], cb));
+        if constexpr (DRES) dxv += to_f32(rv[i].v[e]);
+        o[i].v[e] = from_f32<T>(dxv);
+        acc_g[i][e] = fmaf(dd[i][e], xh[i][e], acc_g[i][e]);
+        acc_b[i][e] += dd[i][e];
       }
-      if (p.dx && ok) xo[v] = o;
-    }
+
+    // Consume the next row and put the one after it in flight, then store this row's dx:
+    // loads and stores share one wait counter, so the stores go out last.
+    widen();
+    load_row(it + 2);
+    const rsrc_t xo = make_rsrc(DX ? DX + row * N : nullptr, nb);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) buf_store(o[i], xo, t + i * tpr);
   }
 
-  // Stage-1 output: one fp32 partial row per block (row stride ld_part, a multiple of 4).
+  // Stage-1 output: one fp32 partial row per block (row stride ld, a multiple of 4).
   const int64_t ld = (N + 3) & ~int64_t(3);
+  const int nvec = static_cast<int>(N / VEC);
   float* outs[2] = {p.part_g, p.part_b};
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
@@ -274,9 +311,14 @@ __global__ __launch_bounds__(1024) void col_reduce_kernel(const ColReduceArgs a)
 
 namespace {
 
-// Vectors per lane of the backward register path: 16 elements per lane for 16-byte vectors of
-// 16-bit types, 8 for fp32 and for the scalar path.
+// Largest vectors per lane instantiated for the backward register path: 16 elements per lane
+// for 16-byte vectors of 16-bit types, 8 for fp32 and for the scalar path.
 constexpr int bwd_max_vpl(int vec, int es) { return vec == 1 ? 8 : (es == 2 ? 2 : 2); }
+
+int env_int_b(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
 
 int next_pow2(int v) {
   int p = 1;
@@ -285,27 +327,32 @@ int next_pow2(int v) {
 }
 
 template <class T, int VEC, int VPL>
-int launch_stage1(const BwdParams& p, int64_t blocks, hipStream_t s) {
-  hipLaunchKernelGGL((bwd_reg_kernel<T, VEC, VPL, 1024>), dim3(blocks), dim3(1024), 0, s, p);
+int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s) {
+  if (p.dres)
+    hipLaunchKernelGGL((bwd_reg_kernel<T, true, VEC, VPL, 1024>), dim3(blocks), dim3(threads), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((bwd_reg_kernel<T, false, VEC, VPL, 1024>), dim3(blocks), dim3(threads),
+                       0, s, p);
   return static_cast<int>(hipGetLastError());
 }
 
 template <class T, int VEC>
-int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, hipStream_t s) {
+int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, hipStream_t s) {
   constexpr int CAP = bwd_max_vpl(VEC, sizeof(T));
   switch (vpl) {
-    case 1: return launch_stage1<T, VEC, 1>(p, blocks, s);
+    case 1: return launch_stage1<T, VEC, 1>(p, blocks, threads, s);
     case 2:
-      if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, s);
+      if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, threads, s);
       return FLN_ERR_INVALID;
     case 4:
-      if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, s);
+      if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, threads, s);
       return FLN_ERR_INVALID;
     case 8:
-      if constexpr (CAP >= 8) return launch_stage1<T, VEC, 8>(p, blocks, s);
+      if constexpr (CAP >= 8) return launch_stage1<T, VEC, 8>(p, blocks, threads, s);
       return FLN_ERR_INVALID;
     case 16:
-      if constexpr (CAP >= 16) return launch_stage1<T, VEC, 16>(p, blocks, s);
+      if constexpr (CAP >= 16) return launch_stage1<T, VEC, 16>(p, blocks, threads, s);
       return FLN_ERR_INVALID;
     default: return FLN_ERR_INVALID;
   }
@@ -321,8 +368,8 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s) {
     return static_cast<int>(hipGetLastError());
   }
   constexpr int VV = 16 / sizeof(T);
-  if (geo.vec == VV) return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, s);
-  return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, s);
+  if (geo.vec == VV) return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, geo.threads, s);
+  return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, geo.threads, s);
 }
 
 }  // namespace
@@ -334,23 +381,30 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   g.vec = (vec_ok && cols % vv == 0) ? vv : 1;
   const int64_t nvec = cols / g.vec;
   auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
-  // At most 16 (16-bit types) or 8 (fp32, scalar path) elements per lane keeps dy, x, gamma and
-  // both fp32 column accumulators of a lane's columns in VGPRs (<= 128, the budget of a
-  // 1024-thread block).
-  const int cap = bwd_max_vpl(g.vec, es);
+  // Elements per lane: 8 by default (x-hat, dy, g, gamma and both column accumulators of a
+  // lane's columns stay in fp32 registers); up to 16 for rows too wide for 16 waves.
+  const int epl = env_int_b("FLN_BWD_EPL", 8);
+  int cap = (epl >= g.vec ? epl : g.vec) / g.vec;
+  if (cap > bwd_max_vpl(g.vec, es)) cap = bwd_max_vpl(g.vec, es);
   int wpr = 1;
   while (per_lane(wpr) > cap && wpr < 16) wpr *= 2;
-  const int forced = getenv("FLN_BWD_WPR") ? atoi(getenv("FLN_BWD_WPR")) : 0;
+  if (per_lane(wpr) > cap) cap = bwd_max_vpl(g.vec, es);
+  const int forced = env_int_b("FLN_BWD_WPR", 0);
   if (forced >= 1 && forced <= 16 && (forced & (forced - 1)) == 0 && per_lane(forced) <= cap)
     wpr = forced;
   g.reg_path = per_lane(wpr) <= cap;
-  g.wpr = wpr;
+  g.wpr = g.reg_path ? wpr : 16;
   g.vpl = g.reg_path ? next_pow2(static_cast<int>(per_lane(wpr))) : 0;
-  g.threads = 1024;
-  g.rgs = g.reg_path ? 1024 / (kWave * wpr) : 1;
-  const int64_t cus = device_cu_count();
+  int threads = env_int_b("FLN_BWD_THREADS", 1024);
+  if (threads != 256 && threads != 512 && threads != 1024) threads = 1024;
+  if (!g.reg_path) threads = 1024;
+  if (threads < kWave * g.wpr) threads = kWave * g.wpr;
+  g.threads = threads;
+  g.rgs = g.reg_path ? threads / (kWave * g.wpr) : 1;
+  // 16 waves per CU in total: 1024 / threads blocks per CU.
+  const int64_t max_blocks = static_cast<int64_t>(device_cu_count()) * (1024 / threads);
   int64_t blocks = (rows + g.rgs - 1) / g.rgs;
-  if (blocks > cus) blocks = cus;
+  if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   g.rows_per_block = (rows + blocks - 1) / blocks;
   g.blocks = (rows + g.rows_per_block - 1) / g.rows_per_block;
@@ -432,7 +486,7 @@ int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int 
 extern "C" size_t fln_backward_workspace_bytes(int64_t rows, int64_t cols, int dtype) {
   (void)dtype;
   if (rows <= 0 || cols <= 0) return 0;
-  int64_t g = fln::device_cu_count();
+  int64_t g = 4 * static_cast<int64_t>(fln::device_cu_count());  // stage-1 blocks, upper bound
   if (rows < g) g = rows;
   const int64_t ld = (cols + 3) & ~int64_t(3);
   return static_cast<size_t>(2 * g * ld) * sizeof(float);

@@ -25,11 +25,97 @@ template <class T, int N> struct alignas(sizeof(T) * N) Pack {
   T v[N];
 };
 
+// Makes a packed value opaque to the optimizer for one use site.  Applied inside a row loop to
+// loop-invariant 16-bit parameter packs, it stops the compiler from hoisting their widening to
+// fp32 out of the loop (which would double their VGPR footprint and cost occupancy).
+template <class T, int N> __device__ __forceinline__ void keep_packed(Pack<T, N>& p) {
+  if constexpr (sizeof(T) == 2 && (sizeof(Pack<T, N>) % 4) == 0) {
+    constexpr int W = sizeof(Pack<T, N>) / 4;
+    struct Words {
+      uint32_t w[W];
+    };
+    Words u = __builtin_bit_cast(Words, p);
+#pragma unroll
+    for (int k = 0; k < W; ++k) asm volatile("" : "+v"(u.w[k]));
+    p = __builtin_bit_cast(Pack<T, N>, u);
+  }
+}
+
 template <class T, int N> __device__ __forceinline__ Pack<T, N> zero_pack() {
   Pack<T, N> p;
 #pragma unroll
   for (int e = 0; e < N; ++e) p.v[e] = static_cast<T>(0.0f);
   return p;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Raw buffer access.  A buffer resource (V#) describes [base, base + nbytes); a raw buffer load
+// whose byte offset falls outside returns zeros and such a store is dropped, by the hardware.
+// The kernels build one resource per row (nbytes = 0 for a row past the end of the tensor), so
+// tails, missing rows and absent tensors need no branches -- which keeps the compiler's wait-count
+// bookkeeping exact and lets a row's prefetch stay in flight across the loop.
+// Word 3 of the V# is 0x00020000 on gfx9-family targets (raw, untyped access).
+// ---------------------------------------------------------------------------------------------
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // an offset no resource here reaches
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           base ? static_cast<int>(nbytes) : 0, 0x00020000);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int BYTES> struct BufIO;
+template <> struct BufIO<16> {
+  using W = u32x4;
+  __device__ static W load(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  }
+  __device__ static void store(W w, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 0);
+  }
+};
+template <> struct BufIO<8> {
+  using W = u32x2;
+  __device__ static W load(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  }
+  __device__ static void store(W w, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, 0);
+  }
+};
+template <> struct BufIO<4> {
+  using W = uint32_t;
+  __device__ static W load(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
+  __device__ static void store(W w, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b32(w, r, off, 0, 0);
+  }
+};
+template <> struct BufIO<2> {
+  using W = uint16_t;
+  __device__ static W load(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  __device__ static void store(W w, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b16(w, r, off, 0, 0);
+  }
+};
+
+// Load / store the v-th Pack of a resource (byte offset v * sizeof(P)).
+template <class P> __device__ __forceinline__ P buf_load(rsrc_t r, uint32_t v) {
+  using IO = BufIO<sizeof(P)>;
+  return __builtin_bit_cast(P, IO::load(r, v * static_cast<uint32_t>(sizeof(P))));
+}
+template <class P> __device__ __forceinline__ void buf_store(const P& p, rsrc_t r, uint32_t v) {
+  using IO = BufIO<sizeof(P)>;
+  IO::store(__builtin_bit_cast(typename IO::W, p), r, v * static_cast<uint32_t>(sizeof(P)));
+}
+__device__ __forceinline__ void buf_store_f32(float x, rsrc_t r, uint32_t byte_off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, byte_off, 0, 0);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -12,6 +12,8 @@ namespace fln {
 // Cross-lane reduction over a row group of `wpr` waves.  The wave step is register-only; with
 // several waves per row each wave publishes its partial in LDS slot[wave] and every wave sums
 // its group's partials in the same fixed order (deterministic, identical in every lane).
+// The barrier only waits for LDS traffic (lgkmcnt), so global loads issued before it (the next
+// row's prefetch) stay in flight across it.
 template <class Op>
 __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, int rg, int wave,
                                                int lane) {
@@ -24,33 +26,45 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
   return r;
 }
 
-template <int VEC>
-__device__ __forceinline__ void store_fp8(uint8_t* q, int v, const float (&a)[VEC], float inv) {
-  if constexpr (VEC == 8) {
-    uint2 w;
-    w.x = fp8x4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-    w.y = fp8x4(a[4] * inv, a[5] * inv, a[6] * inv, a[7] * inv);
-    *reinterpret_cast<uint2*>(q + (int64_t)v * 8) = w;
-  } else if constexpr (VEC == 4) {
-    *reinterpret_cast<uint32_t*>(q + (int64_t)v * 4) =
-        fp8x4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-  } else {
-    static_assert(VEC == 1, "fp8 store supports 1, 4 or 8 elements");
-    q[v] = fp8x1(a[0] * inv);
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
-// Register-resident forward.  Block = rows_per_block row groups of `wpr` waves; thread t of a
-// row group owns vectors t, t + 64*wpr, ... (VPL of them) -- consecutive lanes read consecutive
-// 16-byte vectors, so each wave-wide load is one fully coalesced 1 KiB transaction.
+// Register-resident forward, persistent over rows.
+//
+// Block = rows_per_block row groups of `wpr` waves; thread t of a row group owns vectors
+// t, t + 64*wpr, ... (VPL of them), so consecutive lanes read consecutive 16-byte vectors and
+// every wave-wide access is one coalesced 1 KiB transaction.  The grid holds as many blocks as
+// fit on the device at once; each row group walks rows rb*rows_per_block + rg for
+// rb = blockIdx.x, blockIdx.x + gridDim.x, ...
+//
+// Software pipeline, per row group and iteration (row i in fp32 registers, rows i+1 .. i+PD in
+// flight as raw packed loads):
+//   1. statistics and normalization of row i, outputs packed to the I/O type;
+//   2. wait for row i+1, widen it into the fp32 registers;
+//   3. issue the loads of row i+1+PD into the freed slot;
+//   4. issue the stores of row i.
+// Keeping PD rows in flight per wave is what feeds HBM: at ~2-3 us loaded latency, 8 TB/s
+// needs ~80 KB of reads in flight per CU.
+// Loads and stores share one counter on gfx9-family GPUs and the compiler waits for all of
+// them when both kinds are pending, so the stores go out after the next row has been consumed:
+// by the time step 2 waits again they have had a whole compute phase to complete.
+// All global traffic goes through per-row buffer resources (tails and rows past the end are
+// handled by the hardware range check), so the loop body has no divergent branches.
+// LDS reduction slots are double-buffered by iteration parity: every iteration of a multi-wave
+// row group passes at least one barrier, which separates a slot's reads from its next writes.
+// EXACT: the row is exactly VPL vectors per lane (no masking in the statistics); GELU: 0 none,
+// 1 erf, 2 tanh (a template parameter so the plain kernels carry no GELU code).
 // ---------------------------------------------------------------------------------------------
-template <class T, bool FP8, bool RES, int VEC, int VPL, int MAXT>
+#ifndef FLN_FWD_PREFETCH
+#define FLN_FWD_PREFETCH 2
+#endif
+template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
-  __shared__ float red[3][MAXT / kWave];
+  constexpr int PD = FLN_FWD_PREFETCH;  // rows in flight ahead of the current one
+  __shared__ float red[2][3][MAXT / kWave];
   using P = Pack<T, VEC>;
+  // fp8 output: VEC codes per vector, held as one 4- or 8-byte word.
+  using QW = typename BufIO<(VEC >= 4 ? VEC : 4)>::W;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wpr = p.wpr;
   const int rg = wave / wpr;
   const int t = (wave - rg * wpr) * kWave + lane;
@@ -58,49 +72,79 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
   const int rows_per_block = blockDim.x / tpr;
   const int64_t N = p.cols;
   const int nvec = static_cast<int>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
   const float inv_n = 1.0f / static_cast<float>(N);
+  const T* X = static_cast<const T*>(p.x);
+  const T* R = static_cast<const T*>(p.res);
+  const int64_t stride = gridDim.x;
 
-  for (int64_t rb = blockIdx.x; rb < row_blocks; rb += gridDim.x) {
-    const int64_t row = rb * rows_per_block + rg;
-    const bool row_ok = row < p.rows;
-    float xf[VPL][VEC];
-    {
-      const P* xr = reinterpret_cast<const P*>(static_cast<const T*>(p.x) + row * N);
-      P xv[VPL];
+  // Affine parameters, once per row group (vectors past the row read as zero).
+  const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
+  const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);
+  P gv[VPL], bv[VPL];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int v = t + i * tpr;
-        xv[i] = (row_ok && v < nvec) ? xr[v] : zero_pack<T, VEC>();
-      }
-      if constexpr (RES) {
-        const P* rr = reinterpret_cast<const P*>(static_cast<const T*>(p.res) + row * N);
-        P* hr = p.h ? reinterpret_cast<P*>(static_cast<T*>(p.h) + row * N) : nullptr;
-        P rv[VPL];
+  for (int i = 0; i < VPL; ++i) {  // unconditional: an absent tensor has a zero-byte resource
+    gv[i] = buf_load<P>(g_rs, t + i * tpr);
+    bv[i] = buf_load<P>(b_rs, t + i * tpr);
+  }
+  const bool has_g = p.gamma != nullptr, has_b = p.beta != nullptr;
+
+  auto row_of = [&](int64_t rb) { return rb * rows_per_block + rg; };
+  auto bytes_of = [&](int64_t rb) -> uint32_t {
+    return (rb < row_blocks && row_of(rb) < p.rows) ? row_bytes : 0u;
+  };
+
+  // Ring of raw loads: the PD rows after the current one are in flight.
+  P xv[PD][VPL], rv[PD][VPL];
+  auto load_row = [&](int64_t rb, P (&xd)[VPL], P (&rd)[VPL]) {
+    const int64_t row = row_of(rb);
+    const uint32_t nb = bytes_of(rb);
+    const rsrc_t xr = make_rsrc(X + row * N, nb);
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-          const int v = t + i * tpr;
-          rv[i] = (row_ok && v < nvec) ? rr[v] : zero_pack<T, VEC>();
-        }
+    for (int i = 0; i < VPL; ++i) xd[i] = buf_load<P>(xr, t + i * tpr);
+    if constexpr (RES) {
+      const rsrc_t rr = make_rsrc(R + row * N, nb);
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-          P hv;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            hv.v[e] = from_f32<T>(to_f32(xv[i].v[e]) + to_f32(rv[i].v[e]));
-            xf[i][e] = to_f32(hv.v[e]);
-          }
-          const int v = t + i * tpr;
-          if (hr && row_ok && v < nvec) hr[v] = hv;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) xf[i][e] = to_f32(xv[i].v[e]);
-      }
+      for (int i = 0; i < VPL; ++i) rd[i] = buf_load<P>(rr, t + i * tpr);
     }
+  };
 
-    // Statistics: two passes over registers (mean, then centred sum of squares).
+  float xf[VPL][VEC];  // the row being normalized, fp32
+  P hv[VPL];           // residual sum of that row, in the I/O type (RES only)
+  auto widen = [&](const P (&xd)[VPL], const P (&rd)[VPL]) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if constexpr (RES) {
+          hv[i].v[e] = from_f32<T>(to_f32(xd[i].v[e]) + to_f32(rd[i].v[e]));
+          xf[i][e] = to_f32(hv[i].v[e]);
+        } else {
+          xf[i][e] = to_f32(xd[i].v[e]);
+        }
+      }
+  };
+
+  const int64_t rb0 = blockIdx.x;
+#pragma unroll
+  for (int k = 0; k < PD; ++k) load_row(rb0 + k * stride, xv[k], rv[k]);
+  widen(xv[0], rv[0]);
+  load_row(rb0 + PD * stride, xv[0], rv[0]);
+  int parity = 0;
+  // Row k of this row group is rb0 + k * stride; slot k % PD holds the raw loads of row k + PD
+  // once row k has been widened.  The inner loop is unrolled so every slot index is static.
+  for (int64_t base = rb0; base < row_blocks; base += PD * stride) {
+#pragma unroll
+  for (int s = 0; s < PD; ++s) {
+    const int64_t rb = base + s * stride;
+    if (rb >= row_blocks) break;  // uniform across the block
+    parity ^= 1;
+    const int64_t row = row_of(rb);
+    const uint32_t nb = bytes_of(rb);
+    float(*slots)[MAXT / kWave] = red[parity];
+
+    // 1. Statistics: two passes over registers (mean, then centred sum of squares).  Vectors
+    //    past the row were loaded as zeros, so they drop out of the plain sum.
     float mean = 0.0f;
     if (!p.rms) {
       float s = 0.0f;
@@ -108,75 +152,104 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) s += xf[i][e];
-      mean = row_allreduce<SumOp>(s, red[0], wpr, rg, wave, lane) * inv_n;
+      mean = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane) * inv_n;
     }
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const bool ok = (t + i * tpr) < nvec;
+      const bool ok = EXACT || (t + i * tpr) < nvec;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float d = xf[i][e] - mean;
         q += ok ? d * d : 0.0f;
       }
     }
-    q = row_allreduce<SumOp>(q, red[1], wpr, rg, wave, lane);
+    q = row_allreduce<SumOp>(q, slots[1], wpr, rg, wave, lane);
     const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
-    if (row_ok && t == 0) {
-      if (p.mean) p.mean[row] = mean;
-      if (p.rstd) p.rstd[row] = rstd;
-    }
 
-    // Normalize + affine + epilogue, in place.
-    const P* gr = static_cast<const P*>(p.gamma);
-    const P* br = static_cast<const P*>(p.beta);
+    //    Normalize + affine + epilogue, packed to the output format.
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int v = t + i * tpr;
-      const bool ok = v < nvec;
-      P gv, bv;
-      if (gr) gv = ok ? gr[v] : zero_pack<T, VEC>();
-      if (br) bv = ok ? br[v] : zero_pack<T, VEC>();
+    for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         float a = (xf[i][e] - mean) * rstd;
-        if (gr) a *= to_f32(gv.v[e]);
-        if (br) a += to_f32(bv.v[e]);
-        xf[i][e] = apply_gelu(a, p.gelu);
+        if (has_g) a *= to_f32(gv[i].v[e]);
+        if (has_b) a += to_f32(bv[i].v[e]);
+        if constexpr (GELU == 1) a = gelu_erf(a);
+        if constexpr (GELU == 2) a = gelu_tanh(a);
+        xf[i][e] = a;
       }
-    }
-
+    P yo[VPL];
+    QW qo[VPL];
+    P ho[VPL];
+    float scale = 0.0f;
     if constexpr (!FP8) {
-      P* yr = reinterpret_cast<P*>(static_cast<T*>(p.y) + row * N);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int v = t + i * tpr;
-        if (row_ok && v < nvec) {
-          P o;
+      for (int i = 0; i < VPL; ++i)
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(xf[i][e]);
-          yr[v] = o;
-        }
-      }
+        for (int e = 0; e < VEC; ++e) yo[i].v[e] = from_f32<T>(xf[i][e]);
     } else {
       float am = 0.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
-        const bool ok = (t + i * tpr) < nvec;
+        const bool ok = EXACT || (t + i * tpr) < nvec;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) am = fmaxf(am, ok ? fabsf(xf[i][e]) : 0.0f);
       }
-      am = row_allreduce<MaxOp>(am, red[2], wpr, rg, wave, lane);
+      am = row_allreduce<MaxOp>(am, slots[2], wpr, rg, wave, lane);
       const float inv = am > 0.0f ? 448.0f / am : 0.0f;
-      if (row_ok && t == 0) p.scale[row] = am / 448.0f;
-      uint8_t* qr = static_cast<uint8_t*>(p.y) + row * N;
+      scale = am / 448.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
-        const int v = t + i * tpr;
-        if (row_ok && v < nvec) store_fp8<VEC>(qr, v, xf[i], inv);
+        const float* a = xf[i];
+        if constexpr (VEC == 8) {
+          qo[i].x = fp8x4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+          qo[i].y = fp8x4(a[4] * inv, a[5] * inv, a[6] * inv, a[7] * inv);
+        } else if constexpr (VEC == 4) {
+          qo[i] = fp8x4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+        } else {
+          qo[i] = fp8x1(a[0] * inv);
+        }
       }
     }
-    if (wpr > 1) __syncthreads();  // LDS slots are reused by the next row block
+    if constexpr (RES) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) ho[i] = hv[i];
+    }
+
+    // 2. + 3. Consume the next row, put the row PD after it in flight.
+    const int nxt = (s + 1) % PD;  // static after unrolling
+    widen(xv[nxt], rv[nxt]);
+    load_row(rb + (PD + 1) * stride, xv[nxt], rv[nxt]);
+
+    // 4. Stores of this row (rows past the end have a zero-byte resource: dropped).
+    const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
+    const uint32_t stat_nb = nb ? 4u : 0u;
+    buf_store_f32(mean, make_rsrc(p.mean ? p.mean + row : nullptr, stat_nb), stat_off);
+    buf_store_f32(rstd, make_rsrc(p.rstd ? p.rstd + row : nullptr, stat_nb), stat_off);
+    if constexpr (RES) {
+      const rsrc_t hr = make_rsrc(p.h ? static_cast<T*>(p.h) + row * N : nullptr, nb);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) buf_store(ho[i], hr, t + i * tpr);
+    }
+    if constexpr (!FP8) {
+      const rsrc_t yr = make_rsrc(static_cast<T*>(p.y) + row * N, nb);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) buf_store(yo[i], yr, t + i * tpr);
+    } else {
+      buf_store_f32(scale, make_rsrc(p.scale + row, stat_nb), stat_off);
+      const rsrc_t qr = make_rsrc(static_cast<uint8_t*>(p.y) + row * N,
+                                  nb ? static_cast<uint32_t>(N) : 0u);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        if constexpr (VEC >= 4)
+          BufIO<VEC>::store(qo[i], qr, (t + i * tpr) * static_cast<uint32_t>(VEC));
+        else
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(qo[i]), qr, t + i * tpr,
+                                               0, 0);
+      }
+    }
+  }
   }
 }
 
@@ -285,18 +358,40 @@ inline int env_int(const char* name, int dflt) {
   return (s && *s) ? atoi(s) : dflt;
 }
 
-template <class T, bool FP8, bool RES, int VEC, int VPL>
-int launch_reg(const FwdParams& p, int threads, hipStream_t s) {
+// Blocks of `kernel` that fit on the current device at once.
+template <class K>
+int64_t resident_blocks(K kernel, int threads, int* cache_per_device) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cache_per_device[dev] == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    cache_per_device[dev] = per_cu;
+  }
+  return static_cast<int64_t>(cache_per_device[dev]) * device_cu_count();
+}
+
+template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
+int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   const int rows_per_block = threads / (kWave * p.wpr);
   const int64_t row_blocks = (p.rows + rows_per_block - 1) / rows_per_block;
-  const int64_t grid = row_blocks < kMaxGrid ? row_blocks : kMaxGrid;
-  if (threads <= 256)
-    hipLaunchKernelGGL((fwd_reg_kernel<T, FP8, RES, VEC, VPL, 256>), dim3(grid), dim3(threads), 0,
-                       s, p, row_blocks);
-  else
-    hipLaunchKernelGGL((fwd_reg_kernel<T, FP8, RES, VEC, VPL, 1024>), dim3(grid), dim3(threads),
-                       0, s, p, row_blocks);
+  auto kernel = fwd_reg_kernel<T, FP8, RES, GELU, VEC, VPL, EXACT, MAXT>;
+  static int occupancy_cache[2][64];  // per instantiation; [threads == MAXT][device]
+  int64_t grid = resident_blocks(kernel, threads, occupancy_cache[threads == MAXT]);
+  const int forced = env_int("FLN_FWD_GRID_MULT", 0);
+  if (forced > 0) grid = static_cast<int64_t>(forced) * device_cu_count();
+  if (grid > row_blocks) grid = row_blocks;
+  if (grid > kMaxGrid) grid = kMaxGrid;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, s, p, row_blocks);
   return static_cast<int>(hipGetLastError());
+}
+
+template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT>
+int launch_reg(const FwdParams& p, int threads, hipStream_t s) {
+  if (threads <= 256) return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, EXACT, 256>(p, threads, s);
+  return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, EXACT, 1024>(p, threads, s);
 }
 
 // Largest vectors-per-lane instantiated: 32 elements per lane for 16-byte vectors (keeps a
@@ -304,21 +399,44 @@ int launch_reg(const FwdParams& p, int threads, hipStream_t s) {
 // scalar path.
 template <int VEC> constexpr int max_vpl() { return VEC == 1 ? 16 : 32 / VEC; }
 
-template <class T, bool FP8, bool RES, int VEC>
-int launch_reg_vpl(const FwdParams& p, int vpl, int threads, hipStream_t s) {
+template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL>
+int launch_reg_exact(const FwdParams& p, bool exact, int threads, hipStream_t s) {
+  // The exact (mask-free) variant is only instantiated for 16-byte vectors.
+  if constexpr (VEC > 1)
+    if (exact) return launch_reg<T, FP8, RES, GELU, VEC, VPL, true>(p, threads, s);
+  return launch_reg<T, FP8, RES, GELU, VEC, VPL, false>(p, threads, s);
+}
+
+template <class T, bool FP8, bool RES, int GELU, int VEC>
+int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStream_t s) {
   constexpr int CAP = max_vpl<VEC>();
   switch (vpl) {
-    case 1: return launch_reg<T, FP8, RES, VEC, 1>(p, threads, s);
-    case 2: return launch_reg<T, FP8, RES, VEC, 2>(p, threads, s);
-    case 4: return launch_reg<T, FP8, RES, VEC, 4>(p, threads, s);
+    case 1: return launch_reg_exact<T, FP8, RES, GELU, VEC, 1>(p, exact, threads, s);
+    case 2: return launch_reg_exact<T, FP8, RES, GELU, VEC, 2>(p, exact, threads, s);
+    case 4: return launch_reg_exact<T, FP8, RES, GELU, VEC, 4>(p, exact, threads, s);
     case 8:
-      if constexpr (CAP >= 8) return launch_reg<T, FP8, RES, VEC, 8>(p, threads, s);
+      if constexpr (CAP >= 8)
+        return launch_reg_exact<T, FP8, RES, GELU, VEC, 8>(p, exact, threads, s);
       return FLN_ERR_INVALID;
     case 16:
-      if constexpr (CAP >= 16) return launch_reg<T, FP8, RES, VEC, 16>(p, threads, s);
+      if constexpr (CAP >= 16)
+        return launch_reg_exact<T, FP8, RES, GELU, VEC, 16>(p, exact, threads, s);
       return FLN_ERR_INVALID;
     default: return FLN_ERR_INVALID;
   }
+}
+
+// Flavour dispatch: GELU only exists without residual and fp8 output.
+template <class T, bool FP8, int VEC>
+int launch_reg_flavour(const FwdParams& p, int vpl, bool exact, int threads, hipStream_t s) {
+  if (p.res) return launch_reg_vpl<T, FP8, true, 0, VEC>(p, vpl, exact, threads, s);
+  if constexpr (!FP8) {
+    if (p.gelu == FLN_GELU_ERF)
+      return launch_reg_vpl<T, false, false, 1, VEC>(p, vpl, exact, threads, s);
+    if (p.gelu == FLN_GELU_TANH)
+      return launch_reg_vpl<T, false, false, 2, VEC>(p, vpl, exact, threads, s);
+  }
+  return launch_reg_vpl<T, FP8, false, 0, VEC>(p, vpl, exact, threads, s);
 }
 
 template <class T, class A, bool FP8>
@@ -341,12 +459,18 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     vec_ok = vec_ok && aligned16(p.y);
   if (env_int("FLN_FORCE_LOOP", 0)) return launch_loop<T, float, FP8>(p, s);
   const int vec = vec_ok ? VV : 1;
-  const int cap = vec_ok ? max_vpl<VV>() : max_vpl<1>();
+  // Elements per lane: 16 by default -- with the prefetch ring that keeps a wave near 90 VGPRs
+  // (5 waves per SIMD), more waves per row otherwise.
+  const int epl = env_int("FLN_FWD_EPL", 16);
+  int cap = (epl >= vec ? epl : vec) / vec;
+  const int max_cap = vec_ok ? max_vpl<VV>() : max_vpl<1>();
+  if (cap > max_cap) cap = max_cap;
   const int64_t nvec = N / vec;
   constexpr int max_wpr = 16;
   auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
   int wpr = 1;
   while (per_lane(wpr) > cap && wpr < max_wpr) wpr *= 2;
+  if (per_lane(wpr) > cap) cap = max_cap;  // very long rows: widest register tiles
   if (per_lane(wpr) > cap) return launch_loop<T, float, FP8>(p, s);
   // Few rows: spread each row over more waves so the grid covers more CUs (latency-bound
   // shapes such as 32 x 768 finish in one memory round trip either way, but with fewer serial
@@ -358,14 +482,10 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     wpr = forced;
   p.wpr = wpr;
   const int vpl = next_pow2(static_cast<int>(per_lane(wpr)));
+  const bool exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
   const int threads = wpr <= 4 ? 256 : kWave * wpr;
-  const bool res = p.res != nullptr;
-  if (vec_ok) {
-    return res ? launch_reg_vpl<T, FP8, true, VV>(p, vpl, threads, s)
-               : launch_reg_vpl<T, FP8, false, VV>(p, vpl, threads, s);
-  }
-  return res ? launch_reg_vpl<T, FP8, true, 1>(p, vpl, threads, s)
-             : launch_reg_vpl<T, FP8, false, 1>(p, vpl, threads, s);
+  if (vec_ok) return launch_reg_flavour<T, FP8, VV>(p, vpl, exact, threads, s);
+  return launch_reg_flavour<T, FP8, 1>(p, vpl, false, threads, s);
 }
 
 }  // namespace detail
