@@ -5,7 +5,8 @@
 // first implementation of that contract.
 //
 // Stage 1 (bwd_reg_kernel): each block owns a contiguous chunk of rows, processed by row groups
-// of `wpr` waves.  Per row it computes
+// of `wpr` waves, with the next PD rows of x / dy always in flight (a ring of raw buffer loads;
+// at loaded HBM latency the CU needs tens of KiB of reads outstanding).  Per row it computes
 //     LayerNorm: xhat = (x - mean) rstd, g = dy gamma,
 //                dx = rstd (g - sum(g)/N - xhat sum(g xhat)/N)
 //     RMSNorm:   xhat = x rstd,          dx = rstd (g - xhat sum(g xhat)/N)
@@ -21,9 +22,15 @@
 
 namespace fln {
 
+#ifndef FLN_BWD_PREFETCH
+#define FLN_BWD_PREFETCH 3
+#endif
 template <class T, bool DRES, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
-  __shared__ float red[2][2][MAXT / kWave];  // [double buffer][sum g, sum g*xhat][wave]
+  constexpr int PD = FLN_BWD_PREFETCH;  // rows in flight ahead of the current one
+  constexpr int MAXW = MAXT / kWave;
+  // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
+  __shared__ float red[2][2][MAXW + 16];
   __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
   using P = Pack<T, VEC>;
   const int lane = threadIdx.x & (kWave - 1);
@@ -36,9 +43,13 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   const int64_t N = p.cols;
   const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
   const float inv_n = 1.0f / static_cast<float>(N);
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * p.rows_per_block;
-  const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
-  const int iters = static_cast<int>((p.rows_per_block + rgs - 1) / rgs);
+  // Rows are dealt out grid-stride: iteration `it` of block b handles row group
+  // (it * gridDim.x + b), i.e. rows (it * gridDim.x + b) * rgs + rg.  At any moment all blocks
+  // work on one window of adjacent rows, which keeps HBM page locality like a streaming copy;
+  // each block still accumulates its column partials in a fixed order (deterministic).
+  const int64_t group_stride = static_cast<int64_t>(gridDim.x);
+  const int iters = static_cast<int>(
+      ((p.rows + rgs - 1) / rgs + group_stride - 1 - blockIdx.x) / group_stride);
   const T* X = static_cast<const T*>(p.x);
   const T* DY = static_cast<const T*>(p.dy);
   const T* DR = static_cast<const T*>(p.dres);
@@ -62,57 +73,68 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc_g[i][e] = acc_b[i][e] = 0.0f;
 
-  auto row_of = [&](int it) { return r0 + static_cast<int64_t>(it) * rgs + rg; };
-  auto bytes_of = [&](int it) -> uint32_t { return row_of(it) < r1 ? row_bytes : 0u; };
+  auto row_of = [&](int it) {
+    return (static_cast<int64_t>(it) * group_stride + blockIdx.x) * rgs + rg;
+  };
+  auto bytes_of = [&](int it) -> uint32_t {
+    return (it < iters && row_of(it) < p.rows) ? row_bytes : 0u;
+  };
 
-  // Raw loads of the row in flight (x, dy, dres, mean, rstd); rows past the block's range have
-  // zero-byte resources and read as zeros.
-  P xn[VPL], dn[VPL], rn[VPL];
-  float mun = 0.0f, rsn = 0.0f;
-  auto load_row = [&](int it) {
+  // Ring of raw loads (x, dy, dres, mean, rstd) for the PD rows after the current one; rows
+  // past the block's range have zero-byte resources and read as zeros.
+  P xn[PD][VPL], dn[PD][VPL], rn[PD][VPL];
+  float mun[PD], rsn[PD];
+  auto load_row = [&](int it, int slot) {
     const int64_t row = row_of(it);
     const uint32_t nb = bytes_of(it);
     const rsrc_t xr = make_rsrc(X + row * N, nb);
     const rsrc_t dr = make_rsrc(DY + row * N, nb);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      xn[i] = buf_load<P>(xr, t + i * tpr);
-      dn[i] = buf_load<P>(dr, t + i * tpr);
+      xn[slot][i] = buf_load<P>(xr, t + i * tpr);
+      dn[slot][i] = buf_load<P>(dr, t + i * tpr);
     }
     if constexpr (DRES) {
       const rsrc_t rr = make_rsrc(DR + row * N, nb);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) rn[i] = buf_load<P>(rr, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) rn[slot][i] = buf_load<P>(rr, t + i * tpr);
     }
     const uint32_t sb = nb ? 4u : 0u;
-    mun = __builtin_bit_cast(float,
-                             BufIO<4>::load(make_rsrc(p.rms ? nullptr : p.mean + row, sb), 0));
-    rsn = __builtin_bit_cast(float, BufIO<4>::load(make_rsrc(p.rstd + row, sb), 0));
+    mun[slot] = __builtin_bit_cast(
+        float, BufIO<4>::load(make_rsrc(p.rms ? nullptr : p.mean + row, sb), 0));
+    rsn[slot] = __builtin_bit_cast(float, BufIO<4>::load(make_rsrc(p.rstd + row, sb), 0));
   };
 
   // The row being processed, widened once: xhat, dy and g = dy * gamma in fp32.
   float xh[VPL][VEC], dd[VPL][VEC], gg[VPL][VEC];
   P rv[VPL];
   float rs = 0.0f;
-  auto widen = [&]() {
-    rs = rsn;
-    const float mu = mun;
+  auto widen = [&](int slot) {
+    rs = rsn[slot];
+    const float mu = mun[slot];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        xh[i][e] = (to_f32(xn[i].v[e]) - mu) * rs;
-        dd[i][e] = to_f32(dn[i].v[e]);
+        xh[i][e] = (to_f32(xn[slot][i].v[e]) - mu) * rs;
+        dd[i][e] = to_f32(dn[slot][i].v[e]);
         gg[i][e] = dd[i][e] * gam[i][e];
       }
-      if constexpr (DRES) rv[i] = rn[i];
+      if constexpr (DRES) rv[i] = rn[slot][i];
     }
   };
 
-  load_row(0);
-  widen();
-  load_row(1);
-  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+  for (int k = 0; k < PD; ++k) load_row(k, k);
+  widen(0);
+  load_row(PD, 0);
+  // Row `it` is widened from slot it % PD, which then receives row it + PD; the inner loop is
+  // unrolled so every slot index is static.
+  for (int base = 0; base < iters; base += PD) {
+#pragma unroll
+  for (int sl = 0; sl < PD; ++sl) {
+    const int it = base + sl;
+    if (it >= iters) break;  // uniform across the block
     const int64_t row = row_of(it);
     const uint32_t nb = bytes_of(it);
     // Row sums (elements past the row are zero in dy, hence in g).
@@ -127,18 +149,14 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     s1 = wave_allreduce<SumOp>(s1);
     s2 = wave_allreduce<SumOp>(s2);
     if (wpr > 1) {
-      float(*slot)[MAXT / kWave] = red[it & 1];
+      float(*slot)[MAXW + 16] = red[it & 1];
       if (lane == 0) {
         slot[0][wave] = s1;
         slot[1][wave] = s2;
       }
       __syncthreads();
-      s1 = slot[0][rg * wpr];
-      s2 = slot[1][rg * wpr];
-      for (int k = 1; k < wpr; ++k) {
-        s1 += slot[0][rg * wpr + k];
-        s2 += slot[1][rg * wpr + k];
-      }
+      s1 = combine_partials<SumOp>(slot[0], rg * wpr, wpr, lane, 0.0f);
+      s2 = combine_partials<SumOp>(slot[1], rg * wpr, wpr, lane, 0.0f);
     }
     // dx = rstd (g - sum(g)/N - xhat sum(g xhat)/N) = rstd g + cb + cx xhat.
     const float cb = p.rms ? 0.0f : -rs * (s1 * inv_n);
@@ -155,13 +173,15 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
         acc_b[i][e] += dd[i][e];
       }
 
-    // Consume the next row and put the one after it in flight, then store this row's dx:
+    // Consume the next row and put the row PD after it in flight, then store this row's dx:
     // loads and stores share one wait counter, so the stores go out last.
-    widen();
-    load_row(it + 2);
+    const int nxt = (sl + 1) % PD;  // static after unrolling
+    widen(nxt);
+    load_row(it + 1 + PD, nxt);
     const rsrc_t xo = make_rsrc(DX ? DX + row * N : nullptr, nb);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) buf_store(o[i], xo, t + i * tpr);
+  }
   }
 
   // Stage-1 output: one fp32 partial row per block (row stride ld, a multiple of 4).
@@ -407,7 +427,9 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   g.rows_per_block = (rows + blocks - 1) / blocks;
-  g.blocks = (rows + g.rows_per_block - 1) / g.rows_per_block;
+  // The register path deals row groups out grid-stride over `blocks`; the looped fallback
+  // gives each block a contiguous chunk of rows_per_block rows.
+  g.blocks = g.reg_path ? blocks : (rows + g.rows_per_block - 1) / g.rows_per_block;
   return g;
 }
 

@@ -153,6 +153,23 @@ template <class Op> __device__ __forceinline__ float wave_allreduce(float v) {
   return Op::apply(readlane(v, 0), readlane(v, 32));
 }
 
+// Combine the per-wave partials slot[base .. base + n - 1] (n <= 16) of one row group: lane k
+// reads partial k (one LDS read per lane, all in parallel), lanes k >= n contribute `ident`, and
+// the four DPP steps reduce the first 16-lane row in a fixed order; the result is wave-uniform.
+// slot must be readable up to base + 15 (callers pad it).
+template <class Op>
+__device__ __forceinline__ float combine_partials(const float* slot, int base, int n, int lane,
+                                                  float ident) {
+  const int k = lane & 15;
+  float v = slot[base + k];
+  v = k < n ? v : ident;
+  v = Op::apply(v, dpp<0xB1>(v));
+  v = Op::apply(v, dpp<0x4E>(v));
+  v = Op::apply(v, dpp<0x141>(v));
+  v = Op::apply(v, dpp<0x140>(v));
+  return readlane(v, 0);
+}
+
 // Generic-type wave sum through ds_bpermute (used by the looped fallback kernels, which also
 // handle fp64 accumulation).
 template <class A> __device__ __forceinline__ A wave_sum_generic(A v) {
@@ -194,6 +211,14 @@ __device__ __forceinline__ float sat448(float v) { return __builtin_amdgcn_fmed3
 __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), w, true);
+  return static_cast<uint32_t>(w);
+}
+// Without the clamp, for values already known to lie within +-464 (anything in (448, 464)
+// rounds to 448 under round-to-nearest-even): a row scaled by 448 / max|row| stays within
+// 448 (1 + 2^-23).
+__device__ __forceinline__ uint32_t fp8x4_inrange(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return static_cast<uint32_t>(w);
 }
 __device__ __forceinline__ uint8_t fp8x1(float a) {

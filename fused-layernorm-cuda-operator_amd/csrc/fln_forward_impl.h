@@ -21,9 +21,7 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
   if (wpr == 1) return v;
   if (lane == 0) slot[wave] = v;
   __syncthreads();
-  float r = slot[rg * wpr];
-  for (int k = 1; k < wpr; ++k) r = Op::apply(r, slot[rg * wpr + k]);
-  return r;
+  return combine_partials<Op>(slot, rg * wpr, wpr, lane, 0.0f);  // 0: identity of + and max|.|
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -59,7 +57,8 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
   constexpr int PD = FLN_FWD_PREFETCH;  // rows in flight ahead of the current one
-  __shared__ float red[2][3][MAXT / kWave];
+  constexpr int MAXW = MAXT / kWave;
+  __shared__ float red[2][3][MAXW + 16];  // padded: combine_partials reads 16 past the base
   using P = Pack<T, VEC>;
   // fp8 output: VEC codes per vector, held as one 4- or 8-byte word.
   using QW = typename BufIO<(VEC >= 4 ? VEC : 4)>::W;
@@ -85,9 +84,17 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {  // unconditional: an absent tensor has a zero-byte resource
     gv[i] = buf_load<P>(g_rs, t + i * tpr);
-    bv[i] = buf_load<P>(b_rs, t + i * tpr);
+    bv[i] = buf_load<P>(b_rs, t + i * tpr);  // absent beta reads as zeros: adds nothing
   }
-  const bool has_g = p.gamma != nullptr, has_b = p.beta != nullptr;
+  if (p.gamma == nullptr) {  // absent gamma multiplies by one (uniform, once per kernel)
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) gv[i].v[e] = static_cast<T>(1.0f);
+  }
+  // Vector slot i is complete (no lane past the row) when (i + 1) * tpr <= nvec; only the
+  // other slots need per-element masks in the centred sums and the fp8 row max.
+  auto slot_full = [&](int i) { return EXACT || (i + 1) * tpr <= nvec; };
 
   auto row_of = [&](int64_t rb) { return rb * rows_per_block + rg; };
   auto bytes_of = [&](int64_t rb) -> uint32_t {
@@ -141,7 +148,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     parity ^= 1;
     const int64_t row = row_of(rb);
     const uint32_t nb = bytes_of(rb);
-    float(*slots)[MAXT / kWave] = red[parity];
+    float(*slots)[MAXW + 16] = red[parity];
 
     // 1. Statistics: two passes over registers (mean, then centred sum of squares).  Vectors
     //    past the row were loaded as zeros, so they drop out of the plain sum.
@@ -157,11 +164,19 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const bool ok = EXACT || (t + i * tpr) < nvec;
+      if (slot_full(i)) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float d = xf[i][e] - mean;
-        q += ok ? d * d : 0.0f;
+        for (int e = 0; e < VEC; ++e) {
+          const float d = xf[i][e] - mean;
+          q = fmaf(d, d, q);
+        }
+      } else {
+        const bool ok = (t + i * tpr) < nvec;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float d = xf[i][e] - mean;
+          q += ok ? d * d : 0.0f;
+        }
       }
     }
     q = row_allreduce<SumOp>(q, slots[1], wpr, rg, wave, lane);
@@ -172,9 +187,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float a = (xf[i][e] - mean) * rstd;
-        if (has_g) a *= to_f32(gv[i].v[e]);
-        if (has_b) a += to_f32(bv[i].v[e]);
+        float a = fmaf((xf[i][e] - mean) * rstd, to_f32(gv[i].v[e]), to_f32(bv[i].v[e]));
         if constexpr (GELU == 1) a = gelu_erf(a);
         if constexpr (GELU == 2) a = gelu_tanh(a);
         xf[i][e] = a;
@@ -192,9 +205,14 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       float am = 0.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
-        const bool ok = EXACT || (t + i * tpr) < nvec;
+        if (slot_full(i)) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) am = fmaxf(am, ok ? fabsf(xf[i][e]) : 0.0f);
+          for (int e = 0; e < VEC; ++e) am = fmaxf(am, fabsf(xf[i][e]));
+        } else {
+          const bool ok = (t + i * tpr) < nvec;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) am = fmaxf(am, ok ? fabsf(xf[i][e]) : 0.0f);
+        }
       }
       am = row_allreduce<MaxOp>(am, slots[2], wpr, rg, wave, lane);
       const float inv = am > 0.0f ? 448.0f / am : 0.0f;
@@ -202,11 +220,12 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const float* a = xf[i];
+        // |a * inv| <= 448 (1 + 2^-23): in range for the unclamped conversion.
         if constexpr (VEC == 8) {
-          qo[i].x = fp8x4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-          qo[i].y = fp8x4(a[4] * inv, a[5] * inv, a[6] * inv, a[7] * inv);
+          qo[i].x = fp8x4_inrange(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+          qo[i].y = fp8x4_inrange(a[4] * inv, a[5] * inv, a[6] * inv, a[7] * inv);
         } else if constexpr (VEC == 4) {
-          qo[i] = fp8x4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+          qo[i] = fp8x4_inrange(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
         } else {
           qo[i] = fp8x1(a[0] * inv);
         }
@@ -447,6 +466,66 @@ int launch_loop(const FwdParams& p, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
+// Launch geometry of the register path: waves per row (wpr), vectors per lane (vpl, a power of
+// two <= cap) and block size.  Preference order:
+//   1. the fewest waves per row (power of two) that fit the row in `cap` vectors per lane;
+//   2. if that tiling leaves masked lanes, an exact tiling with any wave count <= 16 (e.g. a
+//      7168-element bf16 row is 7 waves x 64 lanes x 2 vectors), so no lane does masked work;
+//   3. few rows: more waves per row (fewer vectors each) until the grid covers the device.
+// Rows of 1, 2 or 4 waves share 256-thread blocks; other row groups are one block each.
+struct FwdGeometry {
+  int wpr, vpl, threads;
+  bool exact, loop;
+};
+
+inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int max_cap, bool vec_path,
+                                int forced_wpr) {
+  FwdGeometry g{};
+  constexpr int max_wpr = 16;
+  auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
+  int wpr = 1;
+  while (per_lane(wpr) > cap && wpr < max_wpr) wpr *= 2;
+  if (per_lane(wpr) > cap) cap = max_cap;  // very long rows: widest register tiles
+  if (per_lane(wpr) > cap) {
+    g.loop = true;
+    return g;
+  }
+  int vpl = next_pow2(static_cast<int>(per_lane(wpr)));
+  bool exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
+  if (vec_path && !exact) {
+    for (int v = next_pow2(cap) > cap ? next_pow2(cap) / 2 : cap; v >= 1; v >>= 1) {
+      if (nvec % (kWave * v) == 0 && nvec / (kWave * v) <= max_wpr) {
+        wpr = static_cast<int>(nvec / (kWave * v));
+        vpl = v;
+        exact = true;
+        break;
+      }
+    }
+  }
+  const int64_t target_waves = 4 * static_cast<int64_t>(device_cu_count());
+  while (rows * wpr < target_waves && wpr * 2 <= max_wpr) {
+    if (exact && vpl >= 2) {
+      wpr *= 2;
+      vpl /= 2;
+    } else if (!exact && nvec > kWave * wpr * 2) {
+      wpr *= 2;
+      vpl = next_pow2(static_cast<int>(per_lane(wpr)));
+    } else {
+      break;
+    }
+  }
+  if (forced_wpr >= 1 && forced_wpr <= max_wpr && per_lane(forced_wpr) <= max_cap) {
+    wpr = forced_wpr;
+    vpl = next_pow2(static_cast<int>(per_lane(wpr)));
+    exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
+  }
+  g.wpr = wpr;
+  g.vpl = vpl;
+  g.exact = vec_path && exact;
+  g.threads = (4 % wpr == 0) ? 256 : kWave * wpr;
+  return g;
+}
+
 template <class T, bool FP8>
 int dispatch_typed(FwdParams p, hipStream_t s) {
   constexpr int VV = 16 / sizeof(T);  // elements per 16-byte vector
@@ -459,31 +538,24 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     vec_ok = vec_ok && aligned16(p.y);
   if (env_int("FLN_FORCE_LOOP", 0)) return launch_loop<T, float, FP8>(p, s);
   const int vec = vec_ok ? VV : 1;
-  // Elements per lane: 16 by default -- with the prefetch ring that keeps a wave near 90 VGPRs
-  // (5 waves per SIMD), more waves per row otherwise.
-  const int epl = env_int("FLN_FWD_EPL", 16);
+  // Elements per lane: at most 32 by default (measured best or equal on the 4096-8192-wide
+  // benchmark rows); more waves per row beyond that.
+  const int epl = env_int("FLN_FWD_EPL", 32);
   int cap = (epl >= vec ? epl : vec) / vec;
   const int max_cap = vec_ok ? max_vpl<VV>() : max_vpl<1>();
   if (cap > max_cap) cap = max_cap;
   const int64_t nvec = N / vec;
-  constexpr int max_wpr = 16;
-  auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
-  int wpr = 1;
-  while (per_lane(wpr) > cap && wpr < max_wpr) wpr *= 2;
-  if (per_lane(wpr) > cap) cap = max_cap;  // very long rows: widest register tiles
-  if (per_lane(wpr) > cap) return launch_loop<T, float, FP8>(p, s);
-  // Few rows: spread each row over more waves so the grid covers more CUs (latency-bound
-  // shapes such as 32 x 768 finish in one memory round trip either way, but with fewer serial
-  // loads per lane).
-  const int64_t target_waves = 4 * static_cast<int64_t>(device_cu_count());
-  while (p.rows * wpr < target_waves && wpr < max_wpr && nvec > kWave * wpr * 2) wpr *= 2;
-  const int forced = env_int("FLN_FWD_WPR", 0);
-  if (forced >= 1 && forced <= max_wpr && (forced & (forced - 1)) == 0 && per_lane(forced) <= cap)
-    wpr = forced;
-  p.wpr = wpr;
-  const int vpl = next_pow2(static_cast<int>(per_lane(wpr)));
-  const bool exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
-  const int threads = wpr <= 4 ? 256 : kWave * wpr;
+  const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, max_cap, vec_ok,
+                                     env_int("FLN_FWD_WPR", 0));
+  if (env_int("FLN_DEBUG_GEOMETRY", 0))
+    fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d -> %s wpr=%d vpl=%d exact=%d "
+            "threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec, cap,
+            g.loop ? "loop" : "registers", g.wpr, g.vpl, static_cast<int>(g.exact), g.threads);
+  if (g.loop) return launch_loop<T, float, FP8>(p, s);
+  p.wpr = g.wpr;
+  const int vpl = g.vpl;
+  const bool exact = g.exact;
+  const int threads = g.threads;
   if (vec_ok) return launch_reg_flavour<T, FP8, VV>(p, vpl, exact, threads, s);
   return launch_reg_flavour<T, FP8, 1>(p, vpl, false, threads, s);
 }
