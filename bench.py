@@ -3,25 +3,36 @@
 Default workload (the headline metric): LayerNorm forward + backward, bf16, 8192 x 4096 -- one
 "step" is the forward (y, mean, rstd) plus the backward (dx, dgamma, dbeta) over one batch, with
 inputs already resident in HBM.  The RMSNorm forward + backward at the same shape is timed the
-same way and reported under "rms_fwd_bwd".
+same way and reported under "rms_fwd_bwd"; the benchmark configurations C1..C5 are timed under
+"configs" (latency for the small ones, GB/s for the large ones).
 
 The kernels are called through the C ABI (libfln.so) on torch's current HIP stream, with every
-output preallocated; inputs and outputs rotate over enough buffer sets (> 512 MiB) that the
-256 MiB Infinity Cache cannot serve a step from the previous one.
+output preallocated.  Inputs and outputs rotate over at least 4 buffer sets (>= 2 GiB in all,
+8x the 256 MiB Infinity Cache), and a step runs the backward on a different set than the
+forward, so no kernel finds its inputs in a cache from an earlier launch (as in training, where
+a layer's backward comes long after its forward).
 
-Prints ONE JSON line (rank 0).  `value` = algorithmic bytes of one step / measured step time, in
-GB/s.  `roofline` covers the backward launch group (stage-1 kernel + column reduction), timed
-with HIP events on the launch stream; `cpu_baseline` times the C oracle (oracle/fln_oracle.c,
-the "port") on a bounded row sample on the host, single thread.
+Prints ONE JSON line.  `value` = algorithmic bytes of one step / measured step time, in GB/s.
+`roofline` covers the backward call (fln_layernorm_backward: stage-1 kernel + column
+reduction), the larger of the two, timed with HIP events on its launch stream; its `traffic`
+comes from two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over a child run of this
+script (--kernel-loop), each scaled by what the counter reads for a device copy of known size.
+`cpu_baseline` times the C oracle (oracle/fln_oracle.c, the "port") on a bounded row sample on
+the host, single thread.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import platform
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -30,8 +41,13 @@ sys.path.insert(0, PKG)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "HBM GB/s (% of peak) + µs/call, LN/RMSNorm fwd+bwd bf16 8192×4096"
+HEADLINE = "ln_fwd_bwd_bf16_8192x4096"
 HBM_PEAK_GBS = 8000.0
-ROTATE_BYTES = 640 * 2 ** 20
+ROTATE_BYTES = 2 * 2 ** 30
+CALIBRATION_COPY_BYTES = 256 * 2 ** 20
+CONFIGS = ("c1_ln_fwd_fp32_32x768", "c2_ln_gelu_fp32_17x1023", "c2_ln_gelu_fp32_64x4096",
+           "c3_add_ln_fwd_bf16_8192x4096", "c4_rms_fwd_bwd_bf16_16384x8192",
+           "c5_ln_fp8_bf16_32768x7168")
 
 
 def parse():
@@ -40,15 +56,23 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes (roofline.traffic = null)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1..C5 timings")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the LayerNorm headline (no RMSNorm line, no configs); "
+                         "used for per-kernel profiles")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate host time budget of the CPU baseline")
-    ap.add_argument("--all", action="store_true",
-                    help="also time every benchmark config (C1..C5) and report them")
+    ap.add_argument("--kernel-loop", metavar="WORKLOAD", default=None,
+                    help="(profiling child) launch WORKLOAD's forward and backward --iters "
+                         "times each, then a device copy of known size, and exit")
+    ap.add_argument("--iters", type=int, default=20)
     return ap.parse_args()
 
 
 class Runner:
-    """Preallocated buffers + C-ABI launches for one workload."""
+    """Preallocated buffer sets + C-ABI launches for one workload."""
 
     def __init__(self, lib, capi, torch, w, inputs):
         self.lib, self.capi, self.torch, self.w = lib, capi, torch, w
@@ -56,7 +80,7 @@ class Runner:
         x = inputs["x"]
         set_bytes = x.numel() * x.element_size() * (4 if ("dy" in inputs or
                                                          "residual" in inputs) else 2)
-        self.nsets = max(1, -(-ROTATE_BYTES // set_bytes))
+        self.nsets = min(16, max(4, -(-ROTATE_BYTES // set_bytes)))
         self.sets = []
         for k in range(self.nsets):
             s = {n: t.to(dev) for n, t in inputs.items()}
@@ -75,6 +99,7 @@ class Runner:
             self.sets.append(s)
         self.rows, self.cols = w.rows, w.cols
         self.code = capi.dtype_code(self.sets[0]["x"])
+        self.has_bwd = "dy" in inputs
         self.ws_bytes = lib.fln_backward_workspace_bytes(self.rows, self.cols, self.code)
         self.ws = torch.empty(max(1, self.ws_bytes // 4), device=dev)
         self.dg = torch.empty(self.cols, device=dev)
@@ -127,11 +152,18 @@ class Runner:
                                                  self.ws_bytes, stream)
         c.check(rc)
 
+    def prime(self, stream):
+        """One forward per set, so every set holds the statistics its backward reads."""
+        for s in self.sets:
+            self.fwd(s, stream)
+
     def step(self, stream):
-        s = self.sets[self.i % self.nsets]
+        """Forward on set i, backward on set i + 1 (last forwarded nsets - 1 steps earlier)."""
+        k = self.i
         self.i += 1
-        self.fwd(s, stream)
-        self.bwd(s, stream)
+        self.fwd(self.sets[k % self.nsets], stream)
+        if self.has_bwd:
+            self.bwd(self.sets[(k + 1) % self.nsets], stream)
 
     def time_region(self, fn, n, stream_obj):
         torch = self.torch
@@ -157,7 +189,7 @@ def warm_clocks(fn, seconds=0.3):
 
 
 def time_launch_group(runner, which, n, stream, stream_obj):
-    """Average duration (ms) of one forward or backward launch group, rotating buffer sets."""
+    """Average duration (ms) of one forward or backward call, rotating buffer sets."""
     it = [0]
 
     def one():
@@ -170,9 +202,123 @@ def time_launch_group(runner, which, n, stream, stream_obj):
     return runner.time_region(one, n, stream_obj)
 
 
+# ------------------------------------------------------------------------------------------------
+# HBM traffic from hardware counters.
+# ------------------------------------------------------------------------------------------------
+def kernel_loop(args):
+    """Profiling child: forward and backward of one workload --iters times each (after one
+    forward per buffer set), then --iters copies of CALIBRATION_COPY_BYTES for the counter
+    calibration."""
+    import torch
+    import capi
+    from fused_layernorm.testing import WORKLOADS, make_inputs
+
+    lib = capi.load()
+    stream = capi.stream()
+    w = WORKLOADS[args.kernel_loop]
+    r = Runner(lib, capi, torch, w, make_inputs(w))
+    r.prime(stream)
+    for i in range(args.iters):
+        r.fwd(r.sets[i % r.nsets], stream)
+    if r.has_bwd:
+        for i in range(args.iters):
+            r.bwd(r.sets[i % r.nsets], stream)
+    torch.cuda.synchronize()
+    del r
+    torch.cuda.empty_cache()
+    a = torch.empty(CALIBRATION_COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    b = torch.empty_like(a)
+    for _ in range(args.iters):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("kernel loop done", flush=True)
+
+
+def _counter_rows(outdir):
+    files = glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def pmc_traffic(workload, iters=20):
+    """Per-call HBM bytes of the forward and backward of `workload` from two rocprofv3 --pmc
+    passes over `bench.py --kernel-loop`.  FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are each
+    divided by what the same counter reads per byte of a device-to-device copy of known size
+    (torch's copy kernel, CALIBRATION_COPY_BYTES read and written): on gfx950 FETCH_SIZE reads
+    half the copied bytes and WRITE_SIZE all of them.  Returns (dict, None) or (None, reason)."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    base = os.path.join(ROOT, "gpurun_out")
+    os.makedirs(base, exist_ok=True)
+    work = tempfile.mkdtemp(prefix="bench_pmc_", dir=base)
+    env = dict(os.environ, TMPDIR="/tmp")
+    counts = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        outdir = os.path.join(work, counter)
+        cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", counter, "--output-format", "csv",
+               "-d", outdir, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__),
+               "--kernel-loop", workload, "--iters", str(iters)]
+        print(f"bench.py: counter pass {counter}", file=sys.stderr, flush=True)
+        with open(os.path.join(work, counter + ".log"), "w") as log:
+            rc = subprocess.run(cmd, cwd="/tmp", env=env, stdout=log, stderr=subprocess.STDOUT)
+        rows = _counter_rows(outdir)
+        if not rows:
+            return None, f"{counter} pass produced no counter rows (rc {rc.returncode})"
+        rows = [r for r in rows if r.get("Counter_Name") == counter]
+        rows.sort(key=lambda r: int(r.get("Dispatch_Id", 0) or 0))
+        counts[counter] = [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows]
+
+    def avg_kib(counter, pred):
+        vals = [v for name, v in counts[counter] if pred(name)]
+        return statistics.fmean(vals) if vals else None
+
+    def copy_kib(counter):
+        # The calibration copies are the child's last `iters` copy dispatches (earlier ones
+        # are the buffer-set clones).
+        copies = [v for name, v in counts[counter] if "copy" in name.lower()][-iters:]
+        return statistics.fmean(copies) if len(copies) == iters else None
+
+    cal = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        kib = copy_kib(counter)
+        if not kib:
+            return None, f"no calibration copy found in the {counter} pass"
+        cal[counter] = kib * 1024.0 / CALIBRATION_COPY_BYTES  # counted bytes per true byte
+
+    def call_bytes(names):
+        total = 0.0
+        detail = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            b = 0.0
+            for n in names:
+                kib = avg_kib(counter, lambda k, n=n: n in k)
+                if kib is None:
+                    return None, None
+                b += kib * 1024.0 / cal[counter]
+            detail[counter.split("_")[0].lower()] = int(round(b))
+            total += b
+        return int(round(total)), detail
+
+    fwd_total, fwd_detail = call_bytes(["fwd_reg_kernel"])
+    bwd_total, bwd_detail = call_bytes(["bwd_reg_kernel", "col_reduce_kernel"])
+    return {"fwd": fwd_total, "fwd_detail": fwd_detail, "bwd": bwd_total,
+            "bwd_detail": bwd_detail,
+            "calibration": {"FETCH_SIZE": round(cal["FETCH_SIZE"], 4),
+                            "WRITE_SIZE": round(cal["WRITE_SIZE"], 4),
+                            "copy_bytes": CALIBRATION_COPY_BYTES},
+            "passes": f"rocprofv3 --pmc FETCH_SIZE | WRITE_SIZE -- bench.py --kernel-loop "
+                      f"{workload} --iters {iters}"}, None
+
+
+# ------------------------------------------------------------------------------------------------
+# CPU baselines.
+# ------------------------------------------------------------------------------------------------
 def cpu_baseline(w, seconds):
     """Time the C oracle (scalar C port, one thread) on a bounded row sample of the workload."""
-    import numpy as np
     from oracle import c_oracle
     from fused_layernorm.testing import algorithmic_bytes, make_inputs
 
@@ -218,14 +364,14 @@ def cpu_baseline(w, seconds):
     }
 
 
-def torch_cpu_baseline(w, seconds):
-    """The reference's CPU path (torch-CPU F.layer_norm / F.rms_norm + autograd backward) on the
-    same row sample, all host threads."""
+def torch_cpu_baseline(w, seconds, threads=16):
+    """The reference's CPU path (torch-CPU F.layer_norm / F.rms_norm + autograd backward) on a
+    row sample of the same workload, `threads` host threads (the GPU box's CPU share)."""
     import torch
     from fused_layernorm.testing import algorithmic_bytes, make_inputs
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    rows = 256
+    torch.set_num_threads(max(1, min(threads, os.cpu_count() or 1)))
+    rows = 1024
     inp = make_inputs(w, rows)
     x = inp["x"].requires_grad_(True)
     g = inp.get("gamma")
@@ -251,7 +397,31 @@ def torch_cpu_baseline(w, seconds):
     med = statistics.median(times)
     return {"value": round(algorithmic_bytes(w, rows)["total"] / med / 1e9, 3), "unit": "GB/s",
             "threads": torch.get_num_threads(), "kind": "torch-cpu (reference CPU path)",
-            "sample": f"{rows} rows of {w.name}, median of {len(times)}"}
+            "sample": f"{rows} of {w.rows} rows of {w.name}, median of {len(times)} runs"}
+
+
+# ------------------------------------------------------------------------------------------------
+def measure(lib, capi, torch, w, steps, warmup, stream, stream_obj):
+    from fused_layernorm.testing import algorithmic_bytes, make_inputs
+
+    r = Runner(lib, capi, torch, w, make_inputs(w))
+    r.prime(stream)
+    for _ in range(warmup):
+        r.step(stream)
+    warm_clocks(lambda: r.step(stream))
+    ms = r.time_region(lambda: r.step(stream), steps, stream_obj)
+    res = dict(ms=ms, bytes=algorithmic_bytes(w), nsets=r.nsets)
+    n_group = max(20, steps // 2)
+    res["ms_fwd"] = time_launch_group(r, "fwd", n_group, stream, stream_obj)
+    if r.has_bwd:
+        res["ms_bwd"] = time_launch_group(r, "bwd", n_group, stream, stream_obj)
+    del r
+    torch.cuda.empty_cache()
+    return res
+
+
+def gbs(nbytes, ms):
+    return nbytes / (ms * 1e-3) / 1e9
 
 
 def main():
@@ -261,38 +431,35 @@ def main():
               "row-sharded multi-GPU layout is not built or measured here.",
               file=sys.stderr)
         sys.exit(2)
+    if args.kernel_loop:
+        kernel_loop(args)
+        return
+
+    # Counter passes first, in child processes, before this process touches the GPU.
+    traffic, traffic_note = (None, "skipped (--no-traffic)")
+    if not args.no_traffic:
+        traffic, traffic_note = pmc_traffic(HEADLINE)
 
     import torch
     import capi
-    from fused_layernorm.testing import WORKLOADS, algorithmic_bytes, make_inputs
+    from fused_layernorm.testing import WORKLOADS
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     lib = capi.load()
     stream_obj = torch.cuda.current_stream()
     stream = capi.stream()
 
-    results = {}
-    for name in ("ln_fwd_bwd_bf16_8192x4096", "rms_fwd_bwd_bf16_8192x4096"):
-        w = WORKLOADS[name]
-        r = Runner(lib, capi, torch, w, make_inputs(w))
-        for _ in range(args.warmup):
-            r.step(stream)
-        warm_clocks(lambda: r.step(stream))
-        ms = r.time_region(lambda: r.step(stream), args.steps, stream_obj)
-        nb = algorithmic_bytes(w)
-        ms_f = time_launch_group(r, "fwd", max(20, args.steps // 2), stream, stream_obj)
-        ms_b = time_launch_group(r, "bwd", max(20, args.steps // 2), stream, stream_obj)
-        results[name] = dict(ms=ms, bytes=nb, ms_fwd=ms_f, ms_bwd=ms_b, nsets=r.nsets)
-        del r
-        torch.cuda.empty_cache()
-
-    head = results["ln_fwd_bwd_bf16_8192x4096"]
-    gbs = head["bytes"]["total"] / (head["ms"] * 1e-3) / 1e9
-    bwd_gbs = head["bytes"]["bwd"] / (head["ms_bwd"] * 1e-3) / 1e9
-    rms = results["rms_fwd_bwd_bf16_8192x4096"]
+    head = measure(lib, capi, torch, WORKLOADS[HEADLINE], args.steps, args.warmup, stream,
+                   stream_obj)
+    rms = None
+    if not args.headline_only:
+        rms = measure(lib, capi, torch, WORKLOADS["rms_fwd_bwd_bf16_8192x4096"], args.steps,
+                      args.warmup, stream, stream_obj)
+    value = gbs(head["bytes"]["total"], head["ms"])
+    bwd_gbs = gbs(head["bytes"]["bwd"], head["ms_bwd"])
     out = {
         "metric": METRIC,
-        "value": round(gbs, 1),
+        "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -303,36 +470,65 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: seeded torch.randn inputs (x seed 3, gamma 103, beta 203, dy 303)",
-        "config": {"workload": "ln_fwd_bwd_bf16_8192x4096", "rows": 8192, "cols": 4096,
-                   "step": "LayerNorm fwd (y, mean, rstd) + bwd (dx, dgamma, dbeta fp32)",
+        "config": {"workload": HEADLINE, "rows": 8192, "cols": 4096,
+                   "step": "LayerNorm fwd (y, mean, rstd) + bwd (dx, dgamma, dbeta fp32); the "
+                           "bwd runs on another buffer set than the fwd",
                    "algorithmic_bytes_per_step": head["bytes"]["total"],
                    "rotating_buffer_sets": head["nsets"]},
-        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "us_per_call": {"fwd": round(head["ms_fwd"] * 1e3, 2),
                         "bwd": round(head["ms_bwd"] * 1e3, 2),
                         "fwd_bwd": round(head["ms"] * 1e3, 2)},
         "roofline": {
-            "kernel": "layernorm backward launch group (bwd_reg_kernel + col_reduce_kernel)",
+            "kernel": "fln_layernorm_backward (bwd_reg_kernel + col_reduce_kernel, one call)",
             "bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(bwd_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic["bwd"] if traffic and traffic.get("bwd") else None,
             "algorithmic_bytes_per_launch": head["bytes"]["bwd"],
             "avg_launch_us": round(head["ms_bwd"] * 1e3, 2),
         },
         "forward_kernel": {
             "kernel": "fwd_reg_kernel", "algorithmic_bytes_per_launch": head["bytes"]["fwd"],
             "avg_launch_us": round(head["ms_fwd"] * 1e3, 2),
-            "achieved_gbs": round(head["bytes"]["fwd"] / (head["ms_fwd"] * 1e-3) / 1e9, 1),
+            "achieved_gbs": round(gbs(head["bytes"]["fwd"], head["ms_fwd"]), 1),
+            "traffic": traffic["fwd"] if traffic and traffic.get("fwd") else None,
         },
-        "rms_fwd_bwd": {
+    }
+    if rms:
+        out["rms_fwd_bwd"] = {
             "workload": "rms_fwd_bwd_bf16_8192x4096",
-            "value": round(rms["bytes"]["total"] / (rms["ms"] * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "value": round(gbs(rms["bytes"]["total"], rms["ms"]), 1), "unit": "GB/s",
             "us_per_call": {"fwd": round(rms["ms_fwd"] * 1e3, 2),
                             "bwd": round(rms["ms_bwd"] * 1e3, 2),
                             "fwd_bwd": round(rms["ms"] * 1e3, 2)},
-        },
-    }
+        }
+    if traffic:
+        out["roofline"]["traffic_detail"] = {"fetch": traffic["bwd_detail"]["fetch"],
+                                             "write": traffic["bwd_detail"]["write"],
+                                             "calibration": traffic["calibration"],
+                                             "passes": traffic["passes"]}
+    else:
+        out["roofline"]["traffic_note"] = traffic_note
+
+    if not args.no_configs and not args.headline_only:
+        cfg = {}
+        for name in CONFIGS:
+            w = WORKLOADS[name]
+            res = measure(lib, capi, torch, w, max(50, args.steps // 2), args.warmup, stream,
+                          stream_obj)
+            entry = {"us_per_call": round(res["ms_fwd"] * 1e3, 2)}
+            if "ms_bwd" in res:
+                entry["us_per_call"] = {"fwd": round(res["ms_fwd"] * 1e3, 2),
+                                        "bwd": round(res["ms_bwd"] * 1e3, 2),
+                                        "fwd_bwd": round(res["ms"] * 1e3, 2)}
+                entry["gbs"] = round(gbs(res["bytes"]["total"], res["ms"]), 1)
+            else:
+                entry["gbs"] = round(gbs(res["bytes"]["fwd"], res["ms_fwd"]), 1)
+            cfg[name] = entry
+        out["configs"] = cfg
+
     if not args.no_cpu_baseline:
-        w = WORKLOADS["ln_fwd_bwd_bf16_8192x4096"]
+        w = WORKLOADS[HEADLINE]
         out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
         out["cpu_baseline"]["torch_cpu"] = torch_cpu_baseline(w, max(2.0, args.cpu_seconds / 2))
     out["host"] = platform.node()

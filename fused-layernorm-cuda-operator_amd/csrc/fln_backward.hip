@@ -13,8 +13,10 @@
 // and accumulates the column sums dy*xhat (dgamma) and dy (dbeta) for the columns each lane
 // owns in fp32 registers.  At the end the block's row groups are combined through LDS in a
 // fixed order and written as one fp32 partial row per block.
-// Stage 2 (col_reduce_kernel): sums the partial rows per column in a fixed order.  Nothing uses
-// atomics, so dgamma/dbeta are bitwise reproducible run to run.
+// Stage 2 (col_reduce_kernel): sums the partial rows per column in a fixed order, spread over
+// many small blocks (32 columns each).  Nothing uses atomics, so dgamma/dbeta are bitwise
+// reproducible run to run.  (Fusing stage 2 into stage 1 behind a cooperative grid barrier was
+// measured at 2x the time of the two launches on gfx950 and is not used.)
 #include <stdlib.h>
 
 #include "fln_device.h"
@@ -22,8 +24,104 @@
 
 namespace fln {
 
+struct ColReduceArgs {
+  const float* part[2];  // [G, ld] partial arrays (dgamma first, then dbeta)
+  void* out[2];
+  int64_t G;             // partial rows
+  int64_t N;             // columns
+  int ny;                // arrays to reduce (0, 1 or 2)
+  int out_dtype;         // FLN_F32 / FLN_BF16 / FLN_F16
+};
+
+// Stage 2.  The partial arrays are [G, ld] fp32 (ld = cols rounded up to 4).  The work is cut
+// into "quad blocks": 8 column quads (32 columns) of one array each.  A quad block is reduced by
+// 8 * S threads: thread (slice, q) sums partial rows slice, slice + S, ... of quad q with eight
+// loads in flight, then the S slices are folded through LDS in fixed steps of 4 (S -> S/4 -> ...
+// -> at most 8) and one thread per quad adds the last few.  The order depends only on G and S,
+// so the result is bitwise reproducible.
+constexpr int kCrQuads = 8;
+
+__device__ __forceinline__ void add4(float4& a, const float4& b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+__device__ __forceinline__ void store_param(void* out, int dtype, int64_t i, float v) {
+  if (dtype == FLN_F32)
+    static_cast<float*>(out)[i] = v;
+  else if (dtype == FLN_BF16)
+    static_cast<__bf16*>(out)[i] = from_f32<__bf16>(v);
+  else
+    static_cast<_Float16*>(out)[i] = from_f32<_Float16>(v);
+}
+
+__host__ __device__ inline int64_t quad_blocks(const ColReduceArgs& a) {
+  const int64_t ld = (a.N + 3) & ~int64_t(3);
+  return a.ny * (((ld >> 2) + kCrQuads - 1) / kCrQuads);
+}
+
+// Reduce quad block `qb` with the first 8 * S threads of the block (S a power of two >= 4);
+// comb holds 8 * S float4.  Every thread of the block must call this (it contains barriers).
+__device__ __forceinline__ void reduce_quad_block(const ColReduceArgs& a, int64_t qb, int S,
+                                                  float4* comb) {
+  const int tid = threadIdx.x;
+  const int q = tid % kCrQuads, slice = tid / kCrQuads;
+  const int64_t ld = (a.N + 3) & ~int64_t(3);
+  const int64_t nqb = ((ld >> 2) + kCrQuads - 1) / kCrQuads;
+  const int y = static_cast<int>(qb / nqb);
+  const int64_t c = ((qb - y * nqb) * kCrQuads + q) * 4;
+  const bool active = slice < S;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (active && c < ld) {
+    const float* col = a.part[y] + c;
+    int64_t k = slice;
+    for (; k + 7 * S < a.G; k += 8 * S) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(col + (k + u * S) * ld);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) add4(acc, v[u]);
+    }
+    for (; k < a.G; k += S) add4(acc, *reinterpret_cast<const float4*>(col + k * ld));
+  }
+  if (active) comb[slice * kCrQuads + q] = acc;
+  __syncthreads();
+  int n = S;
+  while (n > 8) {
+    n >>= 2;
+    if (slice < n) {
+      float4 r = comb[slice * kCrQuads + q];
+#pragma unroll
+      for (int j = 1; j < 4; ++j) add4(r, comb[(slice + j * n) * kCrQuads + q]);
+      comb[slice * kCrQuads + q] = r;  // slice < n reads only slices >= n (none written here)
+    }
+    __syncthreads();
+  }
+  if (slice == 0 && c < a.N) {
+    float4 r = comb[q];
+    for (int j = 1; j < n; ++j) add4(r, comb[j * kCrQuads + q]);
+    const float rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (c + e < a.N) store_param(a.out[y], a.out_dtype, c + e, rr[e]);
+  }
+  __syncthreads();  // comb is reused by the caller's next quad block
+}
+
 #ifndef FLN_BWD_PREFETCH
 #define FLN_BWD_PREFETCH 3
+#endif
+// Cache policies of the streamed rows: dx is stored non-temporal; x / dy / dres loads keep the
+// default policy.  Measured on MI355X (bf16 forward + backward steps): non-temporal loads as
+// well make the 16384 x 8192 RMSNorm step 2% faster but the 8192 x 4096 LayerNorm step 3%
+// slower.  gamma, the statistics and the column partials keep the default policy.
+#ifndef FLN_BWD_LOAD_POL
+#define FLN_BWD_LOAD_POL kDefault
+#endif
+#ifndef FLN_BWD_STORE_POL
+#define FLN_BWD_STORE_POL kStream
 #endif
 template <class T, bool DRES, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
@@ -91,13 +189,13 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     const rsrc_t dr = make_rsrc(DY + row * N, nb);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      xn[slot][i] = buf_load<P>(xr, t + i * tpr);
-      dn[slot][i] = buf_load<P>(dr, t + i * tpr);
+      xn[slot][i] = buf_load<P, FLN_BWD_LOAD_POL>(xr, t + i * tpr);
+      dn[slot][i] = buf_load<P, FLN_BWD_LOAD_POL>(dr, t + i * tpr);
     }
     if constexpr (DRES) {
       const rsrc_t rr = make_rsrc(DR + row * N, nb);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) rn[slot][i] = buf_load<P>(rr, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) rn[slot][i] = buf_load<P, FLN_BWD_LOAD_POL>(rr, t + i * tpr);
     }
     const uint32_t sb = nb ? 4u : 0u;
     mun[slot] = __builtin_bit_cast(
@@ -180,7 +278,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     load_row(it + 1 + PD, nxt);
     const rsrc_t xo = make_rsrc(DX ? DX + row * N : nullptr, nb);
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) buf_store(o[i], xo, t + i * tpr);
+    for (int i = 0; i < VPL; ++i) buf_store<P, FLN_BWD_STORE_POL>(o[i], xo, t + i * tpr);
   }
   }
 
@@ -285,48 +383,13 @@ __global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
 // Stage 2: out[c] = sum over partial rows k (in order) of part[k][c].  Block = 16 waves over
 // 256 columns: lane l owns 4 columns, wave w sums rows w, w+16, ...; the 16 wave sums are then
 // added in wave order through LDS.  A y-block index selects the array (dgamma or dbeta).
-struct ColReduceArgs {
-  const float* part[2];
-  void* out[2];
-  int64_t G;
-  int64_t N;
-};
+constexpr int kCrSlices = 32;
+constexpr int kCrThreads = kCrQuads * kCrSlices;
 
-template <class TO>
-__global__ __launch_bounds__(1024) void col_reduce_kernel(const ColReduceArgs a) {
-  __shared__ float4 comb[16][64];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const float* part = a.part[blockIdx.y];
-  TO* out = static_cast<TO*>(a.out[blockIdx.y]);
-  const int64_t ld = (a.N + 3) & ~int64_t(3);
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + lane * 4;
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (c < ld) {
-#pragma unroll 8
-    for (int64_t k = wave; k < a.G; k += 16) {
-      const float4 v = *reinterpret_cast<const float4*>(part + k * ld + c);
-      s.x += v.x;
-      s.y += v.y;
-      s.z += v.z;
-      s.w += v.w;
-    }
-  }
-  comb[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0) {
-    float4 r = comb[0][lane];
-    for (int k = 1; k < 16; ++k) {
-      const float4 v = comb[k][lane];
-      r.x += v.x;
-      r.y += v.y;
-      r.z += v.z;
-      r.w += v.w;
-    }
-    const float rr[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (c + e < a.N) out[c + e] = from_f32<TO>(rr[e]);
-  }
+// Stage 2: one quad block per 256-thread block (32 slices), >= 256 blocks at 4096 columns.
+__global__ __launch_bounds__(kCrThreads) void col_reduce_kernel(const ColReduceArgs a) {
+  __shared__ float4 comb[kCrThreads];
+  reduce_quad_block(a, blockIdx.x, kCrSlices, comb);
 }
 
 namespace {
@@ -388,7 +451,8 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s) {
     return static_cast<int>(hipGetLastError());
   }
   constexpr int VV = 16 / sizeof(T);
-  if (geo.vec == VV) return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, geo.threads, s);
+  if (geo.vec == VV)
+    return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, geo.threads, s);
   return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, geo.threads, s);
 }
 
@@ -401,9 +465,11 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   g.vec = (vec_ok && cols % vv == 0) ? vv : 1;
   const int64_t nvec = cols / g.vec;
   auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
-  // Elements per lane: 8 by default (x-hat, dy, g, gamma and both column accumulators of a
-  // lane's columns stay in fp32 registers); up to 16 for rows too wide for 16 waves.
-  const int epl = env_int_b("FLN_BWD_EPL", 8);
+  // Elements per lane: 8 by default for 16-bit types, 4 for fp32 (x-hat, dy, g, gamma, both
+  // column accumulators and the prefetched raw rows of a lane's columns stay in registers;
+  // fp32 rows with 8 per lane exceed the 128-VGPR budget of a 1024-thread block and spill);
+  // more only for rows too wide for 16 waves.
+  const int epl = env_int_b("FLN_BWD_EPL", es == 4 ? 4 : 8);
   int cap = (epl >= g.vec ? epl : g.vec) / g.vec;
   if (cap > bwd_max_vpl(g.vec, es)) cap = bwd_max_vpl(g.vec, es);
   int wpr = 1;
@@ -444,6 +510,15 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   float* ws = p0.part_g;
   p.part_g = dgamma ? ws : nullptr;
   p.part_b = dbeta ? ws + geo.blocks * ld : nullptr;
+  ColReduceArgs a{};
+  if (dgamma) { a.part[a.ny] = p.part_g; a.out[a.ny] = dgamma; ++a.ny; }
+  if (dbeta) { a.part[a.ny] = p.part_b; a.out[a.ny] = dbeta; ++a.ny; }
+  a.G = geo.blocks;
+  a.N = p.cols;
+  a.out_dtype = dparam_dtype;
+  if (a.ny > 0 && dparam_dtype != FLN_F32 && dparam_dtype != FLN_BF16 &&
+      dparam_dtype != FLN_F16)
+    return FLN_ERR_INVALID;
   int rc;
   switch (dtype) {
     case FLN_F32: rc = dispatch_backward<float>(p, geo, s); break;
@@ -451,24 +526,9 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
     case FLN_F16: rc = dispatch_backward<_Float16>(p, geo, s); break;
     default: return FLN_ERR_INVALID;
   }
-  if (rc != 0 || (!dgamma && !dbeta)) return rc;
-
-  ColReduceArgs a{};
-  int ny = 0;
-  if (dgamma) { a.part[ny] = p.part_g; a.out[ny] = dgamma; ++ny; }
-  if (dbeta) { a.part[ny] = p.part_b; a.out[ny] = dbeta; ++ny; }
-  a.G = geo.blocks;
-  a.N = p.cols;
-  const dim3 grid(static_cast<unsigned>((p.cols + 255) / 256), ny);
-  const int od = dparam_dtype;
-  if (od == FLN_F32)
-    hipLaunchKernelGGL((col_reduce_kernel<float>), grid, dim3(1024), 0, s, a);
-  else if (od == FLN_BF16)
-    hipLaunchKernelGGL((col_reduce_kernel<__bf16>), grid, dim3(1024), 0, s, a);
-  else if (od == FLN_F16)
-    hipLaunchKernelGGL((col_reduce_kernel<_Float16>), grid, dim3(1024), 0, s, a);
-  else
-    return FLN_ERR_INVALID;
+  if (rc != 0 || a.ny == 0) return rc;
+  hipLaunchKernelGGL(col_reduce_kernel, dim3(static_cast<unsigned>(quad_blocks(a))),
+                     dim3(kCrThreads), 0, s, a);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -64,54 +64,62 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
                                            base ? static_cast<int>(nbytes) : 0, 0x00020000);
 }
 
+// Cache policy: the last operand of the raw buffer builtins (gfx950 CPol bits: 1 = sc0,
+// 2 = nt, 16 = sc1).  0 is the default policy; kStream (nt) marks data touched once, so it is
+// not kept in the caches at the expense of data that is reused.
+constexpr int kDefault = 0;
+constexpr int kStream = 2;
+
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int BYTES> struct BufIO;
-template <> struct BufIO<16> {
+template <int BYTES, int POL = kDefault> struct BufIO;
+template <int POL> struct BufIO<16, POL> {
   using W = u32x4;
   __device__ static W load(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
   }
   __device__ static void store(W w, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, POL);
   }
 };
-template <> struct BufIO<8> {
+template <int POL> struct BufIO<8, POL> {
   using W = u32x2;
   __device__ static W load(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL);
   }
   __device__ static void store(W w, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, POL);
   }
 };
-template <> struct BufIO<4> {
+template <int POL> struct BufIO<4, POL> {
   using W = uint32_t;
   __device__ static W load(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
   }
   __device__ static void store(W w, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b32(w, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(w, r, off, 0, POL);
   }
 };
-template <> struct BufIO<2> {
+template <int POL> struct BufIO<2, POL> {
   using W = uint16_t;
   __device__ static W load(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, POL);
   }
   __device__ static void store(W w, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b16(w, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(w, r, off, 0, POL);
   }
 };
 
 // Load / store the v-th Pack of a resource (byte offset v * sizeof(P)).
-template <class P> __device__ __forceinline__ P buf_load(rsrc_t r, uint32_t v) {
-  using IO = BufIO<sizeof(P)>;
+template <class P, int POL = kDefault>
+__device__ __forceinline__ P buf_load(rsrc_t r, uint32_t v) {
+  using IO = BufIO<sizeof(P), POL>;
   return __builtin_bit_cast(P, IO::load(r, v * static_cast<uint32_t>(sizeof(P))));
 }
-template <class P> __device__ __forceinline__ void buf_store(const P& p, rsrc_t r, uint32_t v) {
-  using IO = BufIO<sizeof(P)>;
+template <class P, int POL = kDefault>
+__device__ __forceinline__ void buf_store(const P& p, rsrc_t r, uint32_t v) {
+  using IO = BufIO<sizeof(P), POL>;
   IO::store(__builtin_bit_cast(typename IO::W, p), r, v * static_cast<uint32_t>(sizeof(P)));
 }
 __device__ __forceinline__ void buf_store_f32(float x, rsrc_t r, uint32_t byte_off) {

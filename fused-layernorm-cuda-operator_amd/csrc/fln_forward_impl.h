@@ -54,6 +54,16 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 #ifndef FLN_FWD_PREFETCH
 #define FLN_FWD_PREFETCH 2
 #endif
+// Cache policies of the streamed rows: loads of x / residual and stores of y / h / q are
+// non-temporal (each byte is touched once; measured on MI355X this is 3-10% faster than the
+// default policy for every forward flavour, because the streams no longer evict each other's
+// lines or the parameters).  The parameters and per-row statistics keep the default policy.
+#ifndef FLN_FWD_LOAD_POL
+#define FLN_FWD_LOAD_POL kStream
+#endif
+#ifndef FLN_FWD_STORE_POL
+#define FLN_FWD_STORE_POL kStream
+#endif
 template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
   constexpr int PD = FLN_FWD_PREFETCH;  // rows in flight ahead of the current one
@@ -108,11 +118,11 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     const uint32_t nb = bytes_of(rb);
     const rsrc_t xr = make_rsrc(X + row * N, nb);
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) xd[i] = buf_load<P>(xr, t + i * tpr);
+    for (int i = 0; i < VPL; ++i) xd[i] = buf_load<P, FLN_FWD_LOAD_POL>(xr, t + i * tpr);
     if constexpr (RES) {
       const rsrc_t rr = make_rsrc(R + row * N, nb);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) rd[i] = buf_load<P>(rr, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) rd[i] = buf_load<P, FLN_FWD_LOAD_POL>(rr, t + i * tpr);
     }
   };
 
@@ -249,12 +259,12 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     if constexpr (RES) {
       const rsrc_t hr = make_rsrc(p.h ? static_cast<T*>(p.h) + row * N : nullptr, nb);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) buf_store(ho[i], hr, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) buf_store<P, FLN_FWD_STORE_POL>(ho[i], hr, t + i * tpr);
     }
     if constexpr (!FP8) {
       const rsrc_t yr = make_rsrc(static_cast<T*>(p.y) + row * N, nb);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) buf_store(yo[i], yr, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) buf_store<P, FLN_FWD_STORE_POL>(yo[i], yr, t + i * tpr);
     } else {
       buf_store_f32(scale, make_rsrc(p.scale + row, stat_nb), stat_off);
       const rsrc_t qr = make_rsrc(static_cast<uint8_t*>(p.y) + row * N,
@@ -262,10 +272,11 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         if constexpr (VEC >= 4)
-          BufIO<VEC>::store(qo[i], qr, (t + i * tpr) * static_cast<uint32_t>(VEC));
+          BufIO<VEC, FLN_FWD_STORE_POL>::store(qo[i], qr,
+                                               (t + i * tpr) * static_cast<uint32_t>(VEC));
         else
           __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(qo[i]), qr, t + i * tpr,
-                                               0, 0);
+                                               0, FLN_FWD_STORE_POL);
       }
     }
   }

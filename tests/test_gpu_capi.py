@@ -409,6 +409,27 @@ def test_backward_is_deterministic(lib):
             assert torch.equal(a, c)
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [
+    (torch.bfloat16, 1000, 4096), (torch.float16, 333, 1023), (torch.bfloat16, 3, 7168),
+    (torch.float16, 4096, 768)])
+def test_parameter_gradients_in_parameter_dtype(lib, dtype, rows, cols):
+    """dgamma / dbeta written as bf16 / f16 (the fp32 column sums rounded once on store): each
+    element within half an ulp of the parameter type, plus the fp32 reduction tolerance."""
+    gen = torch.Generator().manual_seed(rows * 31 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, dy = cuda(xc), cuda(gc), cuda(dyc)
+    _, mean, rstd = ln_forward(lib, x, g, g, 1e-5)
+    _, dg, db = ln_backward(lib, dy, x, mean, rstd, g, dparam_f32=False)
+    assert dg.dtype == dtype and db.dtype == dtype
+    _, dg_ref, db_ref = norms.layer_norm_bwd(f32(dyc), f32(xc), f32(gc), 1e-5)
+    kind = "bf16" if dtype == torch.bfloat16 else "f16"
+    for got, ref, what in ((dg, dg_ref, "dgamma"), (db, db_ref, "dbeta")):
+        assert_within_ulp(to_np(got), ref, 0.5, atol=1e-4 * np.abs(ref).max(), kind=kind,
+                          what=what)
+
+
 def test_residual_gradient_is_added(lib):
     gen = torch.Generator().manual_seed(9)
     xc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
