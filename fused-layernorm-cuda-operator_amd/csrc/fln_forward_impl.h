@@ -82,7 +82,9 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
   const int64_t N = p.cols;
   const int nvec = static_cast<int>(N / VEC);
   const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
-  const float inv_n = 1.0f / static_cast<float>(N);
+  // Statistics divide by N (correctly rounded, as the reference's sum / N): an exactly summed
+  // constant row then has an exact mean and maps to beta exactly.
+  const float fn = static_cast<float>(N);
   const T* X = static_cast<const T*>(p.x);
   const T* R = static_cast<const T*>(p.res);
   const int64_t stride = gridDim.x;
@@ -113,40 +115,40 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 
   // Ring of raw loads: the PD rows after the current one are in flight.
   P xv[PD][VPL], rv[PD][VPL];
-  auto load_row = [&](int64_t rb, P (&xd)[VPL], P (&rd)[VPL]) {
+  auto load_row = [&](int64_t rb, int slot) {
     const int64_t row = row_of(rb);
     const uint32_t nb = bytes_of(rb);
     const rsrc_t xr = make_rsrc(X + row * N, nb);
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) xd[i] = buf_load<P, FLN_FWD_LOAD_POL>(xr, t + i * tpr);
+    for (int i = 0; i < VPL; ++i) xv[slot][i] = buf_load<P, FLN_FWD_LOAD_POL>(xr, t + i * tpr);
     if constexpr (RES) {
       const rsrc_t rr = make_rsrc(R + row * N, nb);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) rd[i] = buf_load<P, FLN_FWD_LOAD_POL>(rr, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) rv[slot][i] = buf_load<P, FLN_FWD_LOAD_POL>(rr, t + i * tpr);
     }
   };
 
   float xf[VPL][VEC];  // the row being normalized, fp32
   P hv[VPL];           // residual sum of that row, in the I/O type (RES only)
-  auto widen = [&](const P (&xd)[VPL], const P (&rd)[VPL]) {
+  auto widen = [&](int slot) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         if constexpr (RES) {
-          hv[i].v[e] = from_f32<T>(to_f32(xd[i].v[e]) + to_f32(rd[i].v[e]));
+          hv[i].v[e] = from_f32<T>(to_f32(xv[slot][i].v[e]) + to_f32(rv[slot][i].v[e]));
           xf[i][e] = to_f32(hv[i].v[e]);
         } else {
-          xf[i][e] = to_f32(xd[i].v[e]);
+          xf[i][e] = to_f32(xv[slot][i].v[e]);
         }
       }
   };
 
   const int64_t rb0 = blockIdx.x;
 #pragma unroll
-  for (int k = 0; k < PD; ++k) load_row(rb0 + k * stride, xv[k], rv[k]);
-  widen(xv[0], rv[0]);
-  load_row(rb0 + PD * stride, xv[0], rv[0]);
+  for (int k = 0; k < PD; ++k) load_row(rb0 + k * stride, k);
+  widen(0);
+  load_row(rb0 + PD * stride, 0);
   int parity = 0;
   // Row k of this row group is rb0 + k * stride; slot k % PD holds the raw loads of row k + PD
   // once row k has been widened.  The inner loop is unrolled so every slot index is static.
@@ -169,7 +171,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) s += xf[i][e];
-      mean = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane) * inv_n;
+      mean = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane) / fn;
     }
     float q = 0.0f;
 #pragma unroll
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       }
     }
     q = row_allreduce<SumOp>(q, slots[1], wpr, rg, wave, lane);
-    const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
+    const float rstd = 1.0f / sqrtf(q / fn + p.eps);
 
     //    Normalize + affine + epilogue, packed to the output format.
 #pragma unroll
@@ -248,8 +250,8 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 
     // 2. + 3. Consume the next row, put the row PD after it in flight.
     const int nxt = (s + 1) % PD;  // static after unrolling
-    widen(xv[nxt], rv[nxt]);
-    load_row(rb + (PD + 1) * stride, xv[nxt], rv[nxt]);
+    widen(nxt);
+    load_row(rb + (PD + 1) * stride, nxt);
 
     // 4. Stores of this row (rows past the end have a zero-byte resource: dropped).
     const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;

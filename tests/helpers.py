@@ -36,8 +36,9 @@ def assert_within_ulp(got, ref, ulps: float = 1.0, atol: float = 0.0, kind: str 
     bad = err > bound
     if bad.any():
         i = np.unravel_index(np.argmax(err - bound), err.shape)
+        extra = f"{atol:g}" if np.ndim(atol) == 0 else "elementwise atol"
         raise AssertionError(
-            f"{what}: {int(bad.sum())} of {bad.size} elements exceed {ulps} {kind} ulp + {atol:g}; "
+            f"{what}: {int(bad.sum())} of {bad.size} elements exceed {ulps} {kind} ulp + {extra}; "
             f"worst at {i}: got {g[i]!r} ref {r[i]!r} err {err[i]:.3g} bound {bound[i]:.3g}")
 
 
@@ -48,3 +49,24 @@ def assert_close_rel(got, ref, rtol: float, what: str = ""):
     err = np.abs(g - r).max() if g.size else 0.0
     scale = np.abs(r).max() if r.size else 0.0
     assert err <= rtol * max(scale, 1e-30), f"{what}: max err {err:.3g} > {rtol:g} * {scale:.3g}"
+
+
+def fp8_ordinal(codes):
+    """Signed position of an e4m3fn code on the number line (+0 and -0 both map to 0), so that
+    adjacent representable values differ by exactly 1."""
+    c = np.asarray(codes).astype(np.int32)
+    mag = c & 0x7F
+    return np.where(c & 0x80, -mag, mag)
+
+
+def assert_fp8_close(q_got, s_got, q_ref, s_ref, what=""):
+    """fp8 output bar: per-row scales within 1e-6 relative; codes identical except +-1 code on
+    at most 0.1% of the elements."""
+    s_got = np.asarray(s_got, np.float64)
+    s_ref = np.asarray(s_ref, np.float64)
+    rel = np.abs(s_got - s_ref) / np.where(s_ref > 0, s_ref, 1.0)
+    assert rel.max() <= 1e-6, f"{what}: scale rel err {rel.max():.3g}"
+    diff = np.abs(fp8_ordinal(q_got) - fp8_ordinal(q_ref))
+    n_diff = int((diff != 0).sum())
+    assert int(diff.max()) <= 1, f"{what}: a code differs by {int(diff.max())} steps"
+    assert n_diff <= 1e-3 * diff.size, f"{what}: {n_diff} of {diff.size} codes differ"

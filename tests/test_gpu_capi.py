@@ -16,15 +16,13 @@ for the full benchmark sizes) on the same seeded inputs (fused_layernorm.testing
 """
 from __future__ import annotations
 
-import ctypes
-import os
-
 import numpy as np
 import pytest
 import torch
 
 import capi
-from helpers import assert_close_rel, assert_within_ulp, to_np
+from gpu_calls import cuda, f32, ln_backward, ln_forward, rms_backward, rms_forward, workspace
+from helpers import assert_close_rel, assert_fp8_close, assert_within_ulp, to_np
 from oracle import c_oracle, norms
 from fused_layernorm.testing import WORKLOADS, make_inputs
 
@@ -36,67 +34,6 @@ DX_ATOL_REL = 2.0 ** -12
 @pytest.fixture(scope="module")
 def lib(gpu_available):
     return capi.load()
-
-
-def cuda(t):
-    return None if t is None else t.to("cuda")
-
-
-def f32(t):
-    return None if t is None else to_np(t).astype(np.float32)
-
-
-# ------------------------------------------------------------------------------------------------
-# C-ABI call wrappers.
-# ------------------------------------------------------------------------------------------------
-def ln_forward(lib, x, g, b, eps, stats=True):
-    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
-    y = torch.empty_like(x)
-    mean = torch.empty(rows, device=x.device, dtype=torch.float32) if stats else None
-    rstd = torch.empty(rows, device=x.device, dtype=torch.float32) if stats else None
-    capi.check(lib.fln_layernorm_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y),
-                                         capi.ptr(mean), capi.ptr(rstd), rows, cols,
-                                         capi.dtype_code(x), eps, capi.stream()))
-    return y, mean, rstd
-
-
-def rms_forward(lib, x, w, eps):
-    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
-    y = torch.empty_like(x)
-    rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
-    capi.check(lib.fln_rmsnorm_forward(capi.ptr(x), capi.ptr(w), capi.ptr(y), capi.ptr(rstd),
-                                       rows, cols, capi.dtype_code(x), eps, capi.stream()))
-    return y, rstd
-
-
-def workspace(lib, rows, cols, x):
-    n = lib.fln_backward_workspace_bytes(rows, cols, capi.dtype_code(x))
-    return torch.empty(max(1, (n + 3) // 4), device=x.device, dtype=torch.float32), n
-
-
-def ln_backward(lib, dy, x, mean, rstd, g, want_params=True, dres=None, dparam_f32=True):
-    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
-    dx = torch.empty_like(x)
-    pdt = torch.float32 if dparam_f32 else x.dtype
-    dg = torch.empty(cols, device=x.device, dtype=pdt) if want_params else None
-    db = torch.empty(cols, device=x.device, dtype=pdt) if want_params else None
-    ws, n = workspace(lib, rows, cols, x)
-    capi.check(lib.fln_layernorm_backward(
-        capi.ptr(dy), capi.ptr(x), capi.ptr(mean), capi.ptr(rstd), capi.ptr(g), capi.ptr(dres),
-        capi.ptr(dx), capi.ptr(dg), capi.ptr(db), rows, cols, capi.dtype_code(x),
-        capi.F32 if dparam_f32 else capi.dtype_code(x), capi.ptr(ws), n, capi.stream()))
-    return dx, dg, db
-
-
-def rms_backward(lib, dy, x, rstd, w, dres=None):
-    rows, cols = x.numel() // x.shape[-1], x.shape[-1]
-    dx = torch.empty_like(x)
-    dw = torch.empty(cols, device=x.device, dtype=torch.float32) if w is not None else None
-    ws, n = workspace(lib, rows, cols, x)
-    capi.check(lib.fln_rmsnorm_backward(
-        capi.ptr(dy), capi.ptr(x), capi.ptr(rstd), capi.ptr(w), capi.ptr(dres), capi.ptr(dx),
-        capi.ptr(dw), rows, cols, capi.dtype_code(x), capi.F32, capi.ptr(ws), n, capi.stream()))
-    return dx, dw
 
 
 # ------------------------------------------------------------------------------------------------
@@ -212,25 +149,6 @@ def test_c4_rmsnorm_fwd_bwd_bf16_16384x8192(lib):
     _rms_fwd_bwd_check(lib, "c4_rms_fwd_bwd_bf16_16384x8192")
 
 
-def _ordinal(codes):
-    """Signed position of an e4m3fn code on the number line (+0 and -0 both map to 0), so that
-    adjacent representable values differ by exactly 1."""
-    c = codes.astype(np.int32)
-    mag = c & 0x7F
-    return np.where(c & 0x80, -mag, mag)
-
-
-def _fp8_check(q_gpu, s_gpu, q_ref, s_ref, what):
-    s_gpu = s_gpu.astype(np.float64)
-    s_ref = s_ref.astype(np.float64)
-    rel = np.abs(s_gpu - s_ref) / np.where(s_ref > 0, s_ref, 1.0)
-    assert rel.max() <= 1e-6, f"{what}: scale rel err {rel.max():.3g}"
-    diff = np.abs(_ordinal(q_gpu) - _ordinal(q_ref))
-    n_diff = int((diff != 0).sum())
-    assert int(diff.max()) <= 1, f"{what}: a code differs by {int(diff.max())} steps"
-    assert n_diff <= 1e-3 * diff.size, f"{what}: {n_diff} of {diff.size} codes differ"
-
-
 def test_c5_layernorm_fp8_bf16_32768x7168(lib):
     w = WORKLOADS["c5_ln_fp8_bf16_32768x7168"]
     inp = make_inputs(w)
@@ -243,7 +161,7 @@ def test_c5_layernorm_fp8_bf16_32768x7168(lib):
     del x
     q_ref, s_ref = c_oracle.layernorm_fp8(f32(inp["x"]), f32(inp["gamma"]), f32(inp["beta"]),
                                           w.eps)
-    _fp8_check(q.cpu().numpy(), to_np(scale), q_ref, s_ref, "c5")
+    assert_fp8_close(q.cpu().numpy(), to_np(scale), q_ref, s_ref, "c5")
     # The outlier channels must reach the top of the fp8 range in every row.
     assert (np.abs(norms.fp8_e4m3fn_decode(q_ref)).max(axis=1) == 448).all()
 

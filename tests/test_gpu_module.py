@@ -1,0 +1,381 @@
+"""GPU tests of the reference-facing API: the `fused_layernorm` package (modules, autograd,
+functional ops, torch.compile) and the `fused_layernorm_cuda` binding.
+
+The plan follows the reference's tests/test_layernorm.py (forward over its batch/hidden/dtype
+list, 3-D input, no affine, backward, gradient accumulation, epsilon sweep, extreme values,
+memory, functional interface, determinism, edge cases) and tests/edge_cases.py (its size list),
+but every expectation here is PyTorch on the CPU in float64 rather than PyTorch on the same GPU.
+Tolerances: fp32 forward max-abs 1e-5 (the reference's own rtol/atol 1e-5); fp32 gradients
+rtol = atol = 1e-4 (the reference's grad tolerances); bf16/fp16 outputs within 1 ulp of the
+float64 result plus the fp32 rounding of the affine step (2^-21 (|x̂γ| + |β|)).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from helpers import assert_fp8_close, assert_within_ulp, to_np
+from oracle import norms
+
+import fused_layernorm as fl
+import fused_layernorm_cuda
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _gpu(gpu_available):
+    torch.manual_seed(0)
+
+
+def ref_ln(x, shape, w=None, b=None, eps=1e-5):
+    """float64 CPU LayerNorm."""
+    f = lambda t: None if t is None else t.detach().double().cpu()
+    return F.layer_norm(f(x), shape, f(w), f(b), eps)
+
+
+def check_out(y, ref, dtype, x=None, w=None, b=None, eps=1e-5, shape=None):
+    got, r = to_np(y).astype(np.float64), ref.numpy()
+    if dtype == torch.float32:
+        assert np.abs(got - r).max() <= 1e-5
+        return
+    atol = 0.0
+    if x is not None:
+        xh = ref_ln(x, shape, None, None, eps).numpy()
+        wv = 1.0 if w is None else to_np(w).astype(np.float64)
+        bv = 0.0 if b is None else np.abs(to_np(b).astype(np.float64))
+        atol = 2.0 ** -21 * (np.abs(xh * wv) + bv)
+    assert_within_ulp(got, r, 1.0, atol=atol, kind="bf16" if dtype == torch.bfloat16 else "f16",
+                      what="y")
+
+
+def make_ln(hidden, dtype=torch.float32, affine=True, bias=True):
+    ln = fl.FusedLayerNorm(hidden, elementwise_affine=affine, bias=bias).to(DEV, dtype)
+    if affine:
+        with torch.no_grad():
+            ln.weight.copy_(1 + 0.1 * torch.randn(hidden))
+            if ln.bias is not None:
+                ln.bias.copy_(0.1 * torch.randn(hidden))
+    return ln
+
+
+# ------------------------------------------------------------------------------------------------
+# The reference's test plan.
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("batch,hidden,dtype", [
+    (1, 768, torch.float32), (8, 768, torch.float32), (32, 1024, torch.float32),
+    (64, 2048, torch.float32), (128, 4096, torch.float32), (1, 768, torch.float16),
+    (32, 1024, torch.float16), (64, 2048, torch.float16), (32, 1024, torch.bfloat16),
+    (128, 4096, torch.bfloat16)])
+def test_forward_correctness(batch, hidden, dtype):
+    x = torch.randn(batch, hidden, device=DEV, dtype=dtype)
+    ln = make_ln(hidden, dtype)
+    y = ln(x)
+    assert y.dtype == dtype and y.shape == x.shape
+    check_out(y, ref_ln(x, (hidden,), ln.weight, ln.bias), dtype, x, ln.weight, ln.bias,
+              shape=(hidden,))
+
+
+@pytest.mark.parametrize("batch,seq,hidden", [(2, 128, 768), (4, 256, 1024), (8, 512, 2048),
+                                              (1, 1024, 4096)])
+def test_3d_input(batch, seq, hidden):
+    x = torch.randn(batch, seq, hidden, device=DEV)
+    ln = make_ln(hidden)
+    y = ln(x)
+    assert y.shape == x.shape
+    check_out(y, ref_ln(x, (hidden,), ln.weight, ln.bias), torch.float32)
+
+
+@pytest.mark.parametrize("hidden,affine", [(768, True), (768, False), (1024, True),
+                                           (1024, False)])
+def test_no_affine_parameters(hidden, affine):
+    x = torch.randn(16, hidden, device=DEV)
+    ln = make_ln(hidden, affine=affine)
+    assert (ln.weight is None) == (not affine)
+    check_out(ln(x), ref_ln(x, (hidden,), ln.weight, ln.bias), torch.float32)
+
+
+def _grads_f64(x, w, b, dy, shape, eps=1e-5):
+    xd = x.detach().double().cpu().requires_grad_(True)
+    wd = None if w is None else w.detach().double().cpu().requires_grad_(True)
+    bd = None if b is None else b.detach().double().cpu().requires_grad_(True)
+    F.layer_norm(xd, shape, wd, bd, eps).backward(dy.double().cpu())
+    return xd.grad, None if w is None else wd.grad, None if b is None else bd.grad
+
+
+@pytest.mark.parametrize("batch,hidden", [(16, 768), (32, 1024), (64, 2048)])
+def test_backward_correctness(batch, hidden):
+    x = torch.randn(batch, hidden, device=DEV, requires_grad=True)
+    ln = make_ln(hidden)
+    dy = torch.randn(batch, hidden, device=DEV)
+    ln(x).backward(dy)
+    gx, gw, gb = _grads_f64(x, ln.weight, ln.bias, dy, (hidden,))
+    for got, ref in ((x.grad, gx), (ln.weight.grad, gw), (ln.bias.grad, gb)):
+        torch.testing.assert_close(got.double().cpu(), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_gradient_accumulation():
+    x = torch.randn(32, 1024, device=DEV, requires_grad=True)
+    ln = make_ln(1024)
+    dy = torch.randn(32, 1024, device=DEV)
+    ln(x).backward(dy)
+    g1 = (x.grad.clone(), ln.weight.grad.clone(), ln.bias.grad.clone())
+    ln(x).backward(dy)
+    for acc, once in zip((x.grad, ln.weight.grad, ln.bias.grad), g1):
+        assert torch.equal(acc, 2 * once)  # same kernels, same order: exactly twice
+
+
+@pytest.mark.parametrize("eps", [1e-5, 1e-6, 1e-7, 1e-8])
+def test_different_epsilon(eps):
+    x = torch.randn(32, 768, device=DEV)
+    ln = fl.FusedLayerNorm(768, eps=eps).to(DEV)
+    check_out(ln(x), ref_ln(x, (768,), ln.weight, ln.bias, eps), torch.float32)
+
+
+@pytest.mark.parametrize("case", ["tiny_const", "huge_const", "small_var", "large_var",
+                                  "large_mean"])
+def test_numerical_stability(case):
+    b, h = 16, 768
+    x = {"tiny_const": torch.full((b, h), 1e-8), "huge_const": torch.full((b, h), 1e8),
+         "small_var": torch.randn(b, h) * 1e-4, "large_var": torch.randn(b, h) * 1e4,
+         "large_mean": torch.randn(b, h) + 1e4}[case].to(DEV)
+    ln = make_ln(h)
+    y = ln(x)
+    assert torch.isfinite(y).all()
+    ref = ref_ln(x, (h,), ln.weight, ln.bias)
+    # The fp32 bar, plus the fp32 spacing of the row mean, which any fp32 implementation
+    # carries (a 1e4 offset is only known to ~1e-3 in fp32): 4 ulp(mean) * rstd * max|gamma|
+    # (the sum's rounding is ~1.5 ulp(mean) at 768 columns).  The two-pass variance keeps the
+    # offset harmless where E[x^2] - mean^2 would not.  Constant rows (variance 0) map to beta.
+    xd = x.double().cpu()
+    mean, var = xd.mean(-1, keepdim=True), xd.var(-1, unbiased=False, keepdim=True)
+    allow = (2.0 ** -21 * mean.abs() / torch.sqrt(var + 1e-5)
+             * ln.weight.abs().max().item()).numpy()
+    err = np.abs(to_np(y) - ref.numpy())
+    assert (err <= 1e-5 * max(1.0, ref.abs().max().item()) + allow).all(), err.max()
+
+
+def test_memory_efficiency():
+    x = torch.randn(64, 4096, device=DEV)
+    ln_t, ln_f = nn.LayerNorm(4096).to(DEV), fl.FusedLayerNorm(4096).to(DEV)
+
+    def peak(mod):
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        start = torch.cuda.memory_allocated()
+        with torch.no_grad():
+            mod(x)
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() - start
+
+    peak(ln_f)  # first call loads the kernels
+    # The fused forward allocates y plus fp32 mean/rstd and nothing else.
+    assert peak(ln_f) <= x.numel() * 4 + 2 * 64 * 4 + 4096
+    assert peak(ln_f) <= peak(ln_t) + 2 * 64 * 4 + 4096
+
+
+def test_functional_interface():
+    x = torch.randn(32, 1024, device=DEV)
+    w, b = 1 + 0.1 * torch.randn(1024, device=DEV), 0.1 * torch.randn(1024, device=DEV)
+    check_out(fl.fused_layer_norm(x, (1024,), w, b, 1e-5), ref_ln(x, (1024,), w, b),
+              torch.float32)
+    check_out(fl.layer_norm(x, (1024,), w, b, 1e-5), ref_ln(x, (1024,), w, b), torch.float32)
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_deterministic(seed):
+    torch.manual_seed(seed)
+    x = torch.randn(257, 2048, device=DEV, requires_grad=True)
+    ln = make_ln(2048)
+    dy = torch.randn(257, 2048, device=DEV)
+    outs = []
+    for _ in range(3):
+        x.grad = None
+        ln.zero_grad()
+        y = ln(x)
+        y.backward(dy)
+        outs.append((y.detach().clone(), x.grad.clone(), ln.weight.grad.clone(),
+                     ln.bias.grad.clone()))
+    for o in outs[1:]:
+        for a, c in zip(outs[0], o):
+            assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("batch,hidden", [
+    (1, 768), (32, 1), (2, 16384),                                      # test_edge_cases
+    (1, 1), (1, 17), (1000, 1), (1, 100000), (512, 512), (1, 32767),    # edge_cases.py list
+    (1, 65536), (13, 13), (1, 4095), (1, 4097)])
+def test_edge_cases(batch, hidden):
+    x = torch.randn(batch, hidden, device=DEV)
+    ln = nn.LayerNorm(hidden).to(DEV)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(hidden))
+        ln.bias.copy_(0.1 * torch.randn(hidden))
+    y = fused_layernorm_cuda.layernorm(x, ln.weight, ln.bias, 1e-5)
+    assert y.shape == x.shape
+    ref = ref_ln(x, (hidden,), ln.weight, ln.bias).numpy()
+    assert np.abs(to_np(y) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    if hidden == 1:
+        assert torch.equal(y, ln.bias.detach().expand_as(y))
+
+
+# ------------------------------------------------------------------------------------------------
+# The binding (fused_layernorm_cuda), reference names and argument meaning.
+# ------------------------------------------------------------------------------------------------
+def test_binding_layernorm_keyword_and_positional():
+    x = torch.randn(8, 768, device=DEV)
+    w, b = torch.ones(768, device=DEV), torch.zeros(768, device=DEV)
+    y1 = fused_layernorm_cuda.layernorm(x, w, b, 1e-5)
+    y2 = fused_layernorm_cuda.layernorm(x, w, b, eps=1e-5)
+    assert torch.equal(y1, y2)
+    check_out(y1, ref_ln(x, (768,)), torch.float32)
+
+
+@pytest.mark.parametrize("approximate", ["tanh", "none"])
+def test_binding_layernorm_gelu(approximate):
+    x = torch.randn(17, 1023, device=DEV)
+    w, b = 1 + 0.1 * torch.randn(1023, device=DEV), 0.1 * torch.randn(1023, device=DEV)
+    if approximate == "tanh":
+        y = fused_layernorm_cuda.layernorm_gelu(x, w, b, 1e-5)  # the reference's default: tanh
+    else:
+        y = fused_layernorm_cuda.layernorm_gelu(x, w, b, 1e-5, approximate="none")
+    ref = F.gelu(ref_ln(x, (1023,), w, b), approximate=approximate)
+    assert np.abs(to_np(y) - ref.numpy()).max() <= 1e-5
+
+
+@pytest.mark.parametrize("mask", [[True, True, True], [True, False, False],
+                                  [False, True, True], [True, True, False]])
+def test_binding_forward_backward_output_mask(mask):
+    x = torch.randn(64, 1024, device=DEV)
+    w, b = 1 + 0.1 * torch.randn(1024, device=DEV), 0.1 * torch.randn(1024, device=DEV)
+    out, mean, rstd = fused_layernorm_cuda.forward(x, w, b, 1e-5)
+    assert mean.dtype == torch.float32 and rstd.dtype == torch.float32
+    check_out(out, ref_ln(x, (1024,), w, b), torch.float32)
+    dy = torch.randn_like(x)
+    dx, dw, db = fused_layernorm_cuda.backward(dy, x, mean, rstd, w, b, mask)
+    gx, gw, gb = _grads_f64(x, w, b, dy, (1024,))
+    for want, got, ref in zip(mask, (dx, dw, db), (gx, gw, gb)):
+        if not want:
+            assert got is None
+        else:
+            torch.testing.assert_close(got.double().cpu(), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_binding_forward_without_affine_and_utilities():
+    x = torch.randn(4, 512, device=DEV)
+    out, mean, rstd = fused_layernorm_cuda.forward(x)
+    check_out(out, ref_ln(x, (512,)), torch.float32)
+    assert fused_layernorm_cuda.__version__ == "1.0.0"
+    assert isinstance(fused_layernorm_cuda.__cuda_version__, int)
+    assert fused_layernorm_cuda.get_memory_usage(32, 768) > 0
+    assert isinstance(fused_layernorm_cuda.get_performance_hints(32, 768), str)
+
+
+# ------------------------------------------------------------------------------------------------
+# New operators on the same kernels: RMSNorm, residual add, fp8.
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rms_norm_module_forward_backward(dtype):
+    x = torch.randn(128, 4096, device=DEV, dtype=dtype, requires_grad=True)
+    m = fl.FusedRMSNorm(4096, eps=1e-6).to(DEV, dtype)
+    with torch.no_grad():
+        m.weight.copy_(1 + 0.1 * torch.randn(4096))
+    dy = torch.randn(128, 4096, device=DEV, dtype=dtype)
+    y = m(x)
+    y.backward(dy)
+    xd = x.detach().double().cpu().requires_grad_(True)
+    wd = m.weight.detach().double().cpu().requires_grad_(True)
+    yr = F.rms_norm(xd, (4096,), wd, 1e-6)
+    yr.backward(dy.double().cpu())
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - yr.detach().numpy()).max() <= 1e-5
+        torch.testing.assert_close(x.grad.double().cpu(), xd.grad, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(y), yr.detach().numpy(), 1.0, what="rms y")
+        assert_within_ulp(to_np(x.grad), xd.grad.numpy(), 1.0,
+                          atol=2.0 ** -12 * xd.grad.abs().max().item(), what="rms dx")
+    g = wd.grad.numpy()
+    assert np.abs(to_np(m.weight.grad) - g).max() <= 1e-2 * np.abs(g).max()  # bf16-stored dw
+
+
+def test_add_layer_norm_forward_and_gradients():
+    x = torch.randn(64, 2048, device=DEV, requires_grad=True)
+    r = torch.randn(64, 2048, device=DEV, requires_grad=True)
+    w, b = 1 + 0.1 * torch.randn(2048, device=DEV), 0.1 * torch.randn(2048, device=DEV)
+    y, h = fl.add_layer_norm(x, r, (2048,), w, b, 1e-5)
+    assert torch.equal(h, x + r)
+    check_out(y, ref_ln(h, (2048,), w, b), torch.float32)
+    dy, dh = torch.randn_like(y), torch.randn_like(h)
+    (y * dy).sum().add_((h * dh).sum()).backward()
+    hd = (x.detach() + r.detach()).double().cpu().requires_grad_(True)
+    F.layer_norm(hd, (2048,), w.double().cpu(), b.double().cpu(), 1e-5).backward(
+        dy.double().cpu())
+    expect = hd.grad + dh.double().cpu()  # h = x + r feeds both outputs
+    torch.testing.assert_close(x.grad.double().cpu(), expect, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(r.grad.double().cpu(), expect, rtol=1e-4, atol=1e-4)
+
+
+def test_add_rms_norm_forward():
+    x = torch.randn(32, 4096, device=DEV, dtype=torch.bfloat16)
+    r = torch.randn(32, 4096, device=DEV, dtype=torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(4096, device=DEV)).to(torch.bfloat16)
+    y, h = fl.add_rms_norm(x, r, (4096,), w, 1e-6)
+    assert torch.equal(h, x + r)
+    ref = F.rms_norm(h.double().cpu(), (4096,), w.double().cpu(), 1e-6)
+    assert_within_ulp(to_np(y), ref.numpy(), 1.0, what="add rms y")
+
+
+def test_layer_norm_fp8_output_type_and_values():
+    x = torch.randn(96, 7168, device=DEV, dtype=torch.bfloat16)
+    w = (1 + 0.05 * torch.randn(7168, device=DEV)).to(torch.bfloat16)
+    b = (0.05 * torch.randn(7168, device=DEV)).to(torch.bfloat16)
+    q, scale = fl.layer_norm_fp8(x, (7168,), w, b, 1e-5)
+    assert q.dtype == torch.float8_e4m3fn and scale.dtype == torch.float32
+    q_ref, s_ref = norms.layer_norm_fp8_fwd(to_np(x), to_np(w), to_np(b), 1e-5)
+    assert_fp8_close(q.view(torch.uint8).cpu().numpy(), to_np(scale), q_ref, s_ref, "fp8")
+    deq = q.float() * scale[:, None]
+    ref = ref_ln(x, (7168,), w, b)
+    assert (deq.double().cpu() - ref).abs().max().item() <= 2.0 ** -3 * ref.abs().max().item()
+
+
+# ------------------------------------------------------------------------------------------------
+# torch.compile and operator registration.
+# ------------------------------------------------------------------------------------------------
+def test_torch_compile_matches_eager():
+    torch._dynamo.reset()
+    model = nn.Sequential(nn.Linear(512, 1024), fl.FusedLayerNorm(1024), nn.GELU(),
+                          nn.Linear(1024, 512), fl.FusedRMSNorm(512, eps=1e-6)).to(DEV)
+    x = torch.randn(64, 512, device=DEV, requires_grad=True)
+    y_e = model(x)
+    y_e.sum().backward()
+    g_e = x.grad.clone()
+    x.grad = None
+    compiled = torch.compile(model, backend="aot_eager")
+    y_c = compiled(x)
+    y_c.sum().backward()
+    # Same kernels in the same order; only the surrounding GEMMs could pick another algorithm.
+    torch.testing.assert_close(y_c, y_e, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(x.grad, g_e, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("op,args", [
+    ("layer_norm_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
+                                torch.randn(256, device=DEV, requires_grad=True),
+                                torch.randn(256, device=DEV, requires_grad=True), 1e-5)),
+    ("rms_norm_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
+                              torch.randn(256, device=DEV, requires_grad=True), 1e-6)),
+    ("add_layer_norm_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
+                                    torch.randn(8, 256, device=DEV, requires_grad=True),
+                                    torch.randn(256, device=DEV), torch.randn(256, device=DEV),
+                                    1e-5)),
+    ("layer_norm_gelu_fwd", lambda: (torch.randn(8, 256, device=DEV),
+                                     torch.randn(256, device=DEV),
+                                     torch.randn(256, device=DEV), 1e-5, "tanh")),
+])
+def test_opcheck(op, args):
+    torch.library.opcheck(getattr(torch.ops.fused_layernorm, op), args())
