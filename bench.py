@@ -401,7 +401,35 @@ def torch_cpu_baseline(w, seconds, threads=16):
 
 
 # ------------------------------------------------------------------------------------------------
-def measure(lib, capi, torch, w, steps, warmup, stream, stream_obj):
+def time_graph(runner, n_calls=32, replays=20):
+    """GPU-side time (ms) of one forward call: n_calls C-ABI calls captured in one HIP graph
+    (hipStreamBeginCapture under torch.cuda.graph; the forward records no memset nodes), the
+    graph replayed `replays` times between HIP events.  Without the per-call host cost of an
+    eager launch, this is the latency a graph-captured caller sees."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):  # warm the per-device caches outside the capture
+            runner.fwd(runner.sets[i % runner.nsets], runner.capi.stream())
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for i in range(n_calls):
+            runner.fwd(runner.sets[i % runner.nsets], runner.capi.stream())
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (replays * n_calls)
+
+
+def measure(lib, capi, torch, w, steps, warmup, stream, stream_obj, graph=False):
     from fused_layernorm.testing import algorithmic_bytes, make_inputs
 
     r = Runner(lib, capi, torch, w, make_inputs(w))
@@ -415,6 +443,8 @@ def measure(lib, capi, torch, w, steps, warmup, stream, stream_obj):
     res["ms_fwd"] = time_launch_group(r, "fwd", n_group, stream, stream_obj)
     if r.has_bwd:
         res["ms_bwd"] = time_launch_group(r, "bwd", n_group, stream, stream_obj)
+    if graph:
+        res["ms_fwd_graph"] = time_graph(r)
     del r
     torch.cuda.empty_cache()
     return res
@@ -514,9 +544,12 @@ def main():
         cfg = {}
         for name in CONFIGS:
             w = WORKLOADS[name]
+            small = w.op in ("layer_norm", "layer_norm_gelu")
             res = measure(lib, capi, torch, w, max(50, args.steps // 2), args.warmup, stream,
-                          stream_obj)
+                          stream_obj, graph=small)
             entry = {"us_per_call": round(res["ms_fwd"] * 1e3, 2)}
+            if small:
+                entry["us_per_call_graph"] = round(res["ms_fwd_graph"] * 1e3, 2)
             if "ms_bwd" in res:
                 entry["us_per_call"] = {"fwd": round(res["ms_fwd"] * 1e3, 2),
                                         "bwd": round(res["ms_bwd"] * 1e3, 2),

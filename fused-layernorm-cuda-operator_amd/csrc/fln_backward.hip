@@ -4,9 +4,9 @@
 // `layernorm_backward` (csrc/layernorm_cuda.cpp:97-141), but never defines it: this file is the
 // first implementation of that contract.
 //
-// Stage 1 (bwd_reg_kernel): each block owns a contiguous chunk of rows, processed by row groups
-// of `wpr` waves, with the next PD rows of x / dy always in flight (a ring of raw buffer loads;
-// at loaded HBM latency the CU needs tens of KiB of reads outstanding).  Per row it computes
+// Stage 1 (bwd_reg_kernel): row groups of `wpr` waves each take rows grid-stride, with the next
+// PD rows of x / dy always in flight (a ring of raw buffer loads; at loaded HBM latency the CU
+// needs tens of KiB of reads outstanding).  Per row it computes
 //     LayerNorm: xhat = (x - mean) rstd, g = dy gamma,
 //                dx = rstd (g - sum(g)/N - xhat sum(g xhat)/N)
 //     RMSNorm:   xhat = x rstd,          dx = rstd (g - xhat sum(g xhat)/N)
@@ -18,6 +18,8 @@
 // reproducible run to run.  (Fusing stage 2 into stage 1 behind a cooperative grid barrier was
 // measured at 2x the time of the two launches on gfx950 and is not used.)
 #include <stdlib.h>
+
+#include <atomic>
 
 #include "fln_device.h"
 #include "fln_internal.h"
@@ -394,9 +396,9 @@ __global__ __launch_bounds__(kCrThreads) void col_reduce_kernel(const ColReduceA
 
 namespace {
 
-// Largest vectors per lane instantiated for the backward register path: 16 elements per lane
-// for 16-byte vectors of 16-bit types, 8 for fp32 and for the scalar path.
-constexpr int bwd_max_vpl(int vec, int es) { return vec == 1 ? 8 : (es == 2 ? 2 : 2); }
+// Largest vectors per lane instantiated for the backward register path: 2 vectors (16
+// elements of a 16-bit type, 8 of fp32) on the vector path, 8 on the scalar path.
+constexpr int bwd_max_vpl(int vec, int es) { return vec == 1 ? 8 : 2; }
 
 int env_int_b(const char* name, int dflt) {
   const char* v = getenv(name);
@@ -409,51 +411,75 @@ int next_pow2(int v) {
   return p;
 }
 
-template <class T, int VEC, int VPL>
-int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s) {
-  if (p.dres)
-    hipLaunchKernelGGL((bwd_reg_kernel<T, true, VEC, VPL, 1024>), dim3(blocks), dim3(threads), 0,
-                       s, p);
-  else
-    hipLaunchKernelGGL((bwd_reg_kernel<T, false, VEC, VPL, 1024>), dim3(blocks), dim3(threads),
-                       0, s, p);
+// Stage-1 launch (resident == nullptr) or, with `resident`, the number of blocks of that
+// instantiation that fit on the device at once (occupancy x CUs, cached per device).
+template <class T, bool DRES, int VEC, int VPL, int MAXT>
+int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
+                    int64_t* resident) {
+  auto kernel = bwd_reg_kernel<T, DRES, VEC, VPL, MAXT>;
+  if (resident) {
+    static std::atomic<int> per_cu[3][64];  // [threads / 512][device]
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    std::atomic<int>& slot = per_cu[threads / 512][dev];
+    int v = slot.load(std::memory_order_relaxed);
+    if (v == 0) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, threads, 0) != hipSuccess ||
+          v < 1)
+        v = 1;
+      slot.store(v, std::memory_order_relaxed);
+    }
+    *resident = static_cast<int64_t>(v) * device_cu_count();
+    return 0;
+  }
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), 0, s, p);
   return static_cast<int>(hipGetLastError());
 }
 
+template <class T, int VEC, int VPL>
+int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
+                  int64_t* resident) {
+  return p.dres ? launch_stage1_k<T, true, VEC, VPL, 1024>(p, blocks, threads, s, resident)
+                : launch_stage1_k<T, false, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+}
+
 template <class T, int VEC>
-int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, hipStream_t s) {
+int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, hipStream_t s,
+                      int64_t* resident) {
   constexpr int CAP = bwd_max_vpl(VEC, sizeof(T));
   switch (vpl) {
-    case 1: return launch_stage1<T, VEC, 1>(p, blocks, threads, s);
+    case 1: return launch_stage1<T, VEC, 1>(p, blocks, threads, s, resident);
     case 2:
-      if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, threads, s);
+      if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 4:
-      if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, threads, s);
+      if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 8:
-      if constexpr (CAP >= 8) return launch_stage1<T, VEC, 8>(p, blocks, threads, s);
-      return FLN_ERR_INVALID;
-    case 16:
-      if constexpr (CAP >= 16) return launch_stage1<T, VEC, 16>(p, blocks, threads, s);
+      if constexpr (CAP >= 8) return launch_stage1<T, VEC, 8>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     default: return FLN_ERR_INVALID;
   }
 }
 
 template <class T>
-int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s) {
+int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
+                      int64_t* resident = nullptr) {
   p.wpr = geo.wpr;
   p.rgs = geo.rgs;
   p.rows_per_block = geo.rows_per_block;
   if (!geo.reg_path) {
+    if (resident) {
+      *resident = geo.blocks;  // the looped kernel takes any grid
+      return 0;
+    }
     hipLaunchKernelGGL((bwd_loop_kernel<T>), dim3(geo.blocks), dim3(1024), 0, s, p);
     return static_cast<int>(hipGetLastError());
   }
   constexpr int VV = 16 / sizeof(T);
   if (geo.vec == VV)
-    return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, geo.threads, s);
-  return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, geo.threads, s);
+    return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, geo.threads, s, resident);
+  return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, geo.threads, s, resident);
 }
 
 }  // namespace
@@ -505,7 +531,20 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   BwdParams p = p0;
   const bool vec_ok = aligned16(p.x) && aligned16(p.dy) && aligned16(p.dx) &&
                       aligned16(p.gamma) && aligned16(p.dres);
-  const BwdGeometry geo = backward_geometry(p.rows, p.cols, dtype, vec_ok);
+  BwdGeometry geo = backward_geometry(p.rows, p.cols, dtype, vec_ok);
+  if (geo.reg_path) {
+    // Never more blocks than fit at once: a second round of blocks would only add a tail.
+    int64_t resident = geo.blocks;
+    int rc = FLN_ERR_INVALID;
+    switch (dtype) {
+      case FLN_F32: rc = dispatch_backward<float>(p, geo, s, &resident); break;
+      case FLN_BF16: rc = dispatch_backward<__bf16>(p, geo, s, &resident); break;
+      case FLN_F16: rc = dispatch_backward<_Float16>(p, geo, s, &resident); break;
+      default: break;
+    }
+    if (rc != 0) return rc;
+    if (geo.blocks > resident) geo.blocks = resident;
+  }
   const int64_t ld = (p.cols + 3) & ~int64_t(3);
   float* ws = p0.part_g;
   p.part_g = dgamma ? ws : nullptr;

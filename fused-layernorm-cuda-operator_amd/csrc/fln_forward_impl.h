@@ -82,9 +82,11 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
   const int64_t N = p.cols;
   const int nvec = static_cast<int>(N / VEC);
   const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
-  // Statistics divide by N (correctly rounded, as the reference's sum / N): an exactly summed
-  // constant row then has an exact mean and maps to beta exactly.
+  // mean = sum / N as sum * (1/N) plus one FMA correction step, which returns the exact quotient
+  // whenever it is representable (an exactly summed constant row then maps to beta exactly)
+  // without the long correctly-rounded division sequence.
   const float fn = static_cast<float>(N);
+  const float inv_n = 1.0f / fn;
   const T* X = static_cast<const T*>(p.x);
   const T* R = static_cast<const T*>(p.res);
   const int64_t stride = gridDim.x;
@@ -171,7 +173,9 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) s += xf[i][e];
-      mean = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane) / fn;
+      const float sum = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane);
+      mean = sum * inv_n;
+      mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
     }
     float q = 0.0f;
 #pragma unroll
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       }
     }
     q = row_allreduce<SumOp>(q, slots[1], wpr, rg, wave, lane);
-    const float rstd = 1.0f / sqrtf(q / fn + p.eps);
+    const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
 
     //    Normalize + affine + epilogue, packed to the output format.
 #pragma unroll
