@@ -47,32 +47,67 @@ def _next_pow2(v: int) -> int:
     return p
 
 
-def get_optimal_config(batch_size: int, hidden_size: int,
-                       dtype: torch.dtype = torch.float32, num_cus: int = 256) -> dict:
-    """Forward launch geometry the HIP dispatcher picks for a [batch_size, hidden_size] input
-    (aligned, contiguous), plus the reference's keys (functional.py:61-72)."""
-    es = torch.empty((), dtype=dtype).element_size()
-    vec = 16 // es if (hidden_size * es) % 16 == 0 else 1
-    nvec = hidden_size // vec
-    cap = 16 if vec == 1 else 32 // vec
+def _forward_geometry(rows: int, nvec: int, cap: int, max_cap: int, vec_path: bool,
+                      num_cus: int):
+    """The forward dispatcher's geometry rule (csrc/fln_forward_impl.h, fwd_geometry): the
+    fewest power-of-two waves per row that keep <= cap vectors per lane; on the vector path an
+    exact (mask-free) non-power-of-two tiling when one exists; more waves per row while the
+    grid holds fewer than 4 waves per CU.  Returns (loop, wpr, vpl, exact, threads)."""
     per_lane = lambda w: -(-nvec // (64 * w))  # noqa: E731
     wpr = 1
     while per_lane(wpr) > cap and wpr < 16:
         wpr *= 2
-    register_resident = per_lane(wpr) <= cap
-    while register_resident and batch_size * wpr < 4 * num_cus and wpr < 16 and \
-            nvec > 64 * wpr * 2:
-        wpr *= 2
+    if per_lane(wpr) > cap:
+        cap = max_cap
+    if per_lane(wpr) > cap:
+        return True, 0, 0, False, 1024
+    vpl = _next_pow2(per_lane(wpr))
+    exact = nvec == vpl * 64 * wpr
+    if vec_path and not exact:
+        v = _next_pow2(cap) // 2 if _next_pow2(cap) > cap else cap
+        while v >= 1:
+            if nvec % (64 * v) == 0 and nvec // (64 * v) <= 16:
+                wpr, vpl, exact = nvec // (64 * v), v, True
+                break
+            v >>= 1
+    while rows * wpr < 4 * num_cus and wpr * 2 <= 16:
+        if exact and vpl >= 2:
+            wpr, vpl = wpr * 2, vpl // 2
+        elif not exact and nvec > 64 * wpr * 2:
+            wpr *= 2
+            vpl = _next_pow2(per_lane(wpr))
+        else:
+            break
+    threads = 256 if 4 % wpr == 0 else 64 * wpr
+    return False, wpr, vpl, vec_path and exact, threads
+
+
+def get_optimal_config(batch_size: int, hidden_size: int,
+                       dtype: torch.dtype = torch.float32, num_cus: int = 256) -> dict:
+    """Forward launch geometry the HIP dispatcher picks for a [batch_size, hidden_size] input
+    (16-byte aligned, contiguous; default tuning), plus the reference's keys
+    (reference fused_layernorm/functional.py:47-72).  ``num_cus`` is the device's CU count
+    (256 on MI355X)."""
+    es = torch.empty((), dtype=dtype).element_size()
+    vv = 16 // es
+    vec_path = hidden_size % vv == 0
+    vec = vv if vec_path else 1
+    nvec = hidden_size // vec
+    max_cap = 32 // vv if vec_path else 16
+    cap = min(max(32, vec) // vec, max_cap)
+    loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, max_cap,
+                                                       vec_path, num_cus)
     return {
         "use_mixed_precision": dtype in (torch.float16, torch.bfloat16),
-        "threads_per_block": 256 if wpr <= 4 else 64 * wpr,
-        "enable_persistent_kernel": False,
+        "threads_per_block": threads,
+        "enable_persistent_kernel": not loop,  # register path: persistent grid-stride rows
         "use_vectorized_load": vec > 1,
         "use_tensor_cores": False,  # bandwidth-bound: no MFMA on this path
-        "waves_per_row": wpr,
+        "waves_per_row": wpr if not loop else None,
         "vector_elems": vec,
-        "vectors_per_lane": _next_pow2(per_lane(wpr)) if register_resident else None,
-        "register_resident": register_resident,
+        "vectors_per_lane": vpl if not loop else None,
+        "exact_tiling": exact,
+        "register_resident": not loop,
     }
 
 

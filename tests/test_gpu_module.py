@@ -439,3 +439,31 @@ def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay():
         for got, ref in ((y, y_e), (mean, m_e), (rstd, r_e), (dx, dx_e), (dg, dg_e),
                          (db, db_e)):
             assert torch.equal(got, ref), f"replay {k} differs from eager"
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [
+    (8192, 4096, torch.bfloat16), (32768, 7168, torch.bfloat16), (32, 768, torch.float32),
+    (17, 1023, torch.float32), (64, 4096, torch.float32), (1, 100000, torch.float32),
+    (16384, 8192, torch.bfloat16), (5, 5120, torch.float16)])
+def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeypatch):
+    """functional.get_optimal_config restates the forward geometry rule; the dispatcher's own
+    trace (FLN_DEBUG_GEOMETRY=1, one stderr line per launch) must agree with it."""
+    import re
+    x = torch.randn(rows, cols, device=DEV, dtype=dtype)
+    w = torch.ones(cols, device=DEV, dtype=dtype)
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    fused_layernorm_cuda.layernorm(x, w, w, 1e-5)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    line = capfd.readouterr().err.strip().splitlines()[-1]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    cfg = fl.functional.get_optimal_config(rows, cols, dtype, num_cus=cus)
+    if cfg["register_resident"]:
+        m = re.search(r"registers wpr=(\d+) vpl=(\d+) exact=(\d) threads=(\d+)", line)
+        assert m, line
+        assert (int(m[1]), int(m[2]), bool(int(m[3])), int(m[4])) == (
+            cfg["waves_per_row"], cfg["vectors_per_lane"], cfg["exact_tiling"],
+            cfg["threads_per_block"]), line
+    else:
+        assert "-> loop" in line, line

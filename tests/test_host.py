@@ -150,8 +150,10 @@ def test_profiler_utilities():
 
 def test_optimal_config_reports_dispatch_geometry():
     c = fl.functional.get_optimal_config(8192, 4096, torch.bfloat16)
-    assert c["register_resident"] and c["vector_elems"] == 8
-    assert c["waves_per_row"] * 64 * c["vectors_per_lane"] * c["vector_elems"] >= 4096
+    assert c["register_resident"] and c["vector_elems"] == 8 and c["exact_tiling"]
+    assert c["waves_per_row"] * 64 * c["vectors_per_lane"] * c["vector_elems"] == 4096
+    c7 = fl.functional.get_optimal_config(32768, 7168, torch.bfloat16)
+    assert (c7["waves_per_row"], c7["vectors_per_lane"], c7["threads_per_block"]) == (7, 2, 448)
     c2 = fl.functional.get_optimal_config(1, 100000, torch.float32)
     assert not c2["register_resident"]
 
