@@ -125,6 +125,39 @@ extern "C" int fln_layernorm_fp8_forward(const void* x, const void* gamma, const
   return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int fln_rmsnorm_fp8_forward(const void* x, const void* weight, uint8_t* q,
+                                       float* scale, float* rstd, int64_t rows, int64_t cols,
+                                       int dtype, float eps, void* stream) {
+  if (dtype == FLN_F64) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.gamma = weight; p.y = q; p.scale = scale; p.rstd = rstd;
+  p.rows = rows; p.cols = cols; p.eps = eps; p.rms = 1;
+  return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fln_add_layernorm_fp8_forward(const void* x, const void* residual,
+                                             const void* gamma, const void* beta, void* h,
+                                             uint8_t* q, float* scale, float* mean, float* rstd,
+                                             int64_t rows, int64_t cols, int dtype, float eps,
+                                             void* stream) {
+  if (dtype == FLN_F64 || !residual) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.res = residual; p.gamma = gamma; p.beta = beta; p.h = h; p.y = q;
+  p.scale = scale; p.mean = mean; p.rstd = rstd; p.rows = rows; p.cols = cols; p.eps = eps;
+  return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fln_add_rmsnorm_fp8_forward(const void* x, const void* residual,
+                                           const void* weight, void* h, uint8_t* q, float* scale,
+                                           float* rstd, int64_t rows, int64_t cols, int dtype,
+                                           float eps, void* stream) {
+  if (dtype == FLN_F64 || !residual) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.res = residual; p.gamma = weight; p.h = h; p.y = q; p.scale = scale;
+  p.rstd = rstd; p.rows = rows; p.cols = cols; p.eps = eps; p.rms = 1;
+  return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int fln_fp8_e4m3fn_encode(const float* x, uint8_t* q, int64_t n, void* stream) {
   if (n < 0) return FLN_ERR_INVALID;
   if (n == 0) return FLN_OK;

@@ -249,6 +249,69 @@ std::tuple<Tensor, Tensor> layer_norm_fp8_fwd(const Tensor& input, const OptT& g
   return {q, scale};
 }
 
+std::tuple<Tensor, Tensor> rms_norm_fp8_fwd(const Tensor& input, const OptT& weight,
+                                            double eps) {
+  const Shape s = check_input(input, "input", false);
+  check_param(weight, input, s.cols, "weight");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor q = at::empty(input.sizes(), input.options().dtype(at::kFloat8_e4m3fn));
+  Tensor scale = stats_like(input, s.rows);
+  check(fln_rmsnorm_fp8_forward(input.data_ptr(), ptr_or_null(weight),
+                                static_cast<uint8_t*>(q.data_ptr()), scale.data_ptr<float>(),
+                                nullptr, s.rows, s.cols, dtype_code(input),
+                                static_cast<float>(eps), stream_of(input)),
+        "rms_norm fp8 forward");
+  return {q, scale};
+}
+
+void check_residual(const Tensor& residual, const Tensor& input) {
+  check_input(residual, "residual", false);
+  TORCH_CHECK(residual.sizes() == input.sizes() && residual.scalar_type() == input.scalar_type() &&
+                  residual.device() == input.device(),
+              "residual must match the input's shape, dtype and device");
+}
+
+std::tuple<Tensor, Tensor, Tensor> add_layer_norm_fp8_fwd(const Tensor& input,
+                                                          const Tensor& residual,
+                                                          const OptT& gamma, const OptT& beta,
+                                                          double eps) {
+  const Shape s = check_input(input, "input", false);
+  check_residual(residual, input);
+  check_param(gamma, input, s.cols, "gamma");
+  check_param(beta, input, s.cols, "beta");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor q = at::empty(input.sizes(), input.options().dtype(at::kFloat8_e4m3fn));
+  Tensor scale = stats_like(input, s.rows);
+  Tensor h = at::empty_like(input);
+  check(fln_add_layernorm_fp8_forward(input.data_ptr(), residual.data_ptr(), ptr_or_null(gamma),
+                                      ptr_or_null(beta), h.data_ptr(),
+                                      static_cast<uint8_t*>(q.data_ptr()),
+                                      scale.data_ptr<float>(), nullptr, nullptr, s.rows, s.cols,
+                                      dtype_code(input), static_cast<float>(eps),
+                                      stream_of(input)),
+        "add_layer_norm fp8 forward");
+  return {q, scale, h};
+}
+
+std::tuple<Tensor, Tensor, Tensor> add_rms_norm_fp8_fwd(const Tensor& input,
+                                                        const Tensor& residual,
+                                                        const OptT& weight, double eps) {
+  const Shape s = check_input(input, "input", false);
+  check_residual(residual, input);
+  check_param(weight, input, s.cols, "weight");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor q = at::empty(input.sizes(), input.options().dtype(at::kFloat8_e4m3fn));
+  Tensor scale = stats_like(input, s.rows);
+  Tensor h = at::empty_like(input);
+  check(fln_add_rmsnorm_fp8_forward(input.data_ptr(), residual.data_ptr(), ptr_or_null(weight),
+                                    h.data_ptr(), static_cast<uint8_t*>(q.data_ptr()),
+                                    scale.data_ptr<float>(), nullptr, s.rows, s.cols,
+                                    dtype_code(input), static_cast<float>(eps),
+                                    stream_of(input)),
+        "add_rms_norm fp8 forward");
+  return {q, scale, h};
+}
+
 // ------------------------------------------------------------------------------------------
 // Backward family.  Masked-off outputs come back as empty (0-element) tensors through the
 // operator schema and as None through the pybind `backward`.
@@ -382,6 +445,11 @@ TORCH_LIBRARY(fused_layernorm, m) {
         "-> (Tensor, Tensor, Tensor)");
   m.def("layer_norm_fp8_fwd(Tensor input, Tensor? weight, Tensor? bias, float eps) "
         "-> (Tensor, Tensor)");
+  m.def("rms_norm_fp8_fwd(Tensor input, Tensor? weight, float eps) -> (Tensor, Tensor)");
+  m.def("add_layer_norm_fp8_fwd(Tensor input, Tensor residual, Tensor? weight, Tensor? bias, "
+        "float eps) -> (Tensor, Tensor, Tensor)");
+  m.def("add_rms_norm_fp8_fwd(Tensor input, Tensor residual, Tensor? weight, float eps) "
+        "-> (Tensor, Tensor, Tensor)");
 }
 
 // GPU tensors of PyTorch-ROCm carry the CUDA dispatch key.
@@ -394,6 +462,9 @@ TORCH_LIBRARY_IMPL(fused_layernorm, CUDA, m) {
   m.impl("add_layer_norm_fwd", &add_layer_norm_fwd);
   m.impl("add_rms_norm_fwd", &add_rms_norm_fwd);
   m.impl("layer_norm_fp8_fwd", &layer_norm_fp8_fwd);
+  m.impl("rms_norm_fp8_fwd", &rms_norm_fp8_fwd);
+  m.impl("add_layer_norm_fp8_fwd", &add_layer_norm_fp8_fwd);
+  m.impl("add_rms_norm_fp8_fwd", &add_rms_norm_fp8_fwd);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -435,6 +506,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("layernorm_fp8_forward", &layer_norm_fp8_fwd,
         "LayerNorm with OCP fp8 e4m3fn output -> (codes, per-row scale)", py::arg("input"),
         py::arg("gamma") = py::none(), py::arg("beta") = py::none(), py::arg("eps") = 1e-5);
+  m.def("rmsnorm_fp8_forward", &rms_norm_fp8_fwd,
+        "RMSNorm with OCP fp8 e4m3fn output -> (codes, per-row scale)", py::arg("input"),
+        py::arg("weight") = py::none(), py::arg("eps") = 1e-6);
+  m.def("add_layernorm_fp8_forward", &add_layer_norm_fp8_fwd,
+        "Residual add + LayerNorm with fp8 output -> (codes, per-row scale, residual_sum)",
+        py::arg("input"), py::arg("residual"), py::arg("gamma") = py::none(),
+        py::arg("beta") = py::none(), py::arg("eps") = 1e-5);
+  m.def("add_rmsnorm_fp8_forward", &add_rms_norm_fp8_fwd,
+        "Residual add + RMSNorm with fp8 output -> (codes, per-row scale, residual_sum)",
+        py::arg("input"), py::arg("residual"), py::arg("weight") = py::none(),
+        py::arg("eps") = 1e-6);
   m.attr("__version__") = fln_version();
   // The reference exports the CUDA runtime version under this name; here it is HIP's.
   m.attr("__cuda_version__") = fln_hip_version();

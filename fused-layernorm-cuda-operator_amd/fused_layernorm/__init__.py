@@ -8,8 +8,8 @@ variants, all running hand-written HIP kernels.  Importing requires the built ex
 """
 from .layernorm import (FusedLayerNorm, FusedLayerNormFunction, FusedRMSNorm, fused_layer_norm,
                         fused_rms_norm, replace_torch_layernorm, restore_torch_layernorm)
-from .ops import (add_layer_norm, add_rms_norm, layer_norm, layer_norm_fp8, layer_norm_gelu,
-                  rms_norm)
+from .ops import (add_layer_norm, add_layer_norm_fp8, add_rms_norm, add_rms_norm_fp8,
+                  layer_norm, layer_norm_fp8, layer_norm_gelu, rms_norm, rms_norm_fp8)
 from . import functional
 
 __version__ = "1.0.0"
@@ -28,5 +28,8 @@ __all__ = [
     "add_layer_norm",
     "add_rms_norm",
     "layer_norm_fp8",
+    "rms_norm_fp8",
+    "add_layer_norm_fp8",
+    "add_rms_norm_fp8",
     "functional",
 ]

@@ -24,7 +24,7 @@ _ops = torch.ops.fused_layernorm
 
 __all__ = [
     "layer_norm", "layer_norm_gelu", "rms_norm", "add_layer_norm", "add_rms_norm",
-    "layer_norm_fp8",
+    "layer_norm_fp8", "rms_norm_fp8", "add_layer_norm_fp8", "add_rms_norm_fp8",
 ]
 
 
@@ -84,6 +84,24 @@ def _add_rms_fake(input, residual, weight, eps):
 def _ln_fp8_fake(input, weight, bias, eps):
     return (torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device),
             input.new_empty(_stat_shape(input), dtype=torch.float32))
+
+
+@torch.library.register_fake("fused_layernorm::rms_norm_fp8_fwd")
+def _rms_fp8_fake(input, weight, eps):
+    return (torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device),
+            input.new_empty(_stat_shape(input), dtype=torch.float32))
+
+
+@torch.library.register_fake("fused_layernorm::add_layer_norm_fp8_fwd")
+def _add_ln_fp8_fake(input, residual, weight, bias, eps):
+    return (torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device),
+            input.new_empty(_stat_shape(input), dtype=torch.float32), torch.empty_like(input))
+
+
+@torch.library.register_fake("fused_layernorm::add_rms_norm_fp8_fwd")
+def _add_rms_fp8_fake(input, residual, weight, eps):
+    return (torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device),
+            input.new_empty(_stat_shape(input), dtype=torch.float32), torch.empty_like(input))
 
 
 # ---------------------------------------------------------------------------------------------
@@ -177,6 +195,25 @@ torch.library.register_autograd("fused_layernorm::add_rms_norm_fwd", _add_rms_ba
                                 setup_context=_add_rms_setup)
 
 
+# The fp8 outputs (codes, scales) are not differentiable; the residual sum h = x + r is, and
+# its gradient passes through to both addends.
+def _fp8_residual_setup(ctx, inputs, output):
+    q, scale, _h = output
+    ctx.mark_non_differentiable(q, scale)
+
+
+def _fp8_residual_backward(ctx, _gq, _gscale, gh):
+    n_rest = 3 if len(ctx.needs_input_grad) == 5 else 2  # (weight, bias, eps) or (weight, eps)
+    return (gh if ctx.needs_input_grad[0] else None, gh if ctx.needs_input_grad[1] else None,
+            *([None] * n_rest))
+
+
+torch.library.register_autograd("fused_layernorm::add_layer_norm_fp8_fwd",
+                                _fp8_residual_backward, setup_context=_fp8_residual_setup)
+torch.library.register_autograd("fused_layernorm::add_rms_norm_fp8_fwd",
+                                _fp8_residual_backward, setup_context=_fp8_residual_setup)
+
+
 # ---------------------------------------------------------------------------------------------
 # Functional entry points.
 # ---------------------------------------------------------------------------------------------
@@ -261,3 +298,37 @@ def layer_norm_fp8(input: torch.Tensor, normalized_shape: ShapeLike,
     q, scale = _ops.layer_norm_fp8_fwd(x, _flat_param(weight), _flat_param(bias), eps)
     lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
     return q.view(input.shape), scale.view(lead if lead else (1,))
+
+
+def rms_norm_fp8(input: torch.Tensor, normalized_shape: ShapeLike,
+                 weight: Optional[torch.Tensor] = None, eps: float = 1e-6
+                 ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm quantized to OCP fp8 e4m3fn -> (codes, per-row float32 scale)."""
+    x, _ = _flatten(input, normalized_shape)
+    q, scale = _ops.rms_norm_fp8_fwd(x, _flat_param(weight), eps)
+    lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
+    return q.view(input.shape), scale.view(lead if lead else (1,))
+
+
+def add_layer_norm_fp8(input: torch.Tensor, residual: torch.Tensor, normalized_shape: ShapeLike,
+                       weight: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+                       eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused residual add + LayerNorm -> fp8: (codes, per-row scale, h = input + residual).
+    Gradients flow through h only (to input and residual)."""
+    x, _ = _flatten(input, normalized_shape)
+    r, _ = _flatten(residual, normalized_shape)
+    q, scale, h = _ops.add_layer_norm_fp8_fwd(x, r, _flat_param(weight), _flat_param(bias), eps)
+    lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
+    return q.view(input.shape), scale.view(lead if lead else (1,)), h.view(input.shape)
+
+
+def add_rms_norm_fp8(input: torch.Tensor, residual: torch.Tensor, normalized_shape: ShapeLike,
+                     weight: Optional[torch.Tensor] = None, eps: float = 1e-6
+                     ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused residual add + RMSNorm -> fp8 (the pre-norm feeding an fp8 GEMM):
+    (codes, per-row scale, h = input + residual).  Gradients flow through h only."""
+    x, _ = _flatten(input, normalized_shape)
+    r, _ = _flatten(residual, normalized_shape)
+    q, scale, h = _ops.add_rms_norm_fp8_fwd(x, r, _flat_param(weight), eps)
+    lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
+    return q.view(input.shape), scale.view(lead if lead else (1,)), h.view(input.shape)

@@ -107,6 +107,26 @@ int fln_layernorm_fp8_forward(const void* x, const void* gamma, const void* beta
                               float* scale, float* mean, float* rstd, int64_t rows, int64_t cols,
                               int dtype, float eps, void* stream);
 
+/* RMSNorm with fp8 e4m3fn output: v = x rstd [* weight], per-row scale and codes as in
+ * fln_layernorm_fp8_forward.  rstd may be NULL.  No counterpart in the reference. */
+int fln_rmsnorm_fp8_forward(const void* x, const void* weight, uint8_t* q, float* scale,
+                            float* rstd, int64_t rows, int64_t cols, int dtype, float eps,
+                            void* stream);
+
+/* Residual add + LayerNorm with fp8 output: h = x + residual (rounded to dtype, stored when h
+ * is not NULL), then fln_layernorm_fp8_forward of h.  No counterpart in the reference. */
+int fln_add_layernorm_fp8_forward(const void* x, const void* residual, const void* gamma,
+                                  const void* beta, void* h, uint8_t* q, float* scale,
+                                  float* mean, float* rstd, int64_t rows, int64_t cols,
+                                  int dtype, float eps, void* stream);
+
+/* Residual add + RMSNorm with fp8 output (the pre-norm feeding an fp8 GEMM): h = x + residual
+ * (rounded, stored when h is not NULL), then fln_rmsnorm_fp8_forward of h.
+ * No counterpart in the reference. */
+int fln_add_rmsnorm_fp8_forward(const void* x, const void* residual, const void* weight,
+                                void* h, uint8_t* q, float* scale, float* rstd, int64_t rows,
+                                int64_t cols, int dtype, float eps, void* stream);
+
 /* Elementwise fp32 -> OCP fp8 e4m3fn (saturating, round-to-nearest-even) with the same device
  * conversion the fp8 forward uses; n elements, any alignment.  A standalone quantizer for
  * callers that scale themselves (and a direct check of the conversion).

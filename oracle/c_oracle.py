@@ -40,6 +40,7 @@ def load():
         lib.orc_fp8_e4m3fn.argtypes = [ctypes.c_double]
         lib.orc_fp8_e4m3fn.restype = ctypes.c_uint8
         lib.orc_layernorm_fp8.argtypes = [_fp, _fp, _fp, _i64, _i64, ctypes.c_double, _u8p, _fp]
+        lib.orc_rmsnorm_fp8.argtypes = [_fp, _fp, _i64, _i64, ctypes.c_double, _u8p, _fp]
         _lib = lib
     return _lib
 
@@ -104,4 +105,13 @@ def layernorm_fp8(x, gamma=None, beta=None, eps=1e-5):
     scale = np.empty(rows, np.float32)
     load().orc_layernorm_fp8(_p(x, _fp), _p(g, _fp), _p(b, _fp), rows, cols, eps, _p(q, _u8p),
                              _p(scale, _fp))
+    return q, scale
+
+
+def rmsnorm_fp8(x, weight=None, eps=1e-6):
+    x, w = _f32(x), _f32(weight)
+    rows, cols = x.reshape(-1, x.shape[-1]).shape
+    q = np.empty(x.shape, np.uint8)
+    scale = np.empty(rows, np.float32)
+    load().orc_rmsnorm_fp8(_p(x, _fp), _p(w, _fp), rows, cols, eps, _p(q, _u8p), _p(scale, _fp))
     return q, scale

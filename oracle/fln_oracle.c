@@ -167,3 +167,25 @@ void orc_layernorm_fp8(const float* x, const float* gamma, const float* beta, in
     }
   }
 }
+
+/* RMSNorm -> fp8: the same row rule on rms-normalized values (weight may be NULL). */
+void orc_rmsnorm_fp8(const float* x, const float* weight, int64_t rows, int64_t cols, double eps,
+                     uint8_t* q, float* scale) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * cols;
+    const double rs = row_rstd_rms(xr, cols, eps);
+    double amax = 0.0;
+    for (int64_t j = 0; j < cols; ++j) {
+      double v = xr[j] * rs;
+      if (weight) v *= weight[j];
+      if (fabs(v) > amax) amax = fabs(v);
+    }
+    const double sc = amax / 448.0;
+    scale[r] = (float)sc;
+    for (int64_t j = 0; j < cols; ++j) {
+      double v = xr[j] * rs;
+      if (weight) v *= weight[j];
+      q[r * cols + j] = amax > 0.0 ? orc_fp8_e4m3fn(v / sc) : 0;
+    }
+  }
+}

@@ -15,7 +15,8 @@ import numpy as np
 __all__ = [
     "layer_norm_fwd", "layer_norm_gelu_fwd", "gelu", "rms_norm_fwd", "round_to_bf16",
     "round_to_f16", "add_layer_norm_fwd", "add_rms_norm_fwd", "layer_norm_bwd", "rms_norm_bwd",
-    "fp8_e4m3fn_encode", "fp8_e4m3fn_decode", "layer_norm_fp8_fwd", "FP8_E4M3FN_MAX",
+    "fp8_e4m3fn_encode", "fp8_e4m3fn_decode", "layer_norm_fp8_fwd", "rms_norm_fp8_fwd",
+    "add_layer_norm_fp8_fwd", "add_rms_norm_fp8_fwd", "FP8_E4M3FN_MAX",
 ]
 
 FP8_E4M3FN_MAX = 448.0
@@ -199,8 +200,34 @@ def layer_norm_fp8_fwd(x, gamma=None, beta=None, eps=1e-5):
     v = LayerNorm(x) (affine), scale = max|v| / 448 per row, codes = sat_rne_e4m3fn(v / scale);
     a row with max|v| == 0 gets scale 0 and all-zero codes.  No reference code."""
     y, _, _ = layer_norm_fwd(x, gamma, beta, eps)
+    return _row_fp8(y)
+
+
+def _row_fp8(y):
     amax = np.abs(y).max(axis=-1, keepdims=True)
     scale = amax / FP8_E4M3FN_MAX
     with np.errstate(divide="ignore", invalid="ignore"):
         q = np.where(amax > 0, y / np.where(amax > 0, scale, 1.0), 0.0)
     return fp8_e4m3fn_encode(q), scale[..., 0].astype(np.float32)
+
+
+def rms_norm_fp8_fwd(x, weight=None, eps=1e-6):
+    """RMSNorm with fp8 output -> (codes, scale): the row rule of layer_norm_fp8_fwd applied to
+    rms_norm_fwd's output.  No reference code."""
+    y, _ = rms_norm_fwd(x, weight, eps)
+    return _row_fp8(y)
+
+
+def add_layer_norm_fp8_fwd(x, residual, gamma=None, beta=None, eps=1e-5, io_dtype="bf16"):
+    """Residual add + LayerNorm -> fp8: (codes, scale, h); h rounded as in add_layer_norm_fwd.
+    No reference code."""
+    y, h, _, _ = add_layer_norm_fwd(x, residual, gamma, beta, eps, io_dtype)
+    q, scale = _row_fp8(y)
+    return q, scale, h
+
+
+def add_rms_norm_fp8_fwd(x, residual, weight=None, eps=1e-6, io_dtype="bf16"):
+    """Residual add + RMSNorm -> fp8: (codes, scale, h).  No reference code."""
+    y, h, _ = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
+    q, scale = _row_fp8(y)
+    return q, scale, h

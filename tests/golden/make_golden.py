@@ -114,6 +114,18 @@ def main():
                 "fp8_b_bf16": bf16_bits(b), "fp8_q": q.numpy(),
                 "fp8_scale": scale[:, 0].float().numpy()})
 
+    # Residual add + RMSNorm -> fp8 (bf16 in, per-row scale), the pre-norm of an fp8 GEMM.
+    x = randn((8, 4096), 140).to(torch.bfloat16)
+    r = randn((8, 4096), 141).to(torch.bfloat16)
+    w = randn((4096,), 142, 0.05, 1.0).to(torch.bfloat16)
+    h = x + r
+    y = F.rms_norm(h.double(), (4096,), w.double(), 1e-6)
+    amax = y.abs().amax(-1, keepdim=True)
+    q = (y / (amax / 448.0)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+    out.update({"arf_x_bf16": bf16_bits(x), "arf_r_bf16": bf16_bits(r),
+                "arf_w_bf16": bf16_bits(w), "arf_h_bf16": bf16_bits(h), "arf_q": q.numpy(),
+                "arf_scale": (amax[:, 0] / 448.0).float().numpy()})
+
     # fp8 encoder: torch's cast of a value sweep (clamped to +-448 first: saturation).
     v = torch.cat([torch.tensor([0.0, -0.0, 448.0, -448.0, 449.0, 1e6, 2.0 ** -9, 2.0 ** -10,
                                  3 * 2.0 ** -10, 0.0625, 1.0625, 1.1875, 240.0, 232.0]),

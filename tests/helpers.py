@@ -59,14 +59,29 @@ def fp8_ordinal(codes):
     return np.where(c & 0x80, -mag, mag)
 
 
-def assert_fp8_close(q_got, s_got, q_ref, s_ref, what=""):
+def fp8_ambiguous(t, rel=2.0 ** -20):
+    """Elements whose exact (float64) scaled value t lies within `rel` (relative) of an e4m3fn
+    rounding midpoint: an fp32 computation of t (a few ulps of noise) may round them either
+    way.  Exact ties are common when the row scale cancels a normalization factor (RMSNorm of
+    low-precision inputs: t = 448 (h w) / max|h w|)."""
+    from oracle import norms
+    t = np.asarray(t, np.float64)
+    return norms.fp8_e4m3fn_encode(t * (1 - rel)) != norms.fp8_e4m3fn_encode(t * (1 + rel))
+
+
+def assert_fp8_close(q_got, s_got, q_ref, s_ref, what="", t_ref=None):
     """fp8 output bar: per-row scales within 1e-6 relative; codes identical except +-1 code on
-    at most 0.1% of the elements."""
+    at most 0.1% of the elements.  With t_ref (the reference's unquantized scaled values), a
+    +-1 code at an element within fp32 noise of a rounding midpoint (fp8_ambiguous) does not
+    count against the 0.1%."""
     s_got = np.asarray(s_got, np.float64)
     s_ref = np.asarray(s_ref, np.float64)
     rel = np.abs(s_got - s_ref) / np.where(s_ref > 0, s_ref, 1.0)
     assert rel.max() <= 1e-6, f"{what}: scale rel err {rel.max():.3g}"
     diff = np.abs(fp8_ordinal(q_got) - fp8_ordinal(q_ref))
-    n_diff = int((diff != 0).sum())
     assert int(diff.max()) <= 1, f"{what}: a code differs by {int(diff.max())} steps"
+    counted = diff != 0
+    if t_ref is not None:
+        counted &= ~fp8_ambiguous(t_ref)
+    n_diff = int(counted.sum())
     assert n_diff <= 1e-3 * diff.size, f"{what}: {n_diff} of {diff.size} codes differ"

@@ -107,6 +107,14 @@ def test_oracle_fp8(gold):
                           gold["enc_q"])
 
 
+def test_oracle_residual_rms_fp8(gold):
+    x, r = bf16_from_bits(gold["arf_x_bf16"]), bf16_from_bits(gold["arf_r_bf16"])
+    w = bf16_from_bits(gold["arf_w_bf16"])
+    q, s, h = norms.add_rms_norm_fp8_fwd(x, r, w, 1e-6, "bf16")
+    assert np.array_equal(h, bf16_from_bits(gold["arf_h_bf16"]))
+    assert_fp8_close(q, s, gold["arf_q"], gold["arf_scale"], "oracle residual rms fp8")
+
+
 # ------------------------------------------------------------------------------------------------
 # GPU: the kernels reproduce the same fixtures.
 # ------------------------------------------------------------------------------------------------
@@ -215,3 +223,20 @@ def test_gpu_fp8_encoder_matches_torch_cast(lib, gold):
     q = torch.empty(v.numel(), device="cuda", dtype=torch.uint8)
     capi.check(lib.fln_fp8_e4m3fn_encode(capi.ptr(v), capi.ptr(q), v.numel(), capi.stream()))
     assert np.array_equal(q.cpu().numpy(), gold["enc_q"])  # bit-exact
+
+
+@pytest.mark.gpu
+def test_gpu_residual_rms_fp8(lib, gold):
+    x = dev(bf16_from_bits(gold["arf_x_bf16"]), torch.bfloat16)
+    r = dev(bf16_from_bits(gold["arf_r_bf16"]), torch.bfloat16)
+    w = dev(bf16_from_bits(gold["arf_w_bf16"]), torch.bfloat16)
+    rows, cols = x.shape
+    h = torch.empty_like(x)
+    q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+    s = torch.empty(rows, device="cuda")
+    capi.check(lib.fln_add_rmsnorm_fp8_forward(capi.ptr(x), capi.ptr(r), capi.ptr(w),
+                                               capi.ptr(h), capi.ptr(q), capi.ptr(s), None,
+                                               rows, cols, capi.BF16, 1e-6, capi.stream()))
+    assert np.array_equal(to_np(h), bf16_from_bits(gold["arf_h_bf16"])), "h bit-exact"
+    assert_fp8_close(q.cpu().numpy(), to_np(s), gold["arf_q"], gold["arf_scale"],
+                     "gpu residual rms fp8")

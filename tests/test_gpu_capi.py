@@ -348,6 +348,84 @@ def test_parameter_gradients_in_parameter_dtype(lib, dtype, rows, cols):
                           what=what)
 
 
+def test_c6_add_rmsnorm_fp8_bf16_32768x7168(lib):
+    """Residual add + RMSNorm -> fp8 at C5's shape: h bit-exact, codes and scales to the fp8
+    bar against the C oracle (RMSNorm -> fp8 of the bf16-rounded h)."""
+    w = WORKLOADS["c6_add_rms_fp8_bf16_32768x7168"]
+    inp = make_inputs(w)
+    x, r, g = (cuda(inp[k]) for k in ("x", "residual", "gamma"))
+    h = torch.empty_like(x)
+    q = torch.empty(x.shape, device="cuda", dtype=torch.uint8)
+    scale = torch.empty(w.rows, device="cuda", dtype=torch.float32)
+    capi.check(lib.fln_add_rmsnorm_fp8_forward(
+        capi.ptr(x), capi.ptr(r), capi.ptr(g), capi.ptr(h), capi.ptr(q), capi.ptr(scale), None,
+        w.rows, w.cols, capi.BF16, w.eps, capi.stream()))
+    del x, r
+    h_ref = inp["x"] + inp["residual"]  # torch CPU bf16 add
+    assert torch.equal(h.cpu(), h_ref), "h must be bit-exact"
+    q_ref, s_ref = c_oracle.rmsnorm_fp8(f32(h_ref), f32(inp["gamma"]), w.eps)
+    assert_fp8_close(q.cpu().numpy(), to_np(scale), q_ref, s_ref, "c6")
+
+
+def _scaled(y):
+    """Unquantized fp8 values of the row rule: y / (max|y| / 448) per row."""
+    amax = np.abs(y).max(axis=-1, keepdims=True)
+    return np.where(amax > 0, y * 448.0 / np.where(amax > 0, amax, 1.0), 0.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 1023), (33, 7168), (2, 16384)])
+def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
+    """RMSNorm -> fp8, residual + LayerNorm -> fp8, residual + RMSNorm -> fp8 over dtypes and
+    widths (1023: the scalar path; 16384: a wide row), against the numpy oracle."""
+    gen = torch.Generator().manual_seed(rows * 31 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, r, g, b = cuda(xc), cuda(rc), cuda(gc), cuda(bc)
+    kind = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    code = capi.dtype_code(x)
+    q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+    s = torch.empty(rows, device="cuda")
+    h = torch.empty_like(x)
+    p = capi.ptr
+    capi.check(lib.fln_rmsnorm_fp8_forward(p(x), p(g), p(q), p(s), None, rows, cols, code, 1e-6,
+                                           capi.stream()))
+    q_ref, s_ref = norms.rms_norm_fp8_fwd(f32(xc), f32(gc), 1e-6)
+    assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "rms fp8",
+                     t_ref=_scaled(norms.rms_norm_fwd(f32(xc), f32(gc), 1e-6)[0]))
+    h_ref = to_np(xc + rc)  # torch CPU add in the I/O type
+    capi.check(lib.fln_add_layernorm_fp8_forward(p(x), p(r), p(g), p(b), p(h), p(q), p(s), None,
+                                                 None, rows, cols, code, 1e-5, capi.stream()))
+    assert np.array_equal(to_np(h), h_ref), "h bit-exact"
+    q_ref, s_ref, _ = norms.add_layer_norm_fp8_fwd(f32(xc), f32(rc), f32(gc), f32(bc), 1e-5,
+                                                   kind)
+    assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "add ln fp8")
+    h.zero_()
+    capi.check(lib.fln_add_rmsnorm_fp8_forward(p(x), p(r), p(g), p(h), p(q), p(s), None, rows,
+                                               cols, code, 1e-6, capi.stream()))
+    assert np.array_equal(to_np(h), h_ref), "h bit-exact"
+    q_ref, s_ref, h_o = norms.add_rms_norm_fp8_fwd(f32(xc), f32(rc), f32(gc), 1e-6, kind)
+    assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "add rms fp8",
+                     t_ref=_scaled(norms.rms_norm_fwd(h_o, f32(gc), 1e-6)[0]))
+
+
+def test_fp8_variants_reject_bad_arguments(lib):
+    x = torch.randn(4, 64, device="cuda")
+    q = torch.empty(4, 64, device="cuda", dtype=torch.uint8)
+    s = torch.empty(4, device="cuda")
+    p = capi.ptr
+    # residual is required; a scale buffer is required; fp64 has no fp8 path
+    assert lib.fln_add_rmsnorm_fp8_forward(p(x), None, None, None, p(q), p(s), None, 4, 64,
+                                           capi.F32, 1e-6, capi.stream()) == 1
+    assert lib.fln_add_layernorm_fp8_forward(p(x), p(x), None, None, None, p(q), None, None,
+                                             None, 4, 64, capi.F32, 1e-5, capi.stream()) == 1
+    assert lib.fln_rmsnorm_fp8_forward(p(x), None, p(q), p(s), None, 4, 64, capi.F64, 1e-6,
+                                       capi.stream()) == 1
+
+
 def test_residual_gradient_is_added(lib):
     gen = torch.Generator().manual_seed(9)
     xc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)

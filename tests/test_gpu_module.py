@@ -343,6 +343,39 @@ def test_layer_norm_fp8_output_type_and_values():
     assert (deq.double().cpu() - ref).abs().max().item() <= 2.0 ** -3 * ref.abs().max().item()
 
 
+@pytest.mark.parametrize("norm", ["rms", "ln"])
+def test_residual_fp8_functional_and_gradient_pass_through(norm):
+    """(codes, scale, h) from the fused residual ops; only h is differentiable, and its
+    gradient reaches both addends unchanged (h = x + r)."""
+    x = torch.randn(64, 4096, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    r = torch.randn(64, 4096, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    w = (1 + 0.05 * torch.randn(4096, device=DEV)).to(torch.bfloat16)
+    if norm == "rms":
+        q, scale, h = fl.add_rms_norm_fp8(x, r, (4096,), w, 1e-6)
+        q_ref, s_ref, _ = norms.add_rms_norm_fp8_fwd(to_np(x), to_np(r), to_np(w), 1e-6)
+    else:
+        b = (0.05 * torch.randn(4096, device=DEV)).to(torch.bfloat16)
+        q, scale, h = fl.add_layer_norm_fp8(x, r, (4096,), w, b, 1e-5)
+        q_ref, s_ref, _ = norms.add_layer_norm_fp8_fwd(to_np(x), to_np(r), to_np(w), to_np(b),
+                                                       1e-5)
+    assert q.dtype == torch.float8_e4m3fn and not q.requires_grad and not scale.requires_grad
+    assert torch.equal(h, (x + r).detach())
+    assert_fp8_close(q.view(torch.uint8).cpu().numpy(), to_np(scale), q_ref, s_ref, norm)
+    dh = torch.randn_like(h)
+    (h * dh).sum().backward()
+    assert torch.equal(x.grad, dh) and torch.equal(r.grad, dh)
+
+
+def test_rms_norm_fp8_functional():
+    x = torch.randn(4, 16, 2048, device=DEV, dtype=torch.bfloat16)
+    w = (1 + 0.05 * torch.randn(2048, device=DEV)).to(torch.bfloat16)
+    q, scale = fl.rms_norm_fp8(x, (2048,), w, 1e-6)
+    assert q.shape == x.shape and scale.shape == (4, 16)
+    q_ref, s_ref = norms.rms_norm_fp8_fwd(to_np(x).reshape(-1, 2048), to_np(w), 1e-6)
+    assert_fp8_close(q.view(torch.uint8).reshape(-1, 2048).cpu().numpy(),
+                     to_np(scale).reshape(-1), q_ref, s_ref, "rms fp8")
+
+
 # ------------------------------------------------------------------------------------------------
 # torch.compile and operator registration.
 # ------------------------------------------------------------------------------------------------
@@ -376,9 +409,19 @@ def test_torch_compile_matches_eager():
     ("layer_norm_gelu_fwd", lambda: (torch.randn(8, 256, device=DEV),
                                      torch.randn(256, device=DEV),
                                      torch.randn(256, device=DEV), 1e-5, "tanh")),
+    ("add_rms_norm_fp8_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
+                                      torch.randn(8, 256, device=DEV, requires_grad=True),
+                                      torch.randn(256, device=DEV), 1e-6)),
+    ("rms_norm_fp8_fwd", lambda: (torch.randn(8, 256, device=DEV),
+                                  torch.randn(256, device=DEV), 1e-6)),
 ])
 def test_opcheck(op, args):
-    torch.library.opcheck(getattr(torch.ops.fused_layernorm, op), args())
+    # opcheck's AOT-dispatch check sums every output into a loss, and torch has no sum for
+    # float8 tensors: the fp8 ops get the schema, fake-tensor and autograd-registration checks.
+    utils = ("test_schema", "test_autograd_registration", "test_faketensor") \
+        if "fp8" in op else ("test_schema", "test_autograd_registration", "test_faketensor",
+                             "test_aot_dispatch_dynamic")
+    torch.library.opcheck(getattr(torch.ops.fused_layernorm, op), args(), test_utils=utils)
 
 
 # ------------------------------------------------------------------------------------------------

@@ -111,6 +111,14 @@ def test_fake_tensor_shapes_of_every_op():
         assert fl.layer_norm_gelu(x, 64, w, w, approximate="none").shape == x.shape
         y2, h2 = fl.add_rms_norm(x, x, (64,), w)
         assert y2.shape == x.shape == h2.shape
+        q, s = torch.ops.fused_layernorm.rms_norm_fp8_fwd(x, w, 1e-6)
+        assert q.dtype == torch.float8_e4m3fn and s.shape == (3, 5)
+        for q, s, h in (torch.ops.fused_layernorm.add_rms_norm_fp8_fwd(x, x, w, 1e-6),
+                        torch.ops.fused_layernorm.add_layer_norm_fp8_fwd(x, x, w, w, 1e-5)):
+            assert q.shape == x.shape and q.dtype == torch.float8_e4m3fn
+            assert s.shape == (3, 5) and s.dtype == torch.float32 and h.dtype == x.dtype
+        q, s, h = fl.add_rms_norm_fp8(x, x, 64, w)
+        assert q.shape == x.shape and s.shape == (3, 5) and h.shape == x.shape
 
 
 def test_module_state_dict_keys_match_nn_layernorm():

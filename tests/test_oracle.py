@@ -223,6 +223,41 @@ def test_layer_norm_fp8_row_scale_and_codes(rng):
     assert (qz == 0).all() and (sz == 0).all()
 
 
+def _torch_fp8_rows(y64):
+    """PyTorch's own composition of the fp8 row rule: amax / 448 scale, divide, clamp, cast."""
+    amax = y64.abs().amax(-1, keepdim=True)
+    scale = amax / 448.0
+    q = torch.where(amax > 0, y64 / torch.where(amax > 0, scale, torch.ones_like(scale)),
+                    torch.zeros_like(y64))
+    return q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy(), \
+        scale[..., 0].float().numpy()
+
+
+def test_rms_and_residual_fp8_variants_match_torch_composition(rng):
+    x = rng.randn(12, 768).astype(np.float32)
+    x[:, 5] *= 30
+    r = rng.randn(12, 768).astype(np.float32)
+    w = (1 + 0.1 * rng.randn(768)).astype(np.float32)
+    b = (0.1 * rng.randn(768)).astype(np.float32)
+    # RMSNorm -> fp8
+    q, s = norms.rms_norm_fp8_fwd(x, w, 1e-6)
+    qt, st = _torch_fp8_rows(F.rms_norm(t64(x), (768,), t64(w), 1e-6))
+    assert np.array_equal(q, qt) and np.array_equal(s, st)
+    qc, sc = c_oracle.rmsnorm_fp8(x, w, 1e-6)
+    assert np.array_equal(qc, q) and np.array_equal(sc, s)
+    # residual add (bf16 rounding of h, as torch's bf16 add) + RMSNorm / LayerNorm -> fp8
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    rb = torch.from_numpy(r).to(torch.bfloat16)
+    hb = xb + rb
+    q, s, h = norms.add_rms_norm_fp8_fwd(xb.float().numpy(), rb.float().numpy(), w, 1e-6)
+    assert np.array_equal(h, hb.float().numpy())
+    qt, st = _torch_fp8_rows(F.rms_norm(hb.double(), (768,), t64(w), 1e-6))
+    assert np.array_equal(q, qt) and np.array_equal(s, st)
+    q, s, h = norms.add_layer_norm_fp8_fwd(xb.float().numpy(), rb.float().numpy(), w, b, 1e-5)
+    qt, st = _torch_fp8_rows(F.layer_norm(hb.double(), (768,), t64(w), t64(b), 1e-5))
+    assert np.array_equal(q, qt) and np.array_equal(s, st)
+
+
 # ---------------------------------------------------------------- C oracle vs numpy oracle
 def test_c_oracle_matches_numpy_oracle(rng):
     x = rng.randn(9, 1023).astype(np.float32)
