@@ -3,9 +3,9 @@
 Default workload (the headline metric): LayerNorm forward + backward, bf16, 8192 x 4096 -- one
 "step" is the forward (y, mean, rstd) plus the backward (dx, dgamma, dbeta) over one batch, with
 inputs already resident in HBM.  The RMSNorm forward + backward at the same shape is timed the
-same way and reported under "rms_fwd_bwd"; the benchmark configurations C1..C5, and C6 (residual
-add + RMSNorm -> fp8 at C5's shape), are timed under "configs" (latency for the small ones, GB/s
-for the large ones).
+same way and reported under "rms_fwd_bwd"; the benchmark configurations C1..C5, C6 (residual
+add + RMSNorm -> fp8 at C5's shape) and LayerNorm + GELU forward + backward at the headline
+shape are timed under "configs" (latency for the small ones, GB/s for the large ones).
 
 The kernels are called through the C ABI (libfln.so) on torch's current HIP stream, with every
 output preallocated.  Inputs and outputs rotate over at least 4 buffer sets (>= 2 GiB in all,
@@ -48,7 +48,8 @@ ROTATE_BYTES = 2 * 2 ** 30
 CALIBRATION_COPY_BYTES = 256 * 2 ** 20
 CONFIGS = ("c1_ln_fwd_fp32_32x768", "c2_ln_gelu_fp32_17x1023", "c2_ln_gelu_fp32_64x4096",
            "c3_add_ln_fwd_bf16_8192x4096", "c4_rms_fwd_bwd_bf16_16384x8192",
-           "c5_ln_fp8_bf16_32768x7168", "c6_add_rms_fp8_bf16_32768x7168")
+           "c5_ln_fp8_bf16_32768x7168", "c6_add_rms_fp8_bf16_32768x7168",
+           "ln_gelu_fwd_bwd_bf16_8192x4096")
 
 
 def parse():
@@ -131,6 +132,10 @@ class Runner:
                 rc = self.lib.fln_layernorm_gelu(p(s["x"]), p(s.get("gamma")), p(s.get("beta")),
                                                  p(s["y"]), self.rows, self.cols, self.code,
                                                  self.w.eps, gelu, stream)
+        elif self.w.op == "layer_norm_gelu_fwd_bwd":
+            rc = self.lib.fln_layernorm_gelu_forward(
+                p(s["x"]), p(s.get("gamma")), p(s.get("beta")), p(s["y"]), p(s["mean"]),
+                p(s["rstd"]), self.rows, self.cols, self.code, self.w.eps, self._gelu(), stream)
         elif self.w.op.startswith("rms"):
             rc = self.lib.fln_rmsnorm_forward(p(s["x"]), p(s.get("gamma")), p(s["y"]),
                                               p(s["rstd"]), self.rows, self.cols, self.code,
@@ -144,7 +149,12 @@ class Runner:
 
     def bwd(self, s, stream):
         c, p = self.capi, self.capi.ptr
-        if self.w.op.startswith("rms"):
+        if self.w.op == "layer_norm_gelu_fwd_bwd":
+            rc = self.lib.fln_layernorm_gelu_backward(
+                p(s["dy"]), p(s["x"]), p(s["mean"]), p(s["rstd"]), p(s.get("gamma")),
+                p(s.get("beta")), p(s["dx"]), p(self.dg), p(self.db), self.rows, self.cols,
+                self.code, c.F32, self._gelu(), p(self.ws), self.ws_bytes, stream)
+        elif self.w.op.startswith("rms"):
             rc = self.lib.fln_rmsnorm_backward(p(s["dy"]), p(s["x"]), p(s["rstd"]),
                                                p(s.get("gamma")), None, p(s["dx"]), p(self.dg),
                                                self.rows, self.cols, self.code, c.F32,
@@ -156,6 +166,9 @@ class Runner:
                                                  self.cols, self.code, c.F32, p(self.ws),
                                                  self.ws_bytes, stream)
         c.check(rc)
+
+    def _gelu(self):
+        return {"none": self.capi.GELU_ERF, "tanh": self.capi.GELU_TANH}[self.w.approximate]
 
     def prime(self, stream):
         """One forward per set, so every set holds the statistics its backward reads."""

@@ -125,7 +125,11 @@ __device__ __forceinline__ void reduce_quad_block(const ColReduceArgs& a, int64_
 #ifndef FLN_BWD_STORE_POL
 #define FLN_BWD_STORE_POL kStream
 #endif
-template <class T, bool DRES, int VEC, int VPL, int MAXT>
+// GELU (1 erf, 2 tanh): the backward of GELU(LayerNorm(x) * gamma + beta).  The GELU input
+// a = xhat gamma + beta is recomputed from the saved statistics, and dy is replaced by
+// dy GELU'(a) before the LayerNorm algebra (so dgamma / dbeta are sums of dy GELU'(a) xhat and
+// of dy GELU'(a)).
+template <class T, bool DRES, int GELU, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   constexpr int PD = FLN_BWD_PREFETCH;  // rows in flight ahead of the current one
   constexpr int MAXW = MAXT / kWave;
@@ -155,8 +159,10 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   const T* DR = static_cast<const T*>(p.dres);
   T* DX = static_cast<T*>(p.dx);
 
-  // gamma in fp32 registers (ones when absent; zeros past the row).
+  // gamma (and, with GELU, beta) in fp32 registers (gamma ones when absent; zeros past the
+  // row).
   float gam[VPL][VEC];
+  float bet[GELU ? VPL : 1][VEC];
   {
     const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
     const bool has_g = p.gamma != nullptr;
@@ -165,6 +171,15 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       const P gv = buf_load<P>(gr, t + i * tpr);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) gam[i][e] = has_g ? to_f32(gv.v[e]) : 1.0f;
+    }
+    if constexpr (GELU != 0) {
+      const rsrc_t br = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const P bv = buf_load<P>(br, t + i * tpr);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) bet[i][e] = to_f32(bv.v[e]);
+      }
     }
   }
   float acc_g[VPL][VEC], acc_b[VPL][VEC];
@@ -218,6 +233,8 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       for (int e = 0; e < VEC; ++e) {
         xh[i][e] = (to_f32(xn[slot][i].v[e]) - mu) * rs;
         dd[i][e] = to_f32(dn[slot][i].v[e]);
+        if constexpr (GELU == 1) dd[i][e] *= gelu_erf_grad(fmaf(xh[i][e], gam[i][e], bet[i][e]));
+        if constexpr (GELU == 2) dd[i][e] *= gelu_tanh_grad(fmaf(xh[i][e], gam[i][e], bet[i][e]));
         gg[i][e] = dd[i][e] * gam[i][e];
       }
       if constexpr (DRES) rv[i] = rn[slot][i];
@@ -329,6 +346,13 @@ __global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
   const int64_t N = p.cols;
   const int64_t ld = (N + 3) & ~int64_t(3);
   const T* gm = static_cast<const T*>(p.gamma);
+  const T* bt = static_cast<const T*>(p.beta);
+  // Upstream gradient at the LayerNorm output: dy, or dy GELU'(xhat gamma + beta).
+  auto dln = [&](float d, float xh, int64_t j) {
+    if (!p.gelu) return d;
+    const float a = fmaf(xh, gm ? to_f32(gm[j]) : 1.0f, bt ? to_f32(bt[j]) : 0.0f);
+    return d * gelu_grad(a, p.gelu);
+  };
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * p.rows_per_block;
   const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
   float* pg = p.part_g ? p.part_g + static_cast<int64_t>(blockIdx.x) * ld : nullptr;
@@ -347,7 +371,7 @@ __global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
     float s1 = 0.0f, s2 = 0.0f;
     for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
       const float xh = (to_f32(x[j]) - mu) * rs;
-      const float g = to_f32(dy[j]) * (gm ? to_f32(gm[j]) : 1.0f);
+      const float g = dln(to_f32(dy[j]), xh, j) * (gm ? to_f32(gm[j]) : 1.0f);
       s1 += g;
       s2 += g * xh;
     }
@@ -369,7 +393,7 @@ __global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
     const T* dres = p.dres ? static_cast<const T*>(p.dres) + row * N : nullptr;
     for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
       const float xh = (to_f32(x[j]) - mu) * rs;
-      const float d = to_f32(dy[j]);
+      const float d = dln(to_f32(dy[j]), xh, j);
       const float g = d * (gm ? to_f32(gm[j]) : 1.0f);
       if (dx) {
         float v = rs * (g - c1 - xh * c2);
@@ -382,9 +406,6 @@ __global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
   }
 }
 
-// Stage 2: out[c] = sum over partial rows k (in order) of part[k][c].  Block = 16 waves over
-// 256 columns: lane l owns 4 columns, wave w sums rows w, w+16, ...; the 16 wave sums are then
-// added in wave order through LDS.  A y-block index selects the array (dgamma or dbeta).
 constexpr int kCrSlices = 32;
 constexpr int kCrThreads = kCrQuads * kCrSlices;
 
@@ -413,10 +434,10 @@ int next_pow2(int v) {
 
 // Stage-1 launch (resident == nullptr) or, with `resident`, the number of blocks of that
 // instantiation that fit on the device at once (occupancy x CUs, cached per device).
-template <class T, bool DRES, int VEC, int VPL, int MAXT>
+template <class T, bool DRES, int GELU, int VEC, int VPL, int MAXT>
 int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                     int64_t* resident) {
-  auto kernel = bwd_reg_kernel<T, DRES, VEC, VPL, MAXT>;
+  auto kernel = bwd_reg_kernel<T, DRES, GELU, VEC, VPL, MAXT>;
   if (resident) {
     static std::atomic<int> per_cu[3][64];  // [threads / 512][device]
     int dev = 0;
@@ -439,8 +460,14 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
 template <class T, int VEC, int VPL>
 int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                   int64_t* resident) {
-  return p.dres ? launch_stage1_k<T, true, VEC, VPL, 1024>(p, blocks, threads, s, resident)
-                : launch_stage1_k<T, false, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+  // GELU is never combined with a residual gradient (no entry point passes both).
+  if (p.gelu == 1)
+    return launch_stage1_k<T, false, 1, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+  if (p.gelu == 2)
+    return launch_stage1_k<T, false, 2, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+  if (p.dres)
+    return launch_stage1_k<T, true, 0, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+  return launch_stage1_k<T, false, 0, VEC, VPL, 1024>(p, blocks, threads, s, resident);
 }
 
 template <class T, int VEC>
@@ -621,6 +648,20 @@ extern "C" int fln_layernorm_backward(const void* dy, const void* x, const float
   fln::BwdParams p{};
   p.dy = dy; p.x = x; p.mean = mean; p.rstd = rstd; p.gamma = gamma; p.dres = dres; p.dx = dx;
   p.rows = rows; p.cols = cols; p.rms = 0;
+  return backward_common(p, dtype, dgamma, dbeta, dparam_dtype, workspace, workspace_bytes,
+                         stream);
+}
+
+extern "C" int fln_layernorm_gelu_backward(const void* dy, const void* x, const float* mean,
+                                           const float* rstd, const void* gamma,
+                                           const void* beta, void* dx, void* dgamma,
+                                           void* dbeta, int64_t rows, int64_t cols, int dtype,
+                                           int dparam_dtype, int gelu_mode, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  if (gelu_mode != FLN_GELU_ERF && gelu_mode != FLN_GELU_TANH) return FLN_ERR_INVALID;
+  fln::BwdParams p{};
+  p.dy = dy; p.x = x; p.mean = mean; p.rstd = rstd; p.gamma = gamma; p.beta = beta; p.dx = dx;
+  p.rows = rows; p.cols = cols; p.rms = 0; p.gelu = gelu_mode;
   return backward_common(p, dtype, dgamma, dbeta, dparam_dtype, workspace, workspace_bytes,
                          stream);
 }

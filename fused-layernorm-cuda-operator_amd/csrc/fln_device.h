@@ -189,15 +189,52 @@ template <class A> __device__ __forceinline__ A wave_sum_generic(A v) {
 // ---------------------------------------------------------------------------------------------
 // GELU.  mode 1: exact erf form (torch approximate='none'); mode 2: tanh form, the one fused by
 // the reference (csrc/layernorm_cuda_kernel.cu:31-36).
+//
+// The tanh form is evaluated through the identity 0.5 v (1 + tanh(u)) = v sigmoid(2u) =
+// v / (1 + e^(-2u)), u = sqrt(2/pi) (v + 0.044715 v^3): one hardware exp2 (v_exp_f32) and one
+// hardware reciprocal (v_rcp_f32) instead of a tanh, and no cancellation for large negative v (the quotient stays
+// relatively accurate where 1 + tanh(u) would cancel).  Its derivative is
+//   s + 2 v s (1 - s) sqrt(2/pi) (1 + 3 * 0.044715 v^2),   s = sigmoid(2u).
+// The erf form keeps erff; its Gaussian factor uses the hardware exp2:
+//   d/dv = 0.5 (1 + erf(v / sqrt 2)) + v exp(-v^2 / 2) / sqrt(2 pi).
 // ---------------------------------------------------------------------------------------------
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kGeluK0 = 0.79788456080286535588f;  // sqrt(2/pi)
+constexpr float kGeluK1 = 0.044715f;
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// For the tanh form, u = sqrt(2/pi) (v + k1 v^3): e = e^(-2u) and sigmoid(2u) = 1 / (1 + e);
+// 1 - sigmoid(2u) = e / (1 + e) is formed as a product, not a difference (no cancellation where
+// the sigmoid approaches 1).
+struct GeluTanhTerms {
+  float e, sg;
+};
+__device__ __forceinline__ GeluTanhTerms gelu_tanh_terms(float v) {
+  const float two_u = 2.0f * kGeluK0 * fmaf(kGeluK1 * v, v * v, v);
+  const float e = exp2_fast(-two_u * kLog2e);
+  return {e, __builtin_amdgcn_rcpf(1.0f + e)};  // v_rcp_f32: 1 ulp
+}
+__device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_terms(v).sg; }
 __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
 }
-__device__ __forceinline__ float gelu_tanh(float v) {
-  const float k0 = 0.79788456080286535588f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  return 0.5f * v * (1.0f + tanhf(k0 * (v + k1 * v * v * v)));
+__device__ __forceinline__ float gelu_tanh(float v) { return v * gelu_tanh_sigmoid(v); }
+__device__ __forceinline__ float gelu_erf_grad(float v) {
+  const float inv_sqrt_2pi = 0.39894228040143267794f;
+  return 0.5f * (1.0f + erff(v * 0.70710678118654752440f)) +
+         v * inv_sqrt_2pi * exp2_fast(-0.5f * kLog2e * v * v);
 }
+__device__ __forceinline__ float gelu_tanh_grad(float v) {
+  const GeluTanhTerms t = gelu_tanh_terms(v);
+  const float one_minus = t.e * t.sg;  // 1 - sigmoid(2u); 0 when e overflows to inf (sg = 0)
+  return fmaf(2.0f * v * t.sg * (t.e < 3.0e38f ? one_minus : 0.0f),
+              kGeluK0 * fmaf(3.0f * kGeluK1, v * v, 1.0f), t.sg);
+}
+__device__ __forceinline__ float gelu_grad(float v, int mode) {
+  return mode == 1 ? gelu_erf_grad(v) : gelu_tanh_grad(v);
+}
+
 template <class A> __device__ __forceinline__ A apply_gelu(A v, int mode) {
   if (mode == 1) return gelu_erf(static_cast<float>(v));
   if (mode == 2) return gelu_tanh(static_cast<float>(v));

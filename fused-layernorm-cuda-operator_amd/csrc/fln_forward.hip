@@ -75,6 +75,17 @@ extern "C" int fln_layernorm_gelu(const void* x, const void* gamma, const void* 
   return fln::launch_forward(p, dtype, false, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int fln_layernorm_gelu_forward(const void* x, const void* gamma, const void* beta,
+                                          void* y, float* mean, float* rstd, int64_t rows,
+                                          int64_t cols, int dtype, float eps, int gelu_mode,
+                                          void* stream) {
+  if (gelu_mode != FLN_GELU_ERF && gelu_mode != FLN_GELU_TANH) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.gamma = gamma; p.beta = beta; p.y = y; p.mean = mean; p.rstd = rstd;
+  p.rows = rows; p.cols = cols; p.eps = eps; p.gelu = gelu_mode;
+  return fln::launch_forward(p, dtype, false, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int fln_layernorm_forward(const void* x, const void* gamma, const void* beta, void* y,
                                      float* mean, float* rstd, int64_t rows, int64_t cols,
                                      int dtype, float eps, void* stream) {

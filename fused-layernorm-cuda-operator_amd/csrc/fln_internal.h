@@ -35,6 +35,7 @@ struct BwdParams {
   const float* mean;  // LayerNorm only
   const float* rstd;
   const void* gamma;  // or nullptr (treated as ones)
+  const void* beta;   // LayerNorm + GELU only: the affine shift GELU was applied after
   const void* dres;   // gradient added into dx, or nullptr
   void* dx;           // or nullptr
   float* part_g;      // [blocks, cols] stage-1 partial of sum(dy * xhat), or nullptr
@@ -43,8 +44,9 @@ struct BwdParams {
   int64_t cols;
   int64_t rows_per_block;
   int rms;
-  int wpr;  // waves per row
-  int rgs;  // row groups per block
+  int gelu;  // 0, or the GELU form (1 erf, 2 tanh) applied after the LayerNorm affine step
+  int wpr;   // waves per row
+  int rgs;   // row groups per block
 };
 
 int element_size(int dtype);

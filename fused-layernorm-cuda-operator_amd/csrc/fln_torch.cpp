@@ -125,10 +125,38 @@ Tensor layernorm(const Tensor& input, const OptT& gamma, const OptT& beta, doubl
 // Reference `layernorm_gelu(input, gamma, beta, epsilon)` (csrc/bindings.cpp:30-39), whose GELU
 // is the tanh form (csrc/layernorm_cuda_kernel.cu:31-36): that is the default here;
 // approximate="none" selects the exact erf form.
-Tensor layer_norm_gelu_fwd(const Tensor& input, const OptT& gamma, const OptT& beta, double eps,
-                           const std::string& approximate) {
+int gelu_code(const std::string& approximate) {
   TORCH_CHECK(approximate == "tanh" || approximate == "none",
               "approximate must be 'tanh' or 'none', got '", approximate, "'");
+  return approximate == "tanh" ? FLN_GELU_TANH : FLN_GELU_ERF;
+}
+
+// GELU(LayerNorm(x)) -> (y, mean, rstd): the operator form, whose statistics feed the fused
+// backward below.
+std::tuple<Tensor, Tensor, Tensor> layer_norm_gelu_fwd(const Tensor& input, const OptT& gamma,
+                                                       const OptT& beta, double eps,
+                                                       const std::string& approximate) {
+  const int mode = gelu_code(approximate);
+  const Shape s = check_input(input, "input", true);
+  check_param(gamma, input, s.cols, "gamma");
+  check_param(beta, input, s.cols, "beta");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor y = at::empty_like(input);
+  Tensor mean = stats_like(input, s.rows);
+  Tensor rstd = stats_like(input, s.rows);
+  check(fln_layernorm_gelu_forward(input.data_ptr(), ptr_or_null(gamma), ptr_or_null(beta),
+                                   y.data_ptr(), mean.data_ptr<float>(), rstd.data_ptr<float>(),
+                                   s.rows, s.cols, dtype_code(input), static_cast<float>(eps),
+                                   mode, stream_of(input)),
+        "layer_norm_gelu forward");
+  return {y, mean, rstd};
+}
+
+// Reference `layernorm_gelu` (csrc/bindings.cpp:30-39): output only.
+Tensor layernorm_gelu(const Tensor& input, const OptT& gamma, const OptT& beta, double eps,
+                      const std::string& approximate) {
+  check_affine_pair(gamma, beta);
+  const int mode = gelu_code(approximate);
   const Shape s = check_input(input, "input", true);
   check_param(gamma, input, s.cols, "gamma");
   check_param(beta, input, s.cols, "beta");
@@ -136,17 +164,9 @@ Tensor layer_norm_gelu_fwd(const Tensor& input, const OptT& gamma, const OptT& b
   Tensor y = at::empty_like(input);
   check(fln_layernorm_gelu(input.data_ptr(), ptr_or_null(gamma), ptr_or_null(beta),
                            y.data_ptr(), s.rows, s.cols, dtype_code(input),
-                           static_cast<float>(eps),
-                           approximate == "tanh" ? FLN_GELU_TANH : FLN_GELU_ERF,
-                           stream_of(input)),
+                           static_cast<float>(eps), mode, stream_of(input)),
         "layernorm_gelu");
   return y;
-}
-
-Tensor layernorm_gelu(const Tensor& input, const OptT& gamma, const OptT& beta, double eps,
-                      const std::string& approximate) {
-  check_affine_pair(gamma, beta);
-  return layer_norm_gelu_fwd(input, gamma, beta, eps, approximate);
 }
 
 // Reference `forward(input, gamma, beta, epsilon) -> [out, mean, rstd]`
@@ -363,6 +383,45 @@ std::tuple<Tensor, Tensor, Tensor> layer_norm_bwd(const Tensor& grad_out, const 
   return {dx, dg, db};
 }
 
+std::tuple<Tensor, Tensor, Tensor> layer_norm_gelu_bwd(const Tensor& grad_out,
+                                                       const Tensor& input, const Tensor& mean,
+                                                       const Tensor& rstd, const OptT& gamma,
+                                                       const OptT& beta,
+                                                       const std::string& approximate,
+                                                       std::array<bool, 3> output_mask) {
+  const int mode = gelu_code(approximate);
+  const Shape s = check_input(input, "input", false);
+  check_input(grad_out, "grad_output", false);
+  TORCH_CHECK(grad_out.sizes() == input.sizes(), "grad_output shape must match input shape");
+  TORCH_CHECK(grad_out.scalar_type() == input.scalar_type(),
+              "grad_output dtype must match input dtype");
+  check_stats(mean, s.rows, input, "mean");
+  check_stats(rstd, s.rows, input, "rstd");
+  check_param(gamma, input, s.cols, "gamma");
+  check_param(beta, input, s.cols, "beta");
+  c10::hip::HIPGuard guard(input.device().index());
+  const bool want_dx = output_mask[0];
+  const bool want_dg = output_mask[1] && has(gamma);
+  const bool want_db = output_mask[2] && has(beta);
+  Tensor dx = want_dx ? at::empty_like(input) : at::empty({0}, input.options());
+  Tensor dg = want_dg ? at::empty_like(*gamma) : at::empty({0}, input.options());
+  Tensor db = want_db ? at::empty_like(*beta) : at::empty({0}, input.options());
+  Tensor ws;
+  if (want_dg || want_db) ws = workspace_for(input, s.rows, s.cols);
+  check(fln_layernorm_gelu_backward(grad_out.data_ptr(), input.data_ptr(),
+                                    mean.data_ptr<float>(), rstd.data_ptr<float>(),
+                                    ptr_or_null(gamma), ptr_or_null(beta),
+                                    want_dx ? dx.data_ptr() : nullptr,
+                                    want_dg ? dg.data_ptr() : nullptr,
+                                    want_db ? db.data_ptr() : nullptr, s.rows, s.cols,
+                                    dtype_code(input), dtype_code(input), mode,
+                                    ws.defined() ? ws.data_ptr() : nullptr,
+                                    ws.defined() ? static_cast<size_t>(ws.numel()) * 4 : 0,
+                                    stream_of(input)),
+        "layer_norm_gelu backward");
+  return {dx, dg, db};
+}
+
 // Reference `backward(grad_output, input, mean, rstd, gamma, beta, output_mask)`
 // (csrc/layernorm_cuda.cpp:97-141, :208-216).
 std::vector<std::optional<Tensor>> backward(const Tensor& grad_out, const Tensor& input,
@@ -435,7 +494,10 @@ TORCH_LIBRARY(fused_layernorm, m) {
         "Tensor? weight, Tensor? bias, bool[3] output_mask, Tensor? grad_extra) "
         "-> (Tensor, Tensor, Tensor)");
   m.def("layer_norm_gelu_fwd(Tensor input, Tensor? weight, Tensor? bias, float eps, "
-        "str approximate) -> Tensor");
+        "str approximate) -> (Tensor, Tensor, Tensor)");
+  m.def("layer_norm_gelu_bwd(Tensor grad_out, Tensor input, Tensor mean, Tensor rstd, "
+        "Tensor? weight, Tensor? bias, str approximate, bool[3] output_mask) "
+        "-> (Tensor, Tensor, Tensor)");
   m.def("rms_norm_fwd(Tensor input, Tensor? weight, float eps) -> (Tensor, Tensor)");
   m.def("rms_norm_bwd(Tensor grad_out, Tensor input, Tensor rstd, Tensor? weight, "
         "bool[2] output_mask, Tensor? grad_extra) -> (Tensor, Tensor)");
@@ -457,6 +519,7 @@ TORCH_LIBRARY_IMPL(fused_layernorm, CUDA, m) {
   m.impl("layer_norm_fwd", &layer_norm_fwd);
   m.impl("layer_norm_bwd", &layer_norm_bwd);
   m.impl("layer_norm_gelu_fwd", &layer_norm_gelu_fwd);
+  m.impl("layer_norm_gelu_bwd", &layer_norm_gelu_bwd);
   m.impl("rms_norm_fwd", &rms_norm_fwd);
   m.impl("rms_norm_bwd", &rms_norm_bwd);
   m.impl("add_layer_norm_fwd", &add_layer_norm_fwd);

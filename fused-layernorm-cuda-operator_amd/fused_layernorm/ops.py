@@ -52,7 +52,14 @@ def _ln_bwd_fake(grad_out, input, mean, rstd, weight, bias, output_mask, grad_ex
 
 @torch.library.register_fake("fused_layernorm::layer_norm_gelu_fwd")
 def _ln_gelu_fake(input, weight, bias, eps, approximate):
-    return torch.empty_like(input)
+    st = _stat_shape(input)
+    return (torch.empty_like(input), input.new_empty(st, dtype=torch.float32),
+            input.new_empty(st, dtype=torch.float32))
+
+
+@torch.library.register_fake("fused_layernorm::layer_norm_gelu_bwd")
+def _ln_gelu_bwd_fake(grad_out, input, mean, rstd, weight, bias, approximate, output_mask):
+    return _ln_bwd_fake(grad_out, input, mean, rstd, weight, bias, output_mask, None)
 
 
 @torch.library.register_fake("fused_layernorm::rms_norm_fwd")
@@ -143,6 +150,29 @@ def _rms_backward(ctx, gy, _grstd):
 
 torch.library.register_autograd("fused_layernorm::rms_norm_fwd", _rms_backward,
                                 setup_context=_rms_setup)
+
+
+def _ln_gelu_setup(ctx, inputs, output):
+    input, weight, bias, _eps, approximate = inputs
+    _, mean, rstd = output
+    ctx.save_for_backward(input, weight, bias, mean, rstd)
+    ctx.approximate = approximate
+    ctx.mark_non_differentiable(mean, rstd)
+
+
+def _ln_gelu_backward(ctx, gy, _gmean, _grstd):
+    input, weight, bias, mean, rstd = ctx.saved_tensors
+    mask = [bool(ctx.needs_input_grad[0]),
+            weight is not None and bool(ctx.needs_input_grad[1]),
+            bias is not None and bool(ctx.needs_input_grad[2])]
+    dx, dw, db = _ops.layer_norm_gelu_bwd(gy.contiguous(), input, mean, rstd, weight, bias,
+                                          ctx.approximate, mask)
+    return (dx if mask[0] else None, dw if mask[1] else None, db if mask[2] else None, None,
+            None)
+
+
+torch.library.register_autograd("fused_layernorm::layer_norm_gelu_fwd", _ln_gelu_backward,
+                                setup_context=_ln_gelu_setup)
 
 
 def _add_ln_setup(ctx, inputs, output):
@@ -253,9 +283,11 @@ def layer_norm_gelu(input: torch.Tensor, normalized_shape: ShapeLike,
                     weight: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
                     eps: float = 1e-5, approximate: str = "tanh") -> torch.Tensor:
     """GELU(LayerNorm(x)); approximate='tanh' is the reference's fused GELU, 'none' the exact
-    erf form (forward only)."""
+    erf form.  Differentiable: the backward recomputes the GELU input from the saved row
+    statistics and folds GELU' into the fused LayerNorm backward."""
     x, _ = _flatten(input, normalized_shape)
-    y = _ops.layer_norm_gelu_fwd(x, _flat_param(weight), _flat_param(bias), eps, approximate)
+    y, _, _ = _ops.layer_norm_gelu_fwd(x, _flat_param(weight), _flat_param(bias), eps,
+                                       approximate)
     return y.view(input.shape)
 
 

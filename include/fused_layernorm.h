@@ -48,6 +48,13 @@ int fln_layernorm(const void* x, const void* gamma, const void* beta, void* y, i
 int fln_layernorm_gelu(const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
                        int64_t cols, int dtype, float eps, int gelu_mode, void* stream);
 
+/* LayerNorm + GELU forward that also writes the row statistics the backward needs (mean and
+ * rstd of x, fp32; either may be NULL).  The reference's layernorm_gelu_cuda
+ * (csrc/layernorm_cuda_kernel.cu:180-206) returns only y; this is its training form. */
+int fln_layernorm_gelu_forward(const void* x, const void* gamma, const void* beta, void* y,
+                               float* mean, float* rstd, int64_t rows, int64_t cols, int dtype,
+                               float eps, int gelu_mode, void* stream);
+
 /* Training forward: y plus fp32 mean[rows] and rstd[rows] (either may be NULL).
  * Replaces `layernorm_forward_cuda` (csrc/layernorm.h:15-22, csrc/layernorm_cuda.cpp:14-21) and
  * `layernorm_forward_cuda_optimized` (csrc/layernorm_cuda_kernel_optimized.cu:171-212), called
@@ -72,6 +79,17 @@ int fln_layernorm_backward(const void* dy, const void* x, const float* mean, con
                            const void* gamma, const void* dres, void* dx, void* dgamma,
                            void* dbeta, int64_t rows, int64_t cols, int dtype, int dparam_dtype,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward of y = GELU(LayerNorm(x) * gamma + beta) (gelu_mode FLN_GELU_ERF or _TANH, as in
+ * the forward): the GELU input is recomputed from mean / rstd / gamma / beta, then
+ * dx, dgamma = sum dy GELU'(a) xhat, dbeta = sum dy GELU'(a) as fln_layernorm_backward (same
+ * workspace, same NULL rules).  No counterpart in the reference (it has no backward for its
+ * fused LayerNorm + GELU). */
+int fln_layernorm_gelu_backward(const void* dy, const void* x, const float* mean,
+                                const float* rstd, const void* gamma, const void* beta, void* dx,
+                                void* dgamma, void* dbeta, int64_t rows, int64_t cols, int dtype,
+                                int dparam_dtype, int gelu_mode, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /* RMSNorm forward: y = x rstd [* weight], rstd = 1/sqrt(mean(x^2) + eps); rstd[rows] optional.
  * No counterpart in the reference (new capability on the same path). */

@@ -16,7 +16,8 @@ __all__ = [
     "layer_norm_fwd", "layer_norm_gelu_fwd", "gelu", "rms_norm_fwd", "round_to_bf16",
     "round_to_f16", "add_layer_norm_fwd", "add_rms_norm_fwd", "layer_norm_bwd", "rms_norm_bwd",
     "fp8_e4m3fn_encode", "fp8_e4m3fn_decode", "layer_norm_fp8_fwd", "rms_norm_fp8_fwd",
-    "add_layer_norm_fp8_fwd", "add_rms_norm_fp8_fwd", "FP8_E4M3FN_MAX",
+    "add_layer_norm_fp8_fwd", "add_rms_norm_fp8_fwd", "gelu_grad", "layer_norm_gelu_bwd",
+    "FP8_E4M3FN_MAX",
 ]
 
 FP8_E4M3FN_MAX = 448.0
@@ -59,6 +60,21 @@ def gelu(v, approximate="none"):
     if approximate == "none":
         from scipy.special import erf
         return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
+    raise ValueError(approximate)
+
+
+def gelu_grad(v, approximate="none"):
+    """d GELU / dv.  'none': Phi(v) + v phi(v); 'tanh': with u = sqrt(2/pi)(v + 0.044715 v^3),
+    t = tanh(u): 0.5 (1 + t) + 0.5 v (1 - t^2) sqrt(2/pi) (1 + 3 * 0.044715 v^2) -- the
+    derivative of the reference's gelu() (csrc/layernorm_cuda_kernel.cu:31-36)."""
+    v = _f64(v)
+    if approximate == "tanh":
+        k0, k1 = np.sqrt(2.0 / np.pi), 0.044715
+        t = np.tanh(k0 * (v + k1 * v ** 3))
+        return 0.5 * (1.0 + t) + 0.5 * v * (1.0 - t * t) * k0 * (1.0 + 3.0 * k1 * v * v)
+    if approximate == "none":
+        from scipy.special import erf
+        return 0.5 * (1.0 + erf(v / np.sqrt(2.0))) + v * np.exp(-0.5 * v * v) / np.sqrt(2 * np.pi)
     raise ValueError(approximate)
 
 
@@ -141,6 +157,14 @@ def layer_norm_bwd(dy, x, gamma=None, eps=1e-5):
     dx = rstd * (g - g.mean(axis=-1, keepdims=True) - xh * (g * xh).mean(axis=-1, keepdims=True))
     red = tuple(range(dy.ndim - 1))
     return dx, (dy * xh).sum(axis=red), dy.sum(axis=red)
+
+
+def layer_norm_gelu_bwd(dy, x, gamma=None, beta=None, eps=1e-5, approximate="tanh"):
+    """Backward of GELU(LayerNorm(x) gamma + beta) -> (dx, dgamma, dbeta): with a the GELU
+    input, the LayerNorm backward (layer_norm_bwd) of the upstream gradient dy GELU'(a).  No
+    reference code (the reference has no backward for its fused LayerNorm + GELU)."""
+    y, _, _ = layer_norm_fwd(x, gamma, beta, eps)
+    return layer_norm_bwd(_f64(dy) * gelu_grad(y, approximate), x, gamma, eps)
 
 
 def rms_norm_bwd(dy, x, weight=None, eps=1e-6):

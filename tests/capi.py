@@ -28,6 +28,10 @@ SIGNATURES = {
     "fln_layernorm": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _vp], _i32),
     "fln_layernorm_gelu": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _i32, _vp], _i32),
     "fln_layernorm_forward": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _vp], _i32),
+    "fln_layernorm_gelu_forward": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _i32,
+                                    _vp], _i32),
+    "fln_layernorm_gelu_backward": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                     _i32, _i32, _i32, _vp, _sz, _vp], _i32),
     "fln_backward_workspace_bytes": ([_i64, _i64, _i32], _sz),
     "fln_layernorm_backward": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32,
                                 _i32, _vp, _sz, _vp], _i32),

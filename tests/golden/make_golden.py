@@ -60,6 +60,18 @@ def main():
                 "gelu_y_erf": F.gelu(ln).numpy(),
                 "gelu_y_tanh": F.gelu(ln, approximate="tanh").numpy()})
 
+    # Backward of GELU(LayerNorm) through autograd (float64), both GELU forms.
+    x = randn((6, 1024), 45, 1.5, 0.2)
+    g = randn((1024,), 46, 0.1, 1.0)
+    b = randn((1024,), 47, 0.2)
+    dy = randn((6, 1024), 48)
+    out.update({"gb_x": x.numpy(), "gb_g": g.numpy(), "gb_b": b.numpy(), "gb_dy": dy.numpy()})
+    for mode in ("none", "tanh"):
+        xd, gd, bd = (t.double().requires_grad_(True) for t in (x, g, b))
+        F.gelu(F.layer_norm(xd, (1024,), gd, bd, 1e-5), approximate=mode).backward(dy.double())
+        out.update({f"gb_{mode}_dx": xd.grad.numpy(), f"gb_{mode}_dg": gd.grad.numpy(),
+                    f"gb_{mode}_db": bd.grad.numpy()})
+
     # RMSNorm forward.
     for i, (rows, cols) in enumerate([(5, 96), (3, 4096)]):
         x = randn((rows, cols), 50 + i, 2.0, 0.3)

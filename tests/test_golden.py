@@ -67,6 +67,15 @@ def test_oracle_layer_norm_gelu(gold):
         close_f32(y, gold[key], what=mode)
 
 
+@pytest.mark.parametrize("mode", ["none", "tanh"])
+def test_oracle_layer_norm_gelu_backward(gold, mode):
+    dx, dg, db = norms.layer_norm_gelu_bwd(gold["gb_dy"], gold["gb_x"], gold["gb_g"],
+                                           gold["gb_b"], 1e-5, mode)
+    close_f32(dx, gold[f"gb_{mode}_dx"], 1e-6, what="dx")
+    close_f32(dg, gold[f"gb_{mode}_dg"], 1e-6, what="dgamma")
+    close_f32(db, gold[f"gb_{mode}_db"], 1e-6, what="dbeta")
+
+
 @pytest.mark.parametrize("i", [0, 1])
 def test_oracle_rms_norm_forward(gold, i):
     k = f"rms{i}"
@@ -240,3 +249,29 @@ def test_gpu_residual_rms_fp8(lib, gold):
     assert np.array_equal(to_np(h), bf16_from_bits(gold["arf_h_bf16"])), "h bit-exact"
     assert_fp8_close(q.cpu().numpy(), to_np(s), gold["arf_q"], gold["arf_scale"],
                      "gpu residual rms fp8")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["none", "tanh"])
+def test_gpu_layer_norm_gelu_backward_fp32(lib, gold, mode):
+    from gpu_calls import workspace
+    x, g, b, dy = (dev(gold[f"gb_{n}"]) for n in ("x", "g", "b", "dy"))
+    rows, cols = x.shape
+    gm = capi.GELU_ERF if mode == "none" else capi.GELU_TANH
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    capi.check(lib.fln_layernorm_gelu_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y),
+                                              capi.ptr(mean), capi.ptr(rstd), rows, cols,
+                                              capi.F32, 1e-5, gm, capi.stream()))
+    dx, dg, db = torch.empty_like(x), torch.empty_like(g), torch.empty_like(b)
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_layernorm_gelu_backward(
+        capi.ptr(dy), capi.ptr(x), capi.ptr(mean), capi.ptr(rstd), capi.ptr(g), capi.ptr(b),
+        capi.ptr(dx), capi.ptr(dg), capi.ptr(db), rows, cols, capi.F32, capi.F32, gm,
+        capi.ptr(ws), n, capi.stream()))
+    ref = gold[f"gb_{mode}_dx"].astype(np.float64)
+    # fp32 gradients: dx elementwise 1e-4 relative + 1e-5 * max|dx|; column sums 1e-4 max-norm.
+    assert (np.abs(to_np(dx) - ref) <= 1e-4 * np.abs(ref) + 1e-5 * np.abs(ref).max()).all()
+    assert_close_rel(to_np(dg), gold[f"gb_{mode}_dg"], 1e-4, "dgamma")
+    assert_close_rel(to_np(db), gold[f"gb_{mode}_db"], 1e-4, "dbeta")

@@ -426,6 +426,61 @@ def test_fp8_variants_reject_bad_arguments(lib):
                                        capi.stream()) == 1
 
 
+@pytest.mark.parametrize("mode", ["none", "tanh"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (17, 1023), (33, 7168), (2, 16384), (300, 768)])
+def test_layernorm_gelu_backward_matrix(lib, mode, dtype, rows, cols):
+    """Backward of GELU(LayerNorm(x) gamma + beta): the forward with statistics, then the fused
+    backward, against the numpy oracle (LayerNorm backward of dy GELU'(a))."""
+    gen = torch.Generator().manual_seed(rows * 7 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.2 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, b, dy = cuda(xc), cuda(gc), cuda(bc), cuda(dyc)
+    gm = capi.GELU_ERF if mode == "none" else capi.GELU_TANH
+    code = capi.dtype_code(x)
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    p = capi.ptr
+    capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
+                                              cols, code, 1e-5, gm, capi.stream()))
+    dx = torch.empty_like(x)
+    dg = torch.empty(cols, device="cuda")
+    db = torch.empty(cols, device="cuda")
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b), p(dx),
+                                               p(dg), p(db), rows, cols, code, capi.F32, gm,
+                                               p(ws), n, capi.stream()))
+    xs, gs, bs, dys = f32(xc), f32(gc), f32(bc), f32(dyc)
+    y_ref = norms.layer_norm_gelu_fwd(xs, gs, bs, 1e-5, mode)
+    dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, mode)
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        kind = "bf16" if dtype == torch.bfloat16 else "f16"
+        # GELU(a) near a = 0 inherits the affine rounding allowance of a (slope 1/2 there)
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5), kind=kind,
+                          what="y")
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          kind=kind, what="dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+
+
+def test_layernorm_gelu_entry_points_reject_bad_mode(lib):
+    x = torch.randn(4, 64, device="cuda")
+    p = capi.ptr
+    y = torch.empty_like(x)
+    assert lib.fln_layernorm_gelu_forward(p(x), None, None, p(y), None, None, 4, 64, capi.F32,
+                                          1e-5, 0, capi.stream()) == 1
+    assert lib.fln_layernorm_gelu_backward(p(x), p(x), p(x), p(x), None, None, p(y), None, None,
+                                           4, 64, capi.F32, capi.F32, 3, None, 0,
+                                           capi.stream()) == 1
+
+
 def test_residual_gradient_is_added(lib):
     gen = torch.Generator().manual_seed(9)
     xc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)

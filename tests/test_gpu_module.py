@@ -276,6 +276,22 @@ def test_binding_forward_without_affine_and_utilities():
     assert isinstance(fused_layernorm_cuda.get_performance_hints(32, 768), str)
 
 
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_layer_norm_gelu_autograd(approximate):
+    x = torch.randn(96, 2048, device=DEV, requires_grad=True)
+    w = (1 + 0.1 * torch.randn(2048, device=DEV)).requires_grad_(True)
+    b = (0.2 * torch.randn(2048, device=DEV)).requires_grad_(True)
+    dy = torch.randn(96, 2048, device=DEV)
+    y = fl.layer_norm_gelu(x, (2048,), w, b, 1e-5, approximate=approximate)
+    y.backward(dy)
+    xd, wd, bd = (t.detach().double().cpu().requires_grad_(True) for t in (x, w, b))
+    yr = F.gelu(F.layer_norm(xd, (2048,), wd, bd, 1e-5), approximate=approximate)
+    yr.backward(dy.double().cpu())
+    assert np.abs(to_np(y) - yr.detach().numpy()).max() <= 1e-5
+    for got, ref in ((x.grad, xd.grad), (w.grad, wd.grad), (b.grad, bd.grad)):
+        torch.testing.assert_close(got.double().cpu(), ref, rtol=1e-4, atol=1e-4)
+
+
 # ------------------------------------------------------------------------------------------------
 # New operators on the same kernels: RMSNorm, residual add, fp8.
 # ------------------------------------------------------------------------------------------------
@@ -406,9 +422,10 @@ def test_torch_compile_matches_eager():
                                     torch.randn(8, 256, device=DEV, requires_grad=True),
                                     torch.randn(256, device=DEV), torch.randn(256, device=DEV),
                                     1e-5)),
-    ("layer_norm_gelu_fwd", lambda: (torch.randn(8, 256, device=DEV),
-                                     torch.randn(256, device=DEV),
-                                     torch.randn(256, device=DEV), 1e-5, "tanh")),
+    ("layer_norm_gelu_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
+                                     torch.randn(256, device=DEV, requires_grad=True),
+                                     torch.randn(256, device=DEV, requires_grad=True), 1e-5,
+                                     "tanh")),
     ("add_rms_norm_fp8_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
                                       torch.randn(8, 256, device=DEV, requires_grad=True),
                                       torch.randn(256, device=DEV), 1e-6)),

@@ -80,6 +80,22 @@ def test_gelu_matches_torch_and_reference_formula(rng):
     np.testing.assert_allclose(norms.gelu(np.array([40.0, -40.0]), "none"), [40.0, 0.0])
 
 
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_gelu_grad_and_layer_norm_gelu_backward_match_autograd(rng, approximate):
+    v = t64(rng.randn(5000) * 4).requires_grad_(True)
+    F.gelu(v, approximate=approximate).sum().backward()
+    np.testing.assert_allclose(norms.gelu_grad(v.detach().numpy(), approximate), v.grad.numpy(),
+                               rtol=1e-12, atol=1e-14)
+    x = rng.randn(6, 300) * 2 + 0.3
+    g, b, dy = 1 + 0.1 * rng.randn(300), 0.2 * rng.randn(300), rng.randn(6, 300)
+    xt, gt, bt = (t64(a).requires_grad_(True) for a in (x, g, b))
+    F.gelu(F.layer_norm(xt, (300,), gt, bt, 1e-5), approximate=approximate).backward(t64(dy))
+    dx, dg, db = norms.layer_norm_gelu_bwd(dy, x, g, b, 1e-5, approximate)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dg, gt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(db, bt.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
 def test_layer_norm_gelu_composition(rng):
     x, g, b = rng.randn(5, 64), 1 + 0.1 * rng.randn(64), 0.1 * rng.randn(64)
     y = norms.layer_norm_gelu_fwd(x, g, b, 1e-5, "none")
