@@ -7,7 +7,8 @@ variants, all running hand-written HIP kernels.  Importing requires the built ex
 (``python build.py`` next to this package); there is no silent fallback.
 """
 from .layernorm import (FusedLayerNorm, FusedLayerNormFunction, FusedRMSNorm, fused_layer_norm,
-                        fused_rms_norm, replace_torch_layernorm, restore_torch_layernorm)
+                        fused_rms_norm, replace_layernorm_modules, replace_torch_layernorm,
+                        restore_torch_layernorm)
 from .ops import (add_layer_norm, add_layer_norm_fp8, add_rms_norm, add_rms_norm_fp8,
                   layer_norm, layer_norm_fp8, layer_norm_gelu, rms_norm, rms_norm_fp8)
 from . import functional
@@ -20,6 +21,7 @@ __all__ = [
     "fused_layer_norm",
     "replace_torch_layernorm",
     "restore_torch_layernorm",
+    "replace_layernorm_modules",
     "FusedRMSNorm",
     "fused_rms_norm",
     "layer_norm",

@@ -207,6 +207,40 @@ def fused_rms_norm(input: torch.Tensor, normalized_shape, weight: Optional[torch
     return _fops.rms_norm(input, normalized_shape, weight, eps)
 
 
+def _fused_like(child: nn.Module) -> Optional[nn.Module]:
+    """A fused module computing what `child` computes, sharing its Parameter objects."""
+    if isinstance(child, nn.LayerNorm) and not isinstance(child, FusedLayerNorm):
+        fused = FusedLayerNorm(child.normalized_shape, eps=child.eps,
+                               elementwise_affine=False)
+        fused.elementwise_affine = child.elementwise_affine
+        fused.weight, fused.bias = child.weight, child.bias
+        return fused
+    rms_cls = getattr(nn, "RMSNorm", None)
+    if rms_cls is not None and isinstance(child, rms_cls) and not isinstance(child, FusedRMSNorm):
+        fused = FusedRMSNorm(child.normalized_shape, eps=child.eps, elementwise_affine=False)
+        fused.elementwise_affine = child.elementwise_affine
+        fused.weight = child.weight
+        return fused
+    return None
+
+
+def replace_layernorm_modules(module: nn.Module) -> nn.Module:
+    """Swap every nn.LayerNorm (and nn.RMSNorm) inside `module` for FusedLayerNorm
+    (FusedRMSNorm) in place, sharing the same Parameter objects (optimizer state, state_dict
+    keys and tying are unchanged); returns `module`.
+
+    This is the working form of the reference README's replace_layernorm (README.md:103-122),
+    whose setattr of a lambda onto an nn.Module child raises TypeError and whose lambda would
+    hand 3-D activations to a kernel that reads only size(0) / size(1)."""
+    for name, child in list(module.named_children()):
+        fused = _fused_like(child)
+        if fused is not None:
+            setattr(module, name, fused)
+        else:
+            replace_layernorm_modules(child)
+    return module
+
+
 def replace_torch_layernorm():
     """Replace torch.nn.LayerNorm with FusedLayerNorm globally (reference layernorm.py:269-273)."""
     torch.nn.LayerNorm = FusedLayerNorm

@@ -527,3 +527,53 @@ def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeyp
             cfg["threads_per_block"]), line
     else:
         assert "-> loop" in line, line
+
+
+# ------------------------------------------------------------------------------------------------
+# Model-level drop-in: module swap inside transformer blocks, eager and torch.compile.
+# ------------------------------------------------------------------------------------------------
+class _TinyLM(nn.Module):
+    def __init__(self, vocab=1000, d=256, layers=2):
+        super().__init__()
+        self.emb = nn.Embedding(vocab, d)
+        self.blocks = nn.ModuleList(
+            nn.TransformerEncoderLayer(d_model=d, nhead=8, dim_feedforward=4 * d, dropout=0.0,
+                                       batch_first=True, norm_first=True)
+            for _ in range(layers))
+        self.norm = nn.LayerNorm(d)
+        self.head = nn.Linear(d, vocab)
+
+    def forward(self, tokens):
+        h = self.emb(tokens)
+        for blk in self.blocks:
+            h = blk(h)
+        return self.head(self.norm(h))
+
+
+@pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
+def test_transformer_logits_and_gradients_after_module_swap(compiled):
+    """End-to-end parity: a transformer whose nn.LayerNorm modules are swapped for the fused
+    ones (replace_layernorm_modules) gives the same logits and parameter gradients as the
+    original (fp32; the norms differ only in summation order, so 1e-4 relative to the largest
+    logit / gradient).  Train mode: torch's eval fast path would call its own fused encoder op
+    and bypass the norm modules."""
+    import copy
+    torch.manual_seed(0)
+    ref = _TinyLM().to(DEV).train()
+    fused = fl.replace_layernorm_modules(copy.deepcopy(ref))
+    assert all(isinstance(b.norm1, fl.FusedLayerNorm) for b in fused.blocks)
+    run = torch.compile(fused, backend="aot_eager") if compiled else fused
+    if compiled:
+        torch._dynamo.reset()
+    tokens = torch.randint(0, 1000, (8, 128), device=DEV)
+    target = torch.randint(0, 1000, (8, 128), device=DEV)
+    logits_ref = ref(tokens)
+    logits = run(tokens)
+    scale = logits_ref.abs().max().item()
+    assert (logits - logits_ref).abs().max().item() <= 1e-4 * scale
+    F.cross_entropy(logits_ref.flatten(0, 1), target.flatten()).backward()
+    F.cross_entropy(logits.flatten(0, 1), target.flatten()).backward()
+    for (name, p_ref), (_, p) in zip(ref.named_parameters(), fused.named_parameters()):
+        g_ref = p_ref.grad
+        tol = 1e-4 * max(g_ref.abs().max().item(), 1e-12)
+        assert (p.grad - g_ref).abs().max().item() <= tol, name

@@ -179,3 +179,19 @@ def test_byte_model_matches_baseline_figures():
     }
     for name, nbytes in expect.items():
         assert algorithmic_bytes(WORKLOADS[name])["total"] == nbytes, name
+
+
+def test_replace_layernorm_modules_swaps_and_shares_parameters():
+    model = torch.nn.Sequential(
+        torch.nn.TransformerEncoderLayer(d_model=64, nhead=4, dim_feedforward=128, dropout=0.0),
+        torch.nn.LayerNorm(64, elementwise_affine=False), torch.nn.RMSNorm(64, eps=1e-6),
+        torch.nn.Linear(64, 10))
+    keys = list(model.state_dict().keys())
+    w1 = model[0].norm1.weight
+    fl.replace_layernorm_modules(model)
+    assert isinstance(model[0].norm1, fl.FusedLayerNorm)
+    assert isinstance(model[0].norm2, fl.FusedLayerNorm)
+    assert isinstance(model[1], fl.FusedLayerNorm) and model[1].weight is None
+    assert isinstance(model[2], fl.FusedRMSNorm) and model[2].eps == 1e-6
+    assert model[0].norm1.weight is w1  # the same Parameter object
+    assert list(model.state_dict().keys()) == keys
