@@ -3,9 +3,10 @@
 Default workload (the headline metric): LayerNorm forward + backward, bf16, 8192 x 4096 -- one
 "step" is the forward (y, mean, rstd) plus the backward (dx, dgamma, dbeta) over one batch, with
 inputs already resident in HBM.  The RMSNorm forward + backward at the same shape is timed the
-same way and reported under "rms_fwd_bwd"; the benchmark configurations C1..C5, C6 (residual
-add + RMSNorm -> fp8 at C5's shape) and LayerNorm + GELU forward + backward at the headline
-shape are timed under "configs" (latency for the small ones, GB/s for the large ones).
+same way and reported under "rms_fwd_bwd"; the benchmark configurations C1..C5, C6 / C7
+(residual add + RMSNorm -> fp8 with per-row / OCP MX block scales at C5's shape) and LayerNorm +
+GELU forward + backward at the headline shape are timed under "configs" (latency for the small
+ones, GB/s for the large ones).
 
 The kernels are called through the C ABI (libfln.so) on torch's current HIP stream, with every
 output preallocated.  Inputs and outputs rotate over at least 4 buffer sets (>= 2 GiB in all,
@@ -49,7 +50,7 @@ CALIBRATION_COPY_BYTES = 256 * 2 ** 20
 CONFIGS = ("c1_ln_fwd_fp32_32x768", "c2_ln_gelu_fp32_17x1023", "c2_ln_gelu_fp32_64x4096",
            "c3_add_ln_fwd_bf16_8192x4096", "c4_rms_fwd_bwd_bf16_16384x8192",
            "c5_ln_fp8_bf16_32768x7168", "c6_add_rms_fp8_bf16_32768x7168",
-           "ln_gelu_fwd_bwd_bf16_8192x4096")
+           "c7_add_rms_mxfp8_bf16_32768x7168", "ln_gelu_fwd_bwd_bf16_8192x4096")
 
 
 def parse():
@@ -60,7 +61,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes (roofline.traffic = null)")
-    ap.add_argument("--no-configs", action="store_true", help="skip the C1..C6 timings")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1..C7 timings")
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the LayerNorm headline (no RMSNorm line, no configs); "
                          "used for per-kernel profiles")
@@ -89,8 +90,11 @@ class Runner:
             if k > 0:  # distinct buffers, same values
                 s = {n: t.clone() for n, t in s.items()}
             s["y"] = torch.empty_like(s["x"])
-            if w.op in ("add_layer_norm", "add_rms_norm_fp8"):
+            if w.op in ("add_layer_norm", "add_rms_norm_fp8", "add_rms_norm_mxfp8"):
                 s["h"] = torch.empty_like(s["x"])
+            if w.op == "add_rms_norm_mxfp8":
+                s["q"] = torch.empty(s["x"].shape, device=dev, dtype=torch.uint8)
+                s["bscale"] = torch.empty(w.rows, w.cols // 32, device=dev, dtype=torch.uint8)
             if w.op in ("layer_norm_fp8", "add_rms_norm_fp8"):
                 s["q"] = torch.empty(s["x"].shape, device=dev, dtype=torch.uint8)
                 s["scale"] = torch.empty(w.rows, device=dev)
@@ -118,6 +122,10 @@ class Runner:
             rc = self.lib.fln_add_rmsnorm_fp8_forward(
                 p(s["x"]), p(s["residual"]), p(s.get("gamma")), p(s["h"]), p(s["q"]),
                 p(s["scale"]), None, self.rows, self.cols, self.code, self.w.eps, stream)
+        elif self.w.op == "add_rms_norm_mxfp8":
+            rc = self.lib.fln_add_rmsnorm_mxfp8_forward(
+                p(s["x"]), p(s["residual"]), p(s.get("gamma")), p(s["h"]), p(s["q"]),
+                p(s["bscale"]), None, self.rows, self.cols, self.code, self.w.eps, stream)
         elif self.w.op == "layer_norm_fp8":
             rc = self.lib.fln_layernorm_fp8_forward(
                 p(s["x"]), p(s.get("gamma")), p(s.get("beta")), p(s["q"]), p(s["scale"]), None,

@@ -266,6 +266,32 @@ __device__ __forceinline__ uint32_t fp8x4_inrange(float a, float b, float c, flo
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return static_cast<uint32_t>(w);
 }
+// OCP MX (Microscaling v1.0) block scale for E4M3 elements: for a block maximum m, the shared
+// exponent is floor(log2 m) - 8 (8 = emax of E4M3), clamped to [-127, 127]; the E8M0 code is
+// exponent + 127 (2^(code - 127)); elements are v * 2^-exponent, saturated to +-448.  A zero
+// (or subnormal) maximum gives code 0.
+struct MxScale {
+  int code;     // E8M0 byte
+  float mul;    // 2^-exponent (exact)
+};
+__device__ __forceinline__ MxScale mx_scale_e4m3(float block_max) {
+  const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, block_max) >> 23) & 0xFF) - 127;
+  const int e = e_max - 8 < -127 ? -127 : e_max - 8;  // e <= 119 for finite maxima
+  return {e + 127, __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23)};
+}
+
+// Max over aligned groups of G adjacent lanes (G = 2 ... 32), result in every lane of the
+// group.  All lanes of each group must be active.
+template <int G> __device__ __forceinline__ float group_max(float v) {
+  static_assert(G >= 2 && G <= 32 && (G & (G - 1)) == 0, "group of 2..32 lanes");
+  v = fmaxf(v, dpp<0xB1>(v));                        // lane ^ 1
+  if constexpr (G >= 4) v = fmaxf(v, dpp<0x4E>(v));   // lane ^ 2
+  if constexpr (G >= 8) v = fmaxf(v, dpp<0x141>(v));  // mirror within 8
+  if constexpr (G >= 16) v = fmaxf(v, dpp<0x140>(v)); // mirror within 16
+  if constexpr (G >= 32) v = fmaxf(v, swz_xor16(v));  // lane ^ 16
+  return v;
+}
+
 __device__ __forceinline__ uint8_t fp8x1(float a) {
   return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), 0.0f, 0, false) & 0xFF);
 }

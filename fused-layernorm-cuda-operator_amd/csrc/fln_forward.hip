@@ -41,7 +41,8 @@ int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s) {
   if (p.rows == 0 || p.cols == 0) return FLN_OK;
   if (!p.x || !p.y) return FLN_ERR_INVALID;
   if (p.res == nullptr && p.h != nullptr) return FLN_ERR_INVALID;
-  if (out_fp8 && !p.scale) return FLN_ERR_INVALID;
+  if (out_fp8 && !p.mx && !p.scale) return FLN_ERR_INVALID;
+  if (out_fp8 && p.mx && (!p.bscale || p.cols % 32 != 0)) return FLN_ERR_INVALID;
   if (p.rms && p.beta) return FLN_ERR_INVALID;
   switch (dtype) {
     case FLN_F32: return launch_forward_f32(p, out_fp8, s);
@@ -166,6 +167,38 @@ extern "C" int fln_add_rmsnorm_fp8_forward(const void* x, const void* residual,
   FwdParams p{};
   p.x = x; p.res = residual; p.gamma = weight; p.h = h; p.y = q; p.scale = scale;
   p.rstd = rstd; p.rows = rows; p.cols = cols; p.eps = eps; p.rms = 1;
+  return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fln_layernorm_mxfp8_forward(const void* x, const void* gamma, const void* beta,
+                                           uint8_t* q, uint8_t* block_scale, float* mean,
+                                           float* rstd, int64_t rows, int64_t cols, int dtype,
+                                           float eps, void* stream) {
+  if (dtype == FLN_F64) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.gamma = gamma; p.beta = beta; p.y = q; p.bscale = block_scale; p.mx = 1;
+  p.mean = mean; p.rstd = rstd; p.rows = rows; p.cols = cols; p.eps = eps;
+  return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fln_rmsnorm_mxfp8_forward(const void* x, const void* weight, uint8_t* q,
+                                         uint8_t* block_scale, float* rstd, int64_t rows,
+                                         int64_t cols, int dtype, float eps, void* stream) {
+  if (dtype == FLN_F64) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.gamma = weight; p.y = q; p.bscale = block_scale; p.mx = 1; p.rstd = rstd;
+  p.rows = rows; p.cols = cols; p.eps = eps; p.rms = 1;
+  return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fln_add_rmsnorm_mxfp8_forward(const void* x, const void* residual,
+                                             const void* weight, void* h, uint8_t* q,
+                                             uint8_t* block_scale, float* rstd, int64_t rows,
+                                             int64_t cols, int dtype, float eps, void* stream) {
+  if (dtype == FLN_F64 || !residual) return FLN_ERR_INVALID;
+  FwdParams p{};
+  p.x = x; p.res = residual; p.gamma = weight; p.h = h; p.y = q; p.bscale = block_scale;
+  p.mx = 1; p.rstd = rstd; p.rows = rows; p.cols = cols; p.eps = eps; p.rms = 1;
   return fln::launch_forward(p, dtype, true, static_cast<hipStream_t>(stream));
 }
 

@@ -3,6 +3,7 @@
 
 namespace fln {
 int launch_forward_f32(const FwdParams& p, bool out_fp8, hipStream_t s) {
-  return out_fp8 ? detail::dispatch_typed<float, true>(p, s) : detail::dispatch_typed<float, false>(p, s);
+  if (!out_fp8) return detail::dispatch_typed<float, 0>(p, s);
+  return p.mx ? detail::dispatch_typed<float, 2>(p, s) : detail::dispatch_typed<float, 1>(p, s);
 }
 }  // namespace fln

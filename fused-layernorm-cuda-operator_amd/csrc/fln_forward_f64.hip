@@ -3,6 +3,6 @@
 
 namespace fln {
 int launch_forward_f64(const FwdParams& p, hipStream_t s) {
-  return detail::launch_loop<double, double, false>(p, s);
+  return detail::launch_loop<double, double, 0>(p, s);
 }
 }  // namespace fln

@@ -64,7 +64,7 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 #ifndef FLN_FWD_STORE_POL
 #define FLN_FWD_STORE_POL kStream
 #endif
-template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
+template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
   constexpr int PD = FLN_FWD_PREFETCH;  // rows in flight ahead of the current one
   constexpr int MAXW = MAXT / kWave;
@@ -211,12 +211,35 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     P yo[VPL];
     QW qo[VPL];
     P ho[VPL];
+    int mxc[FP8 == 2 ? VPL : 1];  // E8M0 codes of the lane's blocks (MX)
     float scale = 0.0f;
-    if constexpr (!FP8) {
+    if constexpr (FP8 == 0) {
 #pragma unroll
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) yo[i].v[e] = from_f32<T>(xf[i][e]);
+    } else if constexpr (FP8 == 2) {
+      // OCP MX: each 32-element block is G adjacent lanes' vectors; its maximum needs only
+      // DPP steps within the group (blocks never straddle the row end: cols % 32 == 0).
+      constexpr int G = 32 / VEC;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float bm = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(xf[i][e]));
+        const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+        const float* a = xf[i];
+        const float m = ms.mul;  // |a * m| < 512: the saturating conversion clamps to 448
+        if constexpr (VEC == 8) {
+          qo[i].x = fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
+          qo[i].y = fp8x4(a[4] * m, a[5] * m, a[6] * m, a[7] * m);
+        } else if constexpr (VEC == 4) {
+          qo[i] = fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
+        } else {
+          qo[i] = fp8x1(a[0] * m);
+        }
+        mxc[i] = ms.code;
+      }
     } else {
       float am = 0.0f;
 #pragma unroll
@@ -267,12 +290,25 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 #pragma unroll
       for (int i = 0; i < VPL; ++i) buf_store<P, FLN_FWD_STORE_POL>(ho[i], hr, t + i * tpr);
     }
-    if constexpr (!FP8) {
+    if constexpr (FP8 == 0) {
       const rsrc_t yr = make_rsrc(static_cast<T*>(p.y) + row * N, nb);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) buf_store<P, FLN_FWD_STORE_POL>(yo[i], yr, t + i * tpr);
     } else {
-      buf_store_f32(scale, make_rsrc(p.scale + row, stat_nb), stat_off);
+      if constexpr (FP8 == 2) {
+        // One E8M0 byte per block, stored by the block's first lane.
+        constexpr int G = 32 / VEC;
+        const uint32_t nblk = static_cast<uint32_t>(N / 32);
+        const rsrc_t br = make_rsrc(p.bscale + row * nblk, nb ? nblk : 0u);
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+          const uint32_t v = static_cast<uint32_t>(t + i * tpr);
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(mxc[i]), br,
+                                               v % G == 0 ? v / G : kOutOfRange, 0, 0);
+        }
+      } else {
+        buf_store_f32(scale, make_rsrc(p.scale + row, stat_nb), stat_off);
+      }
       const rsrc_t qr = make_rsrc(static_cast<uint8_t*>(p.y) + row * N,
                                   nb ? static_cast<uint32_t>(N) : 0u);
 #pragma unroll
@@ -309,7 +345,7 @@ __device__ __forceinline__ A block_allreduce(A v, A* slot) {
   return r;
 }
 
-template <class T, class A, bool FP8>
+template <class T, class A, int FP8>
 __global__ __launch_bounds__(1024) void fwd_loop_kernel(const FwdParams p) {
   __shared__ A red[3][16];
   const int64_t N = p.cols;
@@ -354,10 +390,23 @@ __global__ __launch_bounds__(1024) void fwd_loop_kernel(const FwdParams p) {
       if (b) a += static_cast<A>(b[j]);
       return apply_gelu(a, p.gelu);
     };
-    if constexpr (!FP8) {
+    if constexpr (FP8 == 0) {
       T* y = static_cast<T*>(p.y);
       for (int64_t j = threadIdx.x; j < N; j += blockDim.x) y[base + j] = static_cast<T>(outv(j));
     } else {
+      if (p.mx) {
+        // Blocks of 32 consecutive elements are 32 adjacent lanes here (blockDim is a multiple
+        // of 64 and cols % 32 == 0, so a block's lanes are all in or all past the row).
+        uint8_t* q8 = static_cast<uint8_t*>(p.y);
+        for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
+          const float a = static_cast<float>(outv(j));
+          const MxScale ms = mx_scale_e4m3(group_max<32>(fabsf(a)));
+          q8[base + j] = fp8x1(a * ms.mul);
+          if ((j & 31) == 0) p.bscale[row * (N / 32) + j / 32] = static_cast<uint8_t>(ms.code);
+        }
+        __syncthreads();
+        continue;
+      }
       A am = 0;
       for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
         const A a = outv(j);
@@ -409,7 +458,7 @@ int64_t resident_blocks(K kernel, int threads, int* cache_per_device) {
   return static_cast<int64_t>(cache_per_device[dev]) * device_cu_count();
 }
 
-template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
+template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   const int rows_per_block = threads / (kWave * p.wpr);
   const int64_t row_blocks = (p.rows + rows_per_block - 1) / rows_per_block;
@@ -424,7 +473,7 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT>
+template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT>
 int launch_reg(const FwdParams& p, int threads, hipStream_t s) {
   if (threads <= 256) return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, EXACT, 256>(p, threads, s);
   return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, EXACT, 1024>(p, threads, s);
@@ -435,7 +484,7 @@ int launch_reg(const FwdParams& p, int threads, hipStream_t s) {
 // scalar path.
 template <int VEC> constexpr int max_vpl() { return VEC == 1 ? 16 : 32 / VEC; }
 
-template <class T, bool FP8, bool RES, int GELU, int VEC, int VPL>
+template <class T, int FP8, bool RES, int GELU, int VEC, int VPL>
 int launch_reg_exact(const FwdParams& p, bool exact, int threads, hipStream_t s) {
   // The exact (mask-free) variant is only instantiated for 16-byte vectors.
   if constexpr (VEC > 1)
@@ -443,7 +492,7 @@ int launch_reg_exact(const FwdParams& p, bool exact, int threads, hipStream_t s)
   return launch_reg<T, FP8, RES, GELU, VEC, VPL, false>(p, threads, s);
 }
 
-template <class T, bool FP8, bool RES, int GELU, int VEC>
+template <class T, int FP8, bool RES, int GELU, int VEC>
 int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStream_t s) {
   constexpr int CAP = max_vpl<VEC>();
   switch (vpl) {
@@ -462,11 +511,12 @@ int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStre
   }
 }
 
-// Flavour dispatch: GELU only exists without residual and fp8 output.
-template <class T, bool FP8, int VEC>
+// Flavour dispatch: GELU only exists without residual and fp8 output.  FP8: 0 none, 1 fp8 with
+// a per-row scale, 2 OCP MX fp8 (E8M0 scale per 32 elements).
+template <class T, int FP8, int VEC>
 int launch_reg_flavour(const FwdParams& p, int vpl, bool exact, int threads, hipStream_t s) {
   if (p.res) return launch_reg_vpl<T, FP8, true, 0, VEC>(p, vpl, exact, threads, s);
-  if constexpr (!FP8) {
+  if constexpr (FP8 == 0) {
     if (p.gelu == FLN_GELU_ERF)
       return launch_reg_vpl<T, false, false, 1, VEC>(p, vpl, exact, threads, s);
     if (p.gelu == FLN_GELU_TANH)
@@ -475,7 +525,7 @@ int launch_reg_flavour(const FwdParams& p, int vpl, bool exact, int threads, hip
   return launch_reg_vpl<T, FP8, false, 0, VEC>(p, vpl, exact, threads, s);
 }
 
-template <class T, class A, bool FP8>
+template <class T, class A, int FP8>
 int launch_loop(const FwdParams& p, hipStream_t s) {
   const int threads = p.cols >= 4096 ? 1024 : 256;
   const int64_t grid = p.rows < kMaxGrid ? p.rows : kMaxGrid;
@@ -543,7 +593,7 @@ inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int max_cap
   return g;
 }
 
-template <class T, bool FP8>
+template <class T, int FP8>
 int dispatch_typed(FwdParams p, hipStream_t s) {
   constexpr int VV = 16 / sizeof(T);  // elements per 16-byte vector
   const int64_t N = p.cols;

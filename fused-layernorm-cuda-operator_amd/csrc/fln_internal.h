@@ -19,12 +19,14 @@ struct FwdParams {
   void* h;            // residual sum output, or nullptr
   float* mean;        // [rows] or nullptr
   float* rstd;        // [rows] or nullptr
-  float* scale;       // [rows] fp8 row scales (out_fp8 only)
+  float* scale;       // [rows] fp8 row scales (out_fp8, per-row scaling)
+  uint8_t* bscale;    // [rows, cols / 32] E8M0 block scales (out_fp8 with mx)
   int64_t rows;
   int64_t cols;
   float eps;
   int rms;   // 1: RMSNorm (no centring, no beta)
   int gelu;  // FLN_GELU_*
+  int mx;    // out_fp8: 0 per-row scale, 1 OCP MX blocks of 32 with E8M0 scales
   int wpr;   // waves per row (register path)
 };
 

@@ -332,6 +332,67 @@ std::tuple<Tensor, Tensor, Tensor> add_rms_norm_fp8_fwd(const Tensor& input,
   return {q, scale, h};
 }
 
+// OCP MX fp8 outputs: codes as float8_e4m3fn [rows, cols], block scales as float8_e8m0fnu
+// [rows, cols / 32] (torch's E8M0 type: the byte e + 127 for the scale 2^e).
+Tensor mx_scales_like(const Tensor& input, const Shape& s) {
+  TORCH_CHECK(s.cols % 32 == 0, "MX fp8 output needs the normalized size to be a multiple of 32, "
+              "got ", s.cols);
+  std::vector<int64_t> shape(input.sizes().begin(), input.sizes().end() - 1);
+  shape.push_back(s.cols / 32);
+  return at::empty(shape, input.options().dtype(at::kFloat8_e8m0fnu));
+}
+
+std::tuple<Tensor, Tensor> layer_norm_mxfp8_fwd(const Tensor& input, const OptT& gamma,
+                                                const OptT& beta, double eps) {
+  const Shape s = check_input(input, "input", false);
+  check_param(gamma, input, s.cols, "gamma");
+  check_param(beta, input, s.cols, "beta");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor q = at::empty(input.sizes(), input.options().dtype(at::kFloat8_e4m3fn));
+  Tensor sc = mx_scales_like(input, s);
+  check(fln_layernorm_mxfp8_forward(input.data_ptr(), ptr_or_null(gamma), ptr_or_null(beta),
+                                    static_cast<uint8_t*>(q.data_ptr()),
+                                    static_cast<uint8_t*>(sc.data_ptr()), nullptr, nullptr,
+                                    s.rows, s.cols, dtype_code(input), static_cast<float>(eps),
+                                    stream_of(input)),
+        "layer_norm mxfp8 forward");
+  return {q, sc};
+}
+
+std::tuple<Tensor, Tensor> rms_norm_mxfp8_fwd(const Tensor& input, const OptT& weight,
+                                              double eps) {
+  const Shape s = check_input(input, "input", false);
+  check_param(weight, input, s.cols, "weight");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor q = at::empty(input.sizes(), input.options().dtype(at::kFloat8_e4m3fn));
+  Tensor sc = mx_scales_like(input, s);
+  check(fln_rmsnorm_mxfp8_forward(input.data_ptr(), ptr_or_null(weight),
+                                  static_cast<uint8_t*>(q.data_ptr()),
+                                  static_cast<uint8_t*>(sc.data_ptr()), nullptr, s.rows, s.cols,
+                                  dtype_code(input), static_cast<float>(eps), stream_of(input)),
+        "rms_norm mxfp8 forward");
+  return {q, sc};
+}
+
+std::tuple<Tensor, Tensor, Tensor> add_rms_norm_mxfp8_fwd(const Tensor& input,
+                                                          const Tensor& residual,
+                                                          const OptT& weight, double eps) {
+  const Shape s = check_input(input, "input", false);
+  check_residual(residual, input);
+  check_param(weight, input, s.cols, "weight");
+  c10::hip::HIPGuard guard(input.device().index());
+  Tensor q = at::empty(input.sizes(), input.options().dtype(at::kFloat8_e4m3fn));
+  Tensor sc = mx_scales_like(input, s);
+  Tensor h = at::empty_like(input);
+  check(fln_add_rmsnorm_mxfp8_forward(input.data_ptr(), residual.data_ptr(), ptr_or_null(weight),
+                                      h.data_ptr(), static_cast<uint8_t*>(q.data_ptr()),
+                                      static_cast<uint8_t*>(sc.data_ptr()), nullptr, s.rows,
+                                      s.cols, dtype_code(input), static_cast<float>(eps),
+                                      stream_of(input)),
+        "add_rms_norm mxfp8 forward");
+  return {q, sc, h};
+}
+
 // ------------------------------------------------------------------------------------------
 // Backward family.  Masked-off outputs come back as empty (0-element) tensors through the
 // operator schema and as None through the pybind `backward`.
@@ -512,6 +573,11 @@ TORCH_LIBRARY(fused_layernorm, m) {
         "float eps) -> (Tensor, Tensor, Tensor)");
   m.def("add_rms_norm_fp8_fwd(Tensor input, Tensor residual, Tensor? weight, float eps) "
         "-> (Tensor, Tensor, Tensor)");
+  m.def("layer_norm_mxfp8_fwd(Tensor input, Tensor? weight, Tensor? bias, float eps) "
+        "-> (Tensor, Tensor)");
+  m.def("rms_norm_mxfp8_fwd(Tensor input, Tensor? weight, float eps) -> (Tensor, Tensor)");
+  m.def("add_rms_norm_mxfp8_fwd(Tensor input, Tensor residual, Tensor? weight, float eps) "
+        "-> (Tensor, Tensor, Tensor)");
 }
 
 // GPU tensors of PyTorch-ROCm carry the CUDA dispatch key.
@@ -528,6 +594,9 @@ TORCH_LIBRARY_IMPL(fused_layernorm, CUDA, m) {
   m.impl("rms_norm_fp8_fwd", &rms_norm_fp8_fwd);
   m.impl("add_layer_norm_fp8_fwd", &add_layer_norm_fp8_fwd);
   m.impl("add_rms_norm_fp8_fwd", &add_rms_norm_fp8_fwd);
+  m.impl("layer_norm_mxfp8_fwd", &layer_norm_mxfp8_fwd);
+  m.impl("rms_norm_mxfp8_fwd", &rms_norm_mxfp8_fwd);
+  m.impl("add_rms_norm_mxfp8_fwd", &add_rms_norm_mxfp8_fwd);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -578,6 +647,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("beta") = py::none(), py::arg("eps") = 1e-5);
   m.def("add_rmsnorm_fp8_forward", &add_rms_norm_fp8_fwd,
         "Residual add + RMSNorm with fp8 output -> (codes, per-row scale, residual_sum)",
+        py::arg("input"), py::arg("residual"), py::arg("weight") = py::none(),
+        py::arg("eps") = 1e-6);
+  m.def("layernorm_mxfp8_forward", &layer_norm_mxfp8_fwd,
+        "LayerNorm with OCP MX fp8 (E4M3) output -> (codes, E8M0 block scales)",
+        py::arg("input"), py::arg("gamma") = py::none(), py::arg("beta") = py::none(),
+        py::arg("eps") = 1e-5);
+  m.def("rmsnorm_mxfp8_forward", &rms_norm_mxfp8_fwd,
+        "RMSNorm with OCP MX fp8 (E4M3) output -> (codes, E8M0 block scales)",
+        py::arg("input"), py::arg("weight") = py::none(), py::arg("eps") = 1e-6);
+  m.def("add_rmsnorm_mxfp8_forward", &add_rms_norm_mxfp8_fwd,
+        "Residual add + RMSNorm with OCP MX fp8 output -> (codes, block scales, residual_sum)",
         py::arg("input"), py::arg("residual"), py::arg("weight") = py::none(),
         py::arg("eps") = 1e-6);
   m.attr("__version__") = fln_version();

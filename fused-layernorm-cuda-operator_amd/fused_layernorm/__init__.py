@@ -10,7 +10,8 @@ from .layernorm import (FusedLayerNorm, FusedLayerNormFunction, FusedRMSNorm, fu
                         fused_rms_norm, replace_layernorm_modules, replace_torch_layernorm,
                         restore_torch_layernorm)
 from .ops import (add_layer_norm, add_layer_norm_fp8, add_rms_norm, add_rms_norm_fp8,
-                  layer_norm, layer_norm_fp8, layer_norm_gelu, rms_norm, rms_norm_fp8)
+                  add_rms_norm_mxfp8, layer_norm, layer_norm_fp8, layer_norm_gelu,
+                  layer_norm_mxfp8, rms_norm, rms_norm_fp8, rms_norm_mxfp8)
 from . import functional
 
 __version__ = "1.0.0"
@@ -33,5 +34,8 @@ __all__ = [
     "rms_norm_fp8",
     "add_layer_norm_fp8",
     "add_rms_norm_fp8",
+    "layer_norm_mxfp8",
+    "rms_norm_mxfp8",
+    "add_rms_norm_mxfp8",
     "functional",
 ]

@@ -25,6 +25,7 @@ _ops = torch.ops.fused_layernorm
 __all__ = [
     "layer_norm", "layer_norm_gelu", "rms_norm", "add_layer_norm", "add_rms_norm",
     "layer_norm_fp8", "rms_norm_fp8", "add_layer_norm_fp8", "add_rms_norm_fp8",
+    "layer_norm_mxfp8", "rms_norm_mxfp8", "add_rms_norm_mxfp8",
 ]
 
 
@@ -103,6 +104,28 @@ def _rms_fp8_fake(input, weight, eps):
 def _add_ln_fp8_fake(input, residual, weight, bias, eps):
     return (torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device),
             input.new_empty(_stat_shape(input), dtype=torch.float32), torch.empty_like(input))
+
+
+def _mx_fake(input):
+    assert input.shape[-1] % 32 == 0, "MX fp8 output needs a multiple of 32 columns"
+    return (torch.empty(input.shape, dtype=torch.float8_e4m3fn, device=input.device),
+            torch.empty((*input.shape[:-1], input.shape[-1] // 32), dtype=torch.float8_e8m0fnu,
+                        device=input.device))
+
+
+@torch.library.register_fake("fused_layernorm::layer_norm_mxfp8_fwd")
+def _ln_mx_fake(input, weight, bias, eps):
+    return _mx_fake(input)
+
+
+@torch.library.register_fake("fused_layernorm::rms_norm_mxfp8_fwd")
+def _rms_mx_fake(input, weight, eps):
+    return _mx_fake(input)
+
+
+@torch.library.register_fake("fused_layernorm::add_rms_norm_mxfp8_fwd")
+def _add_rms_mx_fake(input, residual, weight, eps):
+    return (*_mx_fake(input), torch.empty_like(input))
 
 
 @torch.library.register_fake("fused_layernorm::add_rms_norm_fp8_fwd")
@@ -242,6 +265,8 @@ torch.library.register_autograd("fused_layernorm::add_layer_norm_fp8_fwd",
                                 _fp8_residual_backward, setup_context=_fp8_residual_setup)
 torch.library.register_autograd("fused_layernorm::add_rms_norm_fp8_fwd",
                                 _fp8_residual_backward, setup_context=_fp8_residual_setup)
+torch.library.register_autograd("fused_layernorm::add_rms_norm_mxfp8_fwd",
+                                _fp8_residual_backward, setup_context=_fp8_residual_setup)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -364,3 +389,36 @@ def add_rms_norm_fp8(input: torch.Tensor, residual: torch.Tensor, normalized_sha
     q, scale, h = _ops.add_rms_norm_fp8_fwd(x, r, _flat_param(weight), eps)
     lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
     return q.view(input.shape), scale.view(lead if lead else (1,)), h.view(input.shape)
+
+
+def layer_norm_mxfp8(input: torch.Tensor, normalized_shape: ShapeLike,
+                     weight: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+                     eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor]:
+    """LayerNorm quantized to OCP MXFP8 E4M3 -> (codes float8_e4m3fn, E8M0 block scales
+    float8_e8m0fnu [..., n / 32]); dequantize block-wise with codes.float() * scales.float()."""
+    x, n = _flatten(input, normalized_shape)
+    q, sc = _ops.layer_norm_mxfp8_fwd(x, _flat_param(weight), _flat_param(bias), eps)
+    lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
+    return q.view(input.shape), sc.view(*lead, n // 32)
+
+
+def rms_norm_mxfp8(input: torch.Tensor, normalized_shape: ShapeLike,
+                   weight: Optional[torch.Tensor] = None, eps: float = 1e-6
+                   ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm quantized to OCP MXFP8 E4M3 -> (codes, E8M0 block scales)."""
+    x, n = _flatten(input, normalized_shape)
+    q, sc = _ops.rms_norm_mxfp8_fwd(x, _flat_param(weight), eps)
+    lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
+    return q.view(input.shape), sc.view(*lead, n // 32)
+
+
+def add_rms_norm_mxfp8(input: torch.Tensor, residual: torch.Tensor, normalized_shape: ShapeLike,
+                       weight: Optional[torch.Tensor] = None, eps: float = 1e-6
+                       ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused residual add + RMSNorm -> OCP MXFP8 E4M3: (codes, E8M0 block scales,
+    h = input + residual).  Gradients flow through h only."""
+    x, n = _flatten(input, normalized_shape)
+    r, _ = _flatten(residual, normalized_shape)
+    q, sc, h = _ops.add_rms_norm_mxfp8_fwd(x, r, _flat_param(weight), eps)
+    lead = tuple(input.shape[:input.dim() - len(_norm_shape(normalized_shape))])
+    return q.view(input.shape), sc.view(*lead, n // 32), h.view(input.shape)

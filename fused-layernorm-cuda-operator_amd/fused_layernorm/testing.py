@@ -18,7 +18,7 @@ class Workload:
     name: str
     op: str                 # layer_norm | layer_norm_gelu | add_layer_norm | rms_norm_fwd_bwd |
     #                         layer_norm_fwd_bwd | layer_norm_fp8 | add_rms_norm_fp8 |
-    #                         layer_norm_gelu_fwd_bwd
+    #                         layer_norm_gelu_fwd_bwd | add_rms_norm_mxfp8
     rows: int
     cols: int
     dtype: torch.dtype
@@ -45,6 +45,10 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
     # Residual add + RMSNorm -> fp8 at C5's shape (the pre-norm feeding an fp8 GEMM).
     Workload("c6_add_rms_fp8_bf16_32768x7168", "add_rms_norm_fp8", 32768, 7168, torch.bfloat16,
              6, 1e-6, (1.0, 0.05), None, outlier_channels=7, outlier_scale=20.0),
+    # Residual add + RMSNorm -> OCP MXFP8 (E4M3 codes + E8M0 scales per 32 elements).
+    Workload("c7_add_rms_mxfp8_bf16_32768x7168", "add_rms_norm_mxfp8", 32768, 7168,
+             torch.bfloat16, 6, 1e-6, (1.0, 0.05), None, outlier_channels=7,
+             outlier_scale=20.0),
     # LayerNorm + GELU (tanh, the reference's form) forward + fused backward, headline shape.
     Workload("ln_gelu_fwd_bwd_bf16_8192x4096", "layer_norm_gelu_fwd_bwd", 8192, 4096,
              torch.bfloat16, 7, 1e-5, (1.0, 0.02), (0.0, 0.02), approximate="tanh"),
@@ -75,7 +79,7 @@ def make_inputs(w: Workload, rows: Optional[int] = None) -> Dict[str, torch.Tens
         out["beta"] = w.beta[0] + w.beta[1] * _randn((w.cols,), w.seed + 200)
     if w.op in ("layer_norm_fwd_bwd", "rms_norm_fwd_bwd", "layer_norm_gelu_fwd_bwd"):
         out["dy"] = _randn((w.rows, w.cols), w.seed + 300)
-    if w.op in ("add_layer_norm", "add_rms_norm_fp8"):
+    if w.op in ("add_layer_norm", "add_rms_norm_fp8", "add_rms_norm_mxfp8"):
         out["residual"] = _randn((w.rows, w.cols), w.seed + 400)
     out = {k: v.to(w.dtype) for k, v in out.items()}
     if rows is not None and rows < w.rows:
@@ -104,6 +108,9 @@ def algorithmic_bytes(w: Workload, rows: Optional[int] = None) -> Dict[str, int]
         return {"fwd": fwd, "total": fwd}
     if w.op == "add_rms_norm_fp8":
         fwd = 3 * act + m * n + stats + params  # x, r read; h, codes, scale written
+        return {"fwd": fwd, "total": fwd}
+    if w.op == "add_rms_norm_mxfp8":
+        fwd = 3 * act + m * n + m * (n // 32) + params  # x, r read; h, codes, E8M0 written
         return {"fwd": fwd, "total": fwd}
     if w.op == "layer_norm_gelu_fwd_bwd":
         fwd = 2 * act + params + 2 * stats

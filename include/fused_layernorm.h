@@ -145,6 +145,28 @@ int fln_add_rmsnorm_fp8_forward(const void* x, const void* residual, const void*
                                 void* h, uint8_t* q, float* scale, float* rstd, int64_t rows,
                                 int64_t cols, int dtype, float eps, void* stream);
 
+/* LayerNorm with OCP MX fp8 output (MXFP8 E4M3, OCP Microscaling Formats v1.0): v = LN(x)
+ * [* gamma + beta] in fp32; every block of 32 consecutive elements of a row shares the scale
+ * 2^e, e = floor(log2 max|v_block|) - 8 clamped to [-127, 127], stored as the E8M0 byte e + 127
+ * in block_scale[rows, cols / 32]; q = sat_rne_e4m3fn(v * 2^-e).  cols must be a multiple of
+ * 32.  mean and rstd may be NULL.  No counterpart in the reference. */
+int fln_layernorm_mxfp8_forward(const void* x, const void* gamma, const void* beta, uint8_t* q,
+                                uint8_t* block_scale, float* mean, float* rstd, int64_t rows,
+                                int64_t cols, int dtype, float eps, void* stream);
+
+/* RMSNorm with MXFP8 E4M3 output (block rule of fln_layernorm_mxfp8_forward).
+ * No counterpart in the reference. */
+int fln_rmsnorm_mxfp8_forward(const void* x, const void* weight, uint8_t* q,
+                              uint8_t* block_scale, float* rstd, int64_t rows, int64_t cols,
+                              int dtype, float eps, void* stream);
+
+/* Residual add + RMSNorm with MXFP8 E4M3 output: h = x + residual (rounded, stored when h is
+ * not NULL), then fln_rmsnorm_mxfp8_forward of h.  No counterpart in the reference. */
+int fln_add_rmsnorm_mxfp8_forward(const void* x, const void* residual, const void* weight,
+                                  void* h, uint8_t* q, uint8_t* block_scale, float* rstd,
+                                  int64_t rows, int64_t cols, int dtype, float eps,
+                                  void* stream);
+
 /* Elementwise fp32 -> OCP fp8 e4m3fn (saturating, round-to-nearest-even) with the same device
  * conversion the fp8 forward uses; n elements, any alignment.  A standalone quantizer for
  * callers that scale themselves (and a direct check of the conversion).

@@ -17,10 +17,12 @@ __all__ = [
     "round_to_f16", "add_layer_norm_fwd", "add_rms_norm_fwd", "layer_norm_bwd", "rms_norm_bwd",
     "fp8_e4m3fn_encode", "fp8_e4m3fn_decode", "layer_norm_fp8_fwd", "rms_norm_fp8_fwd",
     "add_layer_norm_fp8_fwd", "add_rms_norm_fp8_fwd", "gelu_grad", "layer_norm_gelu_bwd",
-    "FP8_E4M3FN_MAX",
+    "mx_e4m3_quantize", "layer_norm_mxfp8_fwd", "rms_norm_mxfp8_fwd", "add_rms_norm_mxfp8_fwd",
+    "FP8_E4M3FN_MAX", "MX_BLOCK",
 ]
 
 FP8_E4M3FN_MAX = 448.0
+MX_BLOCK = 32
 
 
 def _f64(a):
@@ -255,3 +257,41 @@ def add_rms_norm_fp8_fwd(x, residual, weight=None, eps=1e-6, io_dtype="bf16"):
     y, h, _ = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
     q, scale = _row_fp8(y)
     return q, scale, h
+
+
+def mx_e4m3_quantize(y, block=MX_BLOCK):
+    """OCP Microscaling (MX v1.0) MXFP8 E4M3 of the last axis -> (codes uint8, E8M0 scales uint8
+    [..., n / block]).  Per block of `block` consecutive elements: shared exponent
+    e = floor(log2(max|y|)) - 8 (8 = emax of E4M3), clamped to [-127, 127] (a zero maximum gives
+    -127); scale byte e + 127; codes = sat_rne_e4m3fn(y 2^-e).  Written from the format
+    definition (no reference code)."""
+    y = _f64(y)
+    n = y.shape[-1]
+    if n % block:
+        raise ValueError("the row length must be a multiple of the block")
+    yb = y.reshape(*y.shape[:-1], n // block, block)
+    amax = np.abs(yb).max(axis=-1)
+    _, k = np.frexp(amax)                    # amax = f 2^k, f in [0.5, 1): floor(log2) = k - 1
+    e = np.where(amax > 0, k - 1 - 8, -127)
+    e = np.clip(e, -127, 127).astype(np.int64)
+    codes = fp8_e4m3fn_encode(yb * np.exp2(-e.astype(np.float64))[..., None])
+    return codes.reshape(y.shape), (e + 127).astype(np.uint8)
+
+
+def layer_norm_mxfp8_fwd(x, gamma=None, beta=None, eps=1e-5):
+    """LayerNorm -> MXFP8 E4M3 (codes, E8M0 block scales).  No reference code."""
+    y, _, _ = layer_norm_fwd(x, gamma, beta, eps)
+    return mx_e4m3_quantize(y)
+
+
+def rms_norm_mxfp8_fwd(x, weight=None, eps=1e-6):
+    """RMSNorm -> MXFP8 E4M3.  No reference code."""
+    y, _ = rms_norm_fwd(x, weight, eps)
+    return mx_e4m3_quantize(y)
+
+
+def add_rms_norm_mxfp8_fwd(x, residual, weight=None, eps=1e-6, io_dtype="bf16"):
+    """Residual add + RMSNorm -> MXFP8 E4M3: (codes, block scales, h).  No reference code."""
+    y, h, _ = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
+    q, sc = mx_e4m3_quantize(y)
+    return q, sc, h

@@ -85,3 +85,30 @@ def assert_fp8_close(q_got, s_got, q_ref, s_ref, what="", t_ref=None):
         counted &= ~fp8_ambiguous(t_ref)
     n_diff = int(counted.sum())
     assert n_diff <= 1e-3 * diff.size, f"{what}: {n_diff} of {diff.size} codes differ"
+
+
+def assert_mx_close(q_got, sc_got, q_ref, sc_ref, y_ref, what="", block=32):
+    """MXFP8 bar.  E8M0 block scales identical, except that a block whose float64 maximum lies
+    within 2^-20 (relative) of a power of two may take the neighbouring exponent (an fp32
+    evaluation of the maximum can land on either side); codes compared in the blocks whose
+    scales agree, to the fp8 bar of assert_fp8_close with ties excused."""
+    from oracle import norms
+    sc_got = np.asarray(sc_got).astype(np.int64)
+    sc_ref = np.asarray(sc_ref).astype(np.int64)
+    y = np.asarray(y_ref, np.float64).reshape(*sc_ref.shape, block)
+    amax = np.abs(y).max(axis=-1)
+    frac, _ = np.frexp(amax)
+    near_pow2 = (np.abs(frac - 0.5) <= 2.0 ** -21) | (np.abs(frac - 1.0) <= 2.0 ** -21)
+    bad = (sc_got != sc_ref) & ~((np.abs(sc_got - sc_ref) == 1) & near_pow2)
+    assert not bad.any(), f"{what}: {int(bad.sum())} block scales differ"
+    same = sc_got == sc_ref
+    t = y * np.exp2(-(sc_ref - 127).astype(np.float64))[..., None]
+    qg = np.asarray(q_got).reshape(y.shape)[same]
+    qr = np.asarray(q_ref).reshape(y.shape)[same]
+    diff = np.abs(fp8_ordinal(qg) - fp8_ordinal(qr))
+    if diff.size:
+        assert int(diff.max()) <= 1, f"{what}: a code differs by {int(diff.max())} steps"
+        counted = (diff != 0) & ~fp8_ambiguous(t[same])
+        assert int(counted.sum()) <= 1e-3 * diff.size, \
+            f"{what}: {int(counted.sum())} of {diff.size} codes differ"
+    del norms

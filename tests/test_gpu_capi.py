@@ -22,7 +22,7 @@ import torch
 
 import capi
 from gpu_calls import cuda, f32, ln_backward, ln_forward, rms_backward, rms_forward, workspace
-from helpers import assert_close_rel, assert_fp8_close, assert_within_ulp, to_np
+from helpers import assert_close_rel, assert_fp8_close, assert_mx_close, assert_within_ulp, to_np
 from oracle import c_oracle, norms
 from fused_layernorm.testing import WORKLOADS, make_inputs
 
@@ -479,6 +479,94 @@ def test_layernorm_gelu_entry_points_reject_bad_mode(lib):
     assert lib.fln_layernorm_gelu_backward(p(x), p(x), p(x), p(x), None, None, p(y), None, None,
                                            4, 64, capi.F32, capi.F32, 3, None, 0,
                                            capi.stream()) == 1
+
+
+def _mx_call(lib, kind, x, r, g, b, q, sc, h, rows, cols, code):
+    p = capi.ptr
+    if kind == "ln":
+        return lib.fln_layernorm_mxfp8_forward(p(x), p(g), p(b), p(q), p(sc), None, None, rows,
+                                               cols, code, 1e-5, capi.stream())
+    if kind == "rms":
+        return lib.fln_rmsnorm_mxfp8_forward(p(x), p(g), p(q), p(sc), None, rows, cols, code,
+                                             1e-6, capi.stream())
+    return lib.fln_add_rmsnorm_mxfp8_forward(p(x), p(r), p(g), p(h), p(q), p(sc), None, rows,
+                                             cols, code, 1e-6, capi.stream())
+
+
+def _mx_ref(kind, xs, rs, gs, bs, io):
+    if kind == "ln":
+        y, _, _ = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
+    elif kind == "rms":
+        y, _ = norms.rms_norm_fwd(xs, gs, 1e-6)
+    else:
+        y, _, _ = norms.add_rms_norm_fwd(xs, rs, gs, 1e-6, io)
+    q, sc = norms.mx_e4m3_quantize(y)
+    return q, sc, y
+
+
+@pytest.mark.parametrize("kind", ["ln", "rms", "add_rms"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols,path", [
+    (64, 4096, "vec"), (33, 7168, "vec"), (9, 96, "vec"), (2, 16384, "vec"),
+    (13, 1024, "scalar"), (3, 2048, "loop")])
+def test_mxfp8_matrix(lib, monkeypatch, kind, dtype, rows, cols, path):
+    """OCP MXFP8 outputs (codes + E8M0 block scales) of LayerNorm, RMSNorm and residual +
+    RMSNorm over dtypes and widths, on the vector path (block = 32 / VEC adjacent lanes), the
+    scalar path (misaligned pointers: block = 32 lanes) and the looped kernel."""
+    gen = torch.Generator().manual_seed(rows * 131 + cols)
+    xc = (torch.randn(rows, cols, generator=gen) * torch.exp(torch.randn(rows, 1, generator=gen))
+          ).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    if path == "scalar":  # one element of offset: 16-byte misaligned device pointers
+        xbuf, rbuf = (torch.zeros(rows * cols + 1, dtype=dtype) for _ in range(2))
+        xbuf[1:] = xc.flatten()
+        rbuf[1:] = rc.flatten()
+        xd, rd = cuda(xbuf)[1:].view(rows, cols), cuda(rbuf)[1:].view(rows, cols)
+    else:
+        xd, rd = cuda(xc), cuda(rc)
+    g, b = cuda(gc), cuda(bc)
+    q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+    sc = torch.empty(rows, cols // 32, device="cuda", dtype=torch.uint8)
+    h = torch.empty(rows, cols, device="cuda", dtype=dtype)
+    if path == "loop":
+        monkeypatch.setenv("FLN_FORCE_LOOP", "1")
+    capi.check(_mx_call(lib, kind, xd, rd, g, b if kind == "ln" else None, q, sc, h, rows, cols,
+                        capi.dtype_code(xd)))
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_FORCE_LOOP", raising=False)
+    io = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    q_ref, sc_ref, y_ref = _mx_ref(kind, f32(xc), f32(rc), f32(gc), f32(bc), io)
+    if kind == "add_rms":
+        assert np.array_equal(to_np(h), to_np(xc + rc)), "h bit-exact"
+    assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, sc_ref, y_ref, f"mx {kind}")
+
+
+def test_mxfp8_add_rmsnorm_bf16_4096x7168(lib):
+    """Residual + RMSNorm -> MXFP8 at C5's width (bf16, 7 outlier channels x20)."""
+    w = WORKLOADS["c5_ln_fp8_bf16_32768x7168"]
+    inp = make_inputs(w, 4096)
+    gen = torch.Generator().manual_seed(77)
+    rc = torch.randn(4096, 7168, generator=gen).to(torch.bfloat16)
+    x, r, g = cuda(inp["x"]), cuda(rc), cuda(inp["gamma"])
+    q = torch.empty(4096, 7168, device="cuda", dtype=torch.uint8)
+    sc = torch.empty(4096, 224, device="cuda", dtype=torch.uint8)
+    h = torch.empty_like(x)
+    capi.check(_mx_call(lib, "add_rms", x, r, g, None, q, sc, h, 4096, 7168, capi.BF16))
+    q_ref, sc_ref, y_ref = _mx_ref("add_rms", f32(inp["x"]), f32(rc), f32(inp["gamma"]), None,
+                                   "bf16")
+    assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, sc_ref, y_ref, "mx 4096x7168")
+
+
+def test_mxfp8_rejects_widths_not_multiple_of_32(lib):
+    x = torch.randn(4, 48, device="cuda")
+    q = torch.empty(4, 48, device="cuda", dtype=torch.uint8)
+    sc = torch.empty(8, device="cuda", dtype=torch.uint8)
+    assert lib.fln_rmsnorm_mxfp8_forward(capi.ptr(x), None, capi.ptr(q), capi.ptr(sc), None, 4,
+                                         48, capi.F32, 1e-6, capi.stream()) == 1
+    assert lib.fln_layernorm_mxfp8_forward(capi.ptr(x), None, None, capi.ptr(q), None, None,
+                                           None, 4, 64, capi.F32, 1e-5, capi.stream()) == 1
 
 
 def test_residual_gradient_is_added(lib):

@@ -382,6 +382,29 @@ def test_residual_fp8_functional_and_gradient_pass_through(norm):
     assert torch.equal(x.grad, dh) and torch.equal(r.grad, dh)
 
 
+def test_mxfp8_functional_dtypes_dequantization_and_pass_through():
+    x = torch.randn(4, 32, 2048, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    r = torch.randn(4, 32, 2048, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    w = (1 + 0.05 * torch.randn(2048, device=DEV)).to(torch.bfloat16)
+    q, sc, h = fl.add_rms_norm_mxfp8(x, r, (2048,), w, 1e-6)
+    assert q.dtype == torch.float8_e4m3fn and sc.dtype == torch.float8_e8m0fnu
+    assert q.shape == x.shape and sc.shape == (4, 32, 64)
+    deq = (q.float().view(4, 32, 64, 32) * sc.float()[..., None]).view(4, 32, 2048)
+    ref = F.rms_norm(h.detach().double().cpu(), (2048,), w.double().cpu(), 1e-6)
+    # e4m3: within 2^-3 of the value, or of the block's subnormal step / saturation
+    x_blk = sc.float().cpu().double()[..., None].expand(4, 32, 64, 32).reshape(4, 32, 2048)
+    err = (deq.double().cpu() - ref).abs()
+    assert (err <= ref.abs() * 2 ** -3 + x_blk * 2 ** -9 + (ref.abs() - 448 * x_blk).clamp(min=0)).all()
+    dh = torch.randn_like(h)
+    (h * dh).sum().backward()
+    assert torch.equal(x.grad, dh) and torch.equal(r.grad, dh)
+    q2, sc2 = fl.layer_norm_mxfp8(x.detach(), 2048, w, None, 1e-5)
+    q3, sc3 = fl.rms_norm_mxfp8(x.detach(), 2048, w, 1e-6)
+    assert sc2.shape == sc3.shape == (4, 32, 64)
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        fl.rms_norm_mxfp8(torch.randn(2, 48, device=DEV), 48)
+
+
 def test_rms_norm_fp8_functional():
     x = torch.randn(4, 16, 2048, device=DEV, dtype=torch.bfloat16)
     w = (1 + 0.05 * torch.randn(2048, device=DEV)).to(torch.bfloat16)
@@ -431,6 +454,11 @@ def test_torch_compile_matches_eager():
                                       torch.randn(256, device=DEV), 1e-6)),
     ("rms_norm_fp8_fwd", lambda: (torch.randn(8, 256, device=DEV),
                                   torch.randn(256, device=DEV), 1e-6)),
+    ("add_rms_norm_mxfp8_fwd", lambda: (torch.randn(8, 256, device=DEV, requires_grad=True),
+                                        torch.randn(8, 256, device=DEV, requires_grad=True),
+                                        torch.randn(256, device=DEV), 1e-6)),
+    ("layer_norm_mxfp8_fwd", lambda: (torch.randn(8, 256, device=DEV),
+                                      torch.randn(256, device=DEV), None, 1e-5)),
 ])
 def test_opcheck(op, args):
     # opcheck's AOT-dispatch check sums every output into a loss, and torch has no sum for

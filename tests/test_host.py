@@ -119,6 +119,11 @@ def test_fake_tensor_shapes_of_every_op():
             assert s.shape == (3, 5) and s.dtype == torch.float32 and h.dtype == x.dtype
         q, s, h = fl.add_rms_norm_fp8(x, x, 64, w)
         assert q.shape == x.shape and s.shape == (3, 5) and h.shape == x.shape
+        q, s = torch.ops.fused_layernorm.layer_norm_mxfp8_fwd(x, w, None, 1e-5)
+        assert q.dtype == torch.float8_e4m3fn and s.dtype == torch.float8_e8m0fnu
+        assert s.shape == (3, 5, 2)
+        q, s, h = fl.add_rms_norm_mxfp8(x, x, 64, w)
+        assert s.shape == (3, 5, 2) and h.shape == x.shape
 
 
 def test_module_state_dict_keys_match_nn_layernorm():

@@ -274,6 +274,42 @@ def test_rms_and_residual_fp8_variants_match_torch_composition(rng):
     assert np.array_equal(q, qt) and np.array_equal(s, st)
 
 
+def test_mx_e4m3_known_answers():
+    # block maxima 448 -> e = 0 (byte 127); 1.0 -> e = -8 (119); 2^-130 and 0 -> clamp (0)
+    y = np.zeros((1, 128))
+    y[0, 0], y[0, 32], y[0, 64] = 448.0, 1.0, 2.0 ** -130
+    y[0, 33] = 0.5
+    q, sc = norms.mx_e4m3_quantize(y)
+    assert list(sc[0]) == [127, 119, 0, 0]
+    assert q[0, 0] == 0x7E                       # 448 * 2^0
+    assert norms.fp8_e4m3fn_decode(q[0, 32:34]).tolist() == [256, 128]  # 1.0, 0.5 at 2^8
+    assert (q[0, 96:] == 0).all()
+    # a maximum just below 2^9 * 2^e: 511.9 -> e = 0 and the element saturates to 448
+    q2, sc2 = norms.mx_e4m3_quantize(np.full((1, 32), 511.9))
+    assert sc2[0, 0] == 127 and (q2 == 0x7E).all()
+
+
+def test_mx_e4m3_matches_torch_casts(rng):
+    y = rng.randn(16, 512) * np.exp(rng.randn(16, 1) * 3)
+    y[:, 40] *= 50
+    q, sc = norms.mx_e4m3_quantize(y)
+    yt = t64(y).reshape(16, 16, 32)
+    amax = yt.abs().amax(-1)
+    e = (torch.frexp(amax).exponent - 1 - 8).clamp(-127, 127)
+    qt = (yt * torch.exp2(-e.double())[..., None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert np.array_equal(q, qt.view(torch.uint8).reshape(16, 512).numpy())
+    e8 = torch.exp2(e.double()).to(torch.float8_e8m0fnu).view(torch.uint8).numpy()
+    assert np.array_equal(sc, e8)           # torch's E8M0 encoding of 2^e is the byte e + 127
+    # dequantization: within half an e4m3 step (2^-4 relative, or half the subnormal step
+    # 2^-10 of the block scale), except block values above 448 2^e, which saturate to it
+    x = 2.0 ** (sc.astype(float) - 127)[..., None]
+    deq = norms.fp8_e4m3fn_decode(q).reshape(16, 16, 32) * x
+    yb = y.reshape(16, 16, 32)
+    sat = np.abs(yb) > 448 * x
+    assert (np.abs(deq - yb) <= np.abs(yb) * 2.0 ** -4 + x * 2.0 ** -10)[~sat].all()
+    assert np.array_equal(deq[sat], np.sign(yb[sat]) * 448 * np.broadcast_to(x, yb.shape)[sat])
+
+
 # ---------------------------------------------------------------- C oracle vs numpy oracle
 def test_c_oracle_matches_numpy_oracle(rng):
     x = rng.randn(9, 1023).astype(np.float32)
