@@ -112,8 +112,12 @@ __device__ __forceinline__ void reduce_quad_block(const ColReduceArgs& a, int64_
   __syncthreads();  // comb is reused by the caller's next quad block
 }
 
+// Rows in flight ahead of the current one.  Measured on MI355X over bf16 / fp16 / fp32 rows of
+// 768 to 16384 columns: 2 rows beat 1 and 3 when a lane holds one vector of a row; with two
+// vectors per lane (16-bit rows wider than 8192 columns, fp32 wider than 4096) a deeper ring no
+// longer fits the 128 VGPRs of a 1024-thread block and spills, so one row is prefetched.
 #ifndef FLN_BWD_PREFETCH
-#define FLN_BWD_PREFETCH 3
+#define FLN_BWD_PREFETCH(VPL) ((VPL) == 1 ? 2 : 1)
 #endif
 // Cache policies of the streamed rows: dx is stored non-temporal; x / dy / dres loads keep the
 // default policy.  Measured on MI355X (bf16 forward + backward steps): non-temporal loads as
@@ -131,7 +135,7 @@ __device__ __forceinline__ void reduce_quad_block(const ColReduceArgs& a, int64_
 // of dy GELU'(a)).
 template <class T, bool DRES, int GELU, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
-  constexpr int PD = FLN_BWD_PREFETCH;  // rows in flight ahead of the current one
+  constexpr int PD = FLN_BWD_PREFETCH(VPL);  // rows in flight ahead of the current one
   constexpr int MAXW = MAXT / kWave;
   // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
   __shared__ float red[2][2][MAXW + 16];
@@ -159,29 +163,29 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   const T* DR = static_cast<const T*>(p.dres);
   T* DX = static_cast<T*>(p.dx);
 
-  // gamma (and, with GELU, beta) in fp32 registers (gamma ones when absent; zeros past the
-  // row).
-  float gam[VPL][VEC];
-  float bet[GELU ? VPL : 1][VEC];
+  // gamma (and, with GELU, beta) stay in registers in the I/O type and are widened at each use
+  // (gamma ones when absent; zeros past the row): half the VGPRs of fp32 copies for 16-bit types.
+  P gmr[VPL];
+  P btr[GELU ? VPL : 1];
   {
     const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
     const bool has_g = p.gamma != nullptr;
+    const T one = from_f32<T>(1.0f);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const P gv = buf_load<P>(gr, t + i * tpr);
+      gmr[i] = buf_load<P>(gr, t + i * tpr);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) gam[i][e] = has_g ? to_f32(gv.v[e]) : 1.0f;
+      for (int e = 0; e < VEC; ++e)
+        if (!has_g) gmr[i].v[e] = one;
     }
     if constexpr (GELU != 0) {
       const rsrc_t br = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const P bv = buf_load<P>(br, t + i * tpr);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) bet[i][e] = to_f32(bv.v[e]);
-      }
+      for (int i = 0; i < VPL; ++i) btr[i] = buf_load<P>(br, t + i * tpr);
     }
   }
+  auto gam = [&](int i, int e) { return to_f32(gmr[i].v[e]); };
+  auto bet = [&](int i, int e) { return to_f32(btr[GELU ? i : 0].v[e]); };
   float acc_g[VPL][VEC], acc_b[VPL][VEC];
 #pragma unroll
   for (int i = 0; i < VPL; ++i)
@@ -220,8 +224,9 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     rsn[slot] = __builtin_bit_cast(float, BufIO<4>::load(make_rsrc(p.rstd + row, sb), 0));
   };
 
-  // The row being processed, widened once: xhat, dy and g = dy * gamma in fp32.
-  float xh[VPL][VEC], dd[VPL][VEC], gg[VPL][VEC];
+  // The row being processed, widened once: xhat and dy in fp32 (g = dy * gamma is formed where
+  // it is used rather than kept: 16 fewer VGPRs for a lane with 16 columns).
+  float xh[VPL][VEC], dd[VPL][VEC];
   P rv[VPL];
   float rs = 0.0f;
   auto widen = [&](int slot) {
@@ -233,9 +238,8 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       for (int e = 0; e < VEC; ++e) {
         xh[i][e] = (to_f32(xn[slot][i].v[e]) - mu) * rs;
         dd[i][e] = to_f32(dn[slot][i].v[e]);
-        if constexpr (GELU == 1) dd[i][e] *= gelu_erf_grad(fmaf(xh[i][e], gam[i][e], bet[i][e]));
-        if constexpr (GELU == 2) dd[i][e] *= gelu_tanh_grad(fmaf(xh[i][e], gam[i][e], bet[i][e]));
-        gg[i][e] = dd[i][e] * gam[i][e];
+        if constexpr (GELU == 1) dd[i][e] *= gelu_erf_grad(fmaf(xh[i][e], gam(i, e), bet(i, e)));
+        if constexpr (GELU == 2) dd[i][e] *= gelu_tanh_grad(fmaf(xh[i][e], gam(i, e), bet(i, e)));
       }
       if constexpr (DRES) rv[i] = rn[slot][i];
     }
@@ -260,8 +264,9 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        s1 += gg[i][e];
-        s2 = fmaf(gg[i][e], xh[i][e], s2);
+        const float g = dd[i][e] * gam(i, e);
+        s1 += g;
+        s2 = fmaf(g, xh[i][e], s2);
       }
     s1 = wave_allreduce<SumOp>(s1);
     s2 = wave_allreduce<SumOp>(s2);
@@ -283,7 +288,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float dxv = fmaf(rs, gg[i][e], fmaf(cx, xh[i][e], cb));
+        float dxv = fmaf(dd[i][e], rs * gam(i, e), fmaf(cx, xh[i][e], cb));
         if constexpr (DRES) dxv += to_f32(rv[i].v[e]);
         o[i].v[e] = from_f32<T>(dxv);
         acc_g[i][e] = fmaf(dd[i][e], xh[i][e], acc_g[i][e]);

@@ -51,8 +51,12 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 // EXACT: the row is exactly VPL vectors per lane (no masking in the statistics); GELU: 0 none,
 // 1 erf, 2 tanh (a template parameter so the plain kernels carry no GELU code).
 // ---------------------------------------------------------------------------------------------
+// Register budget: a 1024-thread block leaves 128 VGPRs per lane.  There a lane with more than
+// 32 bytes of a row prefetches one row instead of two, and a lane with 32 elements (RAW) keeps
+// the row in the I/O type rather than as an fp32 copy, widening it again in each pass (one VALU
+// op per element).  Blocks of at most 256 threads have 256 VGPRs and keep the fp32 copy.
 #ifndef FLN_FWD_PREFETCH
-#define FLN_FWD_PREFETCH 2
+#define FLN_FWD_PREFETCH(ROW_BYTES, MAXT) ((MAXT) > 256 && (ROW_BYTES) > 32 ? 1 : 2)
 #endif
 // Cache policies of the streamed rows: loads of x / residual and stores of y / h / q are
 // non-temporal (each byte is touched once; measured on MI355X this is 3-10% faster than the
@@ -66,7 +70,9 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 #endif
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
-  constexpr int PD = FLN_FWD_PREFETCH;  // rows in flight ahead of the current one
+  // rows in flight ahead of the current one
+  constexpr int PD = FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT);
+  constexpr bool RAW = MAXT > 256 && VPL * VEC >= 32;  // row kept in the I/O type
   constexpr int MAXW = MAXT / kWave;
   __shared__ float red[2][3][MAXW + 16];  // padded: combine_partials reads 16 past the base
   using P = Pack<T, VEC>;
@@ -130,20 +136,26 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     }
   };
 
-  float xf[VPL][VEC];  // the row being normalized, fp32
-  P hv[VPL];           // residual sum of that row, in the I/O type (RES only)
+  float xf[RAW ? 1 : VPL][VEC];  // the row being normalized, fp32 (then its outputs)
+  P hv[VPL];  // residual sum of that row (RES), or the row itself (RAW), in the I/O type
   auto widen = [&](int slot) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        if constexpr (RES) {
+        if constexpr (RES)
           hv[i].v[e] = from_f32<T>(to_f32(xv[slot][i].v[e]) + to_f32(rv[slot][i].v[e]));
-          xf[i][e] = to_f32(hv[i].v[e]);
-        } else {
-          xf[i][e] = to_f32(xv[slot][i].v[e]);
-        }
+        else if constexpr (RAW)
+          hv[i].v[e] = xv[slot][i].v[e];
+        if constexpr (!RAW) xf[i][e] = to_f32(RES ? hv[i].v[e] : xv[slot][i].v[e]);
       }
+  };
+  // Element e of vector slot i of the row, fp32.
+  auto xin = [&](int i, int e) -> float {
+    if constexpr (RAW)
+      return to_f32(hv[i].v[e]);
+    else
+      return xf[i][e];
   };
 
   const int64_t rb0 = blockIdx.x;
@@ -163,6 +175,13 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     const int64_t row = row_of(rb);
     const uint32_t nb = bytes_of(rb);
     float(*slots)[MAXW + 16] = red[parity];
+    if constexpr (MAXT > 256) {  // 128 VGPRs: widen the parameters per row, not once
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        keep_packed(gv[i]);
+        keep_packed(bv[i]);
+      }
+    }
 
     // 1. Statistics: two passes over registers (mean, then centred sum of squares).  Vectors
     //    past the row were loaded as zeros, so they drop out of the plain sum.
@@ -172,7 +191,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 #pragma unroll
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) s += xf[i][e];
+        for (int e = 0; e < VEC; ++e) s += xin(i, e);
       const float sum = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane);
       mean = sum * inv_n;
       mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
@@ -183,14 +202,14 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       if (slot_full(i)) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          const float d = xf[i][e] - mean;
+          const float d = xin(i, e) - mean;
           q = fmaf(d, d, q);
         }
       } else {
         const bool ok = (t + i * tpr) < nvec;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          const float d = xf[i][e] - mean;
+          const float d = xin(i, e) - mean;
           q += ok ? d * d : 0.0f;
         }
       }
@@ -199,15 +218,25 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
 
     //    Normalize + affine + epilogue, packed to the output format.
+    auto affine = [&](int i, int e) -> float {
+      float a = fmaf((xin(i, e) - mean) * rstd, to_f32(gv[i].v[e]), to_f32(bv[i].v[e]));
+      if constexpr (GELU == 1) a = gelu_erf(a);
+      if constexpr (GELU == 2) a = gelu_tanh(a);
+      return a;
+    };
+    if constexpr (!RAW) {
 #pragma unroll
-    for (int i = 0; i < VPL; ++i)
+      for (int i = 0; i < VPL; ++i)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        float a = fmaf((xf[i][e] - mean) * rstd, to_f32(gv[i].v[e]), to_f32(bv[i].v[e]));
-        if constexpr (GELU == 1) a = gelu_erf(a);
-        if constexpr (GELU == 2) a = gelu_tanh(a);
-        xf[i][e] = a;
-      }
+        for (int e = 0; e < VEC; ++e) xf[i][e] = affine(i, e);
+    }
+    // Output element e of vector slot i (RAW: recomputed at each use).
+    auto out = [&](int i, int e) -> float {
+      if constexpr (RAW)
+        return affine(i, e);
+      else
+        return xf[i][e];
+    };
     P yo[VPL];
     QW qo[VPL];
     P ho[VPL];
@@ -217,7 +246,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 #pragma unroll
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) yo[i].v[e] = from_f32<T>(xf[i][e]);
+        for (int e = 0; e < VEC; ++e) yo[i].v[e] = from_f32<T>(out(i, e));
     } else if constexpr (FP8 == 2) {
       // OCP MX: each 32-element block is G adjacent lanes' vectors; its maximum needs only
       // DPP steps within the group (blocks never straddle the row end: cols % 32 == 0).
@@ -226,9 +255,11 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       for (int i = 0; i < VPL; ++i) {
         float bm = 0.0f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(xf[i][e]));
+        for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(out(i, e)));
         const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
-        const float* a = xf[i];
+        float a[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) a[e] = out(i, e);
         const float m = ms.mul;  // |a * m| < 512: the saturating conversion clamps to 448
         if constexpr (VEC == 8) {
           qo[i].x = fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
@@ -246,11 +277,11 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       for (int i = 0; i < VPL; ++i) {
         if (slot_full(i)) {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) am = fmaxf(am, fabsf(xf[i][e]));
+          for (int e = 0; e < VEC; ++e) am = fmaxf(am, fabsf(out(i, e)));
         } else {
           const bool ok = (t + i * tpr) < nvec;
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) am = fmaxf(am, ok ? fabsf(xf[i][e]) : 0.0f);
+          for (int e = 0; e < VEC; ++e) am = fmaxf(am, ok ? fabsf(out(i, e)) : 0.0f);
         }
       }
       am = row_allreduce<MaxOp>(am, slots[2], wpr, rg, wave, lane);
@@ -258,7 +289,9 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       scale = am / 448.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
-        const float* a = xf[i];
+        float a[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) a[e] = out(i, e);
         // |a * inv| <= 448 (1 + 2^-23): in range for the unclamped conversion.
         if constexpr (VEC == 8) {
           qo[i].x = fp8x4_inrange(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
@@ -534,8 +567,11 @@ int launch_loop(const FwdParams& p, hipStream_t s) {
 }
 
 // Launch geometry of the register path: waves per row (wpr), vectors per lane (vpl, a power of
-// two <= cap) and block size.  Preference order:
-//   1. the fewest waves per row (power of two) that fit the row in `cap` vectors per lane;
+// two) and block size.  Rows of up to 4 waves share 256-thread blocks (256 VGPRs per lane) and
+// take up to `cap` vectors per lane; wider rows run in blocks of up to 1024 threads (128 VGPRs)
+// and take up to `wide_cap`, or `max_cap` (the RAW tiles) when nothing narrower fits 16 waves.
+// Preference order:
+//   1. the fewest waves per row (power of two) that fit the row within those caps;
 //   2. if that tiling leaves masked lanes, an exact tiling with any wave count <= 16 (e.g. a
 //      7168-element bf16 row is 7 waves x 64 lanes x 2 vectors), so no lane does masked work;
 //   3. few rows: more waves per row (fewer vectors each) until the grid covers the device.
@@ -545,24 +581,28 @@ struct FwdGeometry {
   bool exact, loop;
 };
 
-inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int max_cap, bool vec_path,
-                                int forced_wpr) {
+inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_cap, int max_cap,
+                                bool vec_path, int forced_wpr) {
   FwdGeometry g{};
   constexpr int max_wpr = 16;
   auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
+  auto cap_of = [&](int w) { return w <= 4 ? cap : wide_cap; };
   int wpr = 1;
-  while (per_lane(wpr) > cap && wpr < max_wpr) wpr *= 2;
-  if (per_lane(wpr) > cap) cap = max_cap;  // very long rows: widest register tiles
-  if (per_lane(wpr) > cap) {
+  while (per_lane(wpr) > cap_of(wpr) && wpr < max_wpr) wpr *= 2;
+  const bool widest = per_lane(wpr) > cap_of(wpr);  // very long rows: widest register tiles
+  if (widest && per_lane(wpr) > max_cap) {
     g.loop = true;
     return g;
   }
+  auto fits = [&](int w, int v) { return v <= (widest ? max_cap : cap_of(w)); };
   int vpl = next_pow2(static_cast<int>(per_lane(wpr)));
   bool exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
   if (vec_path && !exact) {
-    for (int v = next_pow2(cap) > cap ? next_pow2(cap) / 2 : cap; v >= 1; v >>= 1) {
-      if (nvec % (kWave * v) == 0 && nvec / (kWave * v) <= max_wpr) {
-        wpr = static_cast<int>(nvec / (kWave * v));
+    const int top = widest ? max_cap : (cap > wide_cap ? cap : wide_cap);
+    for (int v = next_pow2(top) > top ? next_pow2(top) / 2 : top; v >= 1; v >>= 1) {
+      const int64_t w = nvec / (kWave * v);
+      if (nvec % (kWave * v) == 0 && w <= max_wpr && fits(static_cast<int>(w), v)) {
+        wpr = static_cast<int>(w);
         vpl = v;
         exact = true;
         break;
@@ -611,12 +651,17 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   int cap = (epl >= vec ? epl : vec) / vec;
   const int max_cap = vec_ok ? max_vpl<VV>() : max_vpl<1>();
   if (cap > max_cap) cap = max_cap;
+  // Rows of more than 4 waves: 16 elements per lane (8 on the scalar path) keep every flavour
+  // within the 128 VGPRs of a 1024-thread block.
+  int wide_cap = vec_ok ? 16 / VV : 8;
+  if (wide_cap > cap) wide_cap = cap;
   const int64_t nvec = N / vec;
-  const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, max_cap, vec_ok,
+  const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, max_cap, vec_ok,
                                      env_int("FLN_FWD_WPR", 0));
   if (env_int("FLN_DEBUG_GEOMETRY", 0))
-    fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d -> %s wpr=%d vpl=%d exact=%d "
-            "threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec, cap,
+    fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
+            "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
+            cap, wide_cap,
             g.loop ? "loop" : "registers", g.wpr, g.vpl, static_cast<int>(g.exact), g.threads);
   if (g.loop) return launch_loop<T, float, FP8>(p, s);
   p.wpr = g.wpr;

@@ -47,27 +47,32 @@ def _next_pow2(v: int) -> int:
     return p
 
 
-def _forward_geometry(rows: int, nvec: int, cap: int, max_cap: int, vec_path: bool,
-                      num_cus: int):
+def _forward_geometry(rows: int, nvec: int, cap: int, wide_cap: int, max_cap: int,
+                      vec_path: bool, num_cus: int):
     """The forward dispatcher's geometry rule (csrc/fln_forward_impl.h, fwd_geometry): the
-    fewest power-of-two waves per row that keep <= cap vectors per lane; on the vector path an
-    exact (mask-free) non-power-of-two tiling when one exists; more waves per row while the
-    grid holds fewer than 4 waves per CU.  Returns (loop, wpr, vpl, exact, threads)."""
+    fewest power-of-two waves per row that keep <= cap vectors per lane for rows of up to 4
+    waves and <= wide_cap beyond (max_cap when nothing narrower fits 16 waves); on the vector
+    path an exact (mask-free) non-power-of-two tiling within the same caps when one exists;
+    more waves per row while the grid holds fewer than 4 waves per CU.
+    Returns (loop, wpr, vpl, exact, threads)."""
     per_lane = lambda w: -(-nvec // (64 * w))  # noqa: E731
+    cap_of = lambda w: cap if w <= 4 else wide_cap  # noqa: E731
     wpr = 1
-    while per_lane(wpr) > cap and wpr < 16:
+    while per_lane(wpr) > cap_of(wpr) and wpr < 16:
         wpr *= 2
-    if per_lane(wpr) > cap:
-        cap = max_cap
-    if per_lane(wpr) > cap:
+    widest = per_lane(wpr) > cap_of(wpr)
+    if widest and per_lane(wpr) > max_cap:
         return True, 0, 0, False, 1024
+    fits = lambda w, v: v <= (max_cap if widest else cap_of(w))  # noqa: E731
     vpl = _next_pow2(per_lane(wpr))
     exact = nvec == vpl * 64 * wpr
     if vec_path and not exact:
-        v = _next_pow2(cap) // 2 if _next_pow2(cap) > cap else cap
+        top = max_cap if widest else max(cap, wide_cap)
+        v = _next_pow2(top) // 2 if _next_pow2(top) > top else top
         while v >= 1:
-            if nvec % (64 * v) == 0 and nvec // (64 * v) <= 16:
-                wpr, vpl, exact = nvec // (64 * v), v, True
+            w = nvec // (64 * v)
+            if nvec % (64 * v) == 0 and w <= 16 and fits(w, v):
+                wpr, vpl, exact = w, v, True
                 break
             v >>= 1
     while rows * wpr < 4 * num_cus and wpr * 2 <= 16:
@@ -95,7 +100,8 @@ def get_optimal_config(batch_size: int, hidden_size: int,
     nvec = hidden_size // vec
     max_cap = 32 // vv if vec_path else 16
     cap = min(max(32, vec) // vec, max_cap)
-    loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, max_cap,
+    wide_cap = min(16 // vv if vec_path else 8, cap)
+    loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, wide_cap, max_cap,
                                                        vec_path, num_cus)
     return {
         "use_mixed_precision": dtype in (torch.float16, torch.bfloat16),

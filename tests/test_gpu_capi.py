@@ -215,7 +215,7 @@ def test_edge_shapes_fp32(lib, rows, cols):
 
 DTYPES = [torch.float32, torch.bfloat16, torch.float16]
 SHAPES = [(1, 768), (8, 768), (32, 1024), (64, 2048), (128, 4096), (3, 1023), (5, 5120),
-          (4, 16384), (2, 32768), (33, 7168), (7, 96)]
+          (4, 16384), (2, 32768), (33, 7168), (7, 96), (5, 12288), (300, 20480)]
 
 
 def _tol_fwd(dtype):
@@ -375,7 +375,8 @@ def _scaled(y):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
                          ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 1023), (33, 7168), (2, 16384)])
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 1023), (33, 7168), (2, 16384),
+                                       (3, 12288), (2, 32768)])
 def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
     """RMSNorm -> fp8, residual + LayerNorm -> fp8, residual + RMSNorm -> fp8 over dtypes and
     widths (1023: the scalar path; 16384: a wide row), against the numpy oracle."""
@@ -428,7 +429,8 @@ def test_fp8_variants_reject_bad_arguments(lib):
 
 @pytest.mark.parametrize("mode", ["none", "tanh"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,cols", [(64, 4096), (17, 1023), (33, 7168), (2, 16384), (300, 768)])
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (17, 1023), (33, 7168), (2, 16384), (300, 768),
+                                       (3, 12288), (2, 32768)])
 def test_layernorm_gelu_backward_matrix(lib, mode, dtype, rows, cols):
     """Backward of GELU(LayerNorm(x) gamma + beta): the forward with statistics, then the fused
     backward, against the numpy oracle (LayerNorm backward of dy GELU'(a))."""
@@ -507,7 +509,8 @@ def _mx_ref(kind, xs, rs, gs, bs, io):
 @pytest.mark.parametrize("kind", ["ln", "rms", "add_rms"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols,path", [
-    (64, 4096, "vec"), (33, 7168, "vec"), (9, 96, "vec"), (2, 16384, "vec"),
+    (64, 4096, "vec"), (33, 7168, "vec"), (9, 96, "vec"), (2, 16384, "vec"), (2, 32768, "vec"),
+    (3, 12288, "vec"),
     (13, 1024, "scalar"), (3, 2048, "loop")])
 def test_mxfp8_matrix(lib, monkeypatch, kind, dtype, rows, cols, path):
     """OCP MXFP8 outputs (codes + E8M0 block scales) of LayerNorm, RMSNorm and residual +
@@ -569,12 +572,13 @@ def test_mxfp8_rejects_widths_not_multiple_of_32(lib):
                                            None, 4, 64, capi.F32, 1e-5, capi.stream()) == 1
 
 
-def test_residual_gradient_is_added(lib):
-    gen = torch.Generator().manual_seed(9)
-    xc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
-    dyc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
-    drc = torch.randn(96, 2048, generator=gen).to(torch.bfloat16)
-    gc = (1 + 0.1 * torch.randn(2048, generator=gen)).to(torch.bfloat16)
+@pytest.mark.parametrize("rows,cols", [(96, 2048), (3, 12288), (5, 16384), (2, 32768)])
+def test_residual_gradient_is_added(lib, rows, cols):
+    gen = torch.Generator().manual_seed(9 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
+    dyc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
+    drc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16)
     x, dy, dr, g = cuda(xc), cuda(dyc), cuda(drc), cuda(gc)
     _, mean, rstd = ln_forward(lib, x, g, g, 1e-5)
     dx, _, _ = ln_backward(lib, dy, x, mean, rstd, g, want_params=False, dres=dr)
@@ -588,6 +592,35 @@ def test_residual_gradient_is_added(lib):
     dxr_ref = dxr_ref + f32(drc)
     assert_within_ulp(to_np(dxr), dxr_ref, 1.0, atol=DX_ATOL_REL * np.abs(dxr_ref).max(),
                       what="rms dx + dres")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", [(3, 12288), (5, 16384), (2, 32768), (4, 20480)])
+def test_add_layernorm_wide_rows(lib, dtype, rows, cols):
+    """Residual add + LayerNorm on rows of 12 to 16 waves and on the widest register tiles: h
+    is the rounded sum, y the LayerNorm of h (same bar as the plain forward)."""
+    gen = torch.Generator().manual_seed(rows * 17 + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, r, g, b = cuda(xc), cuda(rc), cuda(gc), cuda(bc)
+    h, y = torch.empty_like(x), torch.empty_like(x)
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    p = capi.ptr
+    capi.check(lib.fln_add_layernorm_forward(p(x), p(r), p(g), p(b), p(h), p(y), p(mean), p(rstd),
+                                             rows, cols, capi.dtype_code(x), 1e-5, capi.stream()))
+    torch.cuda.synchronize()
+    h_ref = (xc.float() + rc.float()).to(dtype)
+    assert torch.equal(h.cpu(), h_ref)
+    hs = f32(h_ref)
+    y_ref, _, _ = norms.layer_norm_fwd(hs, f32(gc), f32(bc), 1e-5)
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+    else:
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(hs, f32(gc), f32(bc), 1e-5),
+                          **_tol_fwd(dtype), what="y")
 
 
 def test_add_rmsnorm_bf16(lib):

@@ -532,7 +532,9 @@ def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay():
 @pytest.mark.parametrize("rows,cols,dtype", [
     (8192, 4096, torch.bfloat16), (32768, 7168, torch.bfloat16), (32, 768, torch.float32),
     (17, 1023, torch.float32), (64, 4096, torch.float32), (1, 100000, torch.float32),
-    (16384, 8192, torch.bfloat16), (5, 5120, torch.float16)])
+    (16384, 8192, torch.bfloat16), (5, 5120, torch.float16), (64, 12288, torch.bfloat16),
+    (64, 16384, torch.float16), (64, 32768, torch.bfloat16), (64, 16384, torch.float32),
+    (3, 20000, torch.float32), (64, 65536, torch.bfloat16)])
 def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeypatch):
     """functional.get_optimal_config restates the forward geometry rule; the dispatcher's own
     trace (FLN_DEBUG_GEOMETRY=1, one stderr line per launch) must agree with it."""

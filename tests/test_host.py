@@ -169,6 +169,16 @@ def test_optimal_config_reports_dispatch_geometry():
     assert (c7["waves_per_row"], c7["vectors_per_lane"], c7["threads_per_block"]) == (7, 2, 448)
     c2 = fl.functional.get_optimal_config(1, 100000, torch.float32)
     assert not c2["register_resident"]
+    # Rows of more than 4 waves: at most 16 elements per lane (1024-thread blocks have 128
+    # VGPRs), exact tilings within that cap, the 32-element tiles only past 16 waves.
+    geo = lambda c: (c["waves_per_row"], c["vectors_per_lane"], c["exact_tiling"],  # noqa: E731
+                     c["threads_per_block"])
+    assert geo(fl.functional.get_optimal_config(4096, 12288, torch.bfloat16)) == (12, 2, True, 768)
+    assert geo(fl.functional.get_optimal_config(4096, 16384, torch.bfloat16)) == (16, 2, True, 1024)
+    assert geo(fl.functional.get_optimal_config(2048, 32768, torch.bfloat16)) == (16, 4, True, 1024)
+    assert geo(fl.functional.get_optimal_config(4096, 16384, torch.float32)) == (16, 4, True, 1024)
+    assert geo(fl.functional.get_optimal_config(8192, 8192, torch.bfloat16)) == (4, 4, True, 256)
+    assert geo(fl.functional.get_optimal_config(4096, 8192, torch.float32)) == (4, 8, True, 256)
 
 
 def test_byte_model_matches_baseline_figures():
