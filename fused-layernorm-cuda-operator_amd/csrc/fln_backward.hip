@@ -340,6 +340,164 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   }
 }
 
+// fp32 rows wider than the register kernel holds (8193..16384 columns): one 1024-thread block
+// per row at a time, thread t owning vectors t + 1024 i
+// (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
+// register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
+// row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them
+// back and writes dx.  A thread reads back only the vectors it parked, so the staging needs no
+// barrier: LDS serves as per-thread spill space for the row (128 KiB at CPT 4).
+constexpr int kLdsThreads = 1024;
+
+template <class T, bool DRES, int GELU, int VEC, int CPT>
+__global__ __launch_bounds__(kLdsThreads) void bwd_lds_kernel(const BwdParams p) {
+  constexpr int kT = kLdsThreads;
+  constexpr int kW = kT / kWave;
+  using P = Pack<T, VEC>;
+  __shared__ P xs[CPT * kT], ds[CPT * kT];
+  __shared__ float red[2][2][kW + 16];  // [parity][sum g, sum g*xhat][wave], padded
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int64_t N = p.cols;
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const float inv_n = 1.0f / static_cast<float>(N);
+  const int64_t stride = gridDim.x;
+  const int iters = static_cast<int>((p.rows - 1 - blockIdx.x) / stride + 1);  // grid <= rows
+  const T* X = static_cast<const T*>(p.x);
+  const T* DY = static_cast<const T*>(p.dy);
+  const T* DR = static_cast<const T*>(p.dres);
+  T* DX = static_cast<T*>(p.dx);
+
+  P gmr[CPT];
+  P btr[GELU ? CPT : 1];
+  {
+    const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
+    const bool has_g = p.gamma != nullptr;
+    const T one = from_f32<T>(1.0f);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      gmr[i] = buf_load<P>(gr, t + i * kT);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if (!has_g) gmr[i].v[e] = one;
+    }
+    if constexpr (GELU != 0) {
+      const rsrc_t br = make_rsrc(p.beta, row_bytes);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) btr[i] = buf_load<P>(br, t + i * kT);
+    }
+  }
+  auto gam = [&](int i, int e) { return to_f32(gmr[i].v[e]); };
+  // Upstream gradient at the LayerNorm output: dy, or dy GELU'(xhat gamma + beta).
+  auto dln = [&](float d, float xh, int i, int e) {
+    if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam(i, e), to_f32(btr[i].v[e])));
+    if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam(i, e), to_f32(btr[i].v[e])));
+    return d;
+  };
+  float acc_g[CPT][VEC], acc_b[CPT][VEC];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc_g[i][e] = acc_b[i][e] = 0.0f;
+
+  // Raw loads of the next row (rows past the block's range read as zeros).
+  P xr[CPT], dr[CPT], rr[DRES ? CPT : 1];
+  float mun = 0.0f, rsn = 0.0f;
+  auto load_row = [&](int it) {
+    const int64_t row = static_cast<int64_t>(it) * stride + blockIdx.x;
+    const uint32_t nb = it < iters ? row_bytes : 0u;
+    const rsrc_t xq = make_rsrc(X + row * N, nb);
+    const rsrc_t dq = make_rsrc(DY + row * N, nb);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      xr[i] = buf_load<P, FLN_BWD_LOAD_POL>(xq, t + i * kT);
+      dr[i] = buf_load<P, FLN_BWD_LOAD_POL>(dq, t + i * kT);
+    }
+    if constexpr (DRES) {
+      const rsrc_t rq = make_rsrc(DR + row * N, nb);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) rr[i] = buf_load<P, FLN_BWD_LOAD_POL>(rq, t + i * kT);
+    }
+    const uint32_t sb = nb ? 4u : 0u;
+    mun = __builtin_bit_cast(
+        float, BufIO<4>::load(make_rsrc(p.rms ? nullptr : p.mean + row, sb), 0));
+    rsn = __builtin_bit_cast(float, BufIO<4>::load(make_rsrc(p.rstd + row, sb), 0));
+  };
+
+  load_row(0);
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row = static_cast<int64_t>(it) * stride + blockIdx.x;
+    const float mu = mun, rs = rsn;
+    // Pass A: column sums, row sums, park the raw row in LDS.
+    P rc[DRES ? CPT : 1];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      xs[i * kT + t] = xr[i];
+      ds[i * kT + t] = dr[i];
+      if constexpr (DRES) rc[i] = rr[i];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xh = (to_f32(xr[i].v[e]) - mu) * rs;
+        const float d = dln(to_f32(dr[i].v[e]), xh, i, e);
+        const float g = d * gam(i, e);
+        s1 += g;
+        s2 = fmaf(g, xh, s2);
+        acc_g[i][e] = fmaf(d, xh, acc_g[i][e]);
+        acc_b[i][e] += d;
+      }
+    }
+    load_row(it + 1);  // in flight during the reduction and pass B
+    s1 = wave_allreduce<SumOp>(s1);
+    s2 = wave_allreduce<SumOp>(s2);
+    {
+      float(*slot)[kW + 16] = red[it & 1];
+      if (lane == 0) {
+        slot[0][wave] = s1;
+        slot[1][wave] = s2;
+      }
+      __syncthreads();
+      s1 = combine_partials<SumOp>(slot[0], 0, kW, lane, 0.0f);
+      s2 = combine_partials<SumOp>(slot[1], 0, kW, lane, 0.0f);
+    }
+    const float cb = p.rms ? 0.0f : -rs * (s1 * inv_n);
+    const float cx = -rs * (s2 * inv_n);
+    // Pass B: dx from the parked row.
+    const rsrc_t xo = make_rsrc(DX ? DX + row * N : nullptr, row_bytes);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const P xv = xs[i * kT + t];
+      const P dv = ds[i * kT + t];
+      P o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xh = (to_f32(xv.v[e]) - mu) * rs;
+        const float d = dln(to_f32(dv.v[e]), xh, i, e);
+        float dxv = fmaf(d, rs * gam(i, e), fmaf(cx, xh, cb));
+        if constexpr (DRES) dxv += to_f32(rc[i].v[e]);
+        o.v[e] = from_f32<T>(dxv);
+      }
+      buf_store<P, FLN_BWD_STORE_POL>(o, xo, t + i * kT);
+    }
+  }
+
+  // Stage-1 output: one fp32 partial row per block (row stride ld, a multiple of 4).
+  const int64_t ld = (N + 3) & ~int64_t(3);
+  const int nvec = static_cast<int>(N / VEC);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int v = t + i * kT;
+    if (v >= nvec) continue;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const int64_t c = static_cast<int64_t>(blockIdx.x) * ld + static_cast<int64_t>(v) * VEC + e;
+      if (p.part_g) p.part_g[c] = acc_g[i][e];
+      if (p.part_b) p.part_b[c] = acc_b[i][e];
+    }
+  }
+}
+
 // Rows too long for the register path: one block per row chunk, three strided passes per row,
 // column partials accumulated in place in the block's partial row (each column is owned by one
 // thread of the block, so the read-modify-write is race free).
@@ -494,12 +652,38 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
   }
 }
 
+template <class T, int VEC, int CPT>
+int launch_lds(const BwdParams& p, int64_t blocks, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kLdsThreads);
+  if (p.gelu == 1)
+    hipLaunchKernelGGL((bwd_lds_kernel<T, false, 1, VEC, CPT>), grid, block, 0, s, p);
+  else if (p.gelu == 2)
+    hipLaunchKernelGGL((bwd_lds_kernel<T, false, 2, VEC, CPT>), grid, block, 0, s, p);
+  else if (p.dres)
+    hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VEC, CPT>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VEC, CPT>), grid, block, 0, s, p);
+  return static_cast<int>(hipGetLastError());
+}
+
 template <class T>
 int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
                       int64_t* resident = nullptr) {
   p.wpr = geo.wpr;
   p.rgs = geo.rgs;
   p.rows_per_block = geo.rows_per_block;
+  constexpr int VV = 16 / sizeof(T);
+  if (geo.lds_cpt > 0) {
+    if (resident) {
+      *resident = geo.blocks;  // one block per CU (the staged row fills most of the LDS)
+      return 0;
+    }
+    if constexpr (sizeof(T) == 4) {
+      if (geo.lds_cpt == 3) return launch_lds<T, VV, 3>(p, geo.blocks, s);
+      if (geo.lds_cpt == 4) return launch_lds<T, VV, 4>(p, geo.blocks, s);
+    }
+    return FLN_ERR_INVALID;
+  }
   if (!geo.reg_path) {
     if (resident) {
       *resident = geo.blocks;  // the looped kernel takes any grid
@@ -508,7 +692,6 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
     hipLaunchKernelGGL((bwd_loop_kernel<T>), dim3(geo.blocks), dim3(1024), 0, s, p);
     return static_cast<int>(hipGetLastError());
   }
-  constexpr int VV = 16 / sizeof(T);
   if (geo.vec == VV)
     return launch_stage1_vpl<T, VV>(p, geo.vpl, geo.blocks, geo.threads, s, resident);
   return launch_stage1_vpl<T, 1>(p, geo.vpl, geo.blocks, geo.threads, s, resident);
@@ -554,6 +737,20 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // The register path deals row groups out grid-stride over `blocks`; the looped fallback
   // gives each block a contiguous chunk of rows_per_block rows.
   g.blocks = g.reg_path ? blocks : (rows + g.rows_per_block - 1) / g.rows_per_block;
+  // fp32 rows too wide for registers but within 4 vectors per thread of a 1024-thread block
+  // (8193..16384 columns): the LDS-staged kernel, one block per CU, rows dealt grid-stride.
+  // (16-bit rows past 16384 columns would need 48-64 VGPRs of column sums per lane on top of
+  // the prefetched row and spill; they keep the looped kernel.)
+  const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
+  if (!g.reg_path && es == 4 && g.vec > 1 && cpt >= 3 && cpt <= 4 &&
+      env_int_b("FLN_BWD_NO_LDS", 0) == 0) {
+    g.lds_cpt = static_cast<int>(cpt);
+    g.threads = kLdsThreads;
+    g.wpr = kLdsThreads / kWave;
+    g.rgs = 1;
+    g.blocks = rows < device_cu_count() ? rows : device_cu_count();
+    g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
+  }
   return g;
 }
 

@@ -62,6 +62,7 @@ int launch_backward(const BwdParams& p, int dtype, void* dgamma, void* dbeta, in
 // Stage-1 geometry of the backward (shared by workspace sizing and the launch).
 struct BwdGeometry {
   bool reg_path;  // register-resident rows
+  int lds_cpt;    // > 0: rows staged through LDS, this many vectors per thread (reg_path false)
   int vec;        // elements per vector access
   int vpl;        // vectors per lane (power of two, <= 16)
   int wpr;        // waves per row

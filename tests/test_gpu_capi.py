@@ -594,6 +594,73 @@ def test_residual_gradient_is_added(lib, rows, cols):
                       what="rms dx + dres")
 
 
+@pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_none", "gelu_tanh"])
+@pytest.mark.parametrize("cols", [8196, 12288, 12292, 16384])
+def test_fp32_wide_row_backward(lib, monkeypatch, kind, cols):
+    """fp32 rows of 8193..16384 columns take the LDS-staged backward (one 1024-thread block per
+    row, several rows per block here): parity with the oracle for every flavour, dgamma/dbeta
+    bitwise reproducible, and agreement with the looped kernel those rows used before."""
+    rows = 600
+    gen = torch.Generator().manual_seed(cols * 3 + len(kind))
+    xc = torch.randn(rows, cols, generator=gen) * 2 + 0.5
+    gc = 1 + 0.1 * torch.randn(cols, generator=gen)
+    bc = 0.2 * torch.randn(cols, generator=gen)
+    dyc = torch.randn(rows, cols, generator=gen)
+    drc = torch.randn(rows, cols, generator=gen)
+    x, g, b, dy, dr = cuda(xc), cuda(gc), cuda(bc), cuda(dyc), cuda(drc)
+    xs, gs, bs, dys = xc.numpy(), gc.numpy(), bc.numpy(), dyc.numpy()
+    p = capi.ptr
+
+    def run():
+        if kind == "rms":
+            _, rs = rms_forward(lib, x, g, 1e-6)
+            dx, dw = rms_backward(lib, dy, x, rs, g)
+            return dx, dw, None
+        if kind.startswith("gelu"):
+            gm = capi.GELU_ERF if kind == "gelu_none" else capi.GELU_TANH
+            y = torch.empty_like(x)
+            mean = torch.empty(rows, device="cuda")
+            rstd = torch.empty(rows, device="cuda")
+            capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd),
+                                                      rows, cols, capi.F32, 1e-5, gm,
+                                                      capi.stream()))
+            dx = torch.empty_like(x)
+            dg = torch.empty(cols, device="cuda")
+            db = torch.empty(cols, device="cuda")
+            ws, n = workspace(lib, rows, cols, x)
+            capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b),
+                                                       p(dx), p(dg), p(db), rows, cols, capi.F32,
+                                                       capi.F32, gm, p(ws), n, capi.stream()))
+            return dx, dg, db
+        _, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+        return ln_backward(lib, dy, x, mean, rstd, g, dres=dr if kind == "ln_dres" else None)
+
+    dx, dg, db = run()
+    if kind == "rms":
+        dx_ref, dg_ref = norms.rms_norm_bwd(dys, xs, gs, 1e-6)
+    elif kind.startswith("gelu"):
+        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, kind[5:])
+    else:
+        dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
+        if kind == "ln_dres":
+            dx_ref = dx_ref + drc.numpy()
+    np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    if db is not None:
+        assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+    again = run()
+    for a, c in zip((dx, dg, db), again):
+        if a is not None:
+            assert torch.equal(a, c)
+    monkeypatch.setenv("FLN_BWD_NO_LDS", "1")
+    looped = run()
+    monkeypatch.delenv("FLN_BWD_NO_LDS")
+    for a, c in zip((dx, dg, db), looped):
+        if a is not None:
+            scale = float(c.abs().max())
+            assert float((a - c).abs().max()) <= 1e-5 * max(1.0, scale)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols", [(3, 12288), (5, 16384), (2, 32768), (4, 20480)])
 def test_add_layernorm_wide_rows(lib, dtype, rows, cols):
