@@ -340,9 +340,9 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   }
 }
 
-// fp32 rows wider than the register kernel holds (8193..16384 columns): one 1024-thread block
-// per row at a time, thread t owning vectors t + 1024 i
-// (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
+// Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384
+// columns; 16-bit rows of 8193..16384 columns with a residual gradient): one 1024-thread block
+// per row at a time, thread t owning vectors t + 1024 i (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them
 // back and writes dx.  A thread reads back only the vectors it parked, so the staging needs no
@@ -681,6 +681,12 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
     if constexpr (sizeof(T) == 4) {
       if (geo.lds_cpt == 3) return launch_lds<T, VV, 3>(p, geo.blocks, s);
       if (geo.lds_cpt == 4) return launch_lds<T, VV, 4>(p, geo.blocks, s);
+    } else {
+      if (geo.lds_cpt == 2 && p.dres && !p.gelu) {
+        hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VV, 2>), dim3(geo.blocks),
+                           dim3(kLdsThreads), 0, s, p);
+        return static_cast<int>(hipGetLastError());
+      }
     }
     return FLN_ERR_INVALID;
   }
@@ -699,7 +705,7 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
 
 }  // namespace
 
-BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok) {
+BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres) {
   BwdGeometry g{};
   const int es = element_size(dtype);
   const int vv = es > 0 ? 16 / es : 1;
@@ -740,10 +746,14 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // fp32 rows too wide for registers but within 4 vectors per thread of a 1024-thread block
   // (8193..16384 columns): the LDS-staged kernel, one block per CU, rows dealt grid-stride.
   // (16-bit rows past 16384 columns would need 48-64 VGPRs of column sums per lane on top of
-  // the prefetched row and spill; they keep the looped kernel.)
+  // the prefetched row and spill; they keep the looped kernel.)  16-bit rows of 8193..16384
+  // columns with a residual gradient also take it (2 vectors per thread): the register kernel
+  // spills there (measured 166 us against 123 us at 4096 x 16384 bf16).
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
-  if (!g.reg_path && es == 4 && g.vec > 1 && cpt >= 3 && cpt <= 4 &&
-      env_int_b("FLN_BWD_NO_LDS", 0) == 0) {
+  const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
+  const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
+  if (g.vec > 1 && (wide_f32 || dres16) && env_int_b("FLN_BWD_NO_LDS", 0) == 0) {
+    g.reg_path = false;
     g.lds_cpt = static_cast<int>(cpt);
     g.threads = kLdsThreads;
     g.wpr = kLdsThreads / kWave;
@@ -760,7 +770,7 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   BwdParams p = p0;
   const bool vec_ok = aligned16(p.x) && aligned16(p.dy) && aligned16(p.dx) &&
                       aligned16(p.gamma) && aligned16(p.dres);
-  BwdGeometry geo = backward_geometry(p.rows, p.cols, dtype, vec_ok);
+  BwdGeometry geo = backward_geometry(p.rows, p.cols, dtype, vec_ok, p.dres != nullptr);
   if (geo.reg_path) {
     // Never more blocks than fit at once: a second round of blocks would only add a tail.
     int64_t resident = geo.blocks;

@@ -71,6 +71,6 @@ struct BwdGeometry {
   int64_t blocks; // stage-1 blocks == partial rows
   int64_t rows_per_block;
 };
-BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok);
+BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres);
 
 }  // namespace fln

@@ -572,25 +572,30 @@ def test_mxfp8_rejects_widths_not_multiple_of_32(lib):
                                            None, 4, 64, capi.F32, 1e-5, capi.stream()) == 1
 
 
-@pytest.mark.parametrize("rows,cols", [(96, 2048), (3, 12288), (5, 16384), (2, 32768)])
-def test_residual_gradient_is_added(lib, rows, cols):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", [(96, 2048), (3, 12288), (5, 16384), (2, 32768),
+                                       (600, 12296)])
+def test_residual_gradient_is_added(lib, dtype, rows, cols):
+    """dx + dres for LayerNorm and RMSNorm; 16-bit rows of 8193..16384 columns take the
+    LDS-staged kernel (600 rows: several per block), wider ones the looped kernel."""
     gen = torch.Generator().manual_seed(9 + cols)
-    xc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
-    dyc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
-    drc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
-    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    drc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
     x, dy, dr, g = cuda(xc), cuda(dyc), cuda(drc), cuda(gc)
     _, mean, rstd = ln_forward(lib, x, g, g, 1e-5)
     dx, _, _ = ln_backward(lib, dy, x, mean, rstd, g, want_params=False, dres=dr)
     dx_ref, _, _ = norms.layer_norm_bwd(f32(dyc), f32(xc), f32(gc), 1e-5)
     dx_ref = dx_ref + f32(drc)
     assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
-                      what="dx + dres")
+                      kind="bf16" if dtype == torch.bfloat16 else "f16", what="dx + dres")
     _, rs = rms_forward(lib, x, g, 1e-6)
     dxr, _ = rms_backward(lib, dy, x, rs, g, dres=dr)
     dxr_ref, _ = norms.rms_norm_bwd(f32(dyc), f32(xc), f32(gc), 1e-6)
     dxr_ref = dxr_ref + f32(drc)
     assert_within_ulp(to_np(dxr), dxr_ref, 1.0, atol=DX_ATOL_REL * np.abs(dxr_ref).max(),
+                      kind="bf16" if dtype == torch.bfloat16 else "f16",
                       what="rms dx + dres")
 
 
