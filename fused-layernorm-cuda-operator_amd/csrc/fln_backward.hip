@@ -498,6 +498,155 @@ __global__ __launch_bounds__(kLdsThreads) void bwd_lds_kernel(const BwdParams p)
   }
 }
 
+// Rows past the register and LDS tiles (16-bit rows of more than 16384 columns, fp32 rows of
+// more than 16384, long rows on the scalar path), any width, in two streaming passes:
+//   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
+//     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
+//     rows grid-stride, four vectors per thread in flight per array;
+//   bwd_colpass_kernel: a thread owns one vector column; over a chunk of rows (four in flight)
+//     it writes dx from the row's statistics and accumulates dgamma / dbeta in registers, then
+//     writes one partial row per chunk for col_reduce_kernel.
+// 5 streams (x, dy twice, dx once) instead of 3, but every access is a coalesced vector stream
+// and no thread holds more than four vectors of a row.
+constexpr int kWideThreads = 256;
+constexpr int kWideUnroll = 4;
+
+template <class T, int GELU, int VEC>
+__global__ __launch_bounds__(kWideThreads) void bwd_rowstat_kernel(const BwdParams p,
+                                                                   float2* stats) {
+  using P = Pack<T, VEC>;
+  constexpr int kW = kWideThreads / kWave;
+  __shared__ float red[2][2][kW + 16];
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int64_t N = p.cols;
+  const int nvec = static_cast<int>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const T* X = static_cast<const T*>(p.x);
+  const T* DY = static_cast<const T*>(p.dy);
+  const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
+  const rsrc_t br = make_rsrc(p.beta, row_bytes);  // GELU only; absent beta reads as zeros
+  const bool has_g = p.gamma != nullptr;
+  int parity = 0;
+  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x, parity ^= 1) {
+    const rsrc_t xr = make_rsrc(X + row * N, row_bytes);
+    const rsrc_t dr = make_rsrc(DY + row * N, row_bytes);
+    const float mu = p.rms ? 0.0f : p.mean[row];
+    const float rs = p.rstd[row];
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int v0 = t; v0 < nvec; v0 += kWideUnroll * kWideThreads) {
+      P xv[kWideUnroll], dv[kWideUnroll], gv[kWideUnroll], bv[GELU ? kWideUnroll : 1];
+#pragma unroll
+      for (int u = 0; u < kWideUnroll; ++u) {  // vectors past the row read as zeros
+        const int v = v0 + u * kWideThreads;
+        xv[u] = buf_load<P, kStream>(xr, v);
+        dv[u] = buf_load<P, kStream>(dr, v);
+        gv[u] = buf_load<P>(gr, v);
+        if constexpr (GELU != 0) bv[u] = buf_load<P>(br, v);
+      }
+#pragma unroll
+      for (int u = 0; u < kWideUnroll; ++u)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float xh = (to_f32(xv[u].v[e]) - mu) * rs;
+          const float gam = has_g ? to_f32(gv[u].v[e]) : 1.0f;
+          float d = to_f32(dv[u].v[e]);
+          if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam, to_f32(bv[u].v[e])));
+          if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam, to_f32(bv[u].v[e])));
+          const float g = d * gam;
+          s1 += g;
+          s2 = fmaf(g, xh, s2);
+        }
+    }
+    s1 = wave_allreduce<SumOp>(s1);
+    s2 = wave_allreduce<SumOp>(s2);
+    float(*slot)[kW + 16] = red[parity];
+    if (lane == 0) {
+      slot[0][wave] = s1;
+      slot[1][wave] = s2;
+    }
+    __syncthreads();
+    s1 = combine_partials<SumOp>(slot[0], 0, kW, lane, 0.0f);
+    s2 = combine_partials<SumOp>(slot[1], 0, kW, lane, 0.0f);
+    if (t == 0) stats[row] = make_float2(s1, s2);
+  }
+}
+
+template <class T, bool DRES, int GELU, int VEC>
+__global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdParams p,
+                                                                   const float2* stats) {
+  using P = Pack<T, VEC>;
+  const int v = blockIdx.x * kWideThreads + threadIdx.x;  // this thread's vector column
+  const int64_t N = p.cols;
+  const int nvec = static_cast<int>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const float inv_n = 1.0f / static_cast<float>(N);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * p.rows_per_block;
+  const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
+  const T* X = static_cast<const T*>(p.x);
+  const T* DY = static_cast<const T*>(p.dy);
+  const T* DR = static_cast<const T*>(p.dres);
+  T* DX = static_cast<T*>(p.dx);
+  P gv = buf_load<P>(make_rsrc(p.gamma, row_bytes), v);
+  if (p.gamma == nullptr)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) gv.v[e] = from_f32<T>(1.0f);
+  P bv{};
+  if constexpr (GELU != 0) bv = buf_load<P>(make_rsrc(p.beta, row_bytes), v);
+  float acc_g[VEC], acc_b[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc_g[e] = acc_b[e] = 0.0f;
+  for (int64_t row = r0; row < r1; row += kWideUnroll) {
+    P xv[kWideUnroll], dv[kWideUnroll], rv[DRES ? kWideUnroll : 1];
+    float mu[kWideUnroll], rs[kWideUnroll], cb[kWideUnroll], cx[kWideUnroll];
+#pragma unroll
+    for (int u = 0; u < kWideUnroll; ++u) {
+      const bool in = row + u < r1;  // uniform
+      const int64_t r = in ? row + u : r1 - 1;
+      const uint32_t nb = in ? row_bytes : 0u;
+      xv[u] = buf_load<P, kStream>(make_rsrc(X + r * N, nb), v);
+      dv[u] = buf_load<P, kStream>(make_rsrc(DY + r * N, nb), v);
+      if constexpr (DRES) rv[u] = buf_load<P, kStream>(make_rsrc(DR + r * N, nb), v);
+      mu[u] = p.rms ? 0.0f : p.mean[r];
+      rs[u] = p.rstd[r];
+      const float2 st = stats[r];
+      cb[u] = p.rms ? 0.0f : -rs[u] * (st.x * inv_n);
+      cx[u] = -rs[u] * (st.y * inv_n);
+    }
+#pragma unroll
+    for (int u = 0; u < kWideUnroll; ++u) {
+      const bool in = row + u < r1;
+      const int64_t r = in ? row + u : r1 - 1;
+      P o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xh = (to_f32(xv[u].v[e]) - mu[u]) * rs[u];
+        const float gam = to_f32(gv.v[e]);
+        float d = to_f32(dv[u].v[e]);
+        if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam, to_f32(bv.v[e])));
+        if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam, to_f32(bv.v[e])));
+        float dxv = fmaf(d, rs[u] * gam, fmaf(cx[u], xh, cb[u]));
+        if constexpr (DRES) dxv += to_f32(rv[u].v[e]);
+        o.v[e] = from_f32<T>(dxv);
+        if (in) {  // rows past the chunk were read as zeros: d = 0, but keep the sums exact
+          acc_g[e] = fmaf(d, xh, acc_g[e]);
+          acc_b[e] += d;
+        }
+      }
+      buf_store<P, kStream>(o, make_rsrc(DX ? DX + r * N : nullptr, in ? row_bytes : 0u), v);
+    }
+  }
+  if (v >= nvec) return;
+  const int64_t ld = (N + 3) & ~int64_t(3);
+  const int64_t c = static_cast<int64_t>(blockIdx.y) * ld + static_cast<int64_t>(v) * VEC;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    if (p.part_g) p.part_g[c + e] = acc_g[e];
+    if (p.part_b) p.part_b[c + e] = acc_b[e];
+  }
+}
+
 // Rows too long for the register path: one block per row chunk, three strided passes per row,
 // column partials accumulated in place in the block's partial row (each column is owned by one
 // thread of the block, so the read-modify-write is race free).
@@ -652,6 +801,30 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
   }
 }
 
+template <class T, int VEC>
+int launch_two_pass(const BwdParams& p, const BwdGeometry& geo, hipStream_t s) {
+  float2* stats = reinterpret_cast<float2*>(p.rowstat);
+  const int64_t cap = 8 * static_cast<int64_t>(device_cu_count());
+  const dim3 g1(static_cast<unsigned>(p.rows < cap ? p.rows : cap)), blk(kWideThreads);
+  const int64_t nvec = p.cols / VEC;
+  const dim3 g2(static_cast<unsigned>((nvec + kWideThreads - 1) / kWideThreads),
+                static_cast<unsigned>(geo.blocks));
+  if (p.gelu == 1) {
+    hipLaunchKernelGGL((bwd_rowstat_kernel<T, 1, VEC>), g1, blk, 0, s, p, stats);
+    hipLaunchKernelGGL((bwd_colpass_kernel<T, false, 1, VEC>), g2, blk, 0, s, p, stats);
+  } else if (p.gelu == 2) {
+    hipLaunchKernelGGL((bwd_rowstat_kernel<T, 2, VEC>), g1, blk, 0, s, p, stats);
+    hipLaunchKernelGGL((bwd_colpass_kernel<T, false, 2, VEC>), g2, blk, 0, s, p, stats);
+  } else {
+    hipLaunchKernelGGL((bwd_rowstat_kernel<T, 0, VEC>), g1, blk, 0, s, p, stats);
+    if (p.dres)
+      hipLaunchKernelGGL((bwd_colpass_kernel<T, true, 0, VEC>), g2, blk, 0, s, p, stats);
+    else
+      hipLaunchKernelGGL((bwd_colpass_kernel<T, false, 0, VEC>), g2, blk, 0, s, p, stats);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
 template <class T, int VEC, int CPT>
 int launch_lds(const BwdParams& p, int64_t blocks, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(blocks)), block(kLdsThreads);
@@ -690,6 +863,14 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
     }
     return FLN_ERR_INVALID;
   }
+  if (geo.two_pass) {
+    if (resident) {
+      *resident = geo.blocks;  // partial rows = row chunks of the column pass
+      return 0;
+    }
+    if (geo.vec == VV) return launch_two_pass<T, VV>(p, geo, s);
+    return launch_two_pass<T, 1>(p, geo, s);
+  }
   if (!geo.reg_path) {
     if (resident) {
       *resident = geo.blocks;  // the looped kernel takes any grid
@@ -705,7 +886,13 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
 
 }  // namespace
 
-BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres) {
+int64_t workspace_partial_rows(int64_t rows) {
+  const int64_t g = 4 * static_cast<int64_t>(device_cu_count());
+  return rows < g ? rows : g;
+}
+
+BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres,
+                              bool have_workspace) {
   BwdGeometry g{};
   const int es = element_size(dtype);
   const int vv = es > 0 ? 16 / es : 1;
@@ -761,16 +948,32 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
     g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
   }
+  // Everything else (any width) in two streaming passes, given the workspace for the row
+  // statistics; without one (dx alone, no workspace passed) the looped kernel.  Row chunks of
+  // the column pass: enough that tiles x chunks fills the device ~8 blocks per CU, at most the
+  // workspace's partial rows.
+  if (!g.reg_path && g.lds_cpt == 0 && have_workspace &&
+      env_int_b("FLN_BWD_NO_TWO_PASS", 0) == 0) {
+    const int64_t tiles = (nvec + kWideThreads - 1) / kWideThreads;
+    int64_t chunks = (8 * static_cast<int64_t>(device_cu_count()) + tiles - 1) / tiles;
+    if (chunks > workspace_partial_rows(rows)) chunks = workspace_partial_rows(rows);
+    if (chunks < 1) chunks = 1;
+    g.two_pass = true;
+    g.threads = kWideThreads;
+    g.rows_per_block = (rows + chunks - 1) / chunks;
+    g.blocks = (rows + g.rows_per_block - 1) / g.rows_per_block;
+  }
   return g;
 }
 
 int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
-                    hipStream_t s) {
+                    bool have_workspace, hipStream_t s) {
   // p0.part_g / p0.part_b carry the workspace base (validated by the caller).
   BwdParams p = p0;
   const bool vec_ok = aligned16(p.x) && aligned16(p.dy) && aligned16(p.dx) &&
                       aligned16(p.gamma) && aligned16(p.dres);
-  BwdGeometry geo = backward_geometry(p.rows, p.cols, dtype, vec_ok, p.dres != nullptr);
+  BwdGeometry geo =
+      backward_geometry(p.rows, p.cols, dtype, vec_ok, p.dres != nullptr, have_workspace);
   if (geo.reg_path) {
     // Never more blocks than fit at once: a second round of blocks would only add a tail.
     int64_t resident = geo.blocks;
@@ -788,6 +991,8 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   float* ws = p0.part_g;
   p.part_g = dgamma ? ws : nullptr;
   p.part_b = dbeta ? ws + geo.blocks * ld : nullptr;
+  // Row statistics after the largest partial block (16-byte aligned: ld is a multiple of 4).
+  p.rowstat = have_workspace ? ws + 2 * workspace_partial_rows(p.rows) * ld : nullptr;
   ColReduceArgs a{};
   if (dgamma) { a.part[a.ny] = p.part_g; a.out[a.ny] = dgamma; ++a.ny; }
   if (dbeta) { a.part[a.ny] = p.part_b; a.out[a.ny] = dbeta; ++a.ny; }
@@ -831,13 +1036,11 @@ int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int 
   }
   if (!p.dy || !p.x || !p.rstd || (!p.rms && !p.mean)) return FLN_ERR_INVALID;
   if (!p.dx && !dgamma && !dbeta) return FLN_OK;
-  if (dgamma || dbeta) {
-    if (!workspace || !fln::aligned16(workspace) ||
-        workspace_bytes < fln_backward_workspace_bytes(p.rows, p.cols, dtype))
-      return FLN_ERR_INVALID;
-  }
-  p.part_g = static_cast<float*>(workspace);
-  return fln::launch_backward(p, dtype, dgamma, dbeta, dparam_dtype,
+  const bool have_workspace = workspace && fln::aligned16(workspace) &&
+                              workspace_bytes >= fln_backward_workspace_bytes(p.rows, p.cols, dtype);
+  if ((dgamma || dbeta) && !have_workspace) return FLN_ERR_INVALID;
+  p.part_g = have_workspace ? static_cast<float*>(workspace) : nullptr;
+  return fln::launch_backward(p, dtype, dgamma, dbeta, dparam_dtype, have_workspace,
                               static_cast<hipStream_t>(stream));
 }
 
@@ -846,10 +1049,11 @@ int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int 
 extern "C" size_t fln_backward_workspace_bytes(int64_t rows, int64_t cols, int dtype) {
   (void)dtype;
   if (rows <= 0 || cols <= 0) return 0;
-  int64_t g = 4 * static_cast<int64_t>(fln::device_cu_count());  // stage-1 blocks, upper bound
-  if (rows < g) g = rows;
+  // Two fp32 partial arrays of up to workspace_partial_rows rows, then the row statistics
+  // (2 floats per row) of the two-pass path.
+  const int64_t g = fln::workspace_partial_rows(rows);
   const int64_t ld = (cols + 3) & ~int64_t(3);
-  return static_cast<size_t>(2 * g * ld) * sizeof(float);
+  return static_cast<size_t>(2 * g * ld + 2 * rows) * sizeof(float);
 }
 
 extern "C" int fln_layernorm_backward(const void* dy, const void* x, const float* mean,

@@ -42,6 +42,7 @@ struct BwdParams {
   void* dx;           // or nullptr
   float* part_g;      // [blocks, cols] stage-1 partial of sum(dy * xhat), or nullptr
   float* part_b;      // [blocks, cols] stage-1 partial of sum(dy), or nullptr
+  float* rowstat;     // [rows, 2] row sums of g and g xhat (two-pass path), in the workspace
   int64_t rows;
   int64_t cols;
   int64_t rows_per_block;
@@ -57,12 +58,13 @@ bool aligned16(const void* p);
 
 int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s);
 int launch_backward(const BwdParams& p, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
-                    hipStream_t s);
+                    bool have_workspace, hipStream_t s);
 
 // Stage-1 geometry of the backward (shared by workspace sizing and the launch).
 struct BwdGeometry {
   bool reg_path;  // register-resident rows
   int lds_cpt;    // > 0: rows staged through LDS, this many vectors per thread (reg_path false)
+  bool two_pass;  // row statistics pass + column pass (rows past the register / LDS tiles)
   int vec;        // elements per vector access
   int vpl;        // vectors per lane (power of two, <= 16)
   int wpr;        // waves per row
@@ -71,6 +73,9 @@ struct BwdGeometry {
   int64_t blocks; // stage-1 blocks == partial rows
   int64_t rows_per_block;
 };
-BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres);
+BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres,
+                              bool have_workspace);
+// Partial rows the backward workspace holds (an upper bound on every path's stage-1 blocks).
+int64_t workspace_partial_rows(int64_t rows);
 
 }  // namespace fln

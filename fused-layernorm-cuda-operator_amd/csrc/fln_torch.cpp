@@ -397,6 +397,8 @@ std::tuple<Tensor, Tensor, Tensor> add_rms_norm_mxfp8_fwd(const Tensor& input,
 // Backward family.  Masked-off outputs come back as empty (0-element) tensors through the
 // operator schema and as None through the pybind `backward`.
 // ------------------------------------------------------------------------------------------
+// Always passed (also for dx alone): rows past the register kernels use it for their row
+// statistics, and torch's caching allocator makes it cheap.
 Tensor workspace_for(const Tensor& x, int64_t rows, int64_t cols) {
   const size_t bytes = fln_backward_workspace_bytes(rows, cols, dtype_code(x));
   return at::empty({static_cast<int64_t>((bytes + 3) / 4)}, x.options().dtype(at::kFloat));
@@ -430,7 +432,7 @@ std::tuple<Tensor, Tensor, Tensor> layer_norm_bwd(const Tensor& grad_out, const 
   Tensor dg = want_dg ? at::empty_like(*gamma) : at::empty({0}, input.options());
   Tensor db = want_db ? at::empty_like(*beta) : at::empty({0}, input.options());
   Tensor ws;
-  if (want_dg || want_db) ws = workspace_for(input, s.rows, s.cols);
+  ws = workspace_for(input, s.rows, s.cols);
   check(fln_layernorm_backward(grad_out.data_ptr(), input.data_ptr(), mean.data_ptr<float>(),
                                rstd.data_ptr<float>(), ptr_or_null(gamma),
                                ptr_or_null(grad_extra), want_dx ? dx.data_ptr() : nullptr,
@@ -468,7 +470,7 @@ std::tuple<Tensor, Tensor, Tensor> layer_norm_gelu_bwd(const Tensor& grad_out,
   Tensor dg = want_dg ? at::empty_like(*gamma) : at::empty({0}, input.options());
   Tensor db = want_db ? at::empty_like(*beta) : at::empty({0}, input.options());
   Tensor ws;
-  if (want_dg || want_db) ws = workspace_for(input, s.rows, s.cols);
+  ws = workspace_for(input, s.rows, s.cols);
   check(fln_layernorm_gelu_backward(grad_out.data_ptr(), input.data_ptr(),
                                     mean.data_ptr<float>(), rstd.data_ptr<float>(),
                                     ptr_or_null(gamma), ptr_or_null(beta),
@@ -517,7 +519,7 @@ std::tuple<Tensor, Tensor> rms_norm_bwd(const Tensor& grad_out, const Tensor& in
   Tensor dx = want_dx ? at::empty_like(input) : at::empty({0}, input.options());
   Tensor dw = want_dw ? at::empty_like(*weight) : at::empty({0}, input.options());
   Tensor ws;
-  if (want_dw) ws = workspace_for(input, s.rows, s.cols);
+  ws = workspace_for(input, s.rows, s.cols);
   check(fln_rmsnorm_backward(grad_out.data_ptr(), input.data_ptr(), rstd.data_ptr<float>(),
                              ptr_or_null(weight), ptr_or_null(grad_extra),
                              want_dx ? dx.data_ptr() : nullptr, want_dw ? dw.data_ptr() : nullptr,

@@ -63,7 +63,11 @@ int fln_layernorm_forward(const void* x, const void* gamma, const void* beta, vo
                           float* rstd, int64_t rows, int64_t cols, int dtype, float eps,
                           void* stream);
 
-/* Workspace (bytes) the backward entry points need for the two-stage column reduction. */
+/* Workspace (bytes) the backward entry points use: the two-stage column reduction's partial
+ * rows and, for rows wider than the register and LDS kernels hold (16-bit or fp32 rows of more
+ * than 16384 columns, long rows on the unaligned path), per-row statistics.  Required whenever
+ * dgamma / dbeta is requested; passing it for dx alone lets such rows take the two-pass
+ * kernels instead of the slower looped one. */
 size_t fln_backward_workspace_bytes(int64_t rows, int64_t cols, int dtype);
 
 /* LayerNorm backward.  dx = rstd (g - mean(g) - xhat mean(g xhat)), g = dy * gamma,

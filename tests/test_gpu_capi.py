@@ -666,6 +666,95 @@ def test_fp32_wide_row_backward(lib, monkeypatch, kind, cols):
             assert float((a - c).abs().max()) <= 1e-5 * max(1.0, scale)
 
 
+@pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_none", "gelu_tanh"])
+@pytest.mark.parametrize("dtype,cols", [(torch.float32, 20480), (torch.bfloat16, 24576),
+                                        (torch.float16, 40000), (torch.bfloat16, 20001)],
+                         ids=["f32-20480", "bf16-24576", "f16-40000", "bf16-20001-scalar"])
+def test_two_pass_backward(lib, monkeypatch, kind, dtype, cols):
+    """Rows past the register and LDS tiles take the two-pass backward (row statistics, then a
+    column pass over row chunks; 257 rows: several chunks): parity with the oracle for every
+    flavour, bitwise reproducible, and agreement with the looped kernel, which is also what a
+    dx-only call without a workspace uses."""
+    rows = 257
+    gen = torch.Generator().manual_seed(cols + 11 * len(kind))
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.2 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    drc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, b, dy, dr = cuda(xc), cuda(gc), cuda(bc), cuda(dyc), cuda(drc)
+    xs, gs, bs, dys = f32(xc), f32(gc), f32(bc), f32(dyc)
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    if kind == "rms":
+        _, rstd = rms_forward(lib, x, g, 1e-6)
+        mean = None
+    else:
+        mean = torch.empty(rows, device="cuda")
+        rstd = torch.empty(rows, device="cuda")
+        y = torch.empty_like(x)
+        if kind.startswith("gelu"):
+            gm = capi.GELU_ERF if kind == "gelu_none" else capi.GELU_TANH
+            capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd),
+                                                      rows, cols, code, 1e-5, gm, capi.stream()))
+        else:
+            capi.check(lib.fln_layernorm_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
+                                                 cols, code, 1e-5, capi.stream()))
+
+    def run(params=True, with_ws=True):
+        dx = torch.empty_like(x)
+        dg = torch.empty(cols, device="cuda") if params else None
+        db = torch.empty(cols, device="cuda") if params and kind != "rms" else None
+        ws, n = workspace(lib, rows, cols, x)
+        wsp, wsn = (p(ws), n) if with_ws else (None, 0)
+        if kind == "rms":
+            capi.check(lib.fln_rmsnorm_backward(p(dy), p(x), p(rstd), p(g), None, p(dx), p(dg),
+                                                rows, cols, code, capi.F32, wsp, wsn,
+                                                capi.stream()))
+        elif kind.startswith("gelu"):
+            capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b),
+                                                       p(dx), p(dg), p(db), rows, cols, code,
+                                                       capi.F32, gm, wsp, wsn, capi.stream()))
+        else:
+            capi.check(lib.fln_layernorm_backward(p(dy), p(x), p(mean), p(rstd), p(g),
+                                                  p(dr) if kind == "ln_dres" else None, p(dx),
+                                                  p(dg), p(db), rows, cols, code, capi.F32, wsp,
+                                                  wsn, capi.stream()))
+        torch.cuda.synchronize()
+        return dx, dg, db
+
+    dx, dg, db = run()
+    if kind == "rms":
+        dx_ref, dg_ref = norms.rms_norm_bwd(dys, xs, gs, 1e-6)
+    elif kind.startswith("gelu"):
+        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, kind[5:])
+    else:
+        dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
+        if kind == "ln_dres":
+            dx_ref = dx_ref + f32(drc)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          kind="bf16" if dtype == torch.bfloat16 else "f16", what="dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    if db is not None:
+        assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+    again = run()
+    for a, c in zip((dx, dg, db), again):
+        if a is not None:
+            assert torch.equal(a, c)
+    monkeypatch.setenv("FLN_BWD_NO_TWO_PASS", "1")
+    looped = run()
+    monkeypatch.delenv("FLN_BWD_NO_TWO_PASS")
+    dx_nows, _, _ = run(params=False, with_ws=False)
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10 if dtype == torch.float16 else 1e-5
+    for a, c in zip((dx, dg, db, dx), looped + (dx_nows,)):
+        if a is not None:
+            af, cf = a.float(), c.float()
+            assert float((af - cf).abs().max()) <= 2 * ulp * max(1.0, float(cf.abs().max()))
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols", [(3, 12288), (5, 16384), (2, 32768), (4, 20480)])
 def test_add_layernorm_wide_rows(lib, dtype, rows, cols):
