@@ -71,6 +71,9 @@ def parse():
                     help="(profiling child) launch WORKLOAD's forward and backward --iters "
                          "times each, then a device copy of known size, and exit")
     ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--traffic-configs", action="store_true",
+                    help="instead of the bench line: HBM traffic (two rocprofv3 counter passes "
+                         "each) and call times of every bandwidth-bound config (C3..C7, LN+GELU)")
     return ap.parse_args()
 
 
@@ -480,6 +483,45 @@ def gbs(nbytes, ms):
     return nbytes / (ms * 1e-3) / 1e9
 
 
+def traffic_configs(args):
+    """--traffic-configs: per bandwidth-bound config (C1 and C2 are latency-bound), the HBM bytes
+    of each forward / backward call from the counter passes, the call times, and both the
+    algorithmic and the HBM-traffic bandwidth.  One JSON object on stdout."""
+    names = [n for n in CONFIGS if not n.startswith(("c1_", "c2_"))]
+    traffic = {}
+    for n in names:  # counter passes first, in child processes, before this one touches the GPU
+        t, note = pmc_traffic(n)
+        traffic[n] = t if t else {"note": note}
+    import torch
+    import capi
+    from fused_layernorm.testing import WORKLOADS
+
+    lib = capi.load()
+    stream_obj = torch.cuda.current_stream()
+    stream = capi.stream()
+    out = {}
+    for n in names:
+        res = measure(lib, capi, torch, WORKLOADS[n], 100, args.warmup, stream, stream_obj)
+        entry = {}
+        for d in ("fwd", "bwd"):
+            ms = res.get(f"ms_{d}")
+            if ms is None:
+                continue
+            ab = res["bytes"][d]
+            tb = traffic[n].get(d)
+            entry[d] = {"us": round(ms * 1e3, 2), "algorithmic_bytes": ab,
+                        "algorithmic_gbs": round(gbs(ab, ms), 1), "traffic_bytes": tb,
+                        "hbm_gbs": round(gbs(tb, ms), 1) if tb else None,
+                        "traffic_over_algorithmic": round(tb / ab, 4) if tb else None}
+        if "note" in traffic[n]:
+            entry["traffic_note"] = traffic[n]["note"]
+        out[n] = entry
+    cal = next((t["calibration"] for t in traffic.values() if "calibration" in t), None)
+    print(json.dumps({"traffic_configs": out, "calibration": cal,
+                      "passes": "rocprofv3 --pmc FETCH_SIZE | WRITE_SIZE -- bench.py "
+                                "--kernel-loop <config> --iters 20"}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -489,6 +531,9 @@ def main():
         sys.exit(2)
     if args.kernel_loop:
         kernel_loop(args)
+        return
+    if args.traffic_configs:
+        traffic_configs(args)
         return
 
     # Counter passes first, in child processes, before this process touches the GPU.
