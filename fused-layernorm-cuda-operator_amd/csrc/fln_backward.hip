@@ -952,7 +952,8 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // statistics; without one (dx alone, no workspace passed) the looped kernel.  Row chunks of
   // the column pass: enough that tiles x chunks fills the device ~8 blocks per CU, at most the
   // workspace's partial rows.
-  if (!g.reg_path && g.lds_cpt == 0 && have_workspace &&
+  // (Buffer resources span at most 4 GiB: rows of 2 GiB or more keep the looped kernel.)
+  if (!g.reg_path && g.lds_cpt == 0 && have_workspace && cols * es < (int64_t(1) << 31) &&
       env_int_b("FLN_BWD_NO_TWO_PASS", 0) == 0) {
     const int64_t tiles = (nvec + kWideThreads - 1) / kWideThreads;
     int64_t chunks = (8 * static_cast<int64_t>(device_cu_count()) + tiles - 1) / tiles;
