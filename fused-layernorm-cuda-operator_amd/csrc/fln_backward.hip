@@ -733,11 +733,6 @@ namespace {
 // elements of a 16-bit type, 8 of fp32) on the vector path, 8 on the scalar path.
 constexpr int bwd_max_vpl(int vec, int es) { return vec == 1 ? 8 : 2; }
 
-int env_int_b(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
-}
-
 int next_pow2(int v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -903,19 +898,20 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // column accumulators and the prefetched raw rows of a lane's columns stay in registers;
   // fp32 rows with 8 per lane exceed the 128-VGPR budget of a 1024-thread block and spill);
   // more only for rows too wide for 16 waves.
-  const int epl = env_int_b("FLN_BWD_EPL", es == 4 ? 4 : 8);
+  const Tuning& tun = tuning();
+  const int epl = tun.bwd_epl > 0 ? tun.bwd_epl : (es == 4 ? 4 : 8);
   int cap = (epl >= g.vec ? epl : g.vec) / g.vec;
   if (cap > bwd_max_vpl(g.vec, es)) cap = bwd_max_vpl(g.vec, es);
   int wpr = 1;
   while (per_lane(wpr) > cap && wpr < 16) wpr *= 2;
   if (per_lane(wpr) > cap) cap = bwd_max_vpl(g.vec, es);
-  const int forced = env_int_b("FLN_BWD_WPR", 0);
+  const int forced = tun.bwd_wpr;
   if (forced >= 1 && forced <= 16 && (forced & (forced - 1)) == 0 && per_lane(forced) <= cap)
     wpr = forced;
   g.reg_path = per_lane(wpr) <= cap;
   g.wpr = g.reg_path ? wpr : 16;
   g.vpl = g.reg_path ? next_pow2(static_cast<int>(per_lane(wpr))) : 0;
-  int threads = env_int_b("FLN_BWD_THREADS", 1024);
+  int threads = tun.bwd_threads > 0 ? tun.bwd_threads : 1024;
   if (threads != 256 && threads != 512 && threads != 1024) threads = 1024;
   if (!g.reg_path) threads = 1024;
   if (threads < kWave * g.wpr) threads = kWave * g.wpr;
@@ -939,7 +935,7 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
   const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
-  if (g.vec > 1 && (wide_f32 || dres16) && env_int_b("FLN_BWD_NO_LDS", 0) == 0) {
+  if (g.vec > 1 && (wide_f32 || dres16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
     g.lds_cpt = static_cast<int>(cpt);
     g.threads = kLdsThreads;
@@ -954,7 +950,7 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // workspace's partial rows.
   // (Buffer resources span at most 4 GiB: rows of 2 GiB or more keep the looped kernel.)
   if (!g.reg_path && g.lds_cpt == 0 && have_workspace && cols * es < (int64_t(1) << 31) &&
-      env_int_b("FLN_BWD_NO_TWO_PASS", 0) == 0) {
+      tun.bwd_no_two_pass == 0) {
     const int64_t tiles = (nvec + kWideThreads - 1) / kWideThreads;
     int64_t chunks = (8 * static_cast<int64_t>(device_cu_count()) + tiles - 1) / tiles;
     if (chunks > workspace_partial_rows(rows)) chunks = workspace_partial_rows(rows);

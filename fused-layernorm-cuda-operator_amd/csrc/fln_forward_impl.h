@@ -471,11 +471,6 @@ inline int next_pow2(int v) {
   return p;
 }
 
-inline int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  return (s && *s) ? atoi(s) : dflt;
-}
-
 // Blocks of `kernel` that fit on the current device at once.
 template <class K>
 int64_t resident_blocks(K kernel, int threads, int* cache_per_device) {
@@ -498,7 +493,7 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   auto kernel = fwd_reg_kernel<T, FP8, RES, GELU, VEC, VPL, EXACT, MAXT>;
   static int occupancy_cache[2][64];  // per instantiation; [threads == MAXT][device]
   int64_t grid = resident_blocks(kernel, threads, occupancy_cache[threads == MAXT]);
-  const int forced = env_int("FLN_FWD_GRID_MULT", 0);
+  const int forced = tuning().fwd_grid_mult;
   if (forced > 0) grid = static_cast<int64_t>(forced) * device_cu_count();
   if (grid > row_blocks) grid = row_blocks;
   if (grid > kMaxGrid) grid = kMaxGrid;
@@ -643,11 +638,12 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(p.y) % VV == 0);
   else
     vec_ok = vec_ok && aligned16(p.y);
-  if (env_int("FLN_FORCE_LOOP", 0)) return launch_loop<T, float, FP8>(p, s);
+  const Tuning& tun = tuning();
+  if (tun.force_loop) return launch_loop<T, float, FP8>(p, s);
   const int vec = vec_ok ? VV : 1;
   // Elements per lane: at most 32 by default (measured best or equal on the 4096-8192-wide
   // benchmark rows); more waves per row beyond that.
-  const int epl = env_int("FLN_FWD_EPL", 32);
+  const int epl = tun.fwd_epl > 0 ? tun.fwd_epl : 32;
   int cap = (epl >= vec ? epl : vec) / vec;
   const int max_cap = vec_ok ? max_vpl<VV>() : max_vpl<1>();
   if (cap > max_cap) cap = max_cap;
@@ -657,8 +653,8 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   if (wide_cap > cap) wide_cap = cap;
   const int64_t nvec = N / vec;
   const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, max_cap, vec_ok,
-                                     env_int("FLN_FWD_WPR", 0));
-  if (env_int("FLN_DEBUG_GEOMETRY", 0))
+                                     tun.fwd_wpr);
+  if (tun.debug_geometry)
     fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
             "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
             cap, wide_cap,

@@ -4,6 +4,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <stdlib.h>
+
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -24,24 +27,71 @@ int element_size(int dtype) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// CU count of the current device, cached per device index.
+// CU count of the current device, cached per device index (lock-free after the first query;
+// two threads racing on the first query store the same value).
 int device_cu_count() {
-  static std::mutex mu;
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  std::lock_guard<std::mutex> lock(mu);
-  if (cache[dev] == 0) {
-    int cus = 0;
+  int cus = cache[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    cache[dev] = cus;
+    cache[dev].store(cus, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return cus;
+}
+
+// Tuning and debugging knobs: getenv scans the whole environment (~0.1 us each with ~100
+// variables), so the knobs are read once, at the first launch, into a snapshot that
+// fln_reload_tuning() replaces.  Replaced snapshots are never freed (a concurrent launch may
+// still be reading one; each is 40 bytes and only tests and tuning sweeps reload).
+namespace {
+int env_knob(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+
+Tuning read_tuning() {
+  Tuning t{};
+  t.force_loop = env_knob("FLN_FORCE_LOOP", 0);
+  t.fwd_epl = env_knob("FLN_FWD_EPL", 0);
+  t.fwd_wpr = env_knob("FLN_FWD_WPR", 0);
+  t.fwd_grid_mult = env_knob("FLN_FWD_GRID_MULT", 0);
+  t.debug_geometry = env_knob("FLN_DEBUG_GEOMETRY", 0);
+  t.bwd_epl = env_knob("FLN_BWD_EPL", 0);
+  t.bwd_wpr = env_knob("FLN_BWD_WPR", 0);
+  t.bwd_threads = env_knob("FLN_BWD_THREADS", 0);
+  t.bwd_no_lds = env_knob("FLN_BWD_NO_LDS", 0);
+  t.bwd_no_two_pass = env_knob("FLN_BWD_NO_TWO_PASS", 0);
+  return t;
+}
+
+std::atomic<const Tuning*> g_tuning{nullptr};
+std::mutex g_tuning_mu;
+}  // namespace
+
+const Tuning& tuning() {
+  const Tuning* t = g_tuning.load(std::memory_order_acquire);
+  if (t) return *t;
+  std::lock_guard<std::mutex> lock(g_tuning_mu);
+  t = g_tuning.load(std::memory_order_acquire);
+  if (!t) {
+    t = new Tuning(read_tuning());
+    g_tuning.store(t, std::memory_order_release);
+  }
+  return *t;
+}
+
+void reload_tuning() {
+  std::lock_guard<std::mutex> lock(g_tuning_mu);
+  g_tuning.store(new Tuning(read_tuning()), std::memory_order_release);
 }
 
 }  // namespace fln
+
+extern "C" void fln_reload_tuning(void) { fln::reload_tuning(); }
 
 // Same estimate as the reference's get_memory_usage (csrc/layernorm_cuda.cpp:144-164):
 // forward in/out + fp32 mean/rstd, backward grad_input + grad_gamma/beta, plus a per-row

@@ -56,6 +56,22 @@ int element_size(int dtype);
 int device_cu_count();
 bool aligned16(const void* p);
 
+// FLN_* tuning / debugging environment variables (0 = unset: the built-in default).
+struct Tuning {
+  int force_loop;      // FLN_FORCE_LOOP: forward through the looped kernel
+  int fwd_epl;         // FLN_FWD_EPL: forward elements per lane for rows of up to 4 waves
+  int fwd_wpr;         // FLN_FWD_WPR: forward waves per row
+  int fwd_grid_mult;   // FLN_FWD_GRID_MULT: forward grid = this many blocks per CU
+  int debug_geometry;  // FLN_DEBUG_GEOMETRY: one stderr line per forward launch
+  int bwd_epl;         // FLN_BWD_EPL: backward elements per lane
+  int bwd_wpr;         // FLN_BWD_WPR: backward waves per row
+  int bwd_threads;     // FLN_BWD_THREADS: backward block size (256, 512, 1024)
+  int bwd_no_lds;      // FLN_BWD_NO_LDS: never the LDS-staged backward
+  int bwd_no_two_pass; // FLN_BWD_NO_TWO_PASS: never the two-pass backward
+};
+const Tuning& tuning();  // read at the first call; fln_reload_tuning() reads again
+void reload_tuning();
+
 int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s);
 int launch_backward(const BwdParams& p, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
                     bool have_workspace, hipStream_t s);

@@ -60,6 +60,7 @@ SIGNATURES = {
     "fln_version": ([], ctypes.c_char_p),
     "fln_hip_version": ([], _i32),
     "fln_error_string": ([_i32], ctypes.c_char_p),
+    "fln_reload_tuning": ([], None),
 }
 
 
@@ -82,6 +83,12 @@ def load():
             fn.restype = res
         _lib = lib
     return _lib
+
+
+def reload_tuning():
+    """Make libfln re-read its FLN_* environment knobs (read once per process otherwise); call
+    after setting or clearing one."""
+    load().fln_reload_tuning()
 
 
 def dtype_code(t):

@@ -32,3 +32,8 @@ def _announce(request):
     if request.node.get_closest_marker("gpu") is not None:
         print(f"\n[gpu-test] {request.node.nodeid}", flush=True)
     yield
+    # libfln reads its FLN_* knobs once; after monkeypatch has restored the environment (this
+    # fixture is torn down after it), re-read them so no test leaves a knob set behind.
+    import capi
+    if capi._lib is not None:
+        capi.reload_tuning()

@@ -535,10 +535,12 @@ def test_mxfp8_matrix(lib, monkeypatch, kind, dtype, rows, cols, path):
     h = torch.empty(rows, cols, device="cuda", dtype=dtype)
     if path == "loop":
         monkeypatch.setenv("FLN_FORCE_LOOP", "1")
+        capi.reload_tuning()
     capi.check(_mx_call(lib, kind, xd, rd, g, b if kind == "ln" else None, q, sc, h, rows, cols,
                         capi.dtype_code(xd)))
     torch.cuda.synchronize()
     monkeypatch.delenv("FLN_FORCE_LOOP", raising=False)
+    capi.reload_tuning()
     io = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
     q_ref, sc_ref, y_ref = _mx_ref(kind, f32(xc), f32(rc), f32(gc), f32(bc), io)
     if kind == "add_rms":
@@ -658,8 +660,10 @@ def test_fp32_wide_row_backward(lib, monkeypatch, kind, cols):
         if a is not None:
             assert torch.equal(a, c)
     monkeypatch.setenv("FLN_BWD_NO_LDS", "1")
+    capi.reload_tuning()
     looped = run()
     monkeypatch.delenv("FLN_BWD_NO_LDS")
+    capi.reload_tuning()
     for a, c in zip((dx, dg, db), looped):
         if a is not None:
             scale = float(c.abs().max())
@@ -745,8 +749,10 @@ def test_two_pass_backward(lib, monkeypatch, kind, dtype, cols):
         if a is not None:
             assert torch.equal(a, c)
     monkeypatch.setenv("FLN_BWD_NO_TWO_PASS", "1")
+    capi.reload_tuning()
     looped = run()
     monkeypatch.delenv("FLN_BWD_NO_TWO_PASS")
+    capi.reload_tuning()
     dx_nows, _, _ = run(params=False, with_ws=False)
     ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10 if dtype == torch.float16 else 1e-5
     for a, c in zip((dx, dg, db, dx), looped + (dx_nows,)):
@@ -807,8 +813,10 @@ def test_looped_fallback_matches_register_path(lib, monkeypatch):
     x, g = cuda(xc), cuda(gc)
     y_reg, m_reg, r_reg = ln_forward(lib, x, g, g, 1e-5)
     monkeypatch.setenv("FLN_FORCE_LOOP", "1")
+    capi.reload_tuning()
     y_loop, m_loop, r_loop = ln_forward(lib, x, g, g, 1e-5)
     monkeypatch.delenv("FLN_FORCE_LOOP")
+    capi.reload_tuning()
     ref, _, _ = norms.layer_norm_fwd(xc.numpy(), gc.numpy(), gc.numpy(), 1e-5)
     assert np.abs(to_np(y_loop) - ref).max() <= 1e-5 * np.abs(ref).max()
     assert np.abs(to_np(y_reg) - ref).max() <= 1e-5 * np.abs(ref).max()

@@ -539,13 +539,16 @@ def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeyp
     """functional.get_optimal_config restates the forward geometry rule; the dispatcher's own
     trace (FLN_DEBUG_GEOMETRY=1, one stderr line per launch) must agree with it."""
     import re
+    import capi
     x = torch.randn(rows, cols, device=DEV, dtype=dtype)
     w = torch.ones(cols, device=DEV, dtype=dtype)
     capfd.readouterr()
     monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
     fused_layernorm_cuda.layernorm(x, w, w, 1e-5)
     torch.cuda.synchronize()
     monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
     line = capfd.readouterr().err.strip().splitlines()[-1]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     cfg = fl.functional.get_optimal_config(rows, cols, dtype, num_cus=cus)
