@@ -359,6 +359,200 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 }
 
 // ---------------------------------------------------------------------------------------------
+// Rows past the register tiles on the vector path (16-bit rows of 32769..65536 columns, fp32 rows
+// of 16385..32768): one 1024-thread block per row at a time, rows grid-stride, thread t owning
+// vectors t + 1024 i (i < CPT) of every row.  The next row's raw loads are in flight in
+// registers while the current row is worked on; the row itself (the rounded residual sum with
+// RES) is parked in LDS, each thread in its own slots, so reading it back needs no barrier.
+// The mean, the centred sum of squares, the fp8 row maximum and the outputs are then passes
+// over LDS: x (and the residual) come from HBM once; gamma / beta are re-read per row (L2).
+// ---------------------------------------------------------------------------------------------
+constexpr int kFwdLdsThreads = 1024;
+constexpr int kFwdLdsCpt = 8;  // vectors per thread: 128 KiB of LDS
+
+template <class T, int FP8, bool RES, int GELU, int VEC>
+__global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams p) {
+  constexpr int kT = kFwdLdsThreads;
+  constexpr int CPT = kFwdLdsCpt;
+  constexpr int kW = kT / kWave;
+  using P = Pack<T, VEC>;
+  using QW = typename BufIO<VEC>::W;  // VEC fp8 codes (VEC is 4 or 8 here)
+  __shared__ P xs[CPT * kT];
+  __shared__ float red[2][3][kW + 16];  // [parity][sum, centred sum of squares, max][wave]
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int64_t N = p.cols;
+  const int nvec = static_cast<int>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const float fn = static_cast<float>(N);
+  const float inv_n = 1.0f / fn;
+  const int64_t stride = gridDim.x;
+  const int iters = static_cast<int>((p.rows - 1 - blockIdx.x) / stride + 1);  // grid <= rows
+  const T* X = static_cast<const T*>(p.x);
+  const T* R = static_cast<const T*>(p.res);
+  const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
+  const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
+  const bool has_g = p.gamma != nullptr;
+
+  P xr[CPT], rr[RES ? CPT : 1];
+  auto load_row = [&](int it) {  // rows past the block's range read as zeros
+    const int64_t row = static_cast<int64_t>(it) * stride + blockIdx.x;
+    const uint32_t nb = it < iters ? row_bytes : 0u;
+    const rsrc_t xq = make_rsrc(X + row * N, nb);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) xr[i] = buf_load<P, FLN_FWD_LOAD_POL>(xq, t + i * kT);
+    if constexpr (RES) {
+      const rsrc_t rq = make_rsrc(R + row * N, nb);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) rr[i] = buf_load<P, FLN_FWD_LOAD_POL>(rq, t + i * kT);
+    }
+  };
+
+  load_row(0);
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row = static_cast<int64_t>(it) * stride + blockIdx.x;
+    float(*slots)[kW + 16] = red[it & 1];
+    // Pass A: park the row in LDS (writing h with RES), plain sum.
+    const rsrc_t hr = make_rsrc(RES && p.h ? static_cast<T*>(p.h) + row * N : nullptr, row_bytes);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      P v = xr[i];
+      if constexpr (RES) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          v.v[e] = from_f32<T>(to_f32(xr[i].v[e]) + to_f32(rr[i].v[e]));
+        buf_store<P, FLN_FWD_STORE_POL>(v, hr, t + i * kT);
+      }
+      xs[i * kT + t] = v;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += to_f32(v.v[e]);
+    }
+    load_row(it + 1);  // in flight during the passes over LDS
+    float mean = 0.0f;
+    if (!p.rms) {
+      const float sum = row_allreduce<SumOp>(s, slots[0], kW, 0, wave, lane);
+      mean = sum * inv_n;
+      mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
+    }
+    // Pass B: centred sum of squares (vectors past the row left out).
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const P v = xs[i * kT + t];
+      if (t + i * kT < nvec) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float d = to_f32(v.v[e]) - mean;
+          q = fmaf(d, d, q);
+        }
+      }
+    }
+    q = row_allreduce<SumOp>(q, slots[1], kW, 0, wave, lane);
+    const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
+
+    // Output element e of vector i of the row.
+    auto affine = [&](int i, int e, const P& xv, const P& gv, const P& bv) -> float {
+      (void)i;
+      float a = fmaf((to_f32(xv.v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
+                     to_f32(bv.v[e]));
+      if constexpr (GELU == 1) a = gelu_erf(a);
+      if constexpr (GELU == 2) a = gelu_tanh(a);
+      return a;
+    };
+    // Pass C: outputs.
+    if constexpr (FP8 == 0) {
+      const rsrc_t yr = make_rsrc(static_cast<T*>(p.y) + row * N, row_bytes);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int v = t + i * kT;
+        const P xv = xs[i * kT + t];
+        const P gv = buf_load<P>(g_rs, v);
+        const P bv = buf_load<P>(b_rs, v);
+        P o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(affine(i, e, xv, gv, bv));
+        buf_store<P, FLN_FWD_STORE_POL>(o, yr, v);
+      }
+    } else {
+      const rsrc_t qr = make_rsrc(static_cast<uint8_t*>(p.y) + row * N, static_cast<uint32_t>(N));
+      auto codes = [&](const float* a, float m, bool in_range) -> QW {
+        QW w;
+        if constexpr (VEC == 8) {
+          w.x = in_range ? fp8x4_inrange(a[0] * m, a[1] * m, a[2] * m, a[3] * m)
+                         : fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
+          w.y = in_range ? fp8x4_inrange(a[4] * m, a[5] * m, a[6] * m, a[7] * m)
+                         : fp8x4(a[4] * m, a[5] * m, a[6] * m, a[7] * m);
+        } else {
+          w = in_range ? fp8x4_inrange(a[0] * m, a[1] * m, a[2] * m, a[3] * m)
+                       : fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
+        }
+        return w;
+      };
+      if constexpr (FP8 == 2) {
+        // OCP MX: a 32-element block is G adjacent lanes' vectors (cols % 32 == 0).
+        constexpr int G = 32 / VEC;
+        const uint32_t nblk = static_cast<uint32_t>(N / 32);
+        const rsrc_t br = make_rsrc(p.bscale + row * nblk, nblk);
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const int v = t + i * kT;
+          const P xv = xs[i * kT + t];
+          const P gv = buf_load<P>(g_rs, v);
+          const P bv = buf_load<P>(b_rs, v);
+          float a[VEC];
+          float bm = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            a[e] = affine(i, e, xv, gv, bv);
+            bm = fmaxf(bm, fabsf(a[e]));
+          }
+          const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+          BufIO<VEC, FLN_FWD_STORE_POL>::store(codes(a, ms.mul, false), qr,
+                                               static_cast<uint32_t>(v) * VEC);
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(ms.code), br,
+                                               v % G == 0 ? v / G : kOutOfRange, 0, 0);
+        }
+      } else {
+        // Per-row scale: the row maximum first (vectors past the row left out), then codes.
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const int v = t + i * kT;
+          const P xv = xs[i * kT + t];
+          const P gv = buf_load<P>(g_rs, v);
+          const P bv = buf_load<P>(b_rs, v);
+          if (v < nvec) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) am = fmaxf(am, fabsf(affine(i, e, xv, gv, bv)));
+          }
+        }
+        am = row_allreduce<MaxOp>(am, slots[2], kW, 0, wave, lane);
+        const float inv = am > 0.0f ? 448.0f / am : 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const int v = t + i * kT;
+          const P xv = xs[i * kT + t];
+          const P gv = buf_load<P>(g_rs, v);
+          const P bv = buf_load<P>(b_rs, v);
+          float a[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) a[e] = affine(i, e, xv, gv, bv);
+          // |a * inv| <= 448 (1 + 2^-23): in range for the unclamped conversion.
+          BufIO<VEC, FLN_FWD_STORE_POL>::store(codes(a, inv, true), qr,
+                                               static_cast<uint32_t>(v) * VEC);
+        }
+        buf_store_f32(am / 448.0f, make_rsrc(p.scale + row, 4u), t == 0 ? 0u : kOutOfRange);
+      }
+    }
+    const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
+    buf_store_f32(mean, make_rsrc(p.mean ? p.mean + row : nullptr, 4u), stat_off);
+    buf_store_f32(rstd, make_rsrc(p.rstd ? p.rstd + row : nullptr, 4u), stat_off);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Looped fallback: one block per row, any length, any alignment; A is the accumulation type
 // (fp32, or fp64 for fp64 I/O).  Same two-pass statistics as the register path.
 // ---------------------------------------------------------------------------------------------
@@ -553,6 +747,23 @@ int launch_reg_flavour(const FwdParams& p, int vpl, bool exact, int threads, hip
   return launch_reg_vpl<T, FP8, false, 0, VEC>(p, vpl, exact, threads, s);
 }
 
+template <class T, int FP8, int VEC>
+int launch_lds(const FwdParams& p, hipStream_t s) {
+  int64_t grid = device_cu_count();  // one block per CU: the parked row fills most of the LDS
+  if (grid > p.rows) grid = p.rows;
+  const dim3 g(static_cast<unsigned>(grid)), b(kFwdLdsThreads);
+  if (p.res) {
+    hipLaunchKernelGGL((fwd_lds_kernel<T, FP8, true, 0, VEC>), g, b, 0, s, p);
+  } else if (FP8 == 0 && p.gelu == FLN_GELU_ERF) {
+    hipLaunchKernelGGL((fwd_lds_kernel<T, 0, false, 1, VEC>), g, b, 0, s, p);
+  } else if (FP8 == 0 && p.gelu == FLN_GELU_TANH) {
+    hipLaunchKernelGGL((fwd_lds_kernel<T, 0, false, 2, VEC>), g, b, 0, s, p);
+  } else {
+    hipLaunchKernelGGL((fwd_lds_kernel<T, FP8, false, 0, VEC>), g, b, 0, s, p);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
 template <class T, class A, int FP8>
 int launch_loop(const FwdParams& p, hipStream_t s) {
   const int threads = p.cols >= 4096 ? 1024 : 256;
@@ -651,14 +862,22 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   // within the 128 VGPRs of a 1024-thread block.
   int wide_cap = vec_ok ? 16 / VV : 8;
   if (wide_cap > cap) wide_cap = cap;
+  // The 32-element RAW tiles only for 16-bit types (fp32 ones would hold 64 VGPRs of gamma /
+  // beta alone and spill); wider fp32 rows go to the LDS-staged kernel.
+  const int raw_cap = (vec_ok && VV < 8) ? wide_cap : max_cap;
   const int64_t nvec = N / vec;
-  const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, max_cap, vec_ok,
+  const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, raw_cap, vec_ok,
                                      tun.fwd_wpr);
+  // Rows past the register tiles: the LDS-staged kernel on the vector path (up to 8 vectors
+  // per thread of a 1024-thread block), the looped kernel otherwise.
+  const bool lds = g.loop && vec_ok && nvec <= int64_t(kFwdLdsCpt) * kFwdLdsThreads &&
+                   !tun.fwd_no_lds;
   if (tun.debug_geometry)
     fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
             "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
-            cap, wide_cap,
-            g.loop ? "loop" : "registers", g.wpr, g.vpl, static_cast<int>(g.exact), g.threads);
+            cap, wide_cap, lds ? "lds" : g.loop ? "loop" : "registers", g.wpr, g.vpl,
+            static_cast<int>(g.exact), g.threads);
+  if (lds) return launch_lds<T, FP8, VV>(p, s);
   if (g.loop) return launch_loop<T, float, FP8>(p, s);
   p.wpr = g.wpr;
   const int vpl = g.vpl;

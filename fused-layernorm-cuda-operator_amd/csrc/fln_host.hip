@@ -46,7 +46,7 @@ int device_cu_count() {
 // Tuning and debugging knobs: getenv scans the whole environment (~0.1 us each with ~100
 // variables), so the knobs are read once, at the first launch, into a snapshot that
 // fln_reload_tuning() replaces.  Replaced snapshots are never freed (a concurrent launch may
-// still be reading one; each is 40 bytes and only tests and tuning sweeps reload).
+// still be reading one; each is 44 bytes and only tests and tuning sweeps reload).
 namespace {
 int env_knob(const char* name, int dflt) {
   const char* v = getenv(name);
@@ -60,6 +60,7 @@ Tuning read_tuning() {
   t.fwd_wpr = env_knob("FLN_FWD_WPR", 0);
   t.fwd_grid_mult = env_knob("FLN_FWD_GRID_MULT", 0);
   t.debug_geometry = env_knob("FLN_DEBUG_GEOMETRY", 0);
+  t.fwd_no_lds = env_knob("FLN_FWD_NO_LDS", 0);
   t.bwd_epl = env_knob("FLN_BWD_EPL", 0);
   t.bwd_wpr = env_knob("FLN_BWD_WPR", 0);
   t.bwd_threads = env_knob("FLN_BWD_THREADS", 0);

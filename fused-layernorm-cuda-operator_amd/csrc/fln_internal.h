@@ -63,6 +63,7 @@ struct Tuning {
   int fwd_wpr;         // FLN_FWD_WPR: forward waves per row
   int fwd_grid_mult;   // FLN_FWD_GRID_MULT: forward grid = this many blocks per CU
   int debug_geometry;  // FLN_DEBUG_GEOMETRY: one stderr line per forward launch
+  int fwd_no_lds;      // FLN_FWD_NO_LDS: never the LDS-staged forward
   int bwd_epl;         // FLN_BWD_EPL: backward elements per lane
   int bwd_wpr;         // FLN_BWD_WPR: backward waves per row
   int bwd_threads;     // FLN_BWD_THREADS: backward block size (256, 512, 1024)

@@ -101,12 +101,16 @@ def get_optimal_config(batch_size: int, hidden_size: int,
     max_cap = 32 // vv if vec_path else 16
     cap = min(max(32, vec) // vec, max_cap)
     wide_cap = min(16 // vv if vec_path else 8, cap)
-    loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, wide_cap, max_cap,
+    raw_cap = wide_cap if (vec_path and vv < 8) else max_cap  # RAW tiles: 16-bit types only
+    loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, wide_cap, raw_cap,
                                                        vec_path, num_cus)
+    # Rows past the register tiles: parked in LDS (vector path, <= 8 vectors per thread of a
+    # 1024-thread block), else the looped kernel.
+    lds = loop and vec_path and nvec <= 8 * 1024
     return {
         "use_mixed_precision": dtype in (torch.float16, torch.bfloat16),
         "threads_per_block": threads,
-        "enable_persistent_kernel": not loop,  # register path: persistent grid-stride rows
+        "enable_persistent_kernel": not loop or lds,  # persistent grid-stride rows
         "use_vectorized_load": vec > 1,
         "use_tensor_cores": False,  # bandwidth-bound: no MFMA on this path
         "waves_per_row": wpr if not loop else None,
@@ -114,6 +118,8 @@ def get_optimal_config(batch_size: int, hidden_size: int,
         "vectors_per_lane": vpl if not loop else None,
         "exact_tiling": exact,
         "register_resident": not loop,
+        "lds_staged": lds,
+        "threads_lds": 1024 if lds else None,
     }
 
 

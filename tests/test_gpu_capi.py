@@ -215,7 +215,8 @@ def test_edge_shapes_fp32(lib, rows, cols):
 
 DTYPES = [torch.float32, torch.bfloat16, torch.float16]
 SHAPES = [(1, 768), (8, 768), (32, 1024), (64, 2048), (128, 4096), (3, 1023), (5, 5120),
-          (4, 16384), (2, 32768), (33, 7168), (7, 96), (5, 12288), (300, 20480)]
+          (4, 16384), (2, 32768), (33, 7168), (7, 96), (5, 12288), (300, 20480), (3, 40960),
+          (2, 65536), (260, 36864)]
 
 
 def _tol_fwd(dtype):
@@ -376,10 +377,11 @@ def _scaled(y):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
                          ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 1023), (33, 7168), (2, 16384),
-                                       (3, 12288), (2, 32768)])
+                                       (3, 12288), (2, 32768), (2, 40960), (300, 65536)])
 def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
-    """RMSNorm -> fp8, residual + LayerNorm -> fp8, residual + RMSNorm -> fp8 over dtypes and
-    widths (1023: the scalar path; 16384: a wide row), against the numpy oracle."""
+    """LayerNorm -> fp8, RMSNorm -> fp8, residual + LayerNorm -> fp8, residual + RMSNorm -> fp8
+    over dtypes and widths (1023: the scalar path; 12288..32768: 12-16 waves and the RAW tiles;
+    40960 / 65536: the LDS-staged kernel, 300 rows: several per block), against the oracle."""
     gen = torch.Generator().manual_seed(rows * 31 + cols)
     xc = torch.randn(rows, cols, generator=gen).to(dtype)
     rc = torch.randn(rows, cols, generator=gen).to(dtype)
@@ -397,6 +399,11 @@ def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
     q_ref, s_ref = norms.rms_norm_fp8_fwd(f32(xc), f32(gc), 1e-6)
     assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "rms fp8",
                      t_ref=_scaled(norms.rms_norm_fwd(f32(xc), f32(gc), 1e-6)[0]))
+    capi.check(lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(q), p(s), None, None, rows,
+                                             cols, code, 1e-5, capi.stream()))
+    q_ref, s_ref = norms.layer_norm_fp8_fwd(f32(xc), f32(gc), f32(bc), 1e-5)
+    assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "ln fp8",
+                     t_ref=_scaled(norms.layer_norm_fwd(f32(xc), f32(gc), f32(bc), 1e-5)[0]))
     h_ref = to_np(xc + rc)  # torch CPU add in the I/O type
     capi.check(lib.fln_add_layernorm_fp8_forward(p(x), p(r), p(g), p(b), p(h), p(q), p(s), None,
                                                  None, rows, cols, code, 1e-5, capi.stream()))
@@ -430,7 +437,7 @@ def test_fp8_variants_reject_bad_arguments(lib):
 @pytest.mark.parametrize("mode", ["none", "tanh"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (17, 1023), (33, 7168), (2, 16384), (300, 768),
-                                       (3, 12288), (2, 32768)])
+                                       (3, 12288), (2, 32768), (2, 40960)])
 def test_layernorm_gelu_backward_matrix(lib, mode, dtype, rows, cols):
     """Backward of GELU(LayerNorm(x) gamma + beta): the forward with statistics, then the fused
     backward, against the numpy oracle (LayerNorm backward of dy GELU'(a))."""
@@ -510,7 +517,7 @@ def _mx_ref(kind, xs, rs, gs, bs, io):
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols,path", [
     (64, 4096, "vec"), (33, 7168, "vec"), (9, 96, "vec"), (2, 16384, "vec"), (2, 32768, "vec"),
-    (3, 12288, "vec"),
+    (3, 12288, "vec"), (2, 40960, "vec"), (300, 65536, "vec"),
     (13, 1024, "scalar"), (3, 2048, "loop")])
 def test_mxfp8_matrix(lib, monkeypatch, kind, dtype, rows, cols, path):
     """OCP MXFP8 outputs (codes + E8M0 block scales) of LayerNorm, RMSNorm and residual +
@@ -762,7 +769,8 @@ def test_two_pass_backward(lib, monkeypatch, kind, dtype, cols):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,cols", [(3, 12288), (5, 16384), (2, 32768), (4, 20480)])
+@pytest.mark.parametrize("rows,cols", [(3, 12288), (5, 16384), (2, 32768), (4, 20480),
+                                       (3, 40960), (300, 65536)])
 def test_add_layernorm_wide_rows(lib, dtype, rows, cols):
     """Residual add + LayerNorm on rows of 12 to 16 waves and on the widest register tiles: h
     is the rounded sum, y the LayerNorm of h (same bar as the plain forward)."""
