@@ -389,6 +389,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
   const float inv_n = 1.0f / fn;
   const int64_t stride = gridDim.x;
   const int iters = static_cast<int>((p.rows - 1 - blockIdx.x) / stride + 1);  // grid <= rows
+  const int cpt = (nvec + kT - 1) / kT;  // vector slots the row needs (uniform; <= CPT)
   const T* X = static_cast<const T*>(p.x);
   const T* R = static_cast<const T*>(p.res);
   const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
@@ -401,11 +402,13 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
     const uint32_t nb = it < iters ? row_bytes : 0u;
     const rsrc_t xq = make_rsrc(X + row * N, nb);
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) xr[i] = buf_load<P, FLN_FWD_LOAD_POL>(xq, t + i * kT);
+    for (int i = 0; i < CPT; ++i)
+      if (i < cpt) xr[i] = buf_load<P, FLN_FWD_LOAD_POL>(xq, t + i * kT);
     if constexpr (RES) {
       const rsrc_t rq = make_rsrc(R + row * N, nb);
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) rr[i] = buf_load<P, FLN_FWD_LOAD_POL>(rq, t + i * kT);
+      for (int i = 0; i < CPT; ++i)
+        if (i < cpt) rr[i] = buf_load<P, FLN_FWD_LOAD_POL>(rq, t + i * kT);
     }
   };
 
@@ -418,6 +421,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
+      if (i >= cpt) break;  // uniform
       P v = xr[i];
       if constexpr (RES) {
 #pragma unroll
@@ -440,6 +444,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
+      if (i >= cpt) break;  // uniform
       const P v = xs[i * kT + t];
       if (t + i * kT < nvec) {
 #pragma unroll
@@ -466,6 +471,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
       const rsrc_t yr = make_rsrc(static_cast<T*>(p.y) + row * N, row_bytes);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
+      if (i >= cpt) break;  // uniform
         const int v = t + i * kT;
         const P xv = xs[i * kT + t];
         const P gv = buf_load<P>(g_rs, v);
@@ -497,6 +503,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
         const rsrc_t br = make_rsrc(p.bscale + row * nblk, nblk);
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
+      if (i >= cpt) break;  // uniform
           const int v = t + i * kT;
           const P xv = xs[i * kT + t];
           const P gv = buf_load<P>(g_rs, v);
@@ -519,6 +526,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
         float am = 0.0f;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
+      if (i >= cpt) break;  // uniform
           const int v = t + i * kT;
           const P xv = xs[i * kT + t];
           const P gv = buf_load<P>(g_rs, v);
@@ -532,6 +540,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
         const float inv = am > 0.0f ? 448.0f / am : 0.0f;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
+      if (i >= cpt) break;  // uniform
           const int v = t + i * kT;
           const P xv = xs[i * kT + t];
           const P gv = buf_load<P>(g_rs, v);
