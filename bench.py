@@ -468,6 +468,41 @@ def torch_cpu_baseline(w, seconds, threads=16):
             "sample": f"{rows} of {w.rows} rows of {w.name}, median of {len(times)} runs"}
 
 
+def stream_ceilings(torch, rows, cols, fwd_bytes, bwd_bytes, warmup=10, n=100):
+    """Streaming rates of plain device copies on the headline shape (bf16 [rows, cols], rotating
+    buffers over >= 2 GiB): torch's copy (1 read + 1 write, the forward's pattern) and add (2
+    reads + 1 write, the backward's).  The step ceiling is the step's algorithmic bytes at
+    those rates."""
+    stream = torch.cuda.current_stream()
+    nbytes = rows * cols * 2
+    nsets = max(4, -(-ROTATE_BYTES // (3 * nbytes)))
+    sets = [[torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16) for _ in range(3)]
+            for _ in range(nsets)]
+
+    def rate(fn, moved):
+        for i in range(warmup):
+            fn(sets[i % nsets])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            fn(sets[i % nsets])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return moved / (e0.elapsed_time(e1) / n * 1e-3) / 1e9
+
+    copy = rate(lambda st: st[2].copy_(st[0]), 2 * nbytes)
+    add = rate(lambda st: torch.add(st[0], st[1], out=st[2]), 3 * nbytes)
+    del sets
+    torch.cuda.empty_cache()
+    step_s = fwd_bytes / (copy * 1e9) + bwd_bytes / (add * 1e9)
+    return {"copy_1r1w_gbs": round(copy, 1), "add_2r1w_gbs": round(add, 1),
+            "step_ceiling_gbs": round((fwd_bytes + bwd_bytes) / step_s / 1e9, 1),
+            "what": "torch device copy (fwd pattern) and add (bwd pattern) on bf16 "
+                    f"[{rows},{cols}], rotating >= 2 GiB; step ceiling = the step's "
+                    "algorithmic bytes at those rates"}
+
+
 def torch_gpu_compare(torch, ours, warmup=10, n=50):
     """PyTorch's own GPU ops on the same seeded inputs and shapes, timed like ours (HIP events,
     rotating buffer sets), and our speedup over them: the reference's published headline is a
@@ -731,6 +766,9 @@ def main():
             "traffic": traffic["fwd"] if traffic and traffic.get("fwd") else None,
         },
     }
+    ceil = stream_ceilings(torch, 8192, 4096, head["bytes"]["fwd"], head["bytes"]["bwd"])
+    ceil["value_over_step_ceiling"] = round(value / ceil["step_ceiling_gbs"], 3)
+    out["stream_ceilings"] = ceil
     if rms:
         out["rms_fwd_bwd"] = {
             "workload": "rms_fwd_bwd_bf16_8192x4096",
