@@ -340,13 +340,14 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   }
 }
 
-// Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384
-// columns; 16-bit rows of 8193..16384 columns with a residual gradient): one 1024-thread block
-// per row at a time, thread t owning vectors t + 1024 i (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
-// register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
-// row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them
-// back and writes dx.  A thread reads back only the vectors it parked, so the staging needs no
-// barrier: LDS serves as per-thread spill space for the row (128 KiB at CPT 4).
+// Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
+// 16-bit rows of 8193..16384 columns with a residual gradient): one 1024-thread block per row at a
+// time, thread t owning vectors t + 1024 i (i < CPT) of every row.  Pass A consumes the row's raw
+// loads (issued one row ahead, like the register kernel's ring), accumulates the column sums of dy
+// xhat and dy in registers, forms the row sums and parks the raw x / dy vectors in LDS; after the
+// row reduction, pass B reads them back and writes dx.  A thread reads back only the vectors it
+// parked, so the staging needs no barrier: LDS serves as per-thread spill space for the row (128
+// KiB at CPT 4).
 constexpr int kLdsThreads = 1024;
 
 template <class T, bool DRES, int GELU, int VEC, int CPT>
@@ -1033,8 +1034,9 @@ int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int 
   }
   if (!p.dy || !p.x || !p.rstd || (!p.rms && !p.mean)) return FLN_ERR_INVALID;
   if (!p.dx && !dgamma && !dbeta) return FLN_OK;
-  const bool have_workspace = workspace && fln::aligned16(workspace) &&
-                              workspace_bytes >= fln_backward_workspace_bytes(p.rows, p.cols, dtype);
+  const bool have_workspace =
+      workspace && fln::aligned16(workspace) &&
+      workspace_bytes >= fln_backward_workspace_bytes(p.rows, p.cols, dtype);
   if ((dgamma || dbeta) && !have_workspace) return FLN_ERR_INVALID;
   p.part_g = have_workspace ? static_cast<float*>(workspace) : nullptr;
   return fln::launch_backward(p, dtype, dgamma, dbeta, dparam_dtype, have_workspace,

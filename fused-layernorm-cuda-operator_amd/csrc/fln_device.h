@@ -148,8 +148,15 @@ __device__ __forceinline__ float readlane(float v, int l) {
 struct SumOp {
   __device__ __forceinline__ static float apply(float a, float b) { return a + b; }
 };
+// Maximum of non-negative floats (every maximum reduced here is of |value|): their IEEE bit
+// patterns order like unsigned integers, so v_max_u32 gives the same result without the NaN
+// canonicalization fmaxf costs (one extra VALU op per step); a NaN propagates, as in amax.
+__device__ __forceinline__ float max_nonneg(float a, float b) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
+  return __builtin_bit_cast(float, x > y ? x : y);
+}
 struct MaxOp {
-  __device__ __forceinline__ static float apply(float a, float b) { return fmaxf(a, b); }
+  __device__ __forceinline__ static float apply(float a, float b) { return max_nonneg(a, b); }
 };
 
 template <class Op> __device__ __forceinline__ float wave_allreduce(float v) {
@@ -280,15 +287,15 @@ __device__ __forceinline__ MxScale mx_scale_e4m3(float block_max) {
   return {e + 127, __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23)};
 }
 
-// Max over aligned groups of G adjacent lanes (G = 2 ... 32), result in every lane of the
-// group.  All lanes of each group must be active.
+// Max over aligned groups of G adjacent lanes (G = 2 ... 32) of non-negative values, result in
+// every lane of the group.  All lanes of each group must be active.
 template <int G> __device__ __forceinline__ float group_max(float v) {
   static_assert(G >= 2 && G <= 32 && (G & (G - 1)) == 0, "group of 2..32 lanes");
-  v = fmaxf(v, dpp<0xB1>(v));                        // lane ^ 1
-  if constexpr (G >= 4) v = fmaxf(v, dpp<0x4E>(v));   // lane ^ 2
-  if constexpr (G >= 8) v = fmaxf(v, dpp<0x141>(v));  // mirror within 8
-  if constexpr (G >= 16) v = fmaxf(v, dpp<0x140>(v)); // mirror within 16
-  if constexpr (G >= 32) v = fmaxf(v, swz_xor16(v));  // lane ^ 16
+  v = max_nonneg(v, dpp<0xB1>(v));                        // lane ^ 1
+  if constexpr (G >= 4) v = max_nonneg(v, dpp<0x4E>(v));   // lane ^ 2
+  if constexpr (G >= 8) v = max_nonneg(v, dpp<0x141>(v));  // mirror within 8
+  if constexpr (G >= 16) v = max_nonneg(v, dpp<0x140>(v)); // mirror within 16
+  if constexpr (G >= 32) v = max_nonneg(v, swz_xor16(v));  // lane ^ 16
   return v;
 }
 

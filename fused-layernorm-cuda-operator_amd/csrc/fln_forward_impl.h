@@ -215,7 +215,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       }
     }
     q = row_allreduce<SumOp>(q, slots[1], wpr, rg, wave, lane);
-    const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
+    const float rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);  // v_rsq_f32, 1 ulp
 
     //    Normalize + affine + epilogue, packed to the output format.
     auto affine = [&](int i, int e) -> float {
@@ -285,14 +285,15 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
         }
       }
       am = row_allreduce<MaxOp>(am, slots[2], wpr, rg, wave, lane);
-      const float inv = am > 0.0f ? 448.0f / am : 0.0f;
-      scale = am / 448.0f;
+      const float inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // 1 ulp
+      scale = am * (1.0f / 448.0f);
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         float a[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) a[e] = out(i, e);
-        // |a * inv| <= 448 (1 + 2^-23): in range for the unclamped conversion.
+        // |a * inv| <= 448 (1 + 2^-22) < 464 (1-ulp reciprocal, two roundings): in range for the
+        // unclamped conversion.
         if constexpr (VEC == 8) {
           qo[i].x = fp8x4_inrange(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
           qo[i].y = fp8x4_inrange(a[4] * inv, a[5] * inv, a[6] * inv, a[7] * inv);
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
       }
     }
     q = row_allreduce<SumOp>(q, slots[1], kW, 0, wave, lane);
-    const float rstd = 1.0f / sqrtf(q * inv_n + p.eps);
+    const float rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);  // v_rsq_f32, 1 ulp
 
     // Output element e of vector i of the row.
     auto affine = [&](int i, int e, const P& xv, const P& gv, const P& bv) -> float {
@@ -537,7 +538,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
           }
         }
         am = row_allreduce<MaxOp>(am, slots[2], kW, 0, wave, lane);
-        const float inv = am > 0.0f ? 448.0f / am : 0.0f;
+        const float inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // 1 ulp
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
       if (i >= cpt) break;  // uniform
@@ -548,11 +549,13 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
           float a[VEC];
 #pragma unroll
           for (int e = 0; e < VEC; ++e) a[e] = affine(i, e, xv, gv, bv);
-          // |a * inv| <= 448 (1 + 2^-23): in range for the unclamped conversion.
+          // |a * inv| <= 448 (1 + 2^-22) < 464 (1-ulp reciprocal, two roundings): in
+          // range for the unclamped conversion.
           BufIO<VEC, FLN_FWD_STORE_POL>::store(codes(a, inv, true), qr,
                                                static_cast<uint32_t>(v) * VEC);
         }
-        buf_store_f32(am / 448.0f, make_rsrc(p.scale + row, 4u), t == 0 ? 0u : kOutOfRange);
+        buf_store_f32(am * (1.0f / 448.0f), make_rsrc(p.scale + row, 4u),
+                      t == 0 ? 0u : kOutOfRange);
       }
     }
     const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
