@@ -341,18 +341,21 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit rows of 8193..16384 columns with a residual gradient): one 1024-thread block per row at a
-// time, thread t owning vectors t + 1024 i (i < CPT) of every row.  Pass A consumes the row's raw
-// loads (issued one row ahead, like the register kernel's ring), accumulates the column sums of dy
-// xhat and dy in registers, forms the row sums and parks the raw x / dy vectors in LDS; after the
-// row reduction, pass B reads them back and writes dx.  A thread reads back only the vectors it
-// parked, so the staging needs no barrier: LDS serves as per-thread spill space for the row (128
-// KiB at CPT 4).
+// 16-bit rows of 8193..16384 columns with a residual gradient; 16-bit LayerNorm / RMSNorm rows of
+// 16385..18432 columns): one NT-thread block per row at a time, thread t owning vectors t + NT i
+// (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
+// register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
+// row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
+// and writes dx.  A thread reads back only the vectors it parked, so the staging needs no barrier:
+// LDS serves as per-thread spill space for the row (128 KiB at CPT 4 and 1024 threads).
+// NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168, which holds the
+// 48 fp32 column sums, the prefetched row and gamma of a 16-bit lane with 3 vectors without spilling.
 constexpr int kLdsThreads = 1024;
+constexpr int kLds16Threads = 768;
 
-template <class T, bool DRES, int GELU, int VEC, int CPT>
-__global__ __launch_bounds__(kLdsThreads) void bwd_lds_kernel(const BwdParams p) {
-  constexpr int kT = kLdsThreads;
+template <class T, bool DRES, int GELU, int VEC, int CPT, int NT = kLdsThreads>
+__global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
+  constexpr int kT = NT;
   constexpr int kW = kT / kWave;
   using P = Pack<T, VEC>;
   __shared__ P xs[CPT * kT], ds[CPT * kT];
@@ -499,8 +502,9 @@ __global__ __launch_bounds__(kLdsThreads) void bwd_lds_kernel(const BwdParams p)
   }
 }
 
-// Rows past the register and LDS tiles (16-bit rows of more than 16384 columns, fp32 rows of
-// more than 16384, long rows on the scalar path), any width, in two streaming passes:
+// Rows past the register and LDS tiles (16-bit rows of more than 16384 columns, save the
+// LayerNorm / RMSNorm rows of up to 18432; fp32 rows of more than 16384; long rows on the scalar
+// path), any width, in two streaming passes:
 //   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
 //     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
 //     rows grid-stride, four vectors per thread in flight per array;
@@ -851,6 +855,11 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
       if (geo.lds_cpt == 3) return launch_lds<T, VV, 3>(p, geo.blocks, s);
       if (geo.lds_cpt == 4) return launch_lds<T, VV, 4>(p, geo.blocks, s);
     } else {
+      if (geo.lds_cpt == 3 && geo.threads == kLds16Threads && !p.dres && !p.gelu) {
+        hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 3, kLds16Threads>),
+                           dim3(geo.blocks), dim3(kLds16Threads), 0, s, p);
+        return static_cast<int>(hipGetLastError());
+      }
       if (geo.lds_cpt == 2 && p.dres && !p.gelu) {
         hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VV, 2>), dim3(geo.blocks),
                            dim3(kLdsThreads), 0, s, p);
@@ -888,7 +897,7 @@ int64_t workspace_partial_rows(int64_t rows) {
 }
 
 BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres,
-                              bool have_workspace) {
+                              bool gelu, bool have_workspace) {
   BwdGeometry g{};
   const int es = element_size(dtype);
   const int vv = es > 0 ? 16 / es : 1;
@@ -929,18 +938,24 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   g.blocks = g.reg_path ? blocks : (rows + g.rows_per_block - 1) / g.rows_per_block;
   // fp32 rows too wide for registers but within 4 vectors per thread of a 1024-thread block
   // (8193..16384 columns): the LDS-staged kernel, one block per CU, rows dealt grid-stride.
-  // (16-bit rows past 16384 columns would need 48-64 VGPRs of column sums per lane on top of
-  // the prefetched row and spill; they keep the looped kernel.)  16-bit rows of 8193..16384
+  // (16-bit rows past 16384 columns need 48-64 VGPRs of column sums per lane on top of the
+  // prefetched row and spill in a 1024-thread block.)  16-bit rows of 8193..16384
   // columns with a residual gradient also take it (2 vectors per thread): the register kernel
-  // spills there (measured 166 us against 123 us at 4096 x 16384 bf16).
+  // spills there (measured 166 us against 123 us at 4096 x 16384 bf16).  16-bit LayerNorm /
+  // RMSNorm rows of 16385..18432 columns take it with 768 threads and 3 vectors per thread
+  // (4096 x 18432 bf16: 161 -> 109 us against the two passes); the GELU and residual flavours
+  // spill there and 4 vectors per thread (up to 24576 columns) spill for every flavour, all
+  // measured slower than the two passes.
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
+  const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
   const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
-  if (g.vec > 1 && (wide_f32 || dres16) && tun.bwd_no_lds == 0) {
+  const bool wide16 = !g.reg_path && es == 2 && cpt16 == 3 && !dres && !gelu;
+  if (g.vec > 1 && (wide_f32 || dres16 || wide16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
-    g.lds_cpt = static_cast<int>(cpt);
-    g.threads = kLdsThreads;
-    g.wpr = kLdsThreads / kWave;
+    g.lds_cpt = wide16 ? 3 : static_cast<int>(cpt);
+    g.threads = wide16 ? kLds16Threads : kLdsThreads;
+    g.wpr = g.threads / kWave;
     g.rgs = 1;
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
     g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
@@ -971,7 +986,8 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   const bool vec_ok = aligned16(p.x) && aligned16(p.dy) && aligned16(p.dx) &&
                       aligned16(p.gamma) && aligned16(p.dres);
   BwdGeometry geo =
-      backward_geometry(p.rows, p.cols, dtype, vec_ok, p.dres != nullptr, have_workspace);
+      backward_geometry(p.rows, p.cols, dtype, vec_ok, p.dres != nullptr, p.gelu != 0,
+                        have_workspace);
   if (geo.reg_path) {
     // Never more blocks than fit at once: a second round of blocks would only add a tail.
     int64_t resident = geo.blocks;

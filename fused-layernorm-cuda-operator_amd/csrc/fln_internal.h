@@ -91,7 +91,7 @@ struct BwdGeometry {
   int64_t rows_per_block;
 };
 BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok, bool dres,
-                              bool have_workspace);
+                              bool gelu, bool have_workspace);
 // Partial rows the backward workspace holds (an upper bound on every path's stage-1 blocks).
 int64_t workspace_partial_rows(int64_t rows);
 
