@@ -341,15 +341,16 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit rows of 8193..16384 columns with a residual gradient; 16-bit LayerNorm / RMSNorm rows of
-// 16385..18432 columns): one NT-thread block per row at a time, thread t owning vectors t + NT i
+// 16-bit rows of 8193..16384 columns with a residual gradient, of 8193..12288 with GELU; 16-bit
+// LayerNorm / RMSNorm rows of 16385..18432 columns): one NT-thread block per row at a time, thread t owning vectors t + NT i
 // (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
 // and writes dx.  A thread reads back only the vectors it parked, so the staging needs no barrier:
 // LDS serves as per-thread spill space for the row (128 KiB at CPT 4 and 1024 threads).
 // NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168, which holds the
-// 48 fp32 column sums, the prefetched row and gamma of a 16-bit lane with 3 vectors without spilling.
+// 48 fp32 column sums, the prefetched row and gamma of a 16-bit lane with 3 vectors, or 2 vectors
+// with GELU's beta and derivative temporaries, without spilling.
 constexpr int kLdsThreads = 1024;
 constexpr int kLds16Threads = 768;
 
@@ -855,9 +856,19 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
       if (geo.lds_cpt == 3) return launch_lds<T, VV, 3>(p, geo.blocks, s);
       if (geo.lds_cpt == 4) return launch_lds<T, VV, 4>(p, geo.blocks, s);
     } else {
-      if (geo.lds_cpt == 3 && geo.threads == kLds16Threads && !p.dres && !p.gelu) {
-        hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 3, kLds16Threads>),
-                           dim3(geo.blocks), dim3(kLds16Threads), 0, s, p);
+      if (geo.threads == kLds16Threads) {
+        const dim3 grid(static_cast<unsigned>(geo.blocks)), block(kLds16Threads);
+        if (geo.lds_cpt == 3 && !p.dres && !p.gelu)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 3, kLds16Threads>), grid, block, 0,
+                             s, p);
+        else if (geo.lds_cpt == 2 && p.gelu == 1)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 1, VV, 2, kLds16Threads>), grid, block, 0,
+                             s, p);
+        else if (geo.lds_cpt == 2 && p.gelu == 2)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 2, VV, 2, kLds16Threads>), grid, block, 0,
+                             s, p);
+        else
+          return FLN_ERR_INVALID;
         return static_cast<int>(hipGetLastError());
       }
       if (geo.lds_cpt == 2 && p.dres && !p.gelu) {
@@ -945,16 +956,21 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // RMSNorm rows of 16385..18432 columns take it with 768 threads and 3 vectors per thread
   // (4096 x 18432 bf16: 161 -> 109 us against the two passes); the GELU and residual flavours
   // spill there and 4 vectors per thread (up to 24576 columns) spill for every flavour, all
-  // measured slower than the two passes.
+  // measured slower than the two passes.  16-bit GELU rows of 8193..12288 columns take it with
+  // 768 threads and 2 vectors per thread (no spill; the register kernel spills 84-232 B per lane
+  // there): 4096 x 12288 bf16 tanh 122.6 -> 109.5 us, erf 302.4 -> 142.8 us.  Wider GELU rows
+  // (12289..16384) keep the register kernel, measured faster than 2 vectors per thread in
+  // 1024-thread blocks (134.8 against 162.1 us at 4096 x 16384).
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
   const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
   const bool wide16 = !g.reg_path && es == 2 && cpt16 == 3 && !dres && !gelu;
-  if (g.vec > 1 && (wide_f32 || dres16 || wide16) && tun.bwd_no_lds == 0) {
+  const bool gelu16 = gelu && g.reg_path && es == 2 && g.vpl == 2 && cpt16 == 2;
+  if (g.vec > 1 && (wide_f32 || dres16 || wide16 || gelu16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
-    g.lds_cpt = wide16 ? 3 : static_cast<int>(cpt);
-    g.threads = wide16 ? kLds16Threads : kLdsThreads;
+    g.lds_cpt = wide16 ? 3 : gelu16 ? 2 : static_cast<int>(cpt);
+    g.threads = (wide16 || gelu16) ? kLds16Threads : kLdsThreads;
     g.wpr = g.threads / kWave;
     g.rgs = 1;
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
