@@ -202,8 +202,10 @@ template <class A> __device__ __forceinline__ A wave_sum_generic(A v) {
 // hardware reciprocal (v_rcp_f32) instead of a tanh, and no cancellation for large negative v (the quotient stays
 // relatively accurate where 1 + tanh(u) would cancel).  Its derivative is
 //   s + 2 v s (1 - s) sqrt(2/pi) (1 + 3 * 0.044715 v^2),   s = sigmoid(2u).
-// The erf form keeps erff; its Gaussian factor uses the hardware exp2:
-//   d/dv = 0.5 (1 + erf(v / sqrt 2)) + v exp(-v^2 / 2) / sqrt(2 pi).
+// The erf form is v Phi(v) with Phi the standard normal CDF, and its derivative
+//   Phi(v) + v exp(-v^2 / 2) / sqrt(2 pi);
+// normal_cdf() below evaluates Phi and the shared Gaussian factor with one hardware exp2 and
+// one hardware reciprocal.
 // ---------------------------------------------------------------------------------------------
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kGeluK0 = 0.79788456080286535588f;  // sqrt(2/pi)
@@ -223,14 +225,37 @@ __device__ __forceinline__ GeluTanhTerms gelu_tanh_terms(float v) {
   return {e, __builtin_amdgcn_rcpf(1.0f + e)};  // v_rcp_f32: 1 ulp
 }
 __device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_terms(v).sg; }
-__device__ __forceinline__ float gelu_erf(float v) {
-  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+
+// Phi(v) and exp(-v^2 / 2).  With x = |v| / sqrt 2 and t = 1 / (1 + 0.4 x),
+//   h = 0.5 erfc(x) = t F(t) exp(-x^2),
+// where F(t) = 0.5 erfcx(x) / t (erfcx(x) = exp(x^2) erfc(x)) is smooth on t in (0, 1] and is
+// replaced by a degree-8 polynomial: a relative-error least-squares fit on Chebyshev nodes, max
+// relative error 1.3e-7 (fit_erfc.py beside this file derives and checks the coefficients).
+// Phi(v) = h for v < 0 and 1 - h otherwise, so the lower tail keeps its relative accuracy
+// where 1 + erf(v / sqrt 2) cancels.  Under an fp32 emulation over |v| <= 13: v Phi(v) within
+// 3.8e-7 (absolute) and 7.3e-6 (relative, |v Phi(v)| > 1e-30) of the float64 value, the
+// derivative within 2.6e-7.  Infinite v gives Phi = 0 or 1; NaN propagates.
+struct NormalCdf {
+  float cdf, gauss;  // Phi(v), exp(-v^2 / 2)
+};
+__device__ __forceinline__ NormalCdf normal_cdf(float v) {
+  constexpr float kF[9] = {1.128379330e-01f, 1.128347963e-01f, 1.039213464e-01f,
+                           8.427099138e-02f, 7.071570307e-02f, -2.803730546e-03f,
+                           8.454266936e-02f, -9.145070612e-02f, 2.513105422e-02f};
+  const float e = exp2_fast((-0.5f * kLog2e * v) * v);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.4f * 0.70710678118654752440f, fabsf(v), 1.0f));
+  float f = kF[8];
+#pragma unroll
+  for (int k = 7; k >= 0; --k) f = fmaf(f, t, kF[k]);
+  const float h = (f * t) * e;
+  return {v < 0.0f ? h : 1.0f - h, e};
 }
+__device__ __forceinline__ float gelu_erf(float v) { return v * normal_cdf(v).cdf; }
 __device__ __forceinline__ float gelu_tanh(float v) { return v * gelu_tanh_sigmoid(v); }
 __device__ __forceinline__ float gelu_erf_grad(float v) {
   const float inv_sqrt_2pi = 0.39894228040143267794f;
-  return 0.5f * (1.0f + erff(v * 0.70710678118654752440f)) +
-         v * inv_sqrt_2pi * exp2_fast(-0.5f * kLog2e * v * v);
+  const NormalCdf n = normal_cdf(v);
+  return fmaf(v, inv_sqrt_2pi * n.gauss, n.cdf);
 }
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const GeluTanhTerms t = gelu_tanh_terms(v);

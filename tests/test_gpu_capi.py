@@ -74,6 +74,53 @@ def test_c2_layernorm_gelu_fp32(lib, name, mode):
     assert np.abs(to_np(y) - ref).max() <= 1e-5
 
 
+@pytest.mark.parametrize("cols", [4096, 12288], ids=["registers", "lds"])
+def test_gelu_erf_tails_fp32(lib, cols):
+    """The exact-erf GELU over a = LayerNorm(x) + beta spanning [-13.6, 13.6] (beta a ramp):
+    within 1e-5 of the oracle everywhere, and within 1e-4 relative in the lower tail (GELU down
+    to 1e-30), which a 0.5 a (1 + erf(a / sqrt 2)) evaluation loses to cancellation -- in fp32,
+    and in float64 too past a = -6, so the tail reference is a Phi(a) with scipy's ndtr on the
+    oracle's float64 a.  The derivative is checked through the backward with dy = 1 against
+    the oracle."""
+    from scipy.special import ndtr
+    rows = 64
+    gen = torch.Generator().manual_seed(cols)
+    xc = torch.rand(rows, cols, generator=gen) * 2 - 1
+    gc = torch.ones(cols)
+    bc = torch.linspace(-12.0, 12.0, cols)
+    x, g, b = cuda(xc), cuda(gc), cuda(bc)
+    p = capi.ptr
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
+                                              cols, capi.F32, 1e-5, capi.GELU_ERF,
+                                              capi.stream()))
+    ref = norms.layer_norm_gelu_fwd(xc.numpy(), gc.numpy(), bc.numpy(), 1e-5, "none")
+    got = to_np(y)
+    assert np.abs(got - ref).max() <= 1e-5
+    a64, _, _ = norms.layer_norm_fwd(xc.numpy(), gc.numpy(), bc.numpy(), 1e-5)
+    exact = a64 * ndtr(a64)
+    # The lower tail only: near a = 0 the relative error is that of a's own fp32 rounding.
+    tail = (a64 < -3.0) & (np.abs(exact) > 1e-30)
+    rel = np.abs(got[tail] - exact[tail]) / np.abs(exact[tail])
+    assert rel.max() <= 1e-4, f"tail relative error {rel.max():.3g}"
+    assert np.abs(exact[tail]).min() < 1e-29  # the tail is exercised
+    dy = torch.ones_like(x)
+    dx = torch.empty_like(x)
+    dg = torch.empty(cols, device="cuda")
+    db = torch.empty(cols, device="cuda")
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b), p(dx),
+                                               p(dg), p(db), rows, cols, capi.F32, capi.F32,
+                                               capi.GELU_ERF, p(ws), n, capi.stream()))
+    dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(np.ones((rows, cols)), xc.numpy(),
+                                                       gc.numpy(), bc.numpy(), 1e-5, "none")
+    np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+
+
 def test_c3_add_layernorm_bf16_8192x4096(lib):
     w = WORKLOADS["c3_add_ln_fwd_bf16_8192x4096"]
     inp = make_inputs(w)
