@@ -51,7 +51,8 @@ CALIBRATION_COPY_BYTES = 256 * 2 ** 20
 CONFIGS = ("c1_ln_fwd_fp32_32x768", "c2_ln_gelu_fp32_17x1023", "c2_ln_gelu_fp32_64x4096",
            "c3_add_ln_fwd_bf16_8192x4096", "c4_rms_fwd_bwd_bf16_16384x8192",
            "c5_ln_fp8_bf16_32768x7168", "c6_add_rms_fp8_bf16_32768x7168",
-           "c7_add_rms_mxfp8_bf16_32768x7168", "ln_gelu_fwd_bwd_bf16_8192x4096")
+           "c7_add_rms_mxfp8_bf16_32768x7168", "ln_gelu_fwd_bwd_bf16_8192x4096",
+           "ln_gelu_erf_fwd_bwd_bf16_8192x4096")
 
 
 def parse():
@@ -571,6 +572,25 @@ def torch_gpu_compare(torch, ours, warmup=10, n=50):
         fb_ms = time_ms(fb, sets)
         entry(name, fb_ms, {"torch_fwd_us": f_ms, "torch_bwd_us": fb_ms - f_ms})
         del sets
+    # LayerNorm + GELU fwd + bwd through autograd (tanh and exact forms).
+    for name in ("ln_gelu_fwd_bwd_bf16_8192x4096", "ln_gelu_erf_fwd_bwd_bf16_8192x4096"):
+        w = WORKLOADS[name]
+        sets = device_sets(w, ("x", "dy"))
+        for st in sets:
+            for k in ("x", "gamma", "beta"):
+                st[k].requires_grad_(True)
+
+        def fwd(st, w=w, grad=True):
+            a = [st[k] if grad else st[k].detach() for k in ("x", "gamma", "beta")]
+            return F.gelu(F.layer_norm(a[0], (w.cols,), a[1], a[2], w.eps),
+                          approximate=w.approximate)
+
+        def fb(st, w=w):
+            torch.autograd.grad(fwd(st), (st["x"], st["gamma"], st["beta"]), st["dy"])
+        f_ms = time_ms(lambda st: fwd(st, grad=False), sets)
+        fb_ms = time_ms(fb, sets)
+        entry(name, fb_ms, {"torch_fwd_us": f_ms, "torch_bwd_us": fb_ms - f_ms})
+        del sets
     # C1 (back to back, latency-bound).
     w = WORKLOADS["c1_ln_fwd_fp32_32x768"]
     sets = device_sets(w)
@@ -809,7 +829,8 @@ def main():
         ours = {HEADLINE: head["ms"], "c1_ln_fwd_fp32_32x768": None,
                 "rms_fwd_bwd_bf16_8192x4096": rms["ms"] if rms else None}
         for name in ("c1_ln_fwd_fp32_32x768", "c3_add_ln_fwd_bf16_8192x4096",
-                     "c4_rms_fwd_bwd_bf16_16384x8192", "c5_ln_fp8_bf16_32768x7168"):
+                     "c4_rms_fwd_bwd_bf16_16384x8192", "c5_ln_fp8_bf16_32768x7168",
+                     "ln_gelu_fwd_bwd_bf16_8192x4096", "ln_gelu_erf_fwd_bwd_bf16_8192x4096"):
             e = out["configs"][name]["us_per_call"]
             ours[name] = (e["fwd_bwd"] if isinstance(e, dict) else e) / 1e3
         out["torch_gpu"] = torch_gpu_compare(torch, ours)

@@ -52,6 +52,9 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
     # LayerNorm + GELU (tanh, the reference's form) forward + fused backward, headline shape.
     Workload("ln_gelu_fwd_bwd_bf16_8192x4096", "layer_norm_gelu_fwd_bwd", 8192, 4096,
              torch.bfloat16, 7, 1e-5, (1.0, 0.02), (0.0, 0.02), approximate="tanh"),
+    # The same with the exact (erf) GELU, torch.nn.GELU's default.
+    Workload("ln_gelu_erf_fwd_bwd_bf16_8192x4096", "layer_norm_gelu_fwd_bwd", 8192, 4096,
+             torch.bfloat16, 7, 1e-5, (1.0, 0.02), (0.0, 0.02), approximate="none"),
     Workload("ln_fwd_bwd_bf16_8192x4096", "layer_norm_fwd_bwd", 8192, 4096, torch.bfloat16, 3,
              1e-5, (1.0, 0.02), (0.0, 0.02)),
     Workload("rms_fwd_bwd_bf16_8192x4096", "rms_norm_fwd_bwd", 8192, 4096, torch.bfloat16, 3,
