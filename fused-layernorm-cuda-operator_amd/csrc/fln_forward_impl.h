@@ -565,6 +565,223 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
 }
 
 // ---------------------------------------------------------------------------------------------
+// Rows past the LDS tile (16-bit rows of more than 65536 columns, fp32 rows of more than 32768)
+// and long rows off the vector path: one 1024-thread block per row at a time, rows
+// grid-stride, each pass streaming the row in steps of U vectors per thread (64 bytes: 4
+// vectors, or 16-32 elements on the scalar path; thread t reads vectors base + t + 1024 u, so
+// every wave-wide access is coalesced):
+//   pass 1, statistics: per thread, each step's valid elements are reduced to (count, mean,
+//     centred sum of squares) and merged into the thread's running triple (the pairwise update
+//     of Chan, Golub and LeVeque); the block's mean is then the sum of count x mean over the
+//     threads / N, and its centred sum of squares the sum of each thread's M2 plus
+//     count (mean_t - mean)^2 -- two block reductions in a fixed order, so the statistics are
+//     bitwise reproducible and need no E[x^2] - mean^2 cancellation.  RMSNorm sums squares;
+//   pass 2, fp8 with a per-row scale only: the row maximum of the outputs;
+//   last pass: outputs (and, with a residual, h = x + r written during pass 1).
+// x (and the residual) are read once per pass; the passes after the first find much of the row
+// in the L2 / Infinity Cache, as the block has just read it (the last pass loads non-temporal).
+// ---------------------------------------------------------------------------------------------
+constexpr int kFwdWideThreads = 1024;
+constexpr int kFwdWideStepBytes = 64;  // bytes of the row per thread and step (4 vectors)
+
+template <class T, int FP8, bool RES, int GELU, int VEC>
+__global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdParams p) {
+  constexpr int kT = kFwdWideThreads;
+  constexpr int kW = kT / kWave;
+  constexpr int U = kFwdWideStepBytes / (VEC * static_cast<int>(sizeof(T)));
+  using P = Pack<T, VEC>;
+  __shared__ float red[2][3][kW + 16];  // [parity][reduction][wave], padded
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int64_t N = p.cols;
+  const uint32_t nvec = static_cast<uint32_t>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const float fn = static_cast<float>(N);
+  const float inv_n = 1.0f / fn;
+  const T* X = static_cast<const T*>(p.x);
+  const T* R = static_cast<const T*>(p.res);
+  const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
+  const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
+  const bool has_g = p.gamma != nullptr;
+
+  int parity = 0;
+  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x, parity ^= 1) {
+    float(*slots)[kW + 16] = red[parity];
+    const rsrc_t xq = make_rsrc(X + row * N, row_bytes);
+    const rsrc_t rq = make_rsrc(RES ? R + row * N : nullptr, row_bytes);
+    // Step `base`: vectors base + t + kT u of the row (zeros past the row); with a residual,
+    // h = x + r rounded to T, as every pass recomputes it.
+    auto load_step = [&](uint32_t base, P (&hv)[U], auto pol) {
+      constexpr int POL = decltype(pol)::value;
+      P rv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        hv[u] = buf_load<P, POL>(xq, base + t + kT * u);
+        if constexpr (RES) rv[u] = buf_load<P, POL>(rq, base + t + kT * u);
+      }
+      if constexpr (RES) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            hv[u].v[e] = from_f32<T>(to_f32(hv[u].v[e]) + to_f32(rv[u].v[e]));
+      }
+    };
+    using Keep = std::integral_constant<int, kDefault>;
+    using Last = std::integral_constant<int, kStream>;
+
+    // Pass 1: statistics (and h).
+    const rsrc_t hr = make_rsrc(RES && p.h ? static_cast<T*>(p.h) + row * N : nullptr,
+                                row_bytes);
+    float mean = 0.0f, rstd;
+    float cnt = 0.0f, mu = 0.0f, m2 = 0.0f;  // this thread's elements: count, mean, M2
+    for (uint32_t base = 0; base < nvec; base += kT * U) {
+      P hv[U];
+      load_step(base, hv, Keep{});
+      if constexpr (RES) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) buf_store<P, FLN_FWD_STORE_POL>(hv[u], hr, base + t + kT * u);
+      }
+      if (p.rms) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) m2 = fmaf(to_f32(hv[u].v[e]), to_f32(hv[u].v[e]), m2);
+        continue;
+      }
+      float c = 0.0f, s = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (base + t + kT * u < nvec) {
+          c += static_cast<float>(VEC);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) s += to_f32(hv[u].v[e]);
+        }
+      }
+      if (c > 0.0f) {
+        const float mg = s / c;
+        float q = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (base + t + kT * u < nvec) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              const float d = to_f32(hv[u].v[e]) - mg;
+              q = fmaf(d, d, q);
+            }
+          }
+        }
+        const float nn = cnt + c;
+        const float d = mg - mu;
+        const float w = c / nn;
+        mu = fmaf(d, w, mu);
+        m2 += fmaf(d * d, cnt * w, q);
+        cnt = nn;
+      }
+    }
+    if (p.rms) {
+      const float q = row_allreduce<SumOp>(m2, slots[0], kW, 0, wave, lane);
+      rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);  // v_rsq_f32, 1 ulp
+    } else {
+      const float sum = row_allreduce<SumOp>(cnt * mu, slots[0], kW, 0, wave, lane);
+      mean = sum * inv_n;
+      mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
+      const float dm = mu - mean;
+      const float q = row_allreduce<SumOp>(fmaf(cnt * dm, dm, m2), slots[1], kW, 0, wave, lane);
+      rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);
+    }
+
+    auto affine = [&](const P& hv, const P& gv, const P& bv, int e) -> float {
+      float a = fmaf((to_f32(hv.v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
+                     to_f32(bv.v[e]));
+      if constexpr (GELU == 1) a = gelu_erf(a);
+      if constexpr (GELU == 2) a = gelu_tanh(a);
+      return a;
+    };
+
+    // Pass 2 (per-row fp8 scale): the row maximum of the outputs.
+    float inv = 0.0f, am = 0.0f;
+    if constexpr (FP8 == 1) {
+      for (uint32_t base = 0; base < nvec; base += kT * U) {
+        P hv[U];
+        load_step(base, hv, Keep{});
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t v = base + t + kT * u;
+          const P gv = buf_load<P>(g_rs, v);
+          const P bv = buf_load<P>(b_rs, v);
+          if (v < nvec) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) am = fmaxf(am, fabsf(affine(hv[u], gv, bv, e)));
+          }
+        }
+      }
+      am = row_allreduce<MaxOp>(am, slots[2], kW, 0, wave, lane);
+      inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // v_rcp_f32, 1 ulp
+    }
+
+    // Last pass: outputs.
+    for (uint32_t base = 0; base < nvec; base += kT * U) {
+      P hv[U];
+      load_step(base, hv, Last{});
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t v = base + t + kT * u;
+        const P gv = buf_load<P>(g_rs, v);
+        const P bv = buf_load<P>(b_rs, v);
+        float a[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) a[e] = affine(hv[u], gv, bv, e);
+        if constexpr (FP8 == 0) {
+          P o;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(a[e]);
+          buf_store<P, FLN_FWD_STORE_POL>(o, make_rsrc(static_cast<T*>(p.y) + row * N, row_bytes),
+                                          v);
+        } else {
+          float m = inv;
+          if constexpr (FP8 == 2) {
+            // OCP MX: a 32-element block is G adjacent lanes' vectors (cols % 32 == 0, and
+            // every step starts on a block boundary).
+            constexpr int G = 32 / VEC;
+            float bm = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(a[e]));
+            const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+            m = ms.mul;  // |a * m| < 512: the saturating conversion clamps to 448
+            const uint32_t nblk = static_cast<uint32_t>(N / 32);
+            __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(ms.code),
+                                                 make_rsrc(p.bscale + row * nblk, nblk),
+                                                 v % G == 0 ? v / G : kOutOfRange, 0, 0);
+          }
+          // Per-row scale: |a * inv| <= 448 (1 + 2^-22) < 464, but the saturating form is kept
+          // (the scalar path converts one element at a time).
+          const rsrc_t qr = make_rsrc(static_cast<uint8_t*>(p.y) + row * N,
+                                      static_cast<uint32_t>(N));
+          if constexpr (VEC == 8) {
+            u32x2 w;
+            w.x = fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
+            w.y = fp8x4(a[4] * m, a[5] * m, a[6] * m, a[7] * m);
+            BufIO<8, FLN_FWD_STORE_POL>::store(w, qr, v * 8u);
+          } else if constexpr (VEC == 4) {
+            BufIO<4, FLN_FWD_STORE_POL>::store(fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m), qr,
+                                               v * 4u);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b8(fp8x1(a[0] * m), qr, v, 0, FLN_FWD_STORE_POL);
+          }
+        }
+      }
+    }
+    const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
+    if constexpr (FP8 == 1)
+      buf_store_f32(am * (1.0f / 448.0f), make_rsrc(p.scale + row, 4u), stat_off);
+    buf_store_f32(mean, make_rsrc(p.mean ? p.mean + row : nullptr, 4u), stat_off);
+    buf_store_f32(rstd, make_rsrc(p.rstd ? p.rstd + row : nullptr, 4u), stat_off);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Looped fallback: one block per row, any length, any alignment; A is the accumulation type
 // (fp32, or fp64 for fp64 I/O).  Same two-pass statistics as the register path.
 // ---------------------------------------------------------------------------------------------
@@ -776,6 +993,24 @@ int launch_lds(const FwdParams& p, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
+template <class T, int FP8, int VEC>
+int launch_wide(const FwdParams& p, hipStream_t s) {
+  auto launch = [&](auto kernel) {
+    static int occupancy_cache[64];  // per instantiation, per device
+    int64_t grid = resident_blocks(kernel, kFwdWideThreads, occupancy_cache);
+    if (grid > p.rows) grid = p.rows;
+    if (grid > kMaxGrid) grid = kMaxGrid;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kFwdWideThreads), 0, s, p);
+    return static_cast<int>(hipGetLastError());
+  };
+  if (p.res) return launch(fwd_wide_kernel<T, FP8, true, 0, VEC>);
+  if constexpr (FP8 == 0) {
+    if (p.gelu == FLN_GELU_ERF) return launch(fwd_wide_kernel<T, 0, false, 1, VEC>);
+    if (p.gelu == FLN_GELU_TANH) return launch(fwd_wide_kernel<T, 0, false, 2, VEC>);
+  }
+  return launch(fwd_wide_kernel<T, FP8, false, 0, VEC>);
+}
+
 template <class T, class A, int FP8>
 int launch_loop(const FwdParams& p, hipStream_t s) {
   const int threads = p.cols >= 4096 ? 1024 : 256;
@@ -881,15 +1116,19 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, raw_cap, vec_ok,
                                      tun.fwd_wpr);
   // Rows past the register tiles: the LDS-staged kernel on the vector path (up to 8 vectors
-  // per thread of a 1024-thread block), the looped kernel otherwise.
+  // per thread of a 1024-thread block), the streamed wide-row kernel otherwise (buffer
+  // resources span at most 4 GiB: rows of 2 GiB or more keep the looped kernel).
   const bool lds = g.loop && vec_ok && nvec <= int64_t(kFwdLdsCpt) * kFwdLdsThreads &&
                    !tun.fwd_no_lds;
+  const bool wide = g.loop && !lds && N * int64_t(sizeof(T)) < (int64_t(1) << 31) &&
+                    !tun.fwd_no_wide;
   if (tun.debug_geometry)
     fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
             "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
-            cap, wide_cap, lds ? "lds" : g.loop ? "loop" : "registers", g.wpr, g.vpl,
-            static_cast<int>(g.exact), g.threads);
+            cap, wide_cap, lds ? "lds" : wide ? "wide" : g.loop ? "loop" : "registers", g.wpr,
+            g.vpl, static_cast<int>(g.exact), g.threads);
   if (lds) return launch_lds<T, FP8, VV>(p, s);
+  if (wide) return vec_ok ? launch_wide<T, FP8, VV>(p, s) : launch_wide<T, FP8, 1>(p, s);
   if (g.loop) return launch_loop<T, float, FP8>(p, s);
   p.wpr = g.wpr;
   const int vpl = g.vpl;

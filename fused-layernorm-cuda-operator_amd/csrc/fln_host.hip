@@ -61,6 +61,7 @@ Tuning read_tuning() {
   t.fwd_grid_mult = env_knob("FLN_FWD_GRID_MULT", 0);
   t.debug_geometry = env_knob("FLN_DEBUG_GEOMETRY", 0);
   t.fwd_no_lds = env_knob("FLN_FWD_NO_LDS", 0);
+  t.fwd_no_wide = env_knob("FLN_FWD_NO_WIDE", 0);
   t.bwd_epl = env_knob("FLN_BWD_EPL", 0);
   t.bwd_wpr = env_knob("FLN_BWD_WPR", 0);
   t.bwd_threads = env_knob("FLN_BWD_THREADS", 0);

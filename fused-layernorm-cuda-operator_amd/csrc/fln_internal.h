@@ -64,6 +64,7 @@ struct Tuning {
   int fwd_grid_mult;   // FLN_FWD_GRID_MULT: forward grid = this many blocks per CU
   int debug_geometry;  // FLN_DEBUG_GEOMETRY: one stderr line per forward launch
   int fwd_no_lds;      // FLN_FWD_NO_LDS: never the LDS-staged forward
+  int fwd_no_wide;     // FLN_FWD_NO_WIDE: the looped forward instead of the streamed wide-row one
   int bwd_epl;         // FLN_BWD_EPL: backward elements per lane
   int bwd_wpr;         // FLN_BWD_WPR: backward waves per row
   int bwd_threads;     // FLN_BWD_THREADS: backward block size (256, 512, 1024)

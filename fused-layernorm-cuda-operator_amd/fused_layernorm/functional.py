@@ -105,12 +105,13 @@ def get_optimal_config(batch_size: int, hidden_size: int,
     loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, wide_cap, raw_cap,
                                                        vec_path, num_cus)
     # Rows past the register tiles: parked in LDS (vector path, <= 8 vectors per thread of a
-    # 1024-thread block), else the looped kernel.
+    # 1024-thread block), else streamed by the wide-row kernel (rows under 2 GiB).
     lds = loop and vec_path and nvec <= 8 * 1024
+    wide = loop and not lds and hidden_size * es < 2 ** 31
     return {
         "use_mixed_precision": dtype in (torch.float16, torch.bfloat16),
         "threads_per_block": threads,
-        "enable_persistent_kernel": not loop or lds,  # persistent grid-stride rows
+        "enable_persistent_kernel": not loop or lds or wide,  # persistent grid-stride rows
         "use_vectorized_load": vec > 1,
         "use_tensor_cores": False,  # bandwidth-bound: no MFMA on this path
         "waves_per_row": wpr if not loop else None,
@@ -120,6 +121,7 @@ def get_optimal_config(batch_size: int, hidden_size: int,
         "register_resident": not loop,
         "lds_staged": lds,
         "threads_lds": 1024 if lds else None,
+        "wide_streamed": wide,
     }
 
 

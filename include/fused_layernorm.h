@@ -189,9 +189,10 @@ const char* fln_version(void);
 int fln_hip_version(void);
 const char* fln_error_string(int code);
 /* Re-reads the FLN_* tuning and debugging environment variables (FLN_FORCE_LOOP, FLN_FWD_EPL,
- * FLN_FWD_WPR, FLN_FWD_GRID_MULT, FLN_FWD_NO_LDS, FLN_DEBUG_GEOMETRY, FLN_BWD_EPL, FLN_BWD_WPR,
- * FLN_BWD_THREADS, FLN_BWD_NO_LDS, FLN_BWD_NO_TWO_PASS); they are otherwise read once, at the
- * first launch.  No counterpart in the reference: for tests and tuning sweeps. */
+ * FLN_FWD_WPR, FLN_FWD_GRID_MULT, FLN_FWD_NO_LDS, FLN_FWD_NO_WIDE, FLN_DEBUG_GEOMETRY,
+ * FLN_BWD_EPL, FLN_BWD_WPR, FLN_BWD_THREADS, FLN_BWD_NO_LDS, FLN_BWD_NO_TWO_PASS); they are
+ * otherwise read once, at the first launch.  No counterpart in the reference: for tests and
+ * tuning sweeps. */
 void fln_reload_tuning(void);
 
 #ifdef __cplusplus

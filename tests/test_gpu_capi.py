@@ -467,6 +467,133 @@ def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
                      t_ref=_scaled(norms.rms_norm_fwd(h_o, f32(gc), 1e-6)[0]))
 
 
+WIDE_KINDS = ["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp8", "rms_fp8",
+              "add_rms_fp8", "ln_mx", "rms_mx", "add_rms_mx"]
+
+
+@pytest.mark.parametrize("kind", WIDE_KINDS)
+@pytest.mark.parametrize("dtype,rows,cols,aligned", [
+    (torch.bfloat16, 3, 131072, True), (torch.float16, 600, 65544, True),
+    (torch.float32, 5, 40000, True), (torch.bfloat16, 1100, 20001, False),
+    (torch.float32, 7, 33344, False)],
+    ids=["bf16-131072", "f16-65544x600", "f32-40000", "bf16-20001-scalar",
+         "f32-33344-scalar"])
+def test_wide_rows_forward(lib, kind, dtype, rows, cols, aligned):
+    """Rows past the LDS tile (16-bit > 65536 columns, fp32 > 32768) and long rows off the
+    vector path (odd widths; 16-byte misaligned pointers) take the streamed wide-row kernel:
+    every forward flavour against the oracle, statistics included, bitwise reproducible
+    (600 / 1100 rows: several rows per block)."""
+    if kind.endswith("_mx") and cols % 32:
+        pytest.skip("MXFP8 needs a multiple of 32 columns")
+    gen = torch.Generator().manual_seed(cols + 17 * WIDE_KINDS.index(kind))
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    if aligned:
+        x, r = cuda(xc), cuda(rc)
+    else:  # one element of offset: 16-byte misaligned device pointers
+        xbuf, rbuf = (torch.zeros(rows * cols + 1, dtype=dtype) for _ in range(2))
+        xbuf[1:] = xc.flatten()
+        rbuf[1:] = rc.flatten()
+        x, r = cuda(xbuf)[1:].view(rows, cols), cuda(rbuf)[1:].view(rows, cols)
+    g, b = cuda(gc), cuda(bc)
+    xs, rs, gs, bs = f32(xc), f32(rc), f32(gc), f32(bc)
+    io = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    # Zero-filled, so the buffers a flavour does not write compare equal between runs.
+    out = torch.zeros(rows, cols, device="cuda", dtype=torch.uint8 if "fp8" in kind or "mx" in
+                      kind else dtype)
+    h = torch.zeros(rows, cols, device="cuda", dtype=dtype)
+    mean = torch.zeros(rows, device="cuda")
+    rstd = torch.zeros(rows, device="cuda")
+    sc = torch.zeros(rows, cols // 32 if kind.endswith("_mx") else 1, device="cuda",
+                     dtype=torch.uint8 if kind.endswith("_mx") else torch.float32)
+
+    def run():
+        st = capi.stream()
+        if kind == "ln":
+            rc_ = lib.fln_layernorm_forward(p(x), p(g), p(b), p(out), p(mean), p(rstd), rows,
+                                            cols, code, 1e-5, st)
+        elif kind == "rms":
+            rc_ = lib.fln_rmsnorm_forward(p(x), p(g), p(out), p(rstd), rows, cols, code, 1e-6,
+                                          st)
+        elif kind == "add_ln":
+            rc_ = lib.fln_add_layernorm_forward(p(x), p(r), p(g), p(b), p(h), p(out), p(mean),
+                                                p(rstd), rows, cols, code, 1e-5, st)
+        elif kind == "add_rms":
+            rc_ = lib.fln_add_rmsnorm_forward(p(x), p(r), p(g), p(h), p(out), p(rstd), rows,
+                                              cols, code, 1e-6, st)
+        elif kind.startswith("gelu"):
+            gm = capi.GELU_ERF if kind == "gelu_none" else capi.GELU_TANH
+            rc_ = lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(out), p(mean), p(rstd),
+                                                 rows, cols, code, 1e-5, gm, st)
+        elif kind == "ln_fp8":
+            rc_ = lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(out), p(sc), p(mean),
+                                                p(rstd), rows, cols, code, 1e-5, st)
+        elif kind == "rms_fp8":
+            rc_ = lib.fln_rmsnorm_fp8_forward(p(x), p(g), p(out), p(sc), p(rstd), rows, cols,
+                                              code, 1e-6, st)
+        elif kind == "add_rms_fp8":
+            rc_ = lib.fln_add_rmsnorm_fp8_forward(p(x), p(r), p(g), p(h), p(out), p(sc),
+                                                  p(rstd), rows, cols, code, 1e-6, st)
+        else:
+            rc_ = _mx_call(lib, kind[:-3], x, r, g, b if kind == "ln_mx" else None, out, sc, h,
+                           rows, cols, code)
+        capi.check(rc_)
+        torch.cuda.synchronize()
+        return out.clone(), sc.clone(), mean.clone(), rstd.clone(), h.clone()
+
+    got, sc_got, m_got, r_got, h_got = run()
+    again = run()
+    for name, a, c in zip(("out", "scale", "mean", "rstd", "h"),
+                          (got, sc_got, m_got, r_got, h_got), again):
+        assert torch.equal(a, c), f"{name} bitwise reproducible"
+    if kind.startswith("add"):
+        h_ref = xc + rc  # torch CPU add in the I/O type
+        assert torch.equal(h_got.cpu(), h_ref), "h bit-exact"
+        hs = f32(h_ref)
+    else:
+        hs = xs
+    rms = "rms" in kind
+    if rms:
+        y_ref, r_ref = norms.rms_norm_fwd(hs, gs, 1e-6)
+        m_ref = None
+    else:
+        y_ref, m_ref, r_ref = norms.layer_norm_fwd(hs, gs, bs, 1e-5)
+    if not kind.endswith("_mx"):  # the MX entry points are called without statistics
+        assert np.abs(to_np(r_got) / np.asarray(r_ref).reshape(-1) - 1).max() <= 1e-5
+        if m_ref is not None:
+            m_ref = np.asarray(m_ref).reshape(-1)
+            assert np.abs(to_np(m_got) - m_ref).max() <= 1e-5 * max(1.0, np.abs(m_ref).max())
+    if kind.endswith("_fp8"):
+        if kind == "ln_fp8":
+            q_ref, s_ref = norms.layer_norm_fp8_fwd(hs, gs, bs, 1e-5)
+        else:
+            q_ref, s_ref = norms.rms_norm_fp8_fwd(hs, gs, 1e-6)
+        assert_fp8_close(got.cpu().numpy(), to_np(sc_got).reshape(-1), q_ref, s_ref, kind,
+                         t_ref=_scaled(y_ref))
+        return
+    if kind.endswith("_mx"):
+        q_ref, s_ref = norms.mx_e4m3_quantize(y_ref)
+        assert_mx_close(got.cpu().numpy(), sc_got.cpu().numpy(), q_ref, s_ref, y_ref, kind)
+        return
+    if kind.startswith("gelu"):
+        y_ref = norms.gelu(y_ref, kind[5:])
+    if dtype == torch.float32:
+        assert np.abs(to_np(got) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+    else:
+        atol = affine_atol(hs, gs, None if rms else bs, 1e-5)
+        if not rms:
+            # These rows have mean ~0.5: the fp32 mean's own rounding (a few ulps of |mean|)
+            # shifts every output by rstd |gamma| times it -- more than an f16 ulp where the
+            # output is subnormal (fixed 2^-24 spacing below 6.1e-5).
+            atol = atol + 2.0 ** -21 * (np.abs(m_ref)[:, None] * np.asarray(r_ref).reshape(-1, 1)
+                                        * np.abs(gs))
+        assert_within_ulp(to_np(got), y_ref, 1.0, atol=atol, **_tol_fwd(dtype), what=kind)
+
+
 def test_fp8_variants_reject_bad_arguments(lib):
     x = torch.randn(4, 64, device="cuda")
     q = torch.empty(4, 64, device="cuda", dtype=torch.uint8)

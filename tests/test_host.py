@@ -168,11 +168,11 @@ def test_optimal_config_reports_dispatch_geometry():
     c7 = fl.functional.get_optimal_config(32768, 7168, torch.bfloat16)
     assert (c7["waves_per_row"], c7["vectors_per_lane"], c7["threads_per_block"]) == (7, 2, 448)
     c2 = fl.functional.get_optimal_config(1, 100000, torch.float32)
-    assert not c2["register_resident"] and not c2["lds_staged"]
+    assert not c2["register_resident"] and not c2["lds_staged"] and c2["wide_streamed"]
     c3 = fl.functional.get_optimal_config(64, 65536, torch.bfloat16)
-    assert not c3["register_resident"] and c3["lds_staged"]
-    c4 = fl.functional.get_optimal_config(64, 40001, torch.bfloat16)  # unaligned: looped
-    assert not c4["register_resident"] and not c4["lds_staged"]
+    assert not c3["register_resident"] and c3["lds_staged"] and not c3["wide_streamed"]
+    c4 = fl.functional.get_optimal_config(64, 40001, torch.bfloat16)  # unaligned: streamed
+    assert not c4["register_resident"] and not c4["lds_staged"] and c4["wide_streamed"]
     c5 = fl.functional.get_optimal_config(64, 20480, torch.float32)  # no fp32 RAW tiles
     assert not c5["register_resident"] and c5["lds_staged"]
     # Rows of more than 4 waves: at most 16 elements per lane (1024-thread blocks have 128
