@@ -620,6 +620,68 @@ def torch_gpu_compare(torch, ours, warmup=10, n=50):
     return res
 
 
+def torch_cpu_configs(seconds=1.5, threads=16):
+    """The reference's CPU path on each config: torch-CPU ops on the same seeded inputs (the
+    config's dtype), `threads` host threads, a bounded row sample of the large configs; median
+    of >= 3 runs, extrapolated to the full row count (rows are independent)."""
+    import torch
+    from fused_layernorm.testing import WORKLOADS, algorithmic_bytes, make_inputs
+    F = torch.nn.functional
+    torch.set_num_threads(max(1, min(threads, os.cpu_count() or 1)))
+    res = {}
+    cases = (("c1_ln_fwd_fp32_32x768", None), ("c2_ln_gelu_fp32_17x1023", None),
+             ("c2_ln_gelu_fp32_64x4096", None), ("c3_add_ln_fwd_bf16_8192x4096", 512),
+             ("c4_rms_fwd_bwd_bf16_16384x8192", 256), ("c5_ln_fp8_bf16_32768x7168", 256))
+    for name, sample in cases:
+        w = WORKLOADS[name]
+        rows = w.rows if sample is None else sample
+        inp = make_inputs(w, rows)
+        x, g, b = inp["x"], inp.get("gamma"), inp.get("beta")
+        shape = (w.cols,)
+        if w.op == "layer_norm":
+            def run():
+                F.layer_norm(x, shape, g, b, w.eps)
+            what = "F.layer_norm"
+        elif w.op == "layer_norm_gelu":
+            def run():
+                F.gelu(F.layer_norm(x, shape, g, b, w.eps), approximate=w.approximate)
+            what = f"F.gelu(F.layer_norm), approximate={w.approximate!r}"
+        elif w.op == "add_layer_norm":
+            r = inp["residual"]
+
+            def run():
+                F.layer_norm(x + r, shape, g, b, w.eps)
+            what = "x + r, F.layer_norm"
+        elif w.op == "rms_norm_fwd_bwd":
+            xg = x.clone().requires_grad_(True)
+            gg = g.clone().requires_grad_(True)
+            dy = inp["dy"]
+
+            def run():
+                torch.autograd.grad(F.rms_norm(xg, shape, gg, w.eps), (xg, gg), dy)
+            what = "F.rms_norm + autograd backward"
+        else:  # layer_norm_fp8
+            def run():
+                y = F.layer_norm(x, shape, g, b, w.eps).float()
+                scale = y.abs().amax(dim=-1, keepdim=True) / 448.0
+                (y / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+            what = "F.layer_norm, row amax, scale, clamp, float8_e4m3fn cast"
+        for _ in range(3):
+            run()
+        times = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        res[name] = {"us_per_call": round(med * (w.rows / rows) * 1e6, 1),
+                     "gbs": round(algorithmic_bytes(w, rows)["total"] / med / 1e9, 2),
+                     "sample": f"{rows} of {w.rows} rows, {what}, median of {len(times)}"}
+    res["threads"] = torch.get_num_threads()
+    return res
+
+
 # ------------------------------------------------------------------------------------------------
 def time_graph(runner, n_calls=32, replays=20):
     """GPU-side time (ms) of one forward call: n_calls C-ABI calls captured in one HIP graph
@@ -839,6 +901,14 @@ def main():
         w = WORKLOADS[HEADLINE]
         out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
         out["cpu_baseline"]["torch_cpu"] = torch_cpu_baseline(w, max(2.0, args.cpu_seconds / 2))
+        if not args.no_configs and not args.headline_only:
+            tc = torch_cpu_configs()
+            for name, e in tc.items():
+                if name in out.get("configs", {}):
+                    mine = out["configs"][name]["us_per_call"]
+                    mine = mine["fwd_bwd"] if isinstance(mine, dict) else mine
+                    e["gpu_speedup"] = round(e["us_per_call"] / mine, 1)
+            out["cpu_baseline"]["torch_cpu_configs"] = tc
     out["host"] = platform.node()
     print(json.dumps(out), flush=True)
 
