@@ -341,16 +341,17 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit rows of 8193..16384 columns with a residual gradient, of 8193..12288 with GELU; 16-bit
-// LayerNorm / RMSNorm rows of 16385..18432 columns): one NT-thread block per row at a time, thread t owning vectors t + NT i
+// 16-bit rows of 8193..16384 columns with a residual gradient, of 8193..12288 with GELU, and
+// 16-bit rows of 16385..18432 columns, or up to 24576 for LayerNorm / RMSNorm without a
+// residual gradient): one NT-thread block per row at a time, thread t owning vectors t + NT i
 // (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
 // and writes dx.  A thread reads back only the vectors it parked, so the staging needs no barrier:
 // LDS serves as per-thread spill space for the row (128 KiB at CPT 4 and 1024 threads).
 // NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168, which holds the
-// 48 fp32 column sums, the prefetched row and gamma of a 16-bit lane with 3 vectors, or 2 vectors
-// with GELU's beta and derivative temporaries, without spilling.
+// fp32 column sums and the prefetched row of a 16-bit lane with 3 vectors (gamma / beta in LDS),
+// or 2 vectors with GELU's parameters and derivative temporaries, without spilling.
 constexpr int kLdsThreads = 1024;
 constexpr int kLds16Threads = 768;
 
@@ -359,7 +360,11 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
   constexpr int kT = NT;
   constexpr int kW = kT / kWave;
   using P = Pack<T, VEC>;
+  // 768-thread blocks with 3-4 vectors per thread keep gamma (and, with GELU, beta) in LDS too,
+  // thread-private like the row: 12-32 VGPRs per lane that would otherwise spill.
+  constexpr bool PARAMS_IN_LDS = NT == kLds16Threads && CPT >= 3;
   __shared__ P xs[CPT * kT], ds[CPT * kT];
+  __shared__ P gs[PARAMS_IN_LDS ? CPT * kT : 1], bs[PARAMS_IN_LDS && GELU ? CPT * kT : 1];
   __shared__ float red[2][2][kW + 16];  // [parity][sum g, sum g*xhat][wave], padded
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
@@ -374,30 +379,50 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
   const T* DR = static_cast<const T*>(p.dres);
   T* DX = static_cast<T*>(p.dx);
 
-  P gmr[CPT];
-  P btr[GELU ? CPT : 1];
+  P gmr[PARAMS_IN_LDS ? 1 : CPT];
+  P btr[GELU && !PARAMS_IN_LDS ? CPT : 1];
   {
     const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
     const bool has_g = p.gamma != nullptr;
     const T one = from_f32<T>(1.0f);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      gmr[i] = buf_load<P>(gr, t + i * kT);
+      P gv = buf_load<P>(gr, t + i * kT);
 #pragma unroll
       for (int e = 0; e < VEC; ++e)
-        if (!has_g) gmr[i].v[e] = one;
+        if (!has_g) gv.v[e] = one;
+      if constexpr (PARAMS_IN_LDS)
+        gs[i * kT + t] = gv;
+      else
+        gmr[i] = gv;
     }
     if constexpr (GELU != 0) {
       const rsrc_t br = make_rsrc(p.beta, row_bytes);
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) btr[i] = buf_load<P>(br, t + i * kT);
+      for (int i = 0; i < CPT; ++i) {
+        if constexpr (PARAMS_IN_LDS)
+          bs[i * kT + t] = buf_load<P>(br, t + i * kT);
+        else
+          btr[i] = buf_load<P>(br, t + i * kT);
+      }
     }
   }
-  auto gam = [&](int i, int e) { return to_f32(gmr[i].v[e]); };
+  auto gam = [&](int i, int e) {
+    if constexpr (PARAMS_IN_LDS)
+      return to_f32(gs[i * kT + t].v[e]);
+    else
+      return to_f32(gmr[i].v[e]);
+  };
+  auto bet = [&](int i, int e) {
+    if constexpr (PARAMS_IN_LDS)
+      return to_f32(bs[i * kT + t].v[e]);
+    else
+      return to_f32(btr[i].v[e]);
+  };
   // Upstream gradient at the LayerNorm output: dy, or dy GELU'(xhat gamma + beta).
   auto dln = [&](float d, float xh, int i, int e) {
-    if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam(i, e), to_f32(btr[i].v[e])));
-    if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam(i, e), to_f32(btr[i].v[e])));
+    if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam(i, e), bet(i, e)));
+    if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam(i, e), bet(i, e)));
     return d;
   };
   float acc_g[CPT][VEC], acc_b[CPT][VEC];
@@ -503,9 +528,9 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
   }
 }
 
-// Rows past the register and LDS tiles (16-bit rows of more than 16384 columns, save the
-// LayerNorm / RMSNorm rows of up to 18432; fp32 rows of more than 16384; long rows on the scalar
-// path), any width, in two streaming passes:
+// Rows past the register and LDS tiles (16-bit rows of more than 18432 columns, save the
+// LayerNorm / RMSNorm rows of up to 24576 without a residual gradient; fp32 rows of more than
+// 16384; long rows on the scalar path), any width, in two streaming passes:
 //   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
 //     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
 //     rows grid-stride, four vectors per thread in flight per array;
@@ -861,6 +886,18 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
         if (geo.lds_cpt == 3 && !p.dres && !p.gelu)
           hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 3, kLds16Threads>), grid, block, 0,
                              s, p);
+        else if (geo.lds_cpt == 3 && p.dres && !p.gelu)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VV, 3, kLds16Threads>), grid, block, 0,
+                             s, p);
+        else if (geo.lds_cpt == 4 && !p.dres && !p.gelu)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 4, kLds16Threads>), grid, block, 0,
+                             s, p);
+        else if (geo.lds_cpt == 3 && p.gelu == 1)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 1, VV, 3, kLds16Threads>), grid, block, 0,
+                             s, p);
+        else if (geo.lds_cpt == 3 && p.gelu == 2)
+          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 2, VV, 3, kLds16Threads>), grid, block, 0,
+                             s, p);
         else if (geo.lds_cpt == 2 && p.gelu == 1)
           hipLaunchKernelGGL((bwd_lds_kernel<T, false, 1, VV, 2, kLds16Threads>), grid, block, 0,
                              s, p);
@@ -952,24 +989,27 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // (16-bit rows past 16384 columns need 48-64 VGPRs of column sums per lane on top of the
   // prefetched row and spill in a 1024-thread block.)  16-bit rows of 8193..16384
   // columns with a residual gradient also take it (2 vectors per thread): the register kernel
-  // spills there (measured 166 us against 123 us at 4096 x 16384 bf16).  16-bit LayerNorm /
-  // RMSNorm rows of 16385..18432 columns take it with 768 threads and 3 vectors per thread
-  // (4096 x 18432 bf16: 161 -> 109 us against the two passes); the GELU and residual flavours
-  // spill there and 4 vectors per thread (up to 24576 columns) spill for every flavour, all
-  // measured slower than the two passes.  16-bit GELU rows of 8193..12288 columns take it with
-  // 768 threads and 2 vectors per thread (no spill; the register kernel spills 84-232 B per lane
-  // there): 4096 x 12288 bf16 tanh 122.6 -> 109.5 us, erf 302.4 -> 142.8 us.  Wider GELU rows
-  // (12289..16384) keep the register kernel, measured faster than 2 vectors per thread in
-  // 1024-thread blocks (134.8 against 162.1 us at 4096 x 16384).
+  // spills there (measured 166 us against 123 us at 4096 x 16384 bf16).  16-bit rows past
+  // 16384 columns take it with 768 threads (gamma / beta parked in LDS as well): 3 vectors per
+  // thread (up to 18432 columns) for every flavour, 4 (up to 24576) for LayerNorm / RMSNorm
+  // without a residual gradient (44 B of spill left), all measured faster than the two passes
+  // (4096 x 18432 bf16: LN 161 -> 108 us, + residual 164 -> 110 us, + GELU 206 -> 163 us;
+  // 4096 x 20480 LN 170 -> 146 us).  16-bit GELU rows of 8193..12288 columns take it with 2
+  // vectors per thread (no spill; the register kernel spills 84-232 B per lane there):
+  // 4096 x 12288 bf16 tanh 122.6 -> 109.5 us, erf 302.4 -> 142.8 us.  GELU rows of
+  // 12289..16384 keep the register kernel, measured faster than 3 vectors per thread in 768
+  // threads or 2 in 1024 (4096 x 16384 tanh 135.7 against 158.0 / 162.1 us: the LDS kernel
+  // evaluates GELU' in both of its passes).
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
   const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
-  const bool wide16 = !g.reg_path && es == 2 && cpt16 == 3 && !dres && !gelu;
-  const bool gelu16 = gelu && g.reg_path && es == 2 && g.vpl == 2 && cpt16 == 2;
+  const bool wide16 = !g.reg_path && es == 2 && !gelu && (cpt16 == 3 || (cpt16 == 4 && !dres));
+  const bool gelu16 = gelu && es == 2 &&
+                      ((g.reg_path && g.vpl == 2 && cpt16 == 2) || (!g.reg_path && cpt16 == 3));
   if (g.vec > 1 && (wide_f32 || dres16 || wide16 || gelu16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
-    g.lds_cpt = wide16 ? 3 : gelu16 ? 2 : static_cast<int>(cpt);
+    g.lds_cpt = (wide16 || gelu16) ? static_cast<int>(cpt16) : static_cast<int>(cpt);
     g.threads = (wide16 || gelu16) ? kLds16Threads : kLdsThreads;
     g.wpr = g.threads / kWave;
     g.rgs = 1;

@@ -852,15 +852,19 @@ def test_fp32_wide_row_backward(lib, monkeypatch, kind, cols):
             assert float((a - c).abs().max()) <= 1e-5 * max(1.0, scale)
 
 
-@pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_tanh"])
+@pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_tanh", "gelu_none"])
 @pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 18432), (torch.float16, 16392),
-                                        (torch.bfloat16, 17416)],
-                         ids=["bf16-18432", "f16-16392", "bf16-17416"])
+                                        (torch.bfloat16, 17416), (torch.bfloat16, 20480),
+                                        (torch.float16, 24576)],
+                         ids=["bf16-18432", "f16-16392", "bf16-17416", "bf16-20480",
+                              "f16-24576"])
 def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
-    """16-bit LayerNorm / RMSNorm rows of 16385..18432 columns take the LDS-staged backward with
-    768-thread blocks (3 vectors per thread, the last ones partly past the row; 600 rows: several
-    per block); the residual and GELU flavours keep the two passes.  Parity with the oracle,
-    bitwise reproducible, and agreement with the two-pass backward (FLN_BWD_NO_LDS)."""
+    """16-bit rows of 16385..18432 columns take the LDS-staged backward with 768-thread blocks
+    (3 vectors per thread, the last ones partly past the row, gamma / beta parked in LDS; 600
+    rows: several per block) for every flavour, LayerNorm / RMSNorm rows of up to 24576 with 4
+    vectors per thread; the residual and GELU flavours past 18432 keep the two passes.  Parity
+    with the oracle, bitwise reproducible, and agreement with the two-pass backward
+    (FLN_BWD_NO_LDS)."""
     rows = 600
     gen = torch.Generator().manual_seed(cols + 5 * len(kind))
     xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
@@ -873,16 +877,16 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
     code = capi.dtype_code(x)
     p = capi.ptr
     ulp_kind = "bf16" if dtype == torch.bfloat16 else "f16"
+    gm = capi.GELU_ERF if kind == "gelu_none" else capi.GELU_TANH
     if kind == "rms":
         _, rstd = rms_forward(lib, x, g, 1e-6)
     else:
         mean = torch.empty(rows, device="cuda")
         rstd = torch.empty(rows, device="cuda")
         y = torch.empty_like(x)
-        if kind == "gelu_tanh":
+        if kind.startswith("gelu"):
             capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd),
-                                                      rows, cols, code, 1e-5, capi.GELU_TANH,
-                                                      capi.stream()))
+                                                      rows, cols, code, 1e-5, gm, capi.stream()))
         else:
             capi.check(lib.fln_layernorm_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
                                                  cols, code, 1e-5, capi.stream()))
@@ -891,15 +895,14 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
         if kind == "rms":
             dx, dw = rms_backward(lib, dy, x, rstd, g)
             return dx, dw, None
-        if kind == "gelu_tanh":
+        if kind.startswith("gelu"):
             dx = torch.empty_like(x)
             dg = torch.empty(cols, device="cuda")
             db = torch.empty(cols, device="cuda")
             ws, n = workspace(lib, rows, cols, x)
             capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b),
                                                        p(dx), p(dg), p(db), rows, cols, code,
-                                                       capi.F32, capi.GELU_TANH, p(ws), n,
-                                                       capi.stream()))
+                                                       capi.F32, gm, p(ws), n, capi.stream()))
             torch.cuda.synchronize()
             return dx, dg, db
         return ln_backward(lib, dy, x, mean, rstd, g, dres=dr if kind == "ln_dres" else None)
@@ -907,8 +910,8 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
     dx, dg, db = run()
     if kind == "rms":
         dx_ref, dg_ref = norms.rms_norm_bwd(dys, xs, gs, 1e-6)
-    elif kind == "gelu_tanh":
-        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, "tanh")
+    elif kind.startswith("gelu"):
+        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, kind[5:])
     else:
         dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
         if kind == "ln_dres":
