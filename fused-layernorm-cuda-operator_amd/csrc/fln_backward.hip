@@ -165,27 +165,51 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 
   // gamma (and, with GELU, beta) stay in registers in the I/O type and are widened at each use
   // (gamma ones when absent; zeros past the row): half the VGPRs of fp32 copies for 16-bit types.
-  P gmr[VPL];
-  P btr[GELU ? VPL : 1];
+  // The 16-bit GELU flavour with two vectors per lane in 1024-thread blocks parks them in LDS
+  // instead, each thread its own copy (64 KiB, no barrier): in registers they made it spill
+  // 84-132 B per lane (4096 x 16384 bf16: tanh 132.4 -> 102.6 us, erf 153.2 -> 96.5 us).
+  constexpr bool PARAMS_IN_LDS = GELU != 0 && VPL == 2 && MAXT == 1024 && sizeof(T) == 2;
+  __shared__ P gsh[PARAMS_IN_LDS ? VPL * MAXT : 1], bsh[PARAMS_IN_LDS ? VPL * MAXT : 1];
+  P gmr[PARAMS_IN_LDS ? 1 : VPL];
+  P btr[GELU && !PARAMS_IN_LDS ? VPL : 1];
   {
     const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
     const bool has_g = p.gamma != nullptr;
     const T one = from_f32<T>(1.0f);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      gmr[i] = buf_load<P>(gr, t + i * tpr);
+      P gv = buf_load<P>(gr, t + i * tpr);
 #pragma unroll
       for (int e = 0; e < VEC; ++e)
-        if (!has_g) gmr[i].v[e] = one;
+        if (!has_g) gv.v[e] = one;
+      if constexpr (PARAMS_IN_LDS)
+        gsh[i * MAXT + threadIdx.x] = gv;
+      else
+        gmr[i] = gv;
     }
     if constexpr (GELU != 0) {
       const rsrc_t br = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) btr[i] = buf_load<P>(br, t + i * tpr);
+      for (int i = 0; i < VPL; ++i) {
+        if constexpr (PARAMS_IN_LDS)
+          bsh[i * MAXT + threadIdx.x] = buf_load<P>(br, t + i * tpr);
+        else
+          btr[i] = buf_load<P>(br, t + i * tpr);
+      }
     }
   }
-  auto gam = [&](int i, int e) { return to_f32(gmr[i].v[e]); };
-  auto bet = [&](int i, int e) { return to_f32(btr[GELU ? i : 0].v[e]); };
+  auto gam = [&](int i, int e) {
+    if constexpr (PARAMS_IN_LDS)
+      return to_f32(gsh[i * MAXT + threadIdx.x].v[e]);
+    else
+      return to_f32(gmr[i].v[e]);
+  };
+  auto bet = [&](int i, int e) {
+    if constexpr (PARAMS_IN_LDS)
+      return to_f32(bsh[i * MAXT + threadIdx.x].v[e]);
+    else
+      return to_f32(btr[GELU ? i : 0].v[e]);
+  };
   float acc_g[VPL][VEC], acc_b[VPL][VEC];
 #pragma unroll
   for (int i = 0; i < VPL; ++i)
@@ -341,17 +365,17 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit rows of 8193..16384 columns with a residual gradient, of 8193..12288 with GELU, and
-// 16-bit rows of 16385..18432 columns, or up to 24576 for LayerNorm / RMSNorm without a
-// residual gradient): one NT-thread block per row at a time, thread t owning vectors t + NT i
+// 16-bit rows of 8193..16384 columns with a residual gradient, and 16-bit rows of 16385..18432
+// columns, or up to 24576 for LayerNorm / RMSNorm without a residual gradient): one NT-thread
+// block per row at a time, thread t owning vectors t + NT i
 // (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
 // and writes dx.  A thread reads back only the vectors it parked, so the staging needs no barrier:
 // LDS serves as per-thread spill space for the row (128 KiB at CPT 4 and 1024 threads).
 // NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168, which holds the
-// fp32 column sums and the prefetched row of a 16-bit lane with 3 vectors (gamma / beta in LDS),
-// or 2 vectors with GELU's parameters and derivative temporaries, without spilling.
+// fp32 column sums and the prefetched row of a 16-bit lane with 3 vectors (gamma / beta in LDS)
+// without spilling.
 constexpr int kLdsThreads = 1024;
 constexpr int kLds16Threads = 768;
 
@@ -898,12 +922,6 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
         else if (geo.lds_cpt == 3 && p.gelu == 2)
           hipLaunchKernelGGL((bwd_lds_kernel<T, false, 2, VV, 3, kLds16Threads>), grid, block, 0,
                              s, p);
-        else if (geo.lds_cpt == 2 && p.gelu == 1)
-          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 1, VV, 2, kLds16Threads>), grid, block, 0,
-                             s, p);
-        else if (geo.lds_cpt == 2 && p.gelu == 2)
-          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 2, VV, 2, kLds16Threads>), grid, block, 0,
-                             s, p);
         else
           return FLN_ERR_INVALID;
         return static_cast<int>(hipGetLastError());
@@ -994,19 +1012,16 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // thread (up to 18432 columns) for every flavour, 4 (up to 24576) for LayerNorm / RMSNorm
   // without a residual gradient (44 B of spill left), all measured faster than the two passes
   // (4096 x 18432 bf16: LN 161 -> 108 us, + residual 164 -> 110 us, + GELU 206 -> 163 us;
-  // 4096 x 20480 LN 170 -> 146 us).  16-bit GELU rows of 8193..12288 columns take it with 2
-  // vectors per thread (no spill; the register kernel spills 84-232 B per lane there):
-  // 4096 x 12288 bf16 tanh 122.6 -> 109.5 us, erf 302.4 -> 142.8 us.  GELU rows of
-  // 12289..16384 keep the register kernel, measured faster than 3 vectors per thread in 768
-  // threads or 2 in 1024 (4096 x 16384 tanh 135.7 against 158.0 / 162.1 us: the LDS kernel
-  // evaluates GELU' in both of its passes).
+  // 4096 x 20480 LN 170 -> 146 us).  16-bit GELU rows of up to 16384 columns keep the register
+  // kernel (gamma / beta in LDS there), measured faster than this kernel, which evaluates GELU'
+  // in both of its passes (4096 x 12288 bf16 tanh 95.6 against 109.6 us with 2 vectors per
+  // thread in 768 threads).
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
   const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
   const bool wide16 = !g.reg_path && es == 2 && !gelu && (cpt16 == 3 || (cpt16 == 4 && !dres));
-  const bool gelu16 = gelu && es == 2 &&
-                      ((g.reg_path && g.vpl == 2 && cpt16 == 2) || (!g.reg_path && cpt16 == 3));
+  const bool gelu16 = gelu && es == 2 && !g.reg_path && cpt16 == 3;
   if (g.vec > 1 && (wide_f32 || dres16 || wide16 || gelu16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
     g.lds_cpt = (wide16 || gelu16) ? static_cast<int>(cpt16) : static_cast<int>(cpt);

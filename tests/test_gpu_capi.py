@@ -615,7 +615,8 @@ def test_fp8_variants_reject_bad_arguments(lib):
 def test_layernorm_gelu_backward_matrix(lib, mode, dtype, rows, cols):
     """Backward of GELU(LayerNorm(x) gamma + beta): the forward with statistics, then the fused
     backward, against the numpy oracle (LayerNorm backward of dy GELU'(a)).  16-bit rows of
-    8193..12288 columns take the 768-thread LDS-staged kernel (600 rows: several per block)."""
+    8193..16384 columns keep gamma / beta in LDS in the register kernel (600 rows: several per
+    block)."""
     gen = torch.Generator().manual_seed(rows * 7 + cols)
     xc = torch.randn(rows, cols, generator=gen).to(dtype)
     gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
