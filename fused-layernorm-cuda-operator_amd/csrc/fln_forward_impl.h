@@ -52,9 +52,10 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 // 1 erf, 2 tanh (a template parameter so the plain kernels carry no GELU code).
 // ---------------------------------------------------------------------------------------------
 // Register budget: a 1024-thread block leaves 128 VGPRs per lane.  There a lane with more than
-// 32 bytes of a row prefetches one row instead of two, and a lane with 32 elements (RAW) keeps
-// the row in the I/O type rather than as an fp32 copy, widening it again in each pass (one VALU
-// op per element).  Blocks of at most 256 threads have 256 VGPRs and keep the fp32 copy.
+// 32 bytes of a row prefetches one row instead of two (two again for the 16-bit RAW tiles without
+// a residual, whose gamma / beta live in LDS), and a lane with 32 elements (RAW) keeps the row in
+// the I/O type rather than as an fp32 copy, widening it again in each pass (one VALU op per
+// element).  Blocks of at most 256 threads have 256 VGPRs and keep the fp32 copy.
 #ifndef FLN_FWD_PREFETCH
 #define FLN_FWD_PREFETCH(ROW_BYTES, MAXT) ((MAXT) > 256 && (ROW_BYTES) > 32 ? 1 : 2)
 #endif
@@ -70,9 +71,21 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 #endif
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
-  // rows in flight ahead of the current one
-  constexpr int PD = FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT);
   constexpr bool RAW = MAXT > 256 && VPL * VEC >= 32;  // row kept in the I/O type
+  // gamma / beta parked in LDS, each thread its own copy (no barrier; 64-128 KiB), for the 16-bit
+  // RAW tiles and the scalar path's 16 elements per lane in 1024-thread blocks: in registers
+  // they made the residual / fp8 flavours spill 16-332 B per lane, and they left room for only
+  // one row in flight elsewhere (bf16, us: residual + LN 2048 x 32768 102.7 -> 89.6, residual +
+  // RMSNorm -> fp8 111.9 -> 82.3; with two rows in flight LN 2048 x 32768 52.8 -> 48.8, RMSNorm
+  // 4096 x 20480 62.6 -> 57.9, LN -> fp8 4096 x 20480 73.5 -> 67.1).
+  constexpr bool PARAMS_IN_LDS =
+      MAXT == 1024 && ((RAW && VEC > 1 && sizeof(T) == 2) || (VEC == 1 && VPL == 16 &&
+                                                                sizeof(T) <= 4));
+  // rows in flight ahead of the current one (the residual flavour's second input leaves room for
+  // one only)
+  constexpr int PD = PARAMS_IN_LDS && RAW && !RES
+                         ? 2
+                         : FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT);
   constexpr int MAXW = MAXT / kWave;
   __shared__ float red[2][3][MAXW + 16];  // padded: combine_partials reads 16 past the base
   using P = Pack<T, VEC>;
@@ -100,13 +113,6 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
   // Affine parameters, once per row group (vectors past the row read as zero).
   const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
   const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);
-  // The 16-bit RAW tiles with a residual or an fp8 output, and the scalar path's 16 elements per
-  // lane in 1024-thread blocks, park them in LDS instead, each thread its own copy (no barrier;
-  // 64-128 KiB): in registers those flavours spilled 16-332 B per lane (bf16 2048 x 32768:
-  // residual + LN 98.6 -> 86.7 us, residual + RMSNorm -> fp8 111.0 -> 81.8 us).
-  constexpr bool PARAMS_IN_LDS =
-      MAXT == 1024 && ((RAW && (RES || FP8 != 0) && VEC > 1 && sizeof(T) == 2) ||
-                       (VEC == 1 && VPL == 16 && sizeof(T) <= 4));
   __shared__ P gsh[PARAMS_IN_LDS ? VPL * MAXT : 1], bsh[PARAMS_IN_LDS ? VPL * MAXT : 1];
   P gv[PARAMS_IN_LDS ? 1 : VPL], bv[PARAMS_IN_LDS ? 1 : VPL];
   if constexpr (PARAMS_IN_LDS) {
