@@ -165,10 +165,13 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 
   // gamma (and, with GELU, beta) stay in registers in the I/O type and are widened at each use
   // (gamma ones when absent; zeros past the row): half the VGPRs of fp32 copies for 16-bit types.
-  // The 16-bit GELU flavour with two vectors per lane in 1024-thread blocks parks them in LDS
-  // instead, each thread its own copy (64 KiB, no barrier): in registers they made it spill
-  // 84-132 B per lane (4096 x 16384 bf16: tanh 132.4 -> 102.6 us, erf 153.2 -> 96.5 us).
-  constexpr bool PARAMS_IN_LDS = GELU != 0 && VPL == 2 && MAXT == 1024 && sizeof(T) == 2;
+  // The 16-bit GELU and residual-gradient flavours with two vectors per lane in 1024-thread
+  // blocks park them in LDS instead, each thread its own copy (64 KiB, no barrier): in registers
+  // they made those flavours spill 84-132 B per lane (4096 x 16384 bf16: GELU tanh 132.4 ->
+  // 102.6 us, erf 153.2 -> 96.5 us; with a residual gradient 97.8 us on the LDS-staged kernel
+  // -> 90.8 us here).
+  constexpr bool PARAMS_IN_LDS = (GELU != 0 || DRES) && VPL == 2 && MAXT == 1024 &&
+                                 sizeof(T) == 2;
   __shared__ P gsh[PARAMS_IN_LDS ? VPL * MAXT : 1], bsh[PARAMS_IN_LDS ? VPL * MAXT : 1];
   P gmr[PARAMS_IN_LDS ? 1 : VPL];
   P btr[GELU && !PARAMS_IN_LDS ? VPL : 1];
@@ -365,9 +368,8 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit rows of 8193..16384 columns with a residual gradient, and 16-bit rows of 16385..18432
-// columns, or up to 24576 for LayerNorm / RMSNorm without a residual gradient): one NT-thread
-// block per row at a time, thread t owning vectors t + NT i
+// 16-bit rows of 16385..18432 columns, or up to 24576 for LayerNorm / RMSNorm without a residual
+// gradient): one NT-thread block per row at a time, thread t owning vectors t + NT i
 // (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
@@ -926,11 +928,6 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
           return FLN_ERR_INVALID;
         return static_cast<int>(hipGetLastError());
       }
-      if (geo.lds_cpt == 2 && p.dres && !p.gelu) {
-        hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VV, 2>), dim3(geo.blocks),
-                           dim3(kLdsThreads), 0, s, p);
-        return static_cast<int>(hipGetLastError());
-      }
     }
     return FLN_ERR_INVALID;
   }
@@ -1005,9 +1002,9 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // fp32 rows too wide for registers but within 4 vectors per thread of a 1024-thread block
   // (8193..16384 columns): the LDS-staged kernel, one block per CU, rows dealt grid-stride.
   // (16-bit rows past 16384 columns need 48-64 VGPRs of column sums per lane on top of the
-  // prefetched row and spill in a 1024-thread block.)  16-bit rows of 8193..16384
-  // columns with a residual gradient also take it (2 vectors per thread): the register kernel
-  // spills there (measured 166 us against 123 us at 4096 x 16384 bf16).  16-bit rows past
+  // prefetched row and spill in a 1024-thread block.)  16-bit rows of 8193..16384 columns with
+  // a residual gradient keep the register kernel (gamma in LDS there), measured faster than 2
+  // vectors per thread here (4096 x 16384 bf16: 90.8 against 97.8 us).  16-bit rows past
   // 16384 columns take it with 768 threads (gamma / beta parked in LDS as well): 3 vectors per
   // thread (up to 18432 columns) for every flavour, 4 (up to 24576) for LayerNorm / RMSNorm
   // without a residual gradient (44 B of spill left), all measured faster than the two passes
@@ -1019,10 +1016,9 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
-  const bool dres16 = dres && g.reg_path && es == 2 && g.vpl == 2 && cpt == 2;
   const bool wide16 = !g.reg_path && es == 2 && !gelu && (cpt16 == 3 || (cpt16 == 4 && !dres));
   const bool gelu16 = gelu && es == 2 && !g.reg_path && cpt16 == 3;
-  if (g.vec > 1 && (wide_f32 || dres16 || wide16 || gelu16) && tun.bwd_no_lds == 0) {
+  if (g.vec > 1 && (wide_f32 || wide16 || gelu16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
     g.lds_cpt = (wide16 || gelu16) ? static_cast<int>(cpt16) : static_cast<int>(cpt);
     g.threads = (wide16 || gelu16) ? kLds16Threads : kLdsThreads;

@@ -762,7 +762,8 @@ def test_mxfp8_rejects_widths_not_multiple_of_32(lib):
                                        (600, 12296)])
 def test_residual_gradient_is_added(lib, dtype, rows, cols):
     """dx + dres for LayerNorm and RMSNorm; 16-bit rows of 8193..16384 columns take the
-    LDS-staged kernel (600 rows: several per block), wider ones the looped kernel."""
+    register kernel with gamma parked in LDS (600 rows: several per block), 32768 the two
+    passes."""
     gen = torch.Generator().manual_seed(9 + cols)
     xc = torch.randn(rows, cols, generator=gen).to(dtype)
     dyc = torch.randn(rows, cols, generator=gen).to(dtype)
