@@ -59,6 +59,15 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
              1e-5, (1.0, 0.02), (0.0, 0.02)),
     Workload("rms_fwd_bwd_bf16_8192x4096", "rms_norm_fwd_bwd", 8192, 4096, torch.bfloat16, 3,
              1e-6, (1.0, 0.02), None),
+    # Wide rows (profiled, not benchmark lines): the RAW-tile forward with the 768-thread
+    # LDS-staged backward; the streamed wide-row forward with the two-pass backward; the GELU
+    # backward with gamma / beta in LDS.
+    Workload("wide_ln_fwd_bwd_bf16_4096x18432", "layer_norm_fwd_bwd", 4096, 18432,
+             torch.bfloat16, 8, 1e-5, (1.0, 0.02), (0.0, 0.02)),
+    Workload("wide_ln_fwd_bwd_bf16_512x131072", "layer_norm_fwd_bwd", 512, 131072,
+             torch.bfloat16, 9, 1e-5, (1.0, 0.02), (0.0, 0.02)),
+    Workload("wide_ln_gelu_erf_fwd_bwd_bf16_4096x16384", "layer_norm_gelu_fwd_bwd", 4096, 16384,
+             torch.bfloat16, 10, 1e-5, (1.0, 0.02), (0.0, 0.02), approximate="none"),
 ]}
 
 

@@ -424,11 +424,13 @@ def _scaled(y):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
                          ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 1023), (33, 7168), (2, 16384),
-                                       (3, 12288), (2, 32768), (2, 40960), (300, 65536)])
+                                       (3, 12288), (2, 32768), (300, 24576), (2, 40960),
+                                       (300, 65536)])
 def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
     """LayerNorm -> fp8, RMSNorm -> fp8, residual + LayerNorm -> fp8, residual + RMSNorm -> fp8
-    over dtypes and widths (1023: the scalar path; 12288..32768: 12-16 waves and the RAW tiles;
-    40960 / 65536: the LDS-staged kernel, 300 rows: several per block), against the oracle."""
+    over dtypes and widths (1023: the scalar path; 12288..32768: 12-16 waves and the RAW tiles,
+    300 x 24576: several rows per block through their prefetch ring; 40960 / 65536: the
+    LDS-staged kernel), against the oracle."""
     gen = torch.Generator().manual_seed(rows * 31 + cols)
     xc = torch.randn(rows, cols, generator=gen).to(dtype)
     rc = torch.randn(rows, cols, generator=gen).to(dtype)
@@ -611,7 +613,8 @@ def test_fp8_variants_reject_bad_arguments(lib):
 @pytest.mark.parametrize("mode", ["none", "tanh"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (17, 1023), (33, 7168), (2, 16384), (300, 768),
-                                       (3, 12288), (600, 10248), (2, 32768), (2, 40960)])
+                                       (3, 12288), (600, 10248), (2, 32768), (300, 24576),
+                                       (2, 40960)])
 def test_layernorm_gelu_backward_matrix(lib, mode, dtype, rows, cols):
     """Backward of GELU(LayerNorm(x) gamma + beta): the forward with statistics, then the fused
     backward, against the numpy oracle (LayerNorm backward of dy GELU'(a)).  16-bit rows of
@@ -693,7 +696,7 @@ def _mx_ref(kind, xs, rs, gs, bs, io):
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,cols,path", [
     (64, 4096, "vec"), (33, 7168, "vec"), (9, 96, "vec"), (2, 16384, "vec"), (2, 32768, "vec"),
-    (3, 12288, "vec"), (2, 40960, "vec"), (300, 65536, "vec"),
+    (300, 24576, "vec"), (3, 12288, "vec"), (2, 40960, "vec"), (300, 65536, "vec"),
     (13, 1024, "scalar"), (3, 2048, "loop")])
 def test_mxfp8_matrix(lib, monkeypatch, kind, dtype, rows, cols, path):
     """OCP MXFP8 outputs (codes + E8M0 block scales) of LayerNorm, RMSNorm and residual +
