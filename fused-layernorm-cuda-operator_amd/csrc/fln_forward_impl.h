@@ -1057,8 +1057,13 @@ int launch_loop(const FwdParams& p, hipStream_t s) {
 // and take up to `wide_cap`, or `max_cap` (the RAW tiles) when nothing narrower fits 16 waves.
 // Preference order:
 //   1. the fewest waves per row (power of two) that fit the row within those caps;
-//   2. if that tiling leaves masked lanes, an exact tiling with any wave count <= 16 (e.g. a
-//      7168-element bf16 row is 7 waves x 64 lanes x 2 vectors), so no lane does masked work;
+//   2. if that tiling leaves masked lanes, an exact tiling with any wave count <= 16 and at least
+//      2 vectors per lane (e.g. a 7168-element bf16 row is 7 waves x 64 lanes x 2 vectors), so no
+//      lane does masked work.  With rows enough to fill the device, exact tilings of one vector
+//      per lane over an odd wave count lose to the power-of-two tiling with masked slots (16384
+//      rows, bf16, us: 2560 columns 5 x 1 35.5 against 2 x 4 32.6; 4608 9 x 1 61.9 / 4 x 4 58.8;
+//      6656 13 x 1 94.4 / 4 x 4 78.2; fp32 3328 97.2 / 78.8): the extra waves only add
+//      cross-wave reductions;
 //   3. few rows: more waves per row (fewer vectors each) until the grid covers the device.
 // Rows of 1, 2 or 4 waves share 256-thread blocks; other row groups are one block each.
 struct FwdGeometry {
@@ -1082,9 +1087,13 @@ inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_ca
   auto fits = [&](int w, int v) { return v <= (widest ? max_cap : cap_of(w)); };
   int vpl = next_pow2(static_cast<int>(per_lane(wpr)));
   bool exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
+  const int64_t target_waves = 4 * static_cast<int64_t>(device_cu_count());
   if (vec_path && !exact) {
     const int top = widest ? max_cap : (cap > wide_cap ? cap : wide_cap);
-    for (int v = next_pow2(top) > top ? next_pow2(top) / 2 : top; v >= 1; v >>= 1) {
+    // One vector per lane only when rows are too few to fill the device (latency-bound calls
+    // want the extra waves; C1, 32 x 768 fp32: 3 x 1 at 2.61 against 2 x 2 at 2.79 us).
+    const int min_v = rows * wpr < target_waves ? 1 : 2;
+    for (int v = next_pow2(top) > top ? next_pow2(top) / 2 : top; v >= min_v; v >>= 1) {
       const int64_t w = nvec / (kWave * v);
       if (nvec % (kWave * v) == 0 && w <= max_wpr && fits(static_cast<int>(w), v)) {
         wpr = static_cast<int>(w);
@@ -1094,7 +1103,6 @@ inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_ca
       }
     }
   }
-  const int64_t target_waves = 4 * static_cast<int64_t>(device_cu_count());
   while (rows * wpr < target_waves && wpr * 2 <= max_wpr) {
     if (exact && vpl >= 2) {
       wpr *= 2;

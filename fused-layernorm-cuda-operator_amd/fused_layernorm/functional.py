@@ -69,7 +69,9 @@ def _forward_geometry(rows: int, nvec: int, cap: int, wide_cap: int, max_cap: in
     if vec_path and not exact:
         top = max_cap if widest else max(cap, wide_cap)
         v = _next_pow2(top) // 2 if _next_pow2(top) > top else top
-        while v >= 1:
+        # exact tilings of one vector per lane only when rows are too few to fill the device
+        min_v = 1 if rows * wpr < 4 * num_cus else 2
+        while v >= min_v:
             w = nvec // (64 * v)
             if nvec % (64 * v) == 0 and w <= 16 and fits(w, v):
                 wpr, vpl, exact = w, v, True

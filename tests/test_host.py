@@ -167,6 +167,12 @@ def test_optimal_config_reports_dispatch_geometry():
     assert c["waves_per_row"] * 64 * c["vectors_per_lane"] * c["vector_elems"] == 4096
     c7 = fl.functional.get_optimal_config(32768, 7168, torch.bfloat16)
     assert (c7["waves_per_row"], c7["vectors_per_lane"], c7["threads_per_block"]) == (7, 2, 448)
+    # Exact tilings of one vector per lane only for rows too few to fill the device (C1);
+    # with many rows the power-of-two tiling with masked slots is taken instead.
+    wt = lambda c: (c["waves_per_row"], c["vectors_per_lane"], c["exact_tiling"])  # noqa: E731
+    assert wt(fl.functional.get_optimal_config(32, 768, torch.float32)) == (3, 1, True)
+    assert wt(fl.functional.get_optimal_config(16384, 2560, torch.bfloat16)) == (2, 4, False)
+    assert wt(fl.functional.get_optimal_config(16384, 6656, torch.bfloat16)) == (4, 4, False)
     c2 = fl.functional.get_optimal_config(1, 100000, torch.float32)
     assert not c2["register_resident"] and not c2["lds_staged"] and c2["wide_streamed"]
     c3 = fl.functional.get_optimal_config(64, 65536, torch.bfloat16)
