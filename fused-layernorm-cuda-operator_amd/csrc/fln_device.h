@@ -199,8 +199,8 @@ template <class A> __device__ __forceinline__ A wave_sum_generic(A v) {
 //
 // The tanh form is evaluated through the identity 0.5 v (1 + tanh(u)) = v sigmoid(2u) =
 // v / (1 + e^(-2u)), u = sqrt(2/pi) (v + 0.044715 v^3): one hardware exp2 (v_exp_f32) and one
-// hardware reciprocal (v_rcp_f32) instead of a tanh, and no cancellation for large negative v (the quotient stays
-// relatively accurate where 1 + tanh(u) would cancel).  Its derivative is
+// hardware reciprocal (v_rcp_f32) instead of a tanh, and no cancellation for large negative v
+// (the quotient stays relatively accurate where 1 + tanh(u) would cancel).  Its derivative is
 //   s + 2 v s (1 - s) sqrt(2/pi) (1 + 3 * 0.044715 v^2),   s = sigmoid(2u).
 // The erf form is v Phi(v) with Phi the standard normal CDF, and its derivative
 //   Phi(v) + v exp(-v^2 / 2) / sqrt(2 pi);
@@ -283,7 +283,9 @@ __device__ __forceinline__ double apply_gelu(double v, int mode) {
 // fp32 values into two bytes of a dword half.  Values are clamped to +-448 first, so the
 // conversion never sees an out-of-range input (saturating semantics).
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ float sat448(float v) { return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f); }
+__device__ __forceinline__ float sat448(float v) {
+  return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f);
+}
 
 __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);

@@ -31,7 +31,8 @@ extern "C" {
 /* GELU flavours for fln_layernorm_gelu. */
 #define FLN_GELU_NONE 0
 #define FLN_GELU_ERF 1  /* 0.5 v (1 + erf(v / sqrt 2)) -- torch approximate='none' */
-#define FLN_GELU_TANH 2 /* 0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3))) -- the reference's gelu() */
+/* 0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3))) -- the reference's gelu() */
+#define FLN_GELU_TANH 2
 
 #define FLN_OK 0
 #define FLN_ERR_INVALID 1 /* == hipErrorInvalidValue */

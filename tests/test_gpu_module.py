@@ -394,7 +394,8 @@ def test_mxfp8_functional_dtypes_dequantization_and_pass_through():
     # e4m3: within 2^-3 of the value, or of the block's subnormal step / saturation
     x_blk = sc.float().cpu().double()[..., None].expand(4, 32, 64, 32).reshape(4, 32, 2048)
     err = (deq.double().cpu() - ref).abs()
-    assert (err <= ref.abs() * 2 ** -3 + x_blk * 2 ** -9 + (ref.abs() - 448 * x_blk).clamp(min=0)).all()
+    bound = ref.abs() * 2 ** -3 + x_blk * 2 ** -9 + (ref.abs() - 448 * x_blk).clamp(min=0)
+    assert (err <= bound).all()
     dh = torch.randn_like(h)
     (h * dh).sum().backward()
     assert torch.equal(x.grad, dh) and torch.equal(r.grad, dh)
