@@ -1064,7 +1064,8 @@ int launch_loop(const FwdParams& p, hipStream_t s) {
 //      rows, bf16, us: 2560 columns 5 x 1 35.5 against 2 x 4 32.6; 4608 9 x 1 61.9 / 4 x 4 58.8;
 //      6656 13 x 1 94.4 / 4 x 4 78.2; fp32 3328 97.2 / 78.8): the extra waves only add
 //      cross-wave reductions;
-//   3. few rows: more waves per row (fewer vectors each) until the grid covers the device.
+//   3. few rows: more waves per row (fewer vectors each), up to 4, until the grid covers the
+//      device.
 // Rows of 1, 2 or 4 waves share 256-thread blocks; other row groups are one block each.
 struct FwdGeometry {
   int wpr, vpl, threads;
@@ -1103,7 +1104,11 @@ inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_ca
       }
     }
   }
-  while (rows * wpr < target_waves && wpr * 2 <= max_wpr) {
+  // Few rows: spread each row over more waves, up to 4 (latency-bound calls, HIP graph replay,
+  // us: 64 x 8192 bf16 16 x 1 4.44 against 4 x 4 3.65; 8 x 4096 bf16 8 x 1 3.36 / 4 x 2 3.10;
+  // 64 x 4096 fp32 + GELU 16 x 1 4.55 / 4 x 4 3.95: wider row groups add cross-wave steps).
+  constexpr int kFewRowsMaxWpr = 4;
+  while (rows * wpr < target_waves && wpr * 2 <= kFewRowsMaxWpr) {
     if (exact && vpl >= 2) {
       wpr *= 2;
       vpl /= 2;

@@ -53,7 +53,7 @@ def _forward_geometry(rows: int, nvec: int, cap: int, wide_cap: int, max_cap: in
     fewest power-of-two waves per row that keep <= cap vectors per lane for rows of up to 4
     waves and <= wide_cap beyond (max_cap when nothing narrower fits 16 waves); on the vector
     path an exact (mask-free) non-power-of-two tiling within the same caps when one exists;
-    more waves per row while the grid holds fewer than 4 waves per CU.
+    more waves per row (up to 4) while the grid holds fewer than 4 waves per CU.
     Returns (loop, wpr, vpl, exact, threads)."""
     per_lane = lambda w: -(-nvec // (64 * w))  # noqa: E731
     cap_of = lambda w: cap if w <= 4 else wide_cap  # noqa: E731
@@ -77,7 +77,7 @@ def _forward_geometry(rows: int, nvec: int, cap: int, wide_cap: int, max_cap: in
                 wpr, vpl, exact = w, v, True
                 break
             v >>= 1
-    while rows * wpr < 4 * num_cus and wpr * 2 <= 16:
+    while rows * wpr < 4 * num_cus and wpr * 2 <= 4:  # few rows: up to 4 waves per row
         if exact and vpl >= 2:
             wpr, vpl = wpr * 2, vpl // 2
         elif not exact and nvec > 64 * wpr * 2:
