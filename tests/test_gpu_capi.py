@@ -857,6 +857,62 @@ def test_fp32_wide_row_backward(lib, monkeypatch, kind, cols):
             assert float((a - c).abs().max()) <= 1e-5 * max(1.0, scale)
 
 
+ROUTE_WIDTHS_16 = [8192, 8200, 16384, 16392, 18432, 18440, 24576, 24584, 32768, 32776, 65536,
+                   65544]
+ROUTE_WIDTHS_32 = [4096, 4100, 8192, 8196, 16384, 16388, 32768, 32772]
+
+
+@pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, c) for c in ROUTE_WIDTHS_16] +
+                         [(torch.float16, c) for c in (18432, 24584, 65544)] +
+                         [(torch.float32, c) for c in ROUTE_WIDTHS_32],
+                         ids=lambda v: str(v).replace("torch.", ""))
+@pytest.mark.parametrize("nrows", ["few", "many"])
+def test_route_boundaries(lib, dtype, nrows, cols):
+    """Widths on both sides of every kernel-route boundary (register tiles, RAW tiles, the
+    768-thread LDS backward with 3 / 4 vectors, the LDS-staged forward, the two passes, the
+    streamed wide forward) at a few rows (small backward blocks) and at several rows per block:
+    LayerNorm fwd + bwd with a residual gradient and RMSNorm fwd + bwd against the oracle."""
+    rows = 37 if nrows == "few" else (700 if cols <= 32776 else 300)
+    gen = torch.Generator().manual_seed(rows * 131 + cols)
+    xc = (torch.randn(rows, cols, generator=gen) * 1.5 + 0.25).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    drc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, b, dy, dr = cuda(xc), cuda(gc), cuda(bc), cuda(dyc), cuda(drc)
+    xs, gs, bs, dys = f32(xc), f32(gc), f32(bc), f32(dyc)
+    y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+    dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g, dres=dr)
+    y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
+    dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
+    dx_ref = dx_ref + f32(drc)
+    assert np.abs(to_np(rstd) / np.asarray(r_ref).reshape(-1) - 1).max() <= 1e-5
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        m = np.asarray(m_ref).reshape(-1, 1)
+        atol = affine_atol(xs, gs, bs, 1e-5) + 2.0 ** -21 * (
+            np.abs(m) * np.asarray(r_ref).reshape(-1, 1) * np.abs(gs))
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=atol, **_tol_fwd(dtype), what="y")
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          **_tol_fwd(dtype), what="dx + dres")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+    yr, rs = rms_forward(lib, x, g, 1e-6)
+    dxr, dw = rms_backward(lib, dy, x, rs, g)
+    yr_ref, _ = norms.rms_norm_fwd(xs, gs, 1e-6)
+    dxr_ref, dw_ref = norms.rms_norm_bwd(dys, xs, gs, 1e-6)
+    if dtype == torch.float32:
+        assert np.abs(to_np(yr) - yr_ref).max() <= 1e-5 * max(1, np.abs(yr_ref).max())
+        np.testing.assert_allclose(to_np(dxr), dxr_ref, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(yr), yr_ref, 1.0, **_tol_fwd(dtype), what="rms y")
+        assert_within_ulp(to_np(dxr), dxr_ref, 1.0, atol=DX_ATOL_REL * np.abs(dxr_ref).max(),
+                          **_tol_fwd(dtype), what="rms dx")
+    assert_close_rel(to_np(dw), dw_ref, 1e-4, "dweight")
+
+
 @pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_tanh", "gelu_none"])
 @pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 18432), (torch.float16, 16392),
                                         (torch.bfloat16, 17416), (torch.bfloat16, 20480),
