@@ -215,13 +215,15 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 
 // For the tanh form, u = sqrt(2/pi) (v + k1 v^3): e = e^(-2u) and sigmoid(2u) = 1 / (1 + e);
 // 1 - sigmoid(2u) = e / (1 + e) is formed as a product, not a difference (no cancellation where
-// the sigmoid approaches 1).
+// the sigmoid approaches 1).  The exponent -2u log2(e) is v (c0 + c1 v^2) with the constants
+// folded (c0 = -2 sqrt(2/pi) log2(e), c1 = c0 k1): one multiply, one FMA and one multiply.
 struct GeluTanhTerms {
   float e, sg;
 };
 __device__ __forceinline__ GeluTanhTerms gelu_tanh_terms(float v) {
-  const float two_u = 2.0f * kGeluK0 * fmaf(kGeluK1 * v, v * v, v);
-  const float e = exp2_fast(-two_u * kLog2e);
+  constexpr float kC0 = -2.0f * 0.79788456080286535588f * 1.44269504088896340736f;
+  constexpr float kC1 = kC0 * 0.044715f;
+  const float e = exp2_fast(v * fmaf(kC1, v * v, kC0));
   return {e, __builtin_amdgcn_rcpf(1.0f + e)};  // v_rcp_f32: 1 ulp
 }
 __device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_terms(v).sg; }
