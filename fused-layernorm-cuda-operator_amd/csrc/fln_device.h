@@ -261,9 +261,12 @@ __device__ __forceinline__ float gelu_erf_grad(float v) {
 }
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const GeluTanhTerms t = gelu_tanh_terms(v);
-  const float one_minus = t.e * t.sg;  // 1 - sigmoid(2u); 0 when e overflows to inf (sg = 0)
-  return fmaf(2.0f * v * t.sg * (t.e < 3.0e38f ? one_minus : 0.0f),
-              kGeluK0 * fmaf(3.0f * kGeluK1, v * v, 1.0f), t.sg);
+  // 1 - sigmoid(2u) = e sigmoid(2u), with e kept finite: where e overflows, sigmoid(2u) = 0 and
+  // the product must not become inf * 0.
+  const float one_minus = fminf(t.e, 3.0e38f) * t.sg;
+  // 2 v s (1 - s) sqrt(2/pi) (1 + 3 k1 v^2) + s, the constants folded into one FMA.
+  constexpr float kD0 = 2.0f * kGeluK0, kD1 = 2.0f * kGeluK0 * 3.0f * kGeluK1;
+  return fmaf(v * fmaf(kD1, v * v, kD0), t.sg * one_minus, t.sg);
 }
 __device__ __forceinline__ float gelu_grad(float v, int mode) {
   return mode == 1 ? gelu_erf_grad(v) : gelu_tanh_grad(v);
