@@ -473,20 +473,29 @@ def test_opcheck(op, args):
 # ------------------------------------------------------------------------------------------------
 # HIP graph capture of the C-ABI calls (launch-bound callers replay a captured graph).
 # ------------------------------------------------------------------------------------------------
-def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay():
-    """LayerNorm forward + backward (stage 1 and column reduction) captured once, replayed with
-    new data copied into the static inputs between replays, with eager work and
-    synchronizations in between; every replay must equal the eager result bit for bit.  No
-    entry point records a memset node (empty batches, the only memset, are not captured)."""
+@pytest.mark.parametrize("rows,cols,dtype", [
+    (1000, 4096, torch.bfloat16),   # register tiles forward and backward
+    (64, 18432, torch.bfloat16),    # RAW forward tiles; 768-thread LDS-staged backward
+    (48, 32768, torch.bfloat16),    # RAW forward tiles; two-pass backward (row sums, column pass)
+    (40, 16384, torch.float32),     # fp32 LDS-staged backward
+    (6, 131072, torch.bfloat16),    # streamed wide-row forward; two-pass backward
+    (0, 4096, torch.float32),       # empty batch: the backward zero-fills dgamma / dbeta
+], ids=["registers", "lds768", "two_pass", "lds_fp32", "wide", "empty"])
+def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay(rows, cols, dtype):
+    """LayerNorm forward + backward (stage 1 and column reduction) captured once per kernel
+    route, replayed with new data copied into the static inputs and the outputs overwritten
+    between replays, with eager work and synchronizations in between; every replay must equal
+    the eager result bit for bit.  No entry point records a memset node (an empty batch's
+    parameter gradients are zeroed by a kernel)."""
     import capi
     from gpu_calls import ln_backward, ln_forward, workspace
 
     lib = capi.load()
-    rows, cols = 1000, 4096
-    xs = torch.empty(rows, cols, device=DEV, dtype=torch.bfloat16)
+    code = capi.dtype_code(torch.empty(0, dtype=dtype))
+    xs = torch.empty(rows, cols, device=DEV, dtype=dtype)
     dys = torch.empty_like(xs)
-    g = (1 + 0.1 * torch.randn(cols, device=DEV)).to(torch.bfloat16)
-    b = (0.1 * torch.randn(cols, device=DEV)).to(torch.bfloat16)
+    g = (1 + 0.1 * torch.randn(cols, device=DEV)).to(dtype)
+    b = (0.1 * torch.randn(cols, device=DEV)).to(dtype)
     y, dx = torch.empty_like(xs), torch.empty_like(xs)
     mean = torch.empty(rows, device=DEV)
     rstd = torch.empty(rows, device=DEV)
@@ -498,10 +507,10 @@ def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay():
     def calls():
         st = capi.stream()
         capi.check(lib.fln_layernorm_forward(p(xs), p(g), p(b), p(y), p(mean), p(rstd), rows,
-                                             cols, capi.BF16, 1e-5, st))
+                                             cols, code, 1e-5, st))
         capi.check(lib.fln_layernorm_backward(p(dys), p(xs), p(mean), p(rstd), p(g), None,
-                                              p(dx), p(dg), p(db), rows, cols, capi.BF16,
-                                              capi.F32, p(ws), nws, st))
+                                              p(dx), p(dg), p(db), rows, cols, code, capi.F32,
+                                              p(ws), nws, st))
 
     xs.normal_()
     dys.normal_()
@@ -516,18 +525,23 @@ def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay():
         calls()
     for k in range(4):
         torch.manual_seed(100 + k)
-        x_new = torch.randn(rows, cols, device=DEV).to(torch.bfloat16)
-        dy_new = torch.randn(rows, cols, device=DEV).to(torch.bfloat16)
+        x_new = torch.randn(rows, cols, device=DEV).to(dtype)
+        dy_new = torch.randn(rows, cols, device=DEV).to(dtype)
         xs.copy_(x_new)
         dys.copy_(dy_new)
+        for out in (y, dx, mean, rstd, dg, db):
+            out.fill_(7.0)
+        torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
         y_e, m_e, r_e = ln_forward(lib, x_new, g, b, 1e-5)
         dx_e, dg_e, db_e = ln_backward(lib, dy_new, x_new, m_e, r_e, g)
         torch.cuda.synchronize()
-        for got, ref in ((y, y_e), (mean, m_e), (rstd, r_e), (dx, dx_e), (dg, dg_e),
-                         (db, db_e)):
-            assert torch.equal(got, ref), f"replay {k} differs from eager"
+        for name, got, ref in (("y", y, y_e), ("mean", mean, m_e), ("rstd", rstd, r_e),
+                               ("dx", dx, dx_e), ("dgamma", dg, dg_e), ("dbeta", db, db_e)):
+            assert torch.equal(got, ref), f"replay {k}: {name} differs from eager"
+        if rows == 0:
+            assert not dg.any() and not db.any()
 
 
 @pytest.mark.parametrize("rows,cols,dtype", [
