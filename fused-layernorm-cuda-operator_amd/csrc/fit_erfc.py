@@ -17,8 +17,8 @@ emulation of the device evaluation.
 import numpy as np
 from scipy.special import erfc, erfcx
 
-P = 0.4
-DEGREE = 8
+P = 0.35
+DEGREE = 7
 
 
 def fit(p=P, deg=DEGREE, nodes=4000, rounds=60):

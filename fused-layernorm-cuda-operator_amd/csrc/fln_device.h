@@ -228,27 +228,27 @@ __device__ __forceinline__ GeluTanhTerms gelu_tanh_terms(float v) {
 }
 __device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_terms(v).sg; }
 
-// Phi(v) and exp(-v^2 / 2).  With x = |v| / sqrt 2 and t = 1 / (1 + 0.4 x),
+// Phi(v) and exp(-v^2 / 2).  With x = |v| / sqrt 2 and t = 1 / (1 + 0.35 x),
 //   h = 0.5 erfc(x) = t F(t) exp(-x^2),
 // where F(t) = 0.5 erfcx(x) / t (erfcx(x) = exp(x^2) erfc(x)) is smooth on t in (0, 1] and is
-// replaced by a degree-8 polynomial: a relative-error least-squares fit on Chebyshev nodes, max
-// relative error 1.3e-7 (fit_erfc.py beside this file derives and checks the coefficients).
+// replaced by a degree-7 polynomial: a relative-error least-squares fit on Chebyshev nodes, max
+// relative error 8.3e-7 (fit_erfc.py beside this file derives and checks the coefficients).
 // Phi(v) = h for v < 0 and 1 - h otherwise, so the lower tail keeps its relative accuracy
 // where 1 + erf(v / sqrt 2) cancels.  Under an fp32 emulation over |v| <= 13: v Phi(v) within
-// 3.8e-7 (absolute) and 7.3e-6 (relative, |v Phi(v)| > 1e-30) of the float64 value, the
-// derivative within 2.6e-7.  Infinite v gives Phi = 0 or 1; NaN propagates.
+// 3.8e-7 (absolute) and 6.9e-6 (relative, |v Phi(v)| > 1e-30) of the float64 value, the
+// derivative within 5.8e-7.  Infinite v gives Phi = 0 or 1; NaN propagates.
 struct NormalCdf {
   float cdf, gauss;  // Phi(v), exp(-v^2 / 2)
 };
 __device__ __forceinline__ NormalCdf normal_cdf(float v) {
-  constexpr float kF[9] = {1.128379330e-01f, 1.128347963e-01f, 1.039213464e-01f,
-                           8.427099138e-02f, 7.071570307e-02f, -2.803730546e-03f,
-                           8.454266936e-02f, -9.145070612e-02f, 2.513105422e-02f};
+  constexpr float kF[8] = {9.873314202e-02f, 9.872655571e-02f, 9.295467287e-02f,
+                           7.733605057e-02f, 8.147227019e-02f, -7.275486365e-03f,
+                           1.006051227e-01f, -4.255273566e-02f};
   const float e = exp2_fast((-0.5f * kLog2e * v) * v);
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.4f * 0.70710678118654752440f, fabsf(v), 1.0f));
-  float f = kF[8];
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.35f * 0.70710678118654752440f, fabsf(v), 1.0f));
+  float f = kF[7];
 #pragma unroll
-  for (int k = 7; k >= 0; --k) f = fmaf(f, t, kF[k]);
+  for (int k = 6; k >= 0; --k) f = fmaf(f, t, kF[k]);
   const float h = (f * t) * e;
   return {v < 0.0f ? h : 1.0f - h, e};
 }
