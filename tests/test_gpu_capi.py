@@ -213,6 +213,66 @@ def test_c5_layernorm_fp8_bf16_32768x7168(lib):
     assert (np.abs(norms.fp8_e4m3fn_decode(q_ref)).max(axis=1) == 448).all()
 
 
+def test_tensors_past_2_to_the_31_elements(lib):
+    """A bf16 batch of 266240 x 8192 (2.18e9 elements, 4.4 GB per tensor): row offsets past 2^31
+    elements and 4 GiB.  LayerNorm forward + backward, RMSNorm forward and LayerNorm -> fp8 on
+    the same x; rows on both sides of the 2^31-element boundary (and the first and last rows)
+    against the oracle, every row's statistics and the column sums dgamma / dbeta (over all
+    rows) against a float64 torch reduction of the same inputs."""
+    rows, cols, eps = 266240, 8192, 1e-5
+    if torch.cuda.mem_get_info()[0] < 40 * 2 ** 30:
+        pytest.skip("needs 40 GiB of free device memory")
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    x = torch.randn(rows, cols, device="cuda", generator=gen).to(torch.bfloat16)
+    dy = torch.randn(rows, cols, device="cuda", generator=gen).to(torch.bfloat16)
+    g = (1 + 0.1 * torch.randn(cols, device="cuda", generator=gen)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(cols, device="cuda", generator=gen)).to(torch.bfloat16)
+    y, mean, rstd = ln_forward(lib, x, g, b, eps)
+    dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+    torch.cuda.synchronize()
+    boundary = (1 << 31) // cols
+    sample = [0, 1, boundary - 2, boundary - 1, boundary, boundary + 1, rows - 2, rows - 1]
+    xs, dys = f32(x[sample]), f32(dy[sample])
+    gs, bs = f32(g), f32(b)
+    y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, eps)
+    assert_within_ulp(to_np(y[sample]), y_ref, 1.0, atol=affine_atol(xs, gs, bs, eps), what="y")
+    dx_ref, _, _ = norms.layer_norm_bwd(dys, xs, gs, eps)
+    assert_within_ulp(to_np(dx[sample]), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                      what="dx")
+    del y, dx
+    # Statistics of every row and the column sums, float64 in chunks of rows.
+    dg_ref = torch.zeros(cols, device="cuda", dtype=torch.float64)
+    db_ref = torch.zeros_like(dg_ref)
+    m_err = r_err = 0.0
+    for r0 in range(0, rows, 16384):
+        xf = x[r0:r0 + 16384].double()
+        mu = xf.mean(dim=1, keepdim=True)
+        xf -= mu
+        rs = torch.rsqrt(xf.square().mean(dim=1, keepdim=True) + eps)
+        xf *= rs
+        dyf = dy[r0:r0 + 16384].double()
+        dg_ref += (dyf * xf).sum(dim=0)
+        db_ref += dyf.sum(dim=0)
+        m_err = max(m_err, (mean[r0:r0 + 16384].double() - mu[:, 0]).abs().max().item())
+        r_err = max(r_err, (rstd[r0:r0 + 16384].double() / rs[:, 0] - 1).abs().max().item())
+        del xf, dyf
+    assert m_err <= 1e-6 and r_err <= 1e-5, (m_err, r_err)
+    assert_close_rel(to_np(dg), to_np(dg_ref), 1e-4, "dgamma")
+    assert_close_rel(to_np(db), to_np(db_ref), 1e-4, "dbeta")
+    del dy
+    y2, rstd2 = rms_forward(lib, x, g, 1e-6)
+    y2_ref, _ = norms.rms_norm_fwd(xs, gs, 1e-6)
+    assert_within_ulp(to_np(y2[sample]), y2_ref, 1.0, what="rms y")
+    del y2
+    q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+    scale = torch.empty(rows, device="cuda", dtype=torch.float32)
+    capi.check(lib.fln_layernorm_fp8_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(q),
+                                             capi.ptr(scale), None, None, rows, cols,
+                                             capi.BF16, eps, capi.stream()))
+    q_ref, s_ref = norms.layer_norm_fp8_fwd(xs, gs, bs, eps)
+    assert_fp8_close(q[sample].cpu().numpy(), to_np(scale[sample]), q_ref, s_ref, "fp8")
+
+
 def test_fp8_encoder_bit_exact(lib):
     """The device conversion (v_cvt_pk_fp8_f32 after a +-448 clamp) against the oracle's
     format-level encoder, over every exponent of the e4m3fn range and beyond, all 8 mantissa
