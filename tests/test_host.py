@@ -21,6 +21,24 @@ def test_c_abi_library_exports_every_declared_symbol():
     assert set(declared) <= set(capi.SIGNATURES), "tests/capi.py lacks a signature"
 
 
+def test_package_without_the_extension_fails_loudly(tmp_path):
+    """No fallback path: a copy of the Python package with no built extension beside it must
+    refuse to import, naming the missing HIP extension."""
+    import os
+    import shutil
+    import subprocess
+    import sys
+    src = os.path.dirname(fl.__file__)
+    shutil.copytree(src, tmp_path / "fused_layernorm",
+                    ignore=shutil.ignore_patterns("__pycache__", "*.so"))
+    env = {k: v for k, v in os.environ.items() if k != "PYTHONPATH"}
+    code = f"import sys; sys.path.insert(0, {str(tmp_path)!r}); import fused_layernorm"
+    r = subprocess.run([sys.executable, "-c", code], cwd=tmp_path, env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0
+    assert "Cannot import fused_layernorm_cuda" in r.stderr, r.stderr[-2000:]
+
+
 def test_c_abi_rejects_bad_arguments_without_a_device():
     lib = capi.load()
     # Every one of these fails validation before any HIP call is made.
