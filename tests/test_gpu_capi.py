@@ -273,6 +273,44 @@ def test_tensors_past_2_to_the_31_elements(lib):
     assert_fp8_close(q[sample].cpu().numpy(), to_np(scale[sample]), q_ref, s_ref, "fp8")
 
 
+def test_fp8_rows_feed_a_rowwise_scaled_gemm(lib):
+    """The step after the norm: LayerNorm -> fp8 codes [M, K] with one fp32 scale per row are
+    exactly the A operand and row-wise A scale of an fp8 GEMM (torch._scaled_mm on hipBLASLt,
+    weight quantized per output channel).  The GEMM output must match a float64 product of the
+    decoded operands (the layout and scale convention y ~ decode(q) * scale), and stay within the
+    fp8 quantization error of LayerNorm(x) @ W^T."""
+    m, k, n, eps = 512, 4096, 1024, 1e-5
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+    g = (1 + 0.1 * torch.randn(k, device="cuda", generator=gen)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(k, device="cuda", generator=gen)).to(torch.bfloat16)
+    w = (torch.randn(n, k, device="cuda", generator=gen) / 64).to(torch.bfloat16)
+    q = torch.empty(m, k, device="cuda", dtype=torch.uint8)
+    scale = torch.empty(m, device="cuda", dtype=torch.float32)
+    capi.check(lib.fln_layernorm_fp8_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(q),
+                                             capi.ptr(scale), None, None, m, k, capi.BF16, eps,
+                                             capi.stream()))
+    w_scale = (w.float().abs().amax(dim=1) / 448.0).clamp_min(1e-12)
+    wq = (w.float() / w_scale[:, None]).to(torch.float8_e4m3fn)
+    try:
+        out = torch._scaled_mm(q.view(torch.float8_e4m3fn), wq.t(), scale_a=scale.view(m, 1),
+                               scale_b=w_scale.view(1, n), out_dtype=torch.bfloat16)
+    except (RuntimeError, NotImplementedError) as e:  # row-wise scaling absent from this build
+        pytest.skip(f"torch._scaled_mm with row-wise scales unavailable: {e}")
+    torch.cuda.synchronize()
+    a64 = norms.fp8_e4m3fn_decode(q.cpu().numpy()) * to_np(scale)[:, None]
+    b64 = wq.float().cpu().numpy().astype(np.float64) * to_np(w_scale)[:, None]
+    ref = a64 @ b64.T
+    got = to_np(out)
+    bound = 2.0 ** -8 * np.abs(ref) + 1e-5 * (np.abs(a64) @ np.abs(b64).T)
+    assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+    y64, _, _ = norms.layer_norm_fwd(f32(x), f32(g), f32(b), eps)
+    exact = y64 @ f32(w).astype(np.float64).T
+    # Both operands carry e4m3 rounding (3 mantissa bits): 3.5% of max|exact| in a CPU
+    # emulation of these shapes.
+    assert np.abs(got - exact).max() <= 0.08 * np.abs(exact).max()
+
+
 def test_fp8_encoder_bit_exact(lib):
     """The device conversion (v_cvt_pk_fp8_f32 after a +-448 clamp) against the oracle's
     format-level encoder, over every exponent of the e4m3fn range and beyond, all 8 mantissa
