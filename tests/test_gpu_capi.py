@@ -311,6 +311,49 @@ def test_fp8_rows_feed_a_rowwise_scaled_gemm(lib):
     assert np.abs(got - exact).max() <= 0.08 * np.abs(exact).max()
 
 
+def test_mxfp8_blocks_feed_a_block_scaled_gemm(lib):
+    """LayerNorm -> MXFP8 (E4M3 codes [M, K], one E8M0 scale per 32 elements of a row in
+    [M, K / 32]) is the A operand of an MX-scaled fp8 GEMM as produced: torch._scaled_mm on
+    hipBLASLt with float8_e8m0fnu block scales, the weight quantized by the same block rule.
+    The output must match a float64 product of the decoded blocks to one bf16 ulp (the GEMM's
+    output rounding) plus fp32 accumulation, and LayerNorm(x) @ W^T to the fp8 quantization
+    error."""
+    m, k, n, eps = 256, 4096, 512, 1e-5
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+    g = (1 + 0.1 * torch.randn(k, device="cuda", generator=gen)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(k, device="cuda", generator=gen)).to(torch.bfloat16)
+    w = (torch.randn(n, k, device="cuda", generator=gen) / 64).to(torch.bfloat16)
+    q = torch.empty(m, k, device="cuda", dtype=torch.uint8)
+    sa = torch.empty(m, k // 32, device="cuda", dtype=torch.uint8)
+    capi.check(lib.fln_layernorm_mxfp8_forward(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(q),
+                                               capi.ptr(sa), None, None, m, k, capi.BF16, eps,
+                                               capi.stream()))
+    # The weight by the same block rule: 2^e, e = floor(log2 max|block|) - 8, codes saturated.
+    wf = w.float().view(n, k // 32, 32)
+    e = (torch.floor(torch.log2(wf.abs().amax(dim=2).clamp_min(2.0 ** -126))) - 8).clamp(-127, 127)
+    wq = (wf * torch.exp2(-e)[:, :, None]).clamp(-448, 448).view(n, k).to(torch.float8_e4m3fn)
+    sb = (e + 127).to(torch.uint8)
+    try:
+        out = torch._scaled_mm(q.view(torch.float8_e4m3fn), wq.t(),
+                               scale_a=sa.view(torch.float8_e8m0fnu),
+                               scale_b=sb.view(torch.float8_e8m0fnu), out_dtype=torch.bfloat16)
+    except (RuntimeError, NotImplementedError) as ex:  # MX scaling absent from this build
+        pytest.skip(f"torch._scaled_mm with E8M0 block scales unavailable: {ex}")
+    torch.cuda.synchronize()
+    a64 = (norms.fp8_e4m3fn_decode(q.cpu().numpy()).reshape(m, k // 32, 32)
+           * np.exp2(sa.cpu().numpy().astype(np.float64) - 127)[:, :, None]).reshape(m, k)
+    b64 = (wq.float().cpu().numpy().astype(np.float64).reshape(n, k // 32, 32)
+           * np.exp2(sb.cpu().numpy().astype(np.float64) - 127)[:, :, None]).reshape(n, k)
+    ref = a64 @ b64.T
+    got = to_np(out)
+    bound = 2.0 ** -7 * np.abs(ref) + 1e-5 * (np.abs(a64) @ np.abs(b64).T)
+    assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+    y64, _, _ = norms.layer_norm_fwd(f32(x), f32(g), f32(b), eps)
+    exact = y64 @ f32(w).astype(np.float64).T
+    assert np.abs(got - exact).max() <= 0.08 * np.abs(exact).max()
+
+
 def test_fp8_encoder_bit_exact(lib):
     """The device conversion (v_cvt_pk_fp8_f32 after a +-448 clamp) against the oracle's
     format-level encoder, over every exponent of the e4m3fn range and beyond, all 8 mantissa
