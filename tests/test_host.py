@@ -39,6 +39,44 @@ def test_package_without_the_extension_fails_loudly(tmp_path):
     assert "Cannot import fused_layernorm_cuda" in r.stderr, r.stderr[-2000:]
 
 
+def test_normal_cdf_constants_in_the_device_header():
+    """The exact-GELU kernels evaluate Phi(v) as 0.5 erfc(|v| / sqrt 2) = t F(t) exp(-v^2 / 2),
+    t = 1 / (1 + p |v| / sqrt 2), F a fitted polynomial.  Parse p and F's coefficients from
+    csrc/fln_device.h, evaluate them under an fp32 emulation of the device code, and check GELU
+    and its derivative against scipy's erfc in float64 over |v| <= 13: a mistyped coefficient
+    or a wrong p fails here, on the CPU."""
+    import os
+    import re
+    import sys
+    import numpy as np
+    from scipy.special import erfc
+    csrc = os.path.join(os.path.dirname(os.path.dirname(fl.__file__)), "csrc")
+    src = open(os.path.join(csrc, "fln_device.h")).read()
+    body = src[src.index("NormalCdf normal_cdf(float v)"):]
+    body = body[:body.index("return {")]
+    coef = [np.float32(float(c)) for c in
+            re.findall(r"[-+]?\d\.\d+e[-+]\d+", body[body.index("kF["):body.index("};")])]
+    p = float(re.search(r"fmaf\(([\d.]+)f \* 0\.7071", body).group(1))
+    assert len(coef) >= 6 and 0.2 < p < 0.6
+    sys.path.insert(0, csrc)
+    try:
+        import fit_erfc
+    finally:
+        sys.path.remove(csrc)
+    v = np.linspace(-13, 13, 260001).astype(np.float32)
+    cdf, e = fit_erfc.emulate(coef, v, p=p)
+    gelu = (v * cdf).astype(np.float32)
+    grad = (v * (np.float32(1 / np.sqrt(2 * np.pi)) * e) + cdf).astype(np.float32)
+    vd = v.astype(np.float64)
+    phi = np.where(vd < 0, 0.5 * erfc(-vd / np.sqrt(2)), 1 - 0.5 * erfc(vd / np.sqrt(2)))
+    g_ref = vd * phi
+    d_ref = phi + vd * np.exp(-vd * vd / 2) / np.sqrt(2 * np.pi)
+    assert np.abs(gelu - g_ref).max() <= 1e-6
+    assert np.abs(grad - d_ref).max() <= 2e-6
+    tail = (vd < -3) & (np.abs(g_ref) > 1e-30)
+    assert (np.abs(gelu[tail] - g_ref[tail]) / np.abs(g_ref[tail])).max() <= 1e-4
+
+
 def test_c_abi_rejects_bad_arguments_without_a_device():
     lib = capi.load()
     # Every one of these fails validation before any HIP call is made.
