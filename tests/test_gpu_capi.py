@@ -626,9 +626,18 @@ def test_wide_rows_forward(lib, kind, dtype, rows, cols, aligned):
     """Rows past the LDS tile (16-bit > 65536 columns, fp32 > 32768) and long rows off the
     vector path (odd widths; 16-byte misaligned pointers) take the streamed wide-row kernel:
     every forward flavour against the oracle, statistics included, bitwise reproducible
-    (600 / 1100 rows: several rows per block)."""
+    (600 / 1100 rows: several rows per block).  MXFP8 at widths that are not a multiple of 32
+    must be refused before any launch, outputs untouched."""
     if kind.endswith("_mx") and cols % 32:
-        pytest.skip("MXFP8 needs a multiple of 32 columns")
+        x = torch.zeros(rows, cols, device="cuda", dtype=dtype)
+        g = torch.ones(cols, device="cuda", dtype=dtype)
+        q = torch.full((rows, cols), 0x5A, device="cuda", dtype=torch.uint8)
+        sc = torch.full((rows, -(-cols // 32)), 0x5A, device="cuda", dtype=torch.uint8)
+        h = torch.empty_like(x)
+        rc = _mx_call(lib, kind[:-3], x, x, g, None, q, sc, h, rows, cols, capi.dtype_code(x))
+        torch.cuda.synchronize()
+        assert rc == 1 and (q == 0x5A).all() and (sc == 0x5A).all()
+        return
     gen = torch.Generator().manual_seed(cols + 17 * WIDE_KINDS.index(kind))
     xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
     rc = torch.randn(rows, cols, generator=gen).to(dtype)
