@@ -68,6 +68,12 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
              torch.bfloat16, 9, 1e-5, (1.0, 0.02), (0.0, 0.02)),
     Workload("wide_ln_gelu_erf_fwd_bwd_bf16_4096x16384", "layer_norm_gelu_fwd_bwd", 4096, 16384,
              torch.bfloat16, 10, 1e-5, (1.0, 0.02), (0.0, 0.02), approximate="none"),
+    # Narrow rows (profiled, not benchmark lines): where the backward's column reduction is a
+    # fixed cost of a short call.
+    Workload("narrow_ln_fwd_bwd_bf16_16384x768", "layer_norm_fwd_bwd", 16384, 768,
+             torch.bfloat16, 11, 1e-5, (1.0, 0.02), (0.0, 0.02)),
+    Workload("narrow_ln_fwd_bwd_bf16_16384x2048", "layer_norm_fwd_bwd", 16384, 2048,
+             torch.bfloat16, 12, 1e-5, (1.0, 0.02), (0.0, 0.02)),
 ]}
 
 
