@@ -10,9 +10,9 @@ ones, GB/s for the large ones).
 
 The kernels are called through the C ABI (libfln.so) on torch's current HIP stream, with every
 output preallocated.  Inputs and outputs rotate over at least 4 buffer sets (>= 2 GiB in all,
-8x the 256 MiB Infinity Cache), and a step runs the backward on a different set than the
-forward, so no kernel finds its inputs in a cache from an earlier launch (as in training, where
-a layer's backward comes long after its forward).
+8x the 256 MiB Infinity Cache), and a step runs the backward on the set half the rotation away
+from the forward's, so no kernel finds its inputs in a cache from an earlier launch (as in
+training, where a layer's backward comes long after its forward).
 
 Prints ONE JSON line.  `value` = algorithmic bytes of one step / measured step time, in GB/s.
 `roofline` covers the backward call (fln_layernorm_backward: stage-1 kernel + column
@@ -227,12 +227,15 @@ class Runner:
             self.fwd(s, stream)
 
     def step(self, stream):
-        """Forward on set i, backward on set i + 1 (last forwarded nsets - 1 steps earlier)."""
+        """Forward on set i, backward on set i + nsets / 2.  Every set a kernel reads was last
+        touched nsets / 2 steps earlier (>= 1 GiB of other traffic since), never by the launch
+        just before it: with the backward on set i + 1, the next step's forward would read the
+        x that backward had just streamed through the Infinity Cache."""
         k = self.i
         self.i += 1
         self.fwd(self.sets[k % self.nsets], stream)
         if self.has_bwd:
-            self.bwd(self.sets[(k + 1) % self.nsets], stream)
+            self.bwd(self.sets[(k + self.nsets // 2) % self.nsets], stream)
 
     def time_region(self, fn, n, stream_obj):
         torch = self.torch

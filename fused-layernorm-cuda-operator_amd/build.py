@@ -4,7 +4,9 @@ Produces, next to this file:
   * ``libfln.so``  -- the C-ABI library (``include/fused_layernorm.h``): HIP kernels for gfx950
     compiled by hipcc directly (no hipify, no CUDA headers, no dual paths);
   * ``fused_layernorm_cuda<EXT_SUFFIX>`` -- the PyTorch binding, the drop-in for the reference's
-    extension module of the same name (reference setup.py:6-10), linked against libfln.so.
+    extension module of the same name (reference setup.py:6-10), linked against libfln.so;
+  * ``libfln_stream.so`` -- streaming reference kernels (``include/fln_stream.h``) that bench.py
+    times as the HBM ceiling of each access pattern (not part of the drop-in).
 
 Run ``python build.py`` (or ``__graft_entry__.build()``).  Object files are cached under
 ``_build/`` and rebuilt when a source or header is newer.
@@ -40,6 +42,8 @@ DEVICE_FLAGS = [
 ]
 
 LIB_NAME = "libfln.so"
+STREAM_SOURCE = "fln_stream.hip"
+STREAM_LIB_NAME = "libfln_stream.so"
 EXT_NAME = "fused_layernorm_cuda" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so")
 
 
@@ -82,6 +86,16 @@ def build_library(verbose: bool = False, force: bool = False) -> str:
     return lib
 
 
+def build_stream_library(verbose: bool = False, force: bool = False) -> str:
+    """Compile the streaming reference kernels into libfln_stream.so; returns its path."""
+    src = os.path.join(CSRC, STREAM_SOURCE)
+    deps = [src, os.path.join(CSRC, "fln_device.h"), os.path.join(INCLUDE, "fln_stream.h")]
+    lib = os.path.join(HERE, STREAM_LIB_NAME)
+    if force or _newer(lib, deps):
+        _run([HIPCC, *DEVICE_FLAGS, "-I", INCLUDE, "-shared", src, "-o", lib], verbose)
+    return lib
+
+
 def build_binding(verbose: bool = False, force: bool = False) -> str:
     """Compile the torch binding (host C++ only) against libfln.so; returns its path."""
     import torch
@@ -110,10 +124,14 @@ def build_binding(verbose: bool = False, force: bool = False) -> str:
 
 
 def build(verbose: bool = False, force: bool = False) -> None:
-    build_library(verbose, force)
+    with ThreadPoolExecutor(max_workers=2) as ex:
+        stream = ex.submit(build_stream_library, verbose, force)
+        build_library(verbose, force)
+        stream.result()
     build_binding(verbose, force)
 
 
 if __name__ == "__main__":
     build(verbose="-v" in sys.argv, force="--force" in sys.argv)
-    print("built", os.path.join(HERE, LIB_NAME), "and", os.path.join(HERE, EXT_NAME))
+    print("built", os.path.join(HERE, LIB_NAME), os.path.join(HERE, STREAM_LIB_NAME), "and",
+          os.path.join(HERE, EXT_NAME))

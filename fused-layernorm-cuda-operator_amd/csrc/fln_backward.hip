@@ -119,12 +119,12 @@ __device__ __forceinline__ void reduce_quad_block(const ColReduceArgs& a, int64_
 #ifndef FLN_BWD_PREFETCH
 #define FLN_BWD_PREFETCH(VPL) ((VPL) == 1 ? 2 : 1)
 #endif
-// Cache policies of the streamed rows: dx is stored non-temporal; x / dy / dres loads keep the
-// default policy.  Measured on MI355X (bf16 forward + backward steps): non-temporal loads as
-// well make the 16384 x 8192 RMSNorm step 2% faster but the 8192 x 4096 LayerNorm step 3%
-// slower.  gamma, the statistics and the column partials keep the default policy.
+// Cache policies of the streamed rows: x / dy / dres loads and dx stores are non-temporal (each
+// byte is touched once).  Measured on MI355X with exact ring waits, bf16 backward calls: 8192 x
+// 4096 LayerNorm 43.6 -> 41.1 us, 16384 x 8192 RMSNorm 146.3 -> 132.4 us against default-policy
+// loads.  gamma, the statistics and the column partials keep the default policy.
 #ifndef FLN_BWD_LOAD_POL
-#define FLN_BWD_LOAD_POL kDefault
+#define FLN_BWD_LOAD_POL kStream
 #endif
 #ifndef FLN_BWD_STORE_POL
 #define FLN_BWD_STORE_POL kStream
@@ -256,9 +256,16 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   float xh[VPL][VEC], dd[VPL][VEC];
   P rv[VPL];
   float rs = 0.0f;
+  // The statistics are the same in every lane of a wave (a wave works on one row), so they are
+  // taken into scalar registers: the ring's VGPRs are free again as soon as the row is widened,
+  // and the next load into the slot needs no register copy at the loop latch (such a copy would
+  // wait for that load and drain the ring).
+  auto uniform = [](float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+  };
   auto widen = [&](int slot) {
-    rs = rsn[slot];
-    const float mu = mun[slot];
+    rs = uniform(rsn[slot]);
+    const float mu = uniform(mun[slot]);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
 #pragma unroll
@@ -272,19 +279,33 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     }
   };
 
+  // Prologue: rows 0 .. PD-1 in slot order, each followed by as many stores as a loop step
+  // issues (zero-byte resources: dropped).  The loop top then sees the same sequence of
+  // outstanding memory operations whether it comes from here or from the previous step, and the
+  // compiler's wait there covers only the slot being consumed: PD rows stay in flight through
+  // the row reduction.  (Without the padding the merged wait drains the ring on every step.)
+  const rsrc_t none = make_rsrc(nullptr, 0);
 #pragma unroll
-  for (int k = 0; k < PD; ++k) load_row(k, k);
-  widen(0);
-  load_row(PD, 0);
-  // Row `it` is widened from slot it % PD, which then receives row it + PD; the inner loop is
-  // unrolled so every slot index is static.
-  for (int base = 0; base < iters; base += PD) {
+  for (int k = 0; k < PD; ++k) {
+    load_row(k, k);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)  // distinct, non-adjacent: none merged away
+      buf_store<P, FLN_BWD_STORE_POL>(zero_pack<T, VEC>(), none, static_cast<uint32_t>(4 * i));
+    asm volatile("" ::: "memory");  // keeps the slots in issue order
+  }
+  // Whole rounds of PD rows: a step past the block's last row reads zeros (its column sums add
+  // nothing) and stores nothing.  An early exit from the unrolled round would make the compiler
+  // wait for every slot at the loop top.
+  const int rounds = (iters + PD - 1) / PD;
+  for (int r = 0; r < rounds; ++r) {
 #pragma unroll
   for (int sl = 0; sl < PD; ++sl) {
-    const int it = base + sl;
-    if (it >= iters) break;  // uniform across the block
+    const int it = r * PD + sl;
     const int64_t row = row_of(it);
     const uint32_t nb = bytes_of(it);
+    // Consume slot sl (row it) and put row it + PD in flight in its place.
+    widen(sl);
+    load_row(it + PD, sl);
     // Row sums (elements past the row are zero in dy, hence in g).
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
@@ -321,15 +342,11 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
         acc_g[i][e] = fmaf(dd[i][e], xh[i][e], acc_g[i][e]);
         acc_b[i][e] += dd[i][e];
       }
-
-    // Consume the next row and put the row PD after it in flight, then store this row's dx:
-    // loads and stores share one wait counter, so the stores go out last.
-    const int nxt = (sl + 1) % PD;  // static after unrolling
-    widen(nxt);
-    load_row(it + 1 + PD, nxt);
     const rsrc_t xo = make_rsrc(DX ? DX + row * N : nullptr, nb);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) buf_store<P, FLN_BWD_STORE_POL>(o[i], xo, t + i * tpr);
+    // The next step's (cheap) widening must not be hoisted above this step's loads and stores.
+    __builtin_amdgcn_sched_barrier(0);
   }
   }
 
@@ -986,6 +1003,9 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   g.vpl = g.reg_path ? next_pow2(static_cast<int>(per_lane(wpr))) : 0;
   int threads = tun.bwd_threads > 0 ? tun.bwd_threads : 1024;
   if (threads != 256 && threads != 512 && threads != 1024) threads = 1024;
+  // Blocks per CU (one block per CU leaves one partial row per CU for the column reduction).
+  int per_cu = 1;
+  bool few_rows = false;
   // Few rows: 1024-thread blocks (1024 / (64 wpr) rows each) would leave CUs idle; take the
   // smallest block that holds a row group and still needs no more blocks than there are CUs
   // (HIP graph latency per call, us: 8 x 4096 bf16 9.21 -> 7.00, 512 x 1024 bf16 9.98 -> 7.84,
@@ -997,16 +1017,30 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
       const int per_block = t / (kWave * g.wpr);
       if ((rows + per_block - 1) / per_block <= device_cu_count()) {
         threads = t;
+        few_rows = true;
         break;
       }
+    }
+    // Many rows, one block per CU: the smaller block (512 threads, 8 waves) as soon as its row
+    // groups move >= 24 KiB per step (x, dy, dx and dres rows; 48 KiB with the GELU epilogue,
+    // whose VALU work wants the waves), 1024 threads otherwise.  Fewer rows in progress keep
+    // DRAM locality: bf16 backward calls on MI355X, us (1024 -> 512 threads): 8192 x 4096
+    // 41.1 -> 40.1, 16384 x 2048 39.9 -> 38.6, 16384 x 1024 24.4 -> 23.4, 65536 x 512 42.0 ->
+    // 39.4; 32768 x 768 (18 KiB at 512 threads) 32.6 -> 35.5, so it keeps 1024.
+    if (!few_rows) {
+      const int64_t moved = cols * es * (dres ? 4 : 3);
+      const int64_t target = gelu ? (48 << 10) : (24 << 10);
+      threads = 1024;
+      if (512 >= kWave * g.wpr && (512 / (kWave * g.wpr)) * moved >= target) threads = 512;
     }
   }
   if (!g.reg_path) threads = 1024;
   if (threads < kWave * g.wpr) threads = kWave * g.wpr;
   g.threads = threads;
   g.rgs = g.reg_path ? threads / (kWave * g.wpr) : 1;
-  // 16 waves per CU in total: 1024 / threads blocks per CU.
-  const int64_t max_blocks = static_cast<int64_t>(device_cu_count()) * (1024 / threads);
+  if (few_rows || tun.bwd_threads > 0) per_cu = 1024 / threads;  // 16 waves per CU in total
+  if (tun.bwd_grid_mult >= 1 && tun.bwd_grid_mult <= 4) per_cu = tun.bwd_grid_mult;
+  const int64_t max_blocks = static_cast<int64_t>(device_cu_count()) * per_cu;
   int64_t blocks = (rows + g.rgs - 1) / g.rgs;
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;

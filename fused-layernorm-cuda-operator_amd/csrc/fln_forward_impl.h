@@ -33,17 +33,16 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 // fit on the device at once; each row group walks rows rb*rows_per_block + rg for
 // rb = blockIdx.x, blockIdx.x + gridDim.x, ...
 //
-// Software pipeline, per row group and iteration (row i in fp32 registers, rows i+1 .. i+PD in
-// flight as raw packed loads):
-//   1. statistics and normalization of row i, outputs packed to the I/O type;
-//   2. wait for row i+1, widen it into the fp32 registers;
-//   3. issue the loads of row i+1+PD into the freed slot;
+// Software pipeline, per row group and step (rows i+1 .. i+PD-1 and then i+PD in flight as raw
+// packed loads while row i is worked on):
+//   1. wait for row i (its ring slot), widen it into registers;
+//   2. issue the loads of row i+PD into the freed slot;
+//   3. statistics and normalization of row i, outputs packed to the output format;
 //   4. issue the stores of row i.
-// Keeping PD rows in flight per wave is what feeds HBM: at ~2-3 us loaded latency, 8 TB/s
-// needs ~80 KB of reads in flight per CU.
-// Loads and stores share one counter on gfx9-family GPUs and the compiler waits for all of
-// them when both kinds are pending, so the stores go out after the next row has been consumed:
-// by the time step 2 waits again they have had a whole compute phase to complete.
+// Loads and stores share one counter (vmcnt) on gfx9-family GPUs, which completes in issue
+// order: the wait in step 1 is exact only if every path into it has the same operations
+// outstanding, hence whole rounds of PD steps (no early exit) and a prologue padded with dropped
+// stores, and scheduling barriers that keep each step's loads and stores in step order.
 // All global traffic goes through per-row buffer resources (tails and rows past the end are
 // handled by the hardware range check), so the loop body has no divergent branches.
 // LDS reduction slots are double-buffered by iteration parity: every iteration of a multi-wave
@@ -185,23 +184,41 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       return xf[i][e];
   };
 
+  // Row k of this row group is rb0 + k * stride; slot k % PD holds its raw loads from step
+  // k - PD on.  Prologue: the first PD rows in slot order, each followed by as many stores as a
+  // loop step issues (zero-byte resource: dropped), so that the loop top sees the same sequence
+  // of outstanding memory operations from here as from the previous step and the compiler's wait
+  // there covers only the slot being consumed.  (Without the padding the merged wait also
+  // drains the other slots.)
   const int64_t rb0 = blockIdx.x;
+  constexpr int kStoresPerRow =
+      2 + (RES ? VPL : 0) + (FP8 == 0 ? VPL : (FP8 == 2 ? 2 * VPL : VPL + 1));
+  const rsrc_t none = make_rsrc(nullptr, 0);
 #pragma unroll
-  for (int k = 0; k < PD; ++k) load_row(rb0 + k * stride, k);
-  widen(0);
-  load_row(rb0 + PD * stride, 0);
+  for (int k = 0; k < PD; ++k) {
+    load_row(rb0 + k * stride, k);
+#pragma unroll
+    for (int j = 0; j < kStoresPerRow; ++j)  // distinct, non-adjacent: none merged away
+      BufIO<4>::store(0u, none, 64u * j);
+    asm volatile("" ::: "memory");  // keeps the slots in issue order
+  }
+  // Whole rounds of PD rows (the inner loop is unrolled so every slot index is static): a step
+  // past the block's last row reads zeros and stores nothing.  An early exit from the unrolled
+  // round would make the compiler wait for every slot at the loop top.
+  const int64_t my_rows = rb0 < row_blocks ? (row_blocks - 1 - rb0) / stride + 1 : 0;
+  const int64_t rounds = (my_rows + PD - 1) / PD;
   int parity = 0;
-  // Row k of this row group is rb0 + k * stride; slot k % PD holds the raw loads of row k + PD
-  // once row k has been widened.  The inner loop is unrolled so every slot index is static.
-  for (int64_t base = rb0; base < row_blocks; base += PD * stride) {
+  for (int64_t r = 0; r < rounds; ++r) {
 #pragma unroll
   for (int s = 0; s < PD; ++s) {
-    const int64_t rb = base + s * stride;
-    if (rb >= row_blocks) break;  // uniform across the block
+    const int64_t rb = rb0 + (r * PD + s) * stride;
     parity ^= 1;
     const int64_t row = row_of(rb);
     const uint32_t nb = bytes_of(rb);
     float(*slots)[MAXW + 16] = red[parity];
+    // Consume slot s (this row) and put the row PD steps ahead in flight in its place.
+    widen(s);
+    load_row(rb + PD * stride, s);
     if constexpr (MAXT > 256 && !PARAMS_IN_LDS) {  // 128 VGPRs: widen per row, not once
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
@@ -341,12 +358,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       for (int i = 0; i < VPL; ++i) ho[i] = hv[i];
     }
 
-    // 2. + 3. Consume the next row, put the row PD after it in flight.
-    const int nxt = (s + 1) % PD;  // static after unrolling
-    widen(nxt);
-    load_row(rb + (PD + 1) * stride, nxt);
-
-    // 4. Stores of this row (rows past the end have a zero-byte resource: dropped).
+    // Stores of this row (rows past the end have a zero-byte resource: dropped).
     const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
     const uint32_t stat_nb = nb ? 4u : 0u;
     buf_store_f32(mean, make_rsrc(p.mean ? p.mean + row : nullptr, stat_nb), stat_off);
@@ -387,6 +399,8 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
                                                0, FLN_FWD_STORE_POL);
       }
     }
+    // The next step's widening must not be hoisted above this step's loads and stores.
+    __builtin_amdgcn_sched_barrier(0);
   }
   }
 }
@@ -947,9 +961,25 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   const int64_t row_blocks = (p.rows + rows_per_block - 1) / rows_per_block;
   auto kernel = fwd_reg_kernel<T, FP8, RES, GELU, VEC, VPL, EXACT, MAXT>;
   static int occupancy_cache[2][64];  // per instantiation; [threads == MAXT][device]
-  int64_t grid = resident_blocks(kernel, threads, occupancy_cache[threads == MAXT]);
+  const int64_t cus = device_cu_count();
+  const int64_t resident = resident_blocks(kernel, threads, occupancy_cache[threads == MAXT]);
+  // Blocks per CU: the fewest that keep enough row bytes in progress per CU to cover the per-row
+  // latency (loads in flight, reductions, barriers): ~16 KiB moved per CU for one-wave rows
+  // (no barrier), ~28 KiB for rows spread over several waves, 7/4 of that with a second
+  // dependent row reduction (fp8 row scale) or the GELU epilogue.  More concurrent rows than
+  // that only cost DRAM locality: measured on MI355X (bf16, us), 8192 x 4096 LN 26.9 at the
+  // occupancy limit (3 blocks per CU) against 24.9 at 1; 32768 x 768 25.5 at 1 block per CU
+  // (12 KiB) against 20.2 at 2; LN -> fp8 32768 x 7168 198 at 1, 147 at 2, 133 at 3.
+  const int64_t es = static_cast<int64_t>(sizeof(T));
+  const int64_t moved_per_row = p.cols * (es * (RES ? 3 : 1) + (FP8 ? 1 : es));
+  const int64_t per_block = moved_per_row * rows_per_block;
+  int64_t target = p.wpr == 1 ? (16 << 10) : (28 << 10);
+  if (FP8 == 1 || GELU != 0) target = target * 7 / 4;
+  int64_t per_cu = per_block > 0 ? (target + per_block - 1) / per_block : 1;
   const int forced = tuning().fwd_grid_mult;
-  if (forced > 0) grid = static_cast<int64_t>(forced) * device_cu_count();
+  if (forced > 0) per_cu = forced;
+  int64_t grid = per_cu * cus;
+  if (grid > resident) grid = resident;
   if (grid > row_blocks) grid = row_blocks;
   if (grid > kMaxGrid) grid = kMaxGrid;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, s, p, row_blocks);

@@ -65,6 +65,7 @@ Tuning read_tuning() {
   t.bwd_epl = env_knob("FLN_BWD_EPL", 0);
   t.bwd_wpr = env_knob("FLN_BWD_WPR", 0);
   t.bwd_threads = env_knob("FLN_BWD_THREADS", 0);
+  t.bwd_grid_mult = env_knob("FLN_BWD_GRID_MULT", 0);
   t.bwd_no_lds = env_knob("FLN_BWD_NO_LDS", 0);
   t.bwd_no_two_pass = env_knob("FLN_BWD_NO_TWO_PASS", 0);
   return t;

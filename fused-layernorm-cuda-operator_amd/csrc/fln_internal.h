@@ -68,6 +68,7 @@ struct Tuning {
   int bwd_epl;         // FLN_BWD_EPL: backward elements per lane
   int bwd_wpr;         // FLN_BWD_WPR: backward waves per row
   int bwd_threads;     // FLN_BWD_THREADS: backward block size (256, 512, 1024)
+  int bwd_grid_mult;   // FLN_BWD_GRID_MULT: backward blocks per CU (1-4)
   int bwd_no_lds;      // FLN_BWD_NO_LDS: never the LDS-staged backward
   int bwd_no_two_pass; // FLN_BWD_NO_TWO_PASS: never the two-pass backward
 };

@@ -21,6 +21,24 @@ def test_c_abi_library_exports_every_declared_symbol():
     assert set(declared) <= set(capi.SIGNATURES), "tests/capi.py lacks a signature"
 
 
+def test_stream_library_exports_every_declared_symbol():
+    # libfln_stream.so (the streaming reference kernels bench.py measures the HBM ceiling with).
+    import os
+    import re
+    header = open(os.path.join(capi.ROOT, "include", "fln_stream.h")).read()
+    declared = sorted(set(re.findall(r"\b(fln_stream_[a-z0-9_]+)\s*\(", header)))
+    assert declared == ["fln_stream_blocks_per_cu", "fln_stream_cu_count", "fln_stream_run"]
+    lib = ctypes.CDLL(os.path.join(capi.PKG, "libfln_stream.so"))
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/fln_stream.h but not exported"
+    lib.fln_stream_run.argtypes = [ctypes.c_int, *[ctypes.c_void_p] * 4, ctypes.c_int64,
+                                   *[ctypes.c_int] * 6, ctypes.c_void_p]
+    # Invalid arguments are refused before anything is launched (no device needed).
+    assert lib.fln_stream_run(0, None, None, None, None, 1 << 20, 256, 1, 1, 1, 0, 0, None) == 1
+    assert lib.fln_stream_run(9, 16, 16, 16, 16, 1 << 20, 256, 1, 1, 1, 0, 0, None) == 1
+    assert lib.fln_stream_run(0, 16, None, 16, None, 1 << 31, 256, 1, 1, 1, 0, 0, None) == 1
+
+
 def test_package_without_the_extension_fails_loudly(tmp_path):
     """No fallback path: a copy of the Python package with no built extension beside it must
     refuse to import, naming the missing HIP extension."""
