@@ -20,6 +20,7 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "fln_device.h"
 #include "fln_internal.h"
@@ -1096,7 +1097,7 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
 }
 
 int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
-                    bool have_workspace, hipStream_t s) {
+                    bool have_workspace, size_t workspace_bytes, hipStream_t s) {
   // p0.part_g / p0.part_b carry the workspace base (validated by the caller).
   BwdParams p = p0;
   const bool vec_ok = aligned16(p.x) && aligned16(p.dy) && aligned16(p.dx) &&
@@ -1119,10 +1120,19 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   }
   const int64_t ld = (p.cols + 3) & ~int64_t(3);
   float* ws = p0.part_g;
+  // Workspace layout: dgamma partials [blocks, ld] and dbeta partials [blocks, ld] when either
+  // gradient is requested, then the row statistics of the two-pass path [rows, 2] (16-byte
+  // aligned: ld is a multiple of 4).  At most fln_backward_workspace_bytes() (blocks <=
+  // workspace_partial_rows on every path).
+  const int64_t part = (dgamma || dbeta) ? 2 * geo.blocks * ld : 0;
+  if (have_workspace) {
+    const size_t need = (static_cast<size_t>(part) +
+                         (geo.two_pass ? 2 * static_cast<size_t>(p.rows) : 0)) * sizeof(float);
+    if (need > workspace_bytes) return FLN_ERR_TOO_LARGE;
+  }
   p.part_g = dgamma ? ws : nullptr;
   p.part_b = dbeta ? ws + geo.blocks * ld : nullptr;
-  // Row statistics after the largest partial block (16-byte aligned: ld is a multiple of 4).
-  p.rowstat = have_workspace ? ws + 2 * workspace_partial_rows(p.rows) * ld : nullptr;
+  p.rowstat = have_workspace ? ws + part : nullptr;
   ColReduceArgs a{};
   if (dgamma) { a.part[a.ny] = p.part_g; a.out[a.ny] = dgamma; ++a.ny; }
   if (dbeta) { a.part[a.ny] = p.part_b; a.out[a.ny] = dbeta; ++a.ny; }
@@ -1160,8 +1170,10 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(uint8_t* a, uint8_t* b, 
   }
 }
 
+// scratch: the workspace is the device's no-allocation scratch (its size checked against what
+// the call's geometry needs, not against the fln_backward_workspace_bytes bound).
 int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
-                    void* workspace, size_t workspace_bytes, void* stream) {
+                    void* workspace, size_t workspace_bytes, void* stream, bool scratch = false) {
   if (p.rows < 0 || p.cols < 0 || p.rows > INT32_MAX || p.cols > INT32_MAX) return FLN_ERR_INVALID;
   if (dtype != FLN_F32 && dtype != FLN_BF16 && dtype != FLN_F16) return FLN_ERR_INVALID;
   if ((dgamma || dbeta) && dparam_dtype != FLN_F32 && dparam_dtype != dtype) return FLN_ERR_INVALID;
@@ -1181,11 +1193,39 @@ int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int 
   if (!p.dx && !dgamma && !dbeta) return FLN_OK;
   const bool have_workspace =
       workspace && fln::aligned16(workspace) &&
-      workspace_bytes >= fln_backward_workspace_bytes(p.rows, p.cols, dtype);
+      (scratch || workspace_bytes >= fln_backward_workspace_bytes(p.rows, p.cols, dtype));
   if ((dgamma || dbeta) && !have_workspace) return FLN_ERR_INVALID;
   p.part_g = have_workspace ? static_cast<float*>(workspace) : nullptr;
   return fln::launch_backward(p, dtype, dgamma, dbeta, dparam_dtype, have_workspace,
-                              static_cast<hipStream_t>(stream));
+                              workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+// Scratch of fln_layernorm_backward_noalloc: the workspace (column partials, row statistics) of
+// one call, for callers that cannot allocate.  Every device that runs that entry point holds its
+// own copy until the process ends.  Host code never names the array itself (on the host it is
+// only a stand-in for the symbol): it uses the device address hipGetSymbolAddress returns, once
+// per device, with that device current.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+
+std::atomic<void*> g_scratch_ptr[64];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on device `dev` (the current device), or nullptr.
+void* scratch_on_device(int dev) {
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr) return ptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  return ptr;
 }
 
 }  // namespace
@@ -1210,6 +1250,28 @@ extern "C" int fln_layernorm_backward(const void* dy, const void* x, const float
   p.rows = rows; p.cols = cols; p.rms = 0;
   return backward_common(p, dtype, dgamma, dbeta, dparam_dtype, workspace, workspace_bytes,
                          stream);
+}
+
+extern "C" int fln_layernorm_backward_noalloc(const void* dy, const void* x, const float* mean,
+                                              const float* rstd, const void* gamma,
+                                              const void* dres, void* dx, void* dgamma,
+                                              void* dbeta, int64_t rows, int64_t cols, int dtype,
+                                              int dparam_dtype, void* stream) {
+  // The scratch is per device: the stream must belong to the current device.
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FLN_ERR_INVALID;
+  if (stream) {
+    int sdev = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess || sdev != dev)
+      return FLN_ERR_INVALID;
+  }
+  void* ws = scratch_on_device(dev);
+  if (!ws) return FLN_ERR_INVALID;
+  fln::BwdParams p{};
+  p.dy = dy; p.x = x; p.mean = mean; p.rstd = rstd; p.gamma = gamma; p.dres = dres; p.dx = dx;
+  p.rows = rows; p.cols = cols; p.rms = 0;
+  return backward_common(p, dtype, dgamma, dbeta, dparam_dtype, ws, kScratchBytes, stream,
+                         /*scratch=*/true);
 }
 
 extern "C" int fln_layernorm_gelu_backward(const void* dy, const void* x, const float* mean,

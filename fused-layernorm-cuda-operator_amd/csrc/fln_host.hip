@@ -136,5 +136,7 @@ extern "C" int fln_hip_version(void) { return HIP_VERSION; }
 extern "C" const char* fln_error_string(int code) {
   if (code == FLN_OK) return "success";
   if (code == FLN_ERR_INVALID) return "invalid argument (shape, dtype, pointer or workspace)";
+  if (code == FLN_ERR_TOO_LARGE)
+    return "problem needs more workspace than the no-allocation scratch holds (32 MiB)";
   return hipGetErrorString(static_cast<hipError_t>(code));
 }

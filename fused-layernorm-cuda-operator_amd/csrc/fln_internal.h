@@ -76,8 +76,10 @@ const Tuning& tuning();  // read at the first call; fln_reload_tuning() reads ag
 void reload_tuning();
 
 int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s);
+// have_workspace: p.part_g points at workspace_bytes of 16-byte aligned workspace; a call whose
+// geometry needs more returns FLN_ERR_TOO_LARGE before anything is launched.
 int launch_backward(const BwdParams& p, int dtype, void* dgamma, void* dbeta, int dparam_dtype,
-                    bool have_workspace, hipStream_t s);
+                    bool have_workspace, size_t workspace_bytes, hipStream_t s);
 
 // Stage-1 geometry of the backward (shared by workspace sizing and the launch).
 struct BwdGeometry {

@@ -36,6 +36,9 @@ extern "C" {
 
 #define FLN_OK 0
 #define FLN_ERR_INVALID 1 /* == hipErrorInvalidValue */
+/* fln_layernorm_backward_noalloc only: the call needs more workspace than its fixed per-device
+ * scratch holds (negative, so it never collides with a hipError_t value). */
+#define FLN_ERR_TOO_LARGE (-2)
 
 /* y = LN(x) [* gamma + beta].  gamma and beta may each be NULL (then that term is skipped).
  * Replaces `layernorm_cuda` (csrc/layernorm_cuda_kernel.cu:152-178) behind
@@ -84,6 +87,21 @@ int fln_layernorm_backward(const void* dy, const void* x, const float* mean, con
                            const void* gamma, const void* dres, void* dx, void* dgamma,
                            void* dbeta, int64_t rows, int64_t cols, int dtype, int dparam_dtype,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* fln_layernorm_backward without a workspace argument, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The workspace is a fixed 32 MiB scratch array in device memory,
+ * one per device that runs this entry point, held until the process ends; nothing is allocated
+ * per call.  Enough for the register and LDS kernels' one partial row per CU up to 16384
+ * columns (8 MiB at 8192 x 4096); a call that needs more returns FLN_ERR_TOO_LARGE before
+ * anything is launched.  Every call on a device shares that device's scratch: calls that
+ * overlap on one device (other streams, other host threads) race, so serialize them.  The
+ * stream must belong to the current device (FLN_ERR_INVALID otherwise).  Results equal
+ * fln_layernorm_backward's bit for bit. */
+int fln_layernorm_backward_noalloc(const void* dy, const void* x, const float* mean,
+                                   const float* rstd, const void* gamma, const void* dres,
+                                   void* dx, void* dgamma, void* dbeta, int64_t rows, int64_t cols,
+                                   int dtype, int dparam_dtype, void* stream);
 
 /* Backward of y = GELU(LayerNorm(x) * gamma + beta) (gelu_mode FLN_GELU_ERF or _TANH, as in
  * the forward): the GELU input is recomputed from mean / rstd / gamma / beta, then

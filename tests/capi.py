@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(PKG, "libfln.so")
 HEADER = os.path.join(ROOT, "include", "fused_layernorm.h")
 
 F32, BF16, F16, F64, F8E4M3FN = 0, 1, 2, 3, 4
+ERR_INVALID, ERR_TOO_LARGE = 1, -2
 GELU_NONE, GELU_ERF, GELU_TANH = 0, 1, 2
 
 _vp = ctypes.c_void_p
@@ -35,6 +36,8 @@ SIGNATURES = {
     "fln_backward_workspace_bytes": ([_i64, _i64, _i32], _sz),
     "fln_layernorm_backward": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32,
                                 _i32, _vp, _sz, _vp], _i32),
+    "fln_layernorm_backward_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                        _i32, _i32, _vp], _i32),
     "fln_rmsnorm_forward": ([_vp, _vp, _vp, _vp, _i64, _i64, _i32, _f32, _vp], _i32),
     "fln_rmsnorm_backward": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
                               _sz, _vp], _i32),
