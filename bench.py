@@ -19,8 +19,11 @@ Prints ONE JSON line.  `value` = algorithmic bytes of one step / measured step t
 reduction), the larger of the two, timed with HIP events on its launch stream; its `traffic`
 comes from two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over a child run of this
 script (--kernel-loop), each scaled by what the counter reads for a device copy of known size.
-`cpu_baseline` times the C oracle (oracle/fln_oracle.c, the "port") on a bounded row sample on
-the host, single thread.
+`stream_ceilings` times hand-written streaming kernels (libfln_stream.so) of each access
+pattern as the HBM ceiling the kernels are judged against.  `cpu_baseline` times the reference's
+CPU path (torch-CPU F.layer_norm + autograd backward, which the reference's module falls back to
+off the GPU) on the full headline workload with the process's host threads; the C oracle
+(oracle/fln_oracle.c, the "port") on a row sample is nested beside it.
 """
 from __future__ import annotations
 
@@ -389,8 +392,78 @@ def pmc_traffic(workload, iters=20):
 # ------------------------------------------------------------------------------------------------
 # CPU baselines.
 # ------------------------------------------------------------------------------------------------
-def cpu_baseline(w, seconds):
-    """Time the C oracle (scalar C port, one thread) on a bounded row sample of the workload."""
+def cpu_threads():
+    """Host threads for the CPU baselines: the process's thread budget (OMP_NUM_THREADS, which
+    the GPU boxes set to their CPU share), else every CPU the host reports."""
+    try:
+        n = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        n = 0
+    return max(1, n if n > 0 else (os.cpu_count() or 1))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(run, seconds, min_runs=3, warmup=2):
+    for _ in range(warmup):
+        run()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def torch_cpu_baseline(w, seconds):
+    """The reference's CPU path on the full workload: its module falls back to
+    torch.nn.functional.layer_norm off the GPU (fused_layernorm/layernorm.py:189-193), here
+    F.layer_norm (F.rms_norm for RMS) plus its autograd backward (dx, dgamma, dbeta) on torch-CPU,
+    in the workload's dtype, on every host thread of the process's budget.  Full size: the
+    tensors (64 MiB each at 8192 x 4096 bf16) exceed the host's last-level cache, as on the GPU."""
+    import torch
+    from fused_layernorm.testing import algorithmic_bytes, make_inputs
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    inp = make_inputs(w)
+    x = inp["x"].requires_grad_(True)
+    g = inp.get("gamma")
+    b = inp.get("beta")
+    params = [t.requires_grad_(True) for t in (g, b) if t is not None]
+    dy = inp["dy"]
+    rms = w.op.startswith("rms")
+
+    def run():
+        if rms:
+            y = torch.nn.functional.rms_norm(x, (w.cols,), g, w.eps)
+        else:
+            y = torch.nn.functional.layer_norm(x, (w.cols,), g, b, w.eps)
+        torch.autograd.grad(y, [x] + params, dy)
+
+    med, n = _median_time(run, seconds)
+    return {"value": round(algorithmic_bytes(w)["total"] / med / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "torch-cpu",
+            "sample": (f"full {w.rows} x {w.cols} {str(w.dtype).replace('torch.', '')} step of "
+                       f"{w.name} (the reference's CPU path: F.layer_norm + autograd backward of "
+                       f"x, gamma, beta), median of {n} runs, {med * 1e3:.1f} ms per step"),
+            "ms_per_step": round(med * 1e3, 2), "torch_threads": torch.get_num_threads(),
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
+
+
+def cpu_port_baseline(w, seconds):
+    """The C oracle (oracle/fln_oracle.c: scalar C port, one thread, fp64 accumulation) on a
+    bounded row sample of the workload."""
     from oracle import c_oracle
     from fused_layernorm.testing import algorithmic_bytes, make_inputs
 
@@ -408,103 +481,91 @@ def cpu_baseline(w, seconds):
             c_oracle.layernorm_fwd(f["x"], f.get("gamma"), f.get("beta"), w.eps)
             c_oracle.layernorm_bwd(f["dy"], f["x"], f.get("gamma"), w.eps)
 
-    run()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    nbytes = algorithmic_bytes(w, rows)["total"]
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as fh:
-            for line in fh:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    med, n = _median_time(run, seconds, warmup=1)
     return {
-        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "value": round(algorithmic_bytes(w, rows)["total"] / med / 1e9, 3), "unit": "GB/s",
+        "cores": 1, "kind": "port",
         "sample": (f"{rows} of {w.rows} rows of the same seeded workload ({w.name}), "
-                   f"C oracle fwd+bwd (fp64 accumulation), median of {len(times)} runs "
+                   f"C oracle fwd+bwd (fp64 accumulation), median of {n} runs "
                    f"({med * 1e3:.1f} ms per {rows}-row fwd+bwd)"),
         "ms_per_step_full_size_extrapolated": round(med * (w.rows / rows) * 1e3, 1),
-        "cpu_model": cpu, "host_cpus": os.cpu_count(),
     }
 
 
-def torch_cpu_baseline(w, seconds, threads=16):
-    """The reference's CPU path (torch-CPU F.layer_norm / F.rms_norm + autograd backward) on a
-    row sample of the same workload, `threads` host threads (the GPU box's CPU share)."""
-    import torch
-    from fused_layernorm.testing import algorithmic_bytes, make_inputs
-
-    torch.set_num_threads(max(1, min(threads, os.cpu_count() or 1)))
-    rows = 1024
-    inp = make_inputs(w, rows)
-    x = inp["x"].requires_grad_(True)
-    g = inp.get("gamma")
-    b = inp.get("beta")
-    dy = inp["dy"]
-    rms = w.op.startswith("rms")
-
-    def run():
-        x.grad = None
-        if rms:
-            y = torch.nn.functional.rms_norm(x, (w.cols,), g, w.eps)
-        else:
-            y = torch.nn.functional.layer_norm(x, (w.cols,), g, b, w.eps)
-        y.backward(dy)
-
-    run()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {"value": round(algorithmic_bytes(w, rows)["total"] / med / 1e9, 3), "unit": "GB/s",
-            "threads": torch.get_num_threads(), "kind": "torch-cpu (reference CPU path)",
-            "sample": f"{rows} of {w.rows} rows of {w.name}, median of {len(times)} runs"}
+# Launch shapes of the streaming reference kernels timed for each access pattern: (threads,
+# blocks per CU, 16-byte vectors per thread per tile, tiles of loads in flight), the best few of a
+# sweep over 256-1024 threads, 1-8 blocks per CU, 1-4 vectors and 1-4 tiles on MI355X (all with
+# non-temporal loads and stores, which beat the default policy for every pattern).
+STREAM_SHAPES = {
+    0: ((512, 1, 2, 1), (256, 2, 1, 2), (256, 4, 1, 1), (512, 2, 2, 2)),
+    1: ((512, 1, 1, 1), (512, 1, 2, 1), (512, 1, 1, 2), (1024, 1, 1, 1)),
+    2: ((256, 2, 1, 4), (256, 1, 2, 3), (512, 1, 1, 1), (256, 1, 1, 2)),
+    3: ((512, 1, 1, 3), (256, 2, 1, 3), (512, 1, 2, 2), (512, 1, 4, 1)),
+}
+STREAM_NAMES = {0: "1r1w", 1: "2r1w", 2: "2r2w", 3: "1r_half_w"}
+STREAM_MOVED = {0: 2.0, 1: 3.0, 2: 4.0, 3: 1.5}  # bytes moved per input-stream byte
 
 
-def stream_ceilings(torch, rows, cols, fwd_bytes, bwd_bytes, warmup=10, n=100):
-    """Streaming rates of plain device copies on the headline shape (bf16 [rows, cols], rotating
-    buffers over >= 2 GiB): torch's copy (1 read + 1 write, the forward's pattern) and add (2
-    reads + 1 write, the backward's).  The step ceiling is the step's algorithmic bytes at
-    those rates."""
-    stream = torch.cuda.current_stream()
-    nbytes = rows * cols * 2
-    nsets = max(4, -(-ROTATE_BYTES // (3 * nbytes)))
-    sets = [[torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16) for _ in range(3)]
+def stream_ceilings(torch, nbytes, fwd_bytes, bwd_bytes, n=100):
+    """HBM ceiling of each access pattern on this device: the streaming reference kernels of
+    libfln_stream.so (include/fln_stream.h; raw buffer loads / stores, persistent grid, a ring of
+    loads in flight: the normalization kernels' own idioms with nothing computed) over streams of
+    `nbytes` each, rotating over >= 2 GiB, best launch shape of STREAM_SHAPES, HIP events on the
+    launch stream.  The step ceiling is the headline step's algorithmic bytes with the forward's
+    at the 1R1W rate and the backward's at the 2R1W rate."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(PKG, "libfln_stream.so"))
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.fln_stream_run.argtypes = [i32, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32, i32, vp]
+    lib.fln_stream_run.restype = i32
+    st = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(st.cuda_stream)
+    cus = lib.fln_stream_cu_count()
+    nsets = max(4, -(-ROTATE_BYTES // (4 * nbytes)))
+    sets = [[torch.empty(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(4)]
             for _ in range(nsets)]
+    for st4 in sets:
+        for t in st4[:2]:
+            t.random_(0, 2 ** 31 - 1)
+    res = {}
+    for pat, shapes in STREAM_SHAPES.items():
+        best = None
+        for thr, bpc, u, pd in shapes:
+            k = [0]
 
-    def rate(fn, moved):
-        for i in range(warmup):
-            fn(sets[i % nsets])
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(n):
-            fn(sets[i % nsets])
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return moved / (e0.elapsed_time(e1) / n * 1e-3) / 1e9
-
-    copy = rate(lambda st: st[2].copy_(st[0]), 2 * nbytes)
-    add = rate(lambda st: torch.add(st[0], st[1], out=st[2]), 3 * nbytes)
+            def one():
+                a, b, c, d = sets[k[0] % nsets]
+                k[0] += 1
+                rc = lib.fln_stream_run(pat, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                        d.data_ptr(), nbytes, thr, bpc * cus, u, pd, 2, 2, sp)
+                if rc != 0:
+                    raise RuntimeError(f"fln_stream_run pattern {pat}: {rc}")
+            for _ in range(10):
+                one()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(n):
+                one()
+            e1.record(st)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / n * 1e3
+            rate = nbytes * STREAM_MOVED[pat] / (us * 1e-6) / 1e9
+            if best is None or rate > best[0]:
+                best = (rate, us, (thr, bpc, u, pd))
+        res[STREAM_NAMES[pat] + "_gbs"] = round(best[0], 1)
+        res[STREAM_NAMES[pat] + "_shape"] = {"threads": best[2][0], "blocks_per_cu": best[2][1],
+                                             "vectors_per_thread": best[2][2],
+                                             "tiles_in_flight": best[2][3],
+                                             "us_per_call": round(best[1], 2)}
     del sets
     torch.cuda.empty_cache()
-    step_s = fwd_bytes / (copy * 1e9) + bwd_bytes / (add * 1e9)
-    return {"copy_1r1w_gbs": round(copy, 1), "add_2r1w_gbs": round(add, 1),
-            "step_ceiling_gbs": round((fwd_bytes + bwd_bytes) / step_s / 1e9, 1),
-            "what": "torch device copy (fwd pattern) and add (bwd pattern) on bf16 "
-                    f"[{rows},{cols}], rotating >= 2 GiB; step ceiling = the step's "
-                    "algorithmic bytes at those rates"}
+    step_s = fwd_bytes / (res["1r1w_gbs"] * 1e9) + bwd_bytes / (res["2r1w_gbs"] * 1e9)
+    res["step_ceiling_gbs"] = round((fwd_bytes + bwd_bytes) / step_s / 1e9, 1)
+    res["what"] = (f"libfln_stream.so kernels, {nbytes >> 20} MiB per stream (the headline's "
+                   "tensor size), rotating >= 2 GiB, best of STREAM_SHAPES; step ceiling = the "
+                   "step's algorithmic bytes at the 1R1W (forward) and 2R1W (backward) rates")
+    return res
 
 
 def torch_gpu_compare(torch, ours, warmup=10, n=50):
@@ -623,18 +684,17 @@ def torch_gpu_compare(torch, ours, warmup=10, n=50):
     return res
 
 
-def torch_cpu_configs(seconds=1.5, threads=16):
+def torch_cpu_configs(seconds=1.5):
     """The reference's CPU path on each config: torch-CPU ops on the same seeded inputs (the
-    config's dtype), `threads` host threads, a bounded row sample of the large configs; median
-    of >= 3 runs, extrapolated to the full row count (rows are independent)."""
+    config's dtype) at full size, the process's host-thread budget; median of >= 3 runs."""
     import torch
     from fused_layernorm.testing import WORKLOADS, algorithmic_bytes, make_inputs
     F = torch.nn.functional
-    torch.set_num_threads(max(1, min(threads, os.cpu_count() or 1)))
+    torch.set_num_threads(cpu_threads())
     res = {}
     cases = (("c1_ln_fwd_fp32_32x768", None), ("c2_ln_gelu_fp32_17x1023", None),
-             ("c2_ln_gelu_fp32_64x4096", None), ("c3_add_ln_fwd_bf16_8192x4096", 512),
-             ("c4_rms_fwd_bwd_bf16_16384x8192", 256), ("c5_ln_fp8_bf16_32768x7168", 256))
+             ("c2_ln_gelu_fp32_64x4096", None), ("c3_add_ln_fwd_bf16_8192x4096", None),
+             ("c4_rms_fwd_bwd_bf16_16384x8192", None), ("c5_ln_fp8_bf16_32768x7168", None))
     for name, sample in cases:
         w = WORKLOADS[name]
         rows = w.rows if sample is None else sample
@@ -669,18 +729,10 @@ def torch_cpu_configs(seconds=1.5, threads=16):
                 scale = y.abs().amax(dim=-1, keepdim=True) / 448.0
                 (y / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
             what = "F.layer_norm, row amax, scale, clamp, float8_e4m3fn cast"
-        for _ in range(3):
-            run()
-        times = []
-        t_end = time.perf_counter() + seconds
-        while time.perf_counter() < t_end or len(times) < 3:
-            t0 = time.perf_counter()
-            run()
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
-        res[name] = {"us_per_call": round(med * (w.rows / rows) * 1e6, 1),
+        med, n = _median_time(run, seconds, warmup=1 if rows * w.cols > 2 ** 24 else 3)
+        res[name] = {"us_per_call": round(med * 1e6, 1),
                      "gbs": round(algorithmic_bytes(w, rows)["total"] / med / 1e9, 2),
-                     "sample": f"{rows} of {w.rows} rows, {what}, median of {len(times)}"}
+                     "sample": f"full {rows} x {w.cols}, {what}, median of {n}"}
     res["threads"] = torch.get_num_threads()
     return res
 
@@ -829,7 +881,7 @@ def main():
         "data": "synthetic: seeded torch.randn inputs (x seed 3, gamma 103, beta 203, dy 303)",
         "config": {"workload": HEADLINE, "rows": 8192, "cols": 4096,
                    "step": "LayerNorm fwd (y, mean, rstd) + bwd (dx, dgamma, dbeta fp32); the "
-                           "bwd runs on another buffer set than the fwd",
+                           "bwd runs on the buffer set half the rotation away from the fwd's",
                    "algorithmic_bytes_per_step": head["bytes"]["total"],
                    "rotating_buffer_sets": head["nsets"]},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
@@ -851,8 +903,10 @@ def main():
             "traffic": traffic["fwd"] if traffic and traffic.get("fwd") else None,
         },
     }
-    ceil = stream_ceilings(torch, 8192, 4096, head["bytes"]["fwd"], head["bytes"]["bwd"])
+    ceil = stream_ceilings(torch, 8192 * 4096 * 2, head["bytes"]["fwd"], head["bytes"]["bwd"])
     ceil["value_over_step_ceiling"] = round(value / ceil["step_ceiling_gbs"], 3)
+    ceil["bwd_over_2r1w"] = round(bwd_gbs / ceil["2r1w_gbs"], 3)
+    ceil["fwd_over_1r1w"] = round(gbs(head["bytes"]["fwd"], head["ms_fwd"]) / ceil["1r1w_gbs"], 3)
     out["stream_ceilings"] = ceil
     if rms:
         out["rms_fwd_bwd"] = {
@@ -902,8 +956,8 @@ def main():
 
     if not args.no_cpu_baseline:
         w = WORKLOADS[HEADLINE]
-        out["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
-        out["cpu_baseline"]["torch_cpu"] = torch_cpu_baseline(w, max(2.0, args.cpu_seconds / 2))
+        out["cpu_baseline"] = torch_cpu_baseline(w, max(2.0, args.cpu_seconds / 2))
+        out["cpu_baseline"]["c_oracle_port"] = cpu_port_baseline(w, args.cpu_seconds / 2)
         if not args.no_configs and not args.headline_only:
             tc = torch_cpu_configs()
             for name, e in tc.items():
