@@ -42,7 +42,13 @@ struct ColReduceArgs {
 // loads in flight, then the S slices are folded through LDS in fixed steps of 4 (S -> S/4 -> ...
 // -> at most 8) and one thread per quad adds the last few.  The order depends only on G and S,
 // so the result is bitwise reproducible.
-constexpr int kCrQuads = 8;
+#ifndef FLN_CR_QUADS
+#define FLN_CR_QUADS 8
+#endif
+#ifndef FLN_CR_SLICES
+#define FLN_CR_SLICES 32
+#endif
+constexpr int kCrQuads = FLN_CR_QUADS;
 
 __device__ __forceinline__ void add4(float4& a, const float4& b) {
   a.x += b.x;
@@ -793,7 +799,7 @@ __global__ __launch_bounds__(1024) void bwd_loop_kernel(const BwdParams p) {
   }
 }
 
-constexpr int kCrSlices = 32;
+constexpr int kCrSlices = FLN_CR_SLICES;
 constexpr int kCrThreads = kCrQuads * kCrSlices;
 
 // Stage 2: one quad block per 256-thread block (32 slices), >= 256 blocks at 4096 columns.

@@ -168,21 +168,27 @@ template <class Op> __device__ __forceinline__ float wave_allreduce(float v) {
   return Op::apply(readlane(v, 0), readlane(v, 32));
 }
 
+// Reduce the values of lanes 0..15 (the first 16-lane row) in a fixed order with four DPP
+// steps; the result is wave-uniform.
+template <class Op> __device__ __forceinline__ float reduce16(float v) {
+  v = Op::apply(v, dpp<0xB1>(v));
+  v = Op::apply(v, dpp<0x4E>(v));
+  v = Op::apply(v, dpp<0x141>(v));
+  v = Op::apply(v, dpp<0x140>(v));
+  return readlane(v, 0);
+}
+
 // Combine the per-wave partials slot[base .. base + n - 1] (n <= 16) of one row group: lane k
 // reads partial k (one LDS read per lane, all in parallel), lanes k >= n contribute `ident`, and
-// the four DPP steps reduce the first 16-lane row in a fixed order; the result is wave-uniform.
-// slot must be readable up to base + 15 (callers pad it).
+// reduce16 combines them; the result is wave-uniform.  slot must be readable up to base + 15
+// (callers pad it).
 template <class Op>
 __device__ __forceinline__ float combine_partials(const float* slot, int base, int n, int lane,
                                                   float ident) {
   const int k = lane & 15;
   float v = slot[base + k];
   v = k < n ? v : ident;
-  v = Op::apply(v, dpp<0xB1>(v));
-  v = Op::apply(v, dpp<0x4E>(v));
-  v = Op::apply(v, dpp<0x141>(v));
-  v = Op::apply(v, dpp<0x140>(v));
-  return readlane(v, 0);
+  return reduce16<Op>(v);
 }
 
 // Generic-type wave sum through ds_bpermute (used by the looped fallback kernels, which also

@@ -50,13 +50,19 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 // EXACT: the row is exactly VPL vectors per lane (no masking in the statistics); GELU: 0 none,
 // 1 erf, 2 tanh (a template parameter so the plain kernels carry no GELU code).
 // ---------------------------------------------------------------------------------------------
+// Rows in flight ahead of the current one: about 64 bytes of loads per lane.  A lane holding 64
+// bytes or more of a row prefetches one row, a smaller slice two (measured with exact ring
+// waits, bf16, us: 8192 x 4096 LN 24.9 -> 24.0 and LN + GELU(erf) 31.4 -> 30.0 with one row of
+// 64 bytes ahead instead of two; LN -> fp8 32768 x 7168, 32 bytes per lane, 146 with one row
+// against 141 with two; three rows ahead were slower everywhere).
 // Register budget: a 1024-thread block leaves 128 VGPRs per lane.  There a lane with more than
-// 32 bytes of a row prefetches one row instead of two (two again for the 16-bit RAW tiles without
-// a residual, whose gamma / beta live in LDS), and a lane with 32 elements (RAW) keeps the row in
-// the I/O type rather than as an fp32 copy, widening it again in each pass (one VALU op per
-// element).  Blocks of at most 256 threads have 256 VGPRs and keep the fp32 copy.
+// 32 bytes of a row prefetches one row (two again for the 16-bit RAW tiles without a residual,
+// whose gamma / beta live in LDS), and a lane with 32 elements (RAW) keeps the row in the I/O
+// type rather than as an fp32 copy, widening it again in each pass (one VALU op per element).
+// Blocks of at most 256 threads have 256 VGPRs and keep the fp32 copy.
 #ifndef FLN_FWD_PREFETCH
-#define FLN_FWD_PREFETCH(ROW_BYTES, MAXT) ((MAXT) > 256 && (ROW_BYTES) > 32 ? 1 : 2)
+#define FLN_FWD_PREFETCH(ROW_BYTES, MAXT) \
+  (((ROW_BYTES) >= 64 || ((MAXT) > 256 && (ROW_BYTES) > 32)) ? 1 : 2)
 #endif
 // Cache policies of the streamed rows: loads of x / residual and stores of y / h / q are
 // non-temporal (each byte is touched once; measured on MI355X this is 3-10% faster than the
@@ -141,6 +147,18 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
   // Vector slot i is complete (no lane past the row) when (i + 1) * tpr <= nvec; only the
   // other slots need per-element masks in the centred sums and the fp8 row max.
   auto slot_full = [&](int i) { return EXACT || (i + 1) * tpr <= nvec; };
+  // Elements of the row held by wave w of a row group (w < wpr), and this wave's reciprocal.
+  auto wave_elems = [&](int w) -> float {
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int left = nvec - (i * tpr + w * kWave);
+      n += left <= 0 ? 0 : (left < kWave ? left : kWave);
+    }
+    return static_cast<float>(n * VEC);
+  };
+  const float own_n = wave_elems(wave - rg * wpr);
+  const float inv_wave_n = own_n > 0.0f ? 1.0f / own_n : 0.0f;
 
   auto row_of = [&](int64_t rb) { return rb * rows_per_block + rg; };
   auto bytes_of = [&](int64_t rb) -> uint32_t {
@@ -227,38 +245,72 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       }
     }
 
-    // 1. Statistics: two passes over registers (mean, then centred sum of squares).  Vectors
-    //    past the row were loaded as zeros, so they drop out of the plain sum.
-    float mean = 0.0f;
-    if (!p.rms) {
+    // 1. Statistics over registers: the mean, then the sum of squares centred on it (two
+    //    passes over the row, no E[x^2] - mean^2 cancellation).  Vectors past the row were
+    //    loaded as zeros, so they drop out of the plain sum.
+    auto centred = [&](float c) {  // sum over this lane's elements of (x - c)^2
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        if (slot_full(i)) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float d = xin(i, e) - c;
+            acc = fmaf(d, d, acc);
+          }
+        } else {
+          const bool ok = (t + i * tpr) < nvec;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float d = xin(i, e) - c;
+            acc += ok ? d * d : 0.0f;
+          }
+        }
+      }
+      return acc;
+    };
+    float mean = 0.0f, q = 0.0f;
+    if (p.rms) {
+      q = row_allreduce<SumOp>(centred(0.0f), slots[1], wpr, rg, wave, lane);
+    } else {
       float s = 0.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) s += xin(i, e);
-      const float sum = row_allreduce<SumOp>(s, slots[0], wpr, rg, wave, lane);
-      mean = sum * inv_n;
-      mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
-    }
-    float q = 0.0f;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      if (slot_full(i)) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float d = xin(i, e) - mean;
-          q = fmaf(d, d, q);
-        }
+      const float sw = wave_allreduce<SumOp>(s);
+      if (wpr == 1) {
+        mean = sw * inv_n;
+        mean = fmaf(fmaf(-mean, fn, sw), inv_n, mean);
+        q = wave_allreduce<SumOp>(centred(mean));
       } else {
-        const bool ok = (t + i * tpr) < nvec;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float d = xin(i, e) - mean;
-          q += ok ? d * d : 0.0f;
+        // A row over several waves takes ONE barrier for both statistics: each wave centres its
+        // own elements on its own mean c_w = S_w / n_w (wave-uniform, known without the other
+        // waves), then the row combines the waves' (S_w, Q_w): mean = sum_w S_w / N (the same
+        // fixed-order sum as a plain two-pass mean, bit for bit) and, by the parallel-variance
+        // identity, sum (x - mean)^2 = sum_w [Q_w + n_w (c_w - mean)^2 + 2 (c_w - mean) r_w],
+        // r_w = S_w - n_w c_w the rounding residue of c_w.
+        const float cw = sw * inv_wave_n;
+        const float qw = wave_allreduce<SumOp>(centred(cw));
+        if (lane == 0) {
+          slots[0][wave] = sw;
+          slots[1][wave] = qw;
         }
+        __syncthreads();
+        const int k = lane & 15;  // lane k of every wave reads wave k's pair of this row group
+        const bool in = k < wpr;
+        const float sk = in ? slots[0][rg * wpr + k] : 0.0f;
+        const float qk = in ? slots[1][rg * wpr + k] : 0.0f;
+        const float sum = reduce16<SumOp>(sk);
+        mean = sum * inv_n;
+        mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
+        const float nk = wave_elems(k);
+        const float ck = sk * (nk > 0.0f ? 1.0f / nk : 0.0f);  // == that wave's c_w
+        const float dk = ck - mean;
+        const float term = in ? qk + dk * fmaf(nk, dk, 2.0f * fmaf(-nk, ck, sk)) : 0.0f;
+        q = reduce16<SumOp>(term);
       }
     }
-    q = row_allreduce<SumOp>(q, slots[1], wpr, rg, wave, lane);
     const float rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);  // v_rsq_f32, 1 ulp
 
     //    Normalize + affine + epilogue, packed to the output format.

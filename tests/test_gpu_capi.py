@@ -1333,3 +1333,72 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
                                       None, None, None, capi.ptr(dg), None, 4, 8, capi.F32,
                                       capi.F32, None, 0, s) == 1
     assert lib.fln_layernorm(capi.ptr(x), None, None, capi.ptr(y), 0, 8, capi.F32, 1e-5, s) == 0
+
+
+# ------------------------------------------------------------------------------------------------
+# The reference's own accuracy scenarios, through fln_layernorm (the reference's `layernorm`
+# entry): its value ranges at 32 x 4096 with nn.LayerNorm's default affine (gamma 1, beta 0)
+# (tests/publication_validation.py:205-214), its normalization check (:242-253) and its
+# "wrong epsilon" case eps = 1e-12 (tests/break_kernel_test.py:39-41).  fp32 outputs against the
+# float64 oracle at max-abs 1e-5; bf16 outputs within 1 bf16 ulp of it.
+# ------------------------------------------------------------------------------------------------
+def _reference_scenario(name, seed=2024):
+    gen = torch.Generator().manual_seed(seed)
+    if name == "mixed_range":  # half the row x1000, half x1e-3
+        return torch.cat([torch.randn(32, 2048, generator=gen) * 1000,
+                          torch.randn(32, 2048, generator=gen) * 1e-3], dim=1)
+    scale = {"normal": 1.0, "large_values": 1000.0, "small_values": 1e-3, "near_zero": 1e-6}[name]
+    return torch.randn(32, 4096, generator=gen) * scale
+
+
+def _ln_plain(lib, x, eps):
+    rows, cols = x.shape
+    y = torch.empty_like(x)
+    g = torch.ones(cols, dtype=x.dtype, device=x.device)
+    b = torch.zeros(cols, dtype=x.dtype, device=x.device)
+    capi.check(lib.fln_layernorm(capi.ptr(x), capi.ptr(g), capi.ptr(b), capi.ptr(y), rows, cols,
+                                 capi.dtype_code(x), eps, capi.stream()))
+    return y
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("scenario", ["normal", "large_values", "small_values", "near_zero",
+                                      "mixed_range"])
+def test_reference_accuracy_scenarios(lib, scenario, dtype):
+    xc = _reference_scenario(scenario).to(dtype)
+    y = _ln_plain(lib, cuda(xc), 1e-5)
+    ref, _, _ = norms.layer_norm_fwd(f32(xc), None, None, 1e-5)
+    assert np.isfinite(to_np(y)).all()
+    if dtype == torch.float32:
+        err = np.abs(to_np(y) - ref).max()
+        assert err <= 1e-5, f"{scenario}: max abs error {err:.3g}"
+        # The reference publishes 4.77e-7 max-abs against nn.LayerNorm for the normal case
+        # (publication_validation_results.json:176-182); torch's own fp32 kernel sits there too.
+        ref_t = torch.nn.functional.layer_norm(xc, (4096,), None, None, 1e-5)
+        assert (y.cpu() - ref_t).abs().max().item() <= 1e-5
+    else:
+        assert_within_ulp(to_np(y), ref, 1.0, what=f"{scenario} y")
+
+
+def test_reference_normalization_check(lib):
+    # publication_validation.py:242-253: with gamma 1 and beta 0 every row of the output has
+    # mean 0 (|mean| < 1e-5) and biased std 1 (|std - 1| < 1e-3).
+    gen = torch.Generator().manual_seed(7)
+    x = cuda(torch.randn(32, 4096, generator=gen))
+    y = _ln_plain(lib, x, 1e-5).double().cpu()
+    assert y.mean(dim=-1).abs().max().item() < 1e-5
+    assert (y.std(dim=-1, unbiased=False) - 1.0).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("scenario", ["normal", "near_zero"])
+def test_reference_epsilon_1e12(lib, scenario, dtype):
+    # break_kernel_test.py:39-41 calls layernorm with eps = 1e-12.  With the near-zero rows
+    # (variance ~1e-12) eps is no longer negligible against the variance: both terms matter.
+    xc = _reference_scenario(scenario, seed=99).to(dtype)
+    y = _ln_plain(lib, cuda(xc), 1e-12)
+    ref, _, _ = norms.layer_norm_fwd(f32(xc), None, None, 1e-12)
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - ref).max() <= 1e-5
+    else:
+        assert_within_ulp(to_np(y), ref, 1.0, what=f"{scenario} eps=1e-12 y")
