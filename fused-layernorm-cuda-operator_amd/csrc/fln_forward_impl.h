@@ -74,6 +74,18 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 #ifndef FLN_FWD_STORE_POL
 #define FLN_FWD_STORE_POL kStream
 #endif
+// Rows of raw loads in flight ahead of the current one, per instantiation (the rule above; the
+// 16-bit RAW tiles without a residual keep two: their gamma / beta live in LDS).
+template <class T, bool RES, int VEC, int VPL, int MAXT> constexpr int fwd_prefetch_depth() {
+  constexpr bool raw = MAXT > 256 && VPL * VEC >= 32;
+  constexpr bool params_in_lds =
+      MAXT == 1024 && ((raw && VEC > 1 && sizeof(T) == 2) || (VEC == 1 && VPL == 16 &&
+                                                               sizeof(T) <= 4));
+  return params_in_lds && raw && !RES
+             ? 2
+             : FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT);
+}
+
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_t row_blocks) {
   constexpr bool RAW = MAXT > 256 && VPL * VEC >= 32;  // row kept in the I/O type
@@ -88,9 +100,11 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
                                                                 sizeof(T) <= 4));
   // rows in flight ahead of the current one (the residual flavour's second input leaves room for
   // one only)
-  constexpr int PD = PARAMS_IN_LDS && RAW && !RES
-                         ? 2
-                         : FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT);
+  constexpr int PD = fwd_prefetch_depth<T, RES, VEC, VPL, MAXT>();
+  static_assert(PD == (PARAMS_IN_LDS && RAW && !RES
+                           ? 2
+                           : FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT)),
+                "fwd_prefetch_depth must match the kernel's ring");
   constexpr int MAXW = MAXT / kWave;
   __shared__ float red[2][3][MAXW + 16];  // padded: combine_partials reads 16 past the base
   using P = Pack<T, VEC>;
@@ -1015,18 +1029,21 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   static int occupancy_cache[2][64];  // per instantiation; [threads == MAXT][device]
   const int64_t cus = device_cu_count();
   const int64_t resident = resident_blocks(kernel, threads, occupancy_cache[threads == MAXT]);
-  // Blocks per CU: the fewest that keep enough row bytes in progress per CU to cover the per-row
-  // latency (loads in flight, reductions, barriers): ~16 KiB moved per CU for one-wave rows
-  // (no barrier), ~28 KiB for rows spread over several waves, 7/4 of that with a second
-  // dependent row reduction (fp8 row scale) or the GELU epilogue.  More concurrent rows than
-  // that only cost DRAM locality: measured on MI355X (bf16, us), 8192 x 4096 LN 26.9 at the
-  // occupancy limit (3 blocks per CU) against 24.9 at 1; 32768 x 768 25.5 at 1 block per CU
-  // (12 KiB) against 20.2 at 2; LN -> fp8 32768 x 7168 198 at 1, 147 at 2, 133 at 3.
+  // Blocks per CU: the fewest whose rows in flight move enough bytes per CU to cover the per-row
+  // latency (loads in flight, reductions, barriers): rows dealt to the CU at once x PD rows of
+  // loads ahead x the bytes each row moves >= 32 KiB for one-wave rows (no barrier), 56 KiB for
+  // rows over several waves, 7/4 of that with a second dependent row reduction (fp8 row scale)
+  // or the exact GELU's VALU work.  More concurrent rows than that only cost DRAM locality.
+  // Measured on MI355X (bf16, us, HIP events; blocks per CU in brackets): 8192 x 4096 LN 26.9 [3]
+  // 24.4 [1] 23.8 [2]; LN + GELU(erf) 31.1 [2] 30.0 [4]; 32768 x 768 25.5 [1] 20.2 [2];
+  // LN -> fp8 32768 x 7168 198 [1] 147 [2] 133 [3]; residual + RMSNorm -> fp8 at that shape 283 [1]
+  // 300 [2].
+  constexpr int PD = fwd_prefetch_depth<T, RES, VEC, VPL, MAXT>();
   const int64_t es = static_cast<int64_t>(sizeof(T));
   const int64_t moved_per_row = p.cols * (es * (RES ? 3 : 1) + (FP8 ? 1 : es));
-  const int64_t per_block = moved_per_row * rows_per_block;
-  int64_t target = p.wpr == 1 ? (16 << 10) : (28 << 10);
-  if (FP8 == 1 || GELU != 0) target = target * 7 / 4;
+  const int64_t per_block = moved_per_row * rows_per_block * PD;
+  int64_t target = p.wpr == 1 ? (32 << 10) : (56 << 10);
+  if (FP8 == 1 || GELU == 1) target = target * 7 / 4;
   int64_t per_cu = per_block > 0 ? (target + per_block - 1) / per_block : 1;
   const int forced = tuning().fwd_grid_mult;
   if (forced > 0) per_cu = forced;
