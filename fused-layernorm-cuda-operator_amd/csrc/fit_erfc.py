@@ -1,4 +1,4 @@
-"""Fits the polynomial behind normal_cdf() in fln_device.h (the exact-erf GELU and its derivative).
+"""Fits the polynomial behind erfc_terms() in fln_device.h (the exact-erf GELU and its derivative).
 
 For x >= 0 and t = 1 / (1 + p x), the scaled complementary error function erfcx(x) =
 exp(x^2) erfc(x) divided by t is smooth on t in (0, 1] (it tends to p / sqrt(pi) as t -> 0 and
@@ -12,7 +12,8 @@ towards the largest residuals (a few dozen rounds approach the minimax fit).
 
 Run with scipy available: prints the coefficients (0.5 folded in, rounded to fp32) and the fit's
 maximum relative error, plus the maximum errors of GELU and its derivative under an fp32
-emulation of the device evaluation.
+emulation of the device evaluation (gelu_erf() and gelu_erf_grad(): the same operations in the
+same order, each rounded to fp32; FMAs rounded once).
 """
 import numpy as np
 from scipy.special import erfc, erfcx
@@ -38,17 +39,42 @@ def fit(p=P, deg=DEGREE, nodes=4000, rounds=60):
     return [np.float32(0.5 * ci) for ci in c], rel
 
 
-def emulate(coef, v, p=P):
-    """fp32 emulation of normal_cdf(): (Phi(v), exp(-v^2 / 2))."""
+def _fma32(a, b, c):
+    """fp32 FMA: the float64 product of two fp32 values is exact; one rounding to fp32."""
+    return (a.astype(np.float64) * b.astype(np.float64) + c).astype(np.float32)
+
+
+def terms(coef, v, p=P):
+    """fp32 emulation of erfc_terms(): (t, exp(-v^2 / 2), F(t))."""
     f32 = np.float32
     v = v.astype(f32)
     e = np.exp2((f32(-0.5 * np.log2(np.e)) * v) * v).astype(f32)
-    t = (f32(1) / (f32(p / np.sqrt(2)) * np.abs(v) + f32(1))).astype(f32)
+    t = (f32(1) / _fma32(np.full_like(v, f32(p / np.sqrt(2))), np.abs(v), f32(1))).astype(f32)
     acc = np.full_like(t, coef[-1])
     for ci in coef[-2::-1]:
-        acc = (acc * t + ci).astype(f32)
-    h = ((acc * t) * e).astype(f32)
-    return np.where(v < 0, h, f32(1) - h).astype(f32), e
+        acc = _fma32(acc, t, ci)
+    return t, e, acc
+
+
+def gelu(coef, v, p=P):
+    """fp32 emulation of gelu_erf(): max(v, 0) - (|v| (t e)) F(t), |v| (t e) = 0 where t e = 0."""
+    f32 = np.float32
+    v = v.astype(f32)
+    t, e, f = terms(coef, v, p)
+    te = (t * e).astype(f32)
+    with np.errstate(invalid="ignore"):
+        q = np.where(te == 0, f32(0), (np.abs(v) * te).astype(f32))
+    return _fma32(-q, f, np.maximum(v, f32(0)))
+
+
+def gelu_grad(coef, v, p=P):
+    """fp32 emulation of gelu_erf_grad(): 1/2 + copysign(1/2 - e (t F - |v| / sqrt(2 pi)), v)."""
+    f32 = np.float32
+    v = v.astype(f32)
+    t, e, f = terms(coef, v, p)
+    w = _fma32(np.full_like(v, f32(-1 / np.sqrt(2 * np.pi))), np.abs(v), (t * f).astype(f32))
+    y = _fma32(-e, w, f32(0.5))
+    return (f32(0.5) + np.copysign(y, v)).astype(f32)
 
 
 if __name__ == "__main__":
@@ -56,14 +82,13 @@ if __name__ == "__main__":
     print("p =", P, "degree =", DEGREE, "fit max relative error %.3g" % rel)
     print("coefficients:", ", ".join("%.9ef" % c for c in coef))
     v = np.linspace(-13, 13, 2600001).astype(np.float32)
-    cdf, e = emulate(coef, v)
-    gelu = (v * cdf).astype(np.float32)
-    grad = (v * (np.float32(1 / np.sqrt(2 * np.pi)) * e) + cdf).astype(np.float32)
+    g = gelu(coef, v)
+    d = gelu_grad(coef, v)
     vd = v.astype(np.float64)
     phi = np.where(vd < 0, 0.5 * erfc(-vd / np.sqrt(2)), 1 - 0.5 * erfc(vd / np.sqrt(2)))
     gref = vd * phi
     dref = phi + vd * np.exp(-vd * vd / 2) / np.sqrt(2 * np.pi)
     big = np.abs(gref) > 1e-30
     print("GELU max abs error %.3g, max relative error %.3g (|GELU| > 1e-30)"
-          % (np.abs(gelu - gref).max(), (np.abs(gelu - gref)[big] / np.abs(gref[big])).max()))
-    print("derivative max abs error %.3g" % np.abs(grad - dref).max())
+          % (np.abs(g - gref).max(), (np.abs(g - gref)[big] / np.abs(gref[big])).max()))
+    print("derivative max abs error %.3g" % np.abs(d - dref).max())

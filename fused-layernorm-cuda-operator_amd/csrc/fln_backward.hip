@@ -313,15 +313,19 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     // Consume slot sl (row it) and put row it + PD in flight in its place.
     widen(sl);
     load_row(it + PD, sl);
-    // Row sums (elements past the row are zero in dy, hence in g).
+    // Row sums (elements past the row are zero in dy, hence in g).  A lane with 8 columns keeps
+    // g = dy gamma for dx below (one multiply per element serves both); with 16 the extra VGPRs
+    // would spill, and dx forms dy (rstd gamma) instead.
+    constexpr bool KEEP_G = VPL * VEC <= 8;
     float s1 = 0.0f, s2 = 0.0f;
+    float gd[VPL][VEC];
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const float g = dd[i][e] * gam(i, e);
-        s1 += g;
-        s2 = fmaf(g, xh[i][e], s2);
+        gd[i][e] = dd[i][e] * gam(i, e);
+        s1 += gd[i][e];
+        s2 = fmaf(gd[i][e], xh[i][e], s2);
       }
     s1 = wave_allreduce<SumOp>(s1);
     s2 = wave_allreduce<SumOp>(s2);
@@ -343,7 +347,8 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float dxv = fmaf(dd[i][e], rs * gam(i, e), fmaf(cx, xh[i][e], cb));
+        float dxv = KEEP_G ? fmaf(rs, gd[i][e], fmaf(cx, xh[i][e], cb))
+                           : fmaf(dd[i][e], rs * gam(i, e), fmaf(cx, xh[i][e], cb));
         if constexpr (DRES) dxv += to_f32(rv[i].v[e]);
         o[i].v[e] = from_f32<T>(dxv);
         acc_g[i][e] = fmaf(dd[i][e], xh[i][e], acc_g[i][e]);

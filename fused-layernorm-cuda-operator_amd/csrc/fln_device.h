@@ -210,8 +210,7 @@ template <class A> __device__ __forceinline__ A wave_sum_generic(A v) {
 //   s + 2 v s (1 - s) sqrt(2/pi) (1 + 3 * 0.044715 v^2),   s = sigmoid(2u).
 // The erf form is v Phi(v) with Phi the standard normal CDF, and its derivative
 //   Phi(v) + v exp(-v^2 / 2) / sqrt(2 pi);
-// normal_cdf() below evaluates Phi and the shared Gaussian factor with one hardware exp2 and
-// one hardware reciprocal.
+// erfc_terms() below gives both from one hardware exp2 and one hardware reciprocal.
 // ---------------------------------------------------------------------------------------------
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kGeluK0 = 0.79788456080286535588f;  // sqrt(2/pi)
@@ -234,19 +233,28 @@ __device__ __forceinline__ GeluTanhTerms gelu_tanh_terms(float v) {
 }
 __device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_terms(v).sg; }
 
-// Phi(v) and exp(-v^2 / 2).  With x = |v| / sqrt 2 and t = 1 / (1 + 0.35 x),
+// The erf form.  With x = |v| / sqrt 2 and t = 1 / (1 + 0.35 x),
 //   h = 0.5 erfc(x) = t F(t) exp(-x^2),
 // where F(t) = 0.5 erfcx(x) / t (erfcx(x) = exp(x^2) erfc(x)) is smooth on t in (0, 1] and is
 // replaced by a degree-7 polynomial: a relative-error least-squares fit on Chebyshev nodes, max
 // relative error 8.3e-7 (fit_erfc.py beside this file derives and checks the coefficients).
-// Phi(v) = h for v < 0 and 1 - h otherwise, so the lower tail keeps its relative accuracy
-// where 1 + erf(v / sqrt 2) cancels.  Under an fp32 emulation over |v| <= 13: v Phi(v) within
-// 3.8e-7 (absolute) and 6.9e-6 (relative, |v Phi(v)| > 1e-30) of the float64 value, the
-// derivative within 5.8e-7.  Infinite v gives Phi = 0 or 1; NaN propagates.
-struct NormalCdf {
-  float cdf, gauss;  // Phi(v), exp(-v^2 / 2)
+// Phi(v) = h for v < 0 and 1 - h otherwise, so
+//   GELU(v)  = v Phi(v) = max(v, 0) - |v| h
+//   GELU'(v) = Phi(v) + v exp(-v^2 / 2) / sqrt(2 pi) = 1/2 + sign(v) (1/2 - exp(-x^2) w),
+//   w = t F(t) - |v| / sqrt(2 pi)
+// (for v >= 0 it is 1 - e w, for v < 0 it is e w: Phi and v phi(v) share the Gaussian factor).
+// GELU is a difference only where v >= 0 and then at most v / 2 is taken off, so its lower tail
+// keeps the relative accuracy of h where 0.5 v (1 + erf(v / sqrt 2)) cancels; the derivative's
+// error is absolute (about one ulp of 1/2 in the tail, like that of Phi + v phi in fp32).
+// Each costs one hardware exp2 (v_exp_f32), one hardware reciprocal (v_rcp_f32), seven FMAs
+// for F and four (GELU) or five (derivative) more VALU operations.  Under an fp32 emulation
+// over |v| <= 13: GELU within 2.4e-7 (absolute) and 6.9e-6 (relative, |GELU| > 1e-30) of the
+// float64 value, the derivative within 5.6e-7.  GELU(+inf) = +inf, GELU(-inf) = 0; NaN
+// propagates.
+struct ErfcTerms {
+  float t, e, f;  // t, exp(-v^2 / 2), F(t)
 };
-__device__ __forceinline__ NormalCdf normal_cdf(float v) {
+__device__ __forceinline__ ErfcTerms erfc_terms(float v) {
   constexpr float kF[8] = {9.873314202e-02f, 9.872655571e-02f, 9.295467287e-02f,
                            7.733605057e-02f, 8.147227019e-02f, -7.275486365e-03f,
                            1.006051227e-01f, -4.255273566e-02f};
@@ -255,15 +263,27 @@ __device__ __forceinline__ NormalCdf normal_cdf(float v) {
   float f = kF[7];
 #pragma unroll
   for (int k = 6; k >= 0; --k) f = fmaf(f, t, kF[k]);
-  const float h = (f * t) * e;
-  return {v < 0.0f ? h : 1.0f - h, e};
+  return {t, e, f};
 }
-__device__ __forceinline__ float gelu_erf(float v) { return v * normal_cdf(v).cdf; }
+// |a| * b with 0 * anything = 0 (v_mul_legacy_f32): |v| (t e) stays 0 at v = +-inf, where
+// t e = 0.  Neither operand may be the direct result of a transcendental instruction (v_rcp,
+// v_exp, ...): a VALU read of such a result needs a wait state, which the compiler does not
+// insert in front of inline assembly.  Callers pass an affine output and a v_mul product.
+__device__ __forceinline__ float abs_mul_zero_wins(float a, float b) {
+  float r;
+  asm("v_mul_legacy_f32 %0, |%1|, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float gelu_erf(float v) {
+  const ErfcTerms k = erfc_terms(v);
+  return fmaf(-abs_mul_zero_wins(v, k.t * k.e), k.f, fmaxf(v, 0.0f));
+}
 __device__ __forceinline__ float gelu_tanh(float v) { return v * gelu_tanh_sigmoid(v); }
 __device__ __forceinline__ float gelu_erf_grad(float v) {
-  const float inv_sqrt_2pi = 0.39894228040143267794f;
-  const NormalCdf n = normal_cdf(v);
-  return fmaf(v, inv_sqrt_2pi * n.gauss, n.cdf);
+  constexpr float kInvSqrt2Pi = 0.39894228040143267794f;
+  const ErfcTerms k = erfc_terms(v);
+  const float w = fmaf(-kInvSqrt2Pi, fabsf(v), k.t * k.f);
+  return 0.5f + __builtin_copysignf(fmaf(-k.e, w, 0.5f), v);
 }
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const GeluTanhTerms t = gelu_tanh_terms(v);

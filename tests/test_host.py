@@ -57,12 +57,13 @@ def test_package_without_the_extension_fails_loudly(tmp_path):
     assert "Cannot import fused_layernorm_cuda" in r.stderr, r.stderr[-2000:]
 
 
-def test_normal_cdf_constants_in_the_device_header():
-    """The exact-GELU kernels evaluate Phi(v) as 0.5 erfc(|v| / sqrt 2) = t F(t) exp(-v^2 / 2),
+def test_erfc_terms_constants_in_the_device_header():
+    """The exact-GELU kernels evaluate Phi(v) through 0.5 erfc(|v| / sqrt 2) = t F(t) exp(-v^2 / 2),
     t = 1 / (1 + p |v| / sqrt 2), F a fitted polynomial.  Parse p and F's coefficients from
-    csrc/fln_device.h, evaluate them under an fp32 emulation of the device code, and check GELU
-    and its derivative against scipy's erfc in float64 over |v| <= 13: a mistyped coefficient
-    or a wrong p fails here, on the CPU."""
+    csrc/fln_device.h, evaluate GELU and its derivative under an fp32 emulation of the device
+    code, and check them against scipy's erfc in float64 over |v| <= 13 (plus the infinities): a
+    mistyped coefficient or a wrong p fails here, on the CPU, and so does a sign slip in either
+    formula (the planted cases below)."""
     import os
     import re
     import sys
@@ -70,7 +71,7 @@ def test_normal_cdf_constants_in_the_device_header():
     from scipy.special import erfc
     csrc = os.path.join(os.path.dirname(os.path.dirname(fl.__file__)), "csrc")
     src = open(os.path.join(csrc, "fln_device.h")).read()
-    body = src[src.index("NormalCdf normal_cdf(float v)"):]
+    body = src[src.index("ErfcTerms erfc_terms(float v)"):]
     body = body[:body.index("return {")]
     coef = [np.float32(float(c)) for c in
             re.findall(r"[-+]?\d\.\d+e[-+]\d+", body[body.index("kF["):body.index("};")])]
@@ -82,17 +83,110 @@ def test_normal_cdf_constants_in_the_device_header():
     finally:
         sys.path.remove(csrc)
     v = np.linspace(-13, 13, 260001).astype(np.float32)
-    cdf, e = fit_erfc.emulate(coef, v, p=p)
-    gelu = (v * cdf).astype(np.float32)
-    grad = (v * (np.float32(1 / np.sqrt(2 * np.pi)) * e) + cdf).astype(np.float32)
     vd = v.astype(np.float64)
     phi = np.where(vd < 0, 0.5 * erfc(-vd / np.sqrt(2)), 1 - 0.5 * erfc(vd / np.sqrt(2)))
     g_ref = vd * phi
     d_ref = phi + vd * np.exp(-vd * vd / 2) / np.sqrt(2 * np.pi)
-    assert np.abs(gelu - g_ref).max() <= 1e-6
-    assert np.abs(grad - d_ref).max() <= 2e-6
     tail = (vd < -3) & (np.abs(g_ref) > 1e-30)
-    assert (np.abs(gelu[tail] - g_ref[tail]) / np.abs(g_ref[tail])).max() <= 1e-4
+
+    def errors(gelu, grad):
+        return (np.abs(gelu - g_ref).max(), np.abs(grad - d_ref).max(),
+                (np.abs(gelu[tail] - g_ref[tail]) / np.abs(g_ref[tail])).max())
+
+    gelu = fit_erfc.gelu(coef, v, p=p)
+    grad = fit_erfc.gelu_grad(coef, v, p=p)
+    g_abs, d_abs, g_tail = errors(gelu, grad)
+    assert g_abs <= 1e-6 and d_abs <= 2e-6 and g_tail <= 1e-4, (g_abs, d_abs, g_tail)
+    special = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0], np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        gs = fit_erfc.gelu(coef, special, p=p)
+        ds = fit_erfc.gelu_grad(coef, special, p=p)
+    assert gs[0] == np.inf and gs[1] == 0.0 and np.isnan(gs[2]) and gs[3] == 0.0 and gs[4] == 0.0
+    assert np.isnan(ds[2]) and abs(ds[3] - 0.5) < 1e-6 and abs(ds[4] - 0.5) < 1e-6
+    # Planted mistakes (in the emulation, on the CPU): each must fail the bounds above.
+    bad_coef = list(coef)
+    bad_coef[3] = np.float32(bad_coef[3] * (1 + 1e-4))
+    planted = [
+        errors(fit_erfc.gelu(bad_coef, v, p=p), fit_erfc.gelu_grad(bad_coef, v, p=p)),
+        errors(fit_erfc.gelu(coef, v, p=p * 1.001), fit_erfc.gelu_grad(coef, v, p=p * 1.001)),
+        errors(gelu, (np.float32(0.5) - (grad - np.float32(0.5))).astype(np.float32)),
+        errors(np.maximum(v, 0) - (gelu - np.maximum(v, 0)), grad),
+    ]
+    for k, (ga, da, gt) in enumerate(planted):
+        assert ga > 1e-6 or da > 2e-6 or gt > 1e-4, f"planted mistake {k} passed"
+
+
+def _gfx950_disassembly(lib_path, tmp_path):
+    """Disassemble every gfx950 code object bundled in a library built here (its .hip_fatbin
+    section holds one clang offload bundle per translation unit)."""
+    import os
+    import subprocess
+    tools = "/opt/rocm/llvm/bin"
+    need = [os.path.join(tools, t) for t in ("llvm-objcopy", "clang-offload-bundler",
+                                             "llvm-objdump")]
+    if not all(os.path.exists(t) for t in need):
+        pytest.skip("ROCm LLVM tools not installed")
+    fat = tmp_path / "fatbin.bin"
+    subprocess.run([need[0], f"--dump-section=.hip_fatbin={fat}", lib_path, os.devnull],
+                   check=True, capture_output=True)
+    data = fat.read_bytes()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    starts = []
+    at = data.find(magic)
+    while at >= 0:
+        starts.append(at)
+        at = data.find(magic, at + 1)
+    text = []
+    for n, a in enumerate(starts):
+        b = starts[n + 1] if n + 1 < len(starts) else len(data)
+        bundle, code = tmp_path / f"b{n}.bin", tmp_path / f"b{n}.co"
+        bundle.write_bytes(data[a:b])
+        r = subprocess.run([need[1], "--unbundle", "--type=o",
+                            "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={bundle}",
+                            f"--output={code}"], capture_output=True)
+        if r.returncode != 0 or not code.exists() or code.stat().st_size == 0:
+            continue
+        text.append(subprocess.run([need[2], "-d", "--mcpu=gfx950", str(code)], check=True,
+                                   capture_output=True, text=True).stdout)
+    assert text, "no gfx950 code object found"
+    return text
+
+
+def _vgprs(operand):
+    """VGPR numbers an operand names (v7, |v7|, -v7, v[4:7]); empty for anything else."""
+    import re
+    m = re.fullmatch(r"[-|]*v(\d+)\|?", operand) or re.fullmatch(r"[-|]*v\[(\d+):(\d+)\]\|?",
+                                                                 operand)
+    if not m:
+        return set()
+    lo = int(m.group(1))
+    hi = int(m.group(2)) if m.lastindex == 2 else lo
+    return set(range(lo, hi + 1))
+
+
+def test_no_valu_reads_a_transcendental_result_without_a_wait_state(tmp_path):
+    """gfx950 needs one wait state between a transcendental instruction (v_exp, v_rcp, v_rsq,
+    ...) and a non-transcendental VALU instruction that reads its result.  The compiler inserts it
+    (an s_nop or any other instruction) for code it generates, but not in front of inline
+    assembly; the exact-GELU kernels use one inline v_mul_legacy_f32, so a source change that
+    hands it a v_rcp / v_exp result would read a stale register on the GPU.  Scan the built
+    library's gfx950 code for any such back-to-back pair."""
+    import re
+    trans = re.compile(r"v_(exp|log|rcp|rsq|sqrt|sin|cos)_")
+    bad = []
+    for text in _gfx950_disassembly(capi.LIB_PATH, tmp_path):
+        prev_dst = None  # VGPRs written by the previous instruction if it was transcendental
+        for line in text.splitlines():
+            m = re.match(r"\s+([a-z_0-9]+)(?:\s+(.*?))?\s*(//.*)?$", line)
+            if not m or line.strip().endswith(">:"):
+                continue
+            op, args = m.group(1), (m.group(2) or "")
+            ops = [a.strip() for a in args.split(",")] if args else []
+            if prev_dst and op.startswith("v_") and not trans.match(op):
+                if any(prev_dst & _vgprs(a) for a in ops[1:]):
+                    bad.append(line.strip())
+            prev_dst = _vgprs(ops[0]) if trans.match(op) and ops else None
+    assert not bad, f"{len(bad)} reads of a transcendental result with no wait state: {bad[:5]}"
 
 
 def test_c_abi_rejects_bad_arguments_without_a_device():
