@@ -77,6 +77,26 @@ def gelu_grad(coef, v, p=P):
     return (f32(0.5) + np.copysign(y, v)).astype(f32)
 
 
+K_U = np.sqrt(np.log2(np.e) / 2)  # kGeluU: u = v sqrt(log2(e) / 2), exp(-v^2 / 2) = 2^(-u^2)
+
+
+def gelu_grad_scaled(coef, v, p=P):
+    """fp32 emulation of gelu_erf_grad2_sign() on u = fp32(K_U v): the derivative it implies,
+    (1 + s) / 2 with s = copysign(1 - e (t 2F - (2 / (sqrt(2 pi) K_U)) |u|), u)."""
+    f32 = np.float32
+    u = (f32(K_U) * v.astype(f32)).astype(f32)
+    e = np.exp2(-(u * u).astype(f32)).astype(f32)
+    a = f32(p / np.sqrt(2) / K_U)
+    t = (f32(1) / _fma32(np.full_like(u, a), np.abs(u), f32(1))).astype(f32)
+    acc = np.full_like(t, f32(2) * coef[-1])
+    for ci in coef[-2::-1]:
+        acc = _fma32(acc, t, f32(2) * ci)
+    k2 = f32(2 / np.sqrt(2 * np.pi) / K_U)
+    w2 = _fma32(np.full_like(u, -k2), np.abs(u), (t * acc).astype(f32))
+    sgn = np.copysign(_fma32(-e, w2, f32(1)), u)
+    return ((f32(1) + sgn) * f32(0.5)).astype(f32)
+
+
 if __name__ == "__main__":
     coef, rel = fit()
     print("p =", P, "degree =", DEGREE, "fit max relative error %.3g" % rel)
@@ -92,3 +112,5 @@ if __name__ == "__main__":
     print("GELU max abs error %.3g, max relative error %.3g (|GELU| > 1e-30)"
           % (np.abs(g - gref).max(), (np.abs(g - gref)[big] / np.abs(gref[big])).max()))
     print("derivative max abs error %.3g" % np.abs(d - dref).max())
+    d2 = gelu_grad_scaled(coef, v)
+    print("derivative (scaled input) max abs error %.3g" % np.abs(d2 - dref).max())

@@ -259,7 +259,10 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   };
 
   // The row being processed, widened once: xhat and dy in fp32 (g = dy * gamma is formed where
-  // it is used rather than kept: 16 fewer VGPRs for a lane with 16 columns).
+  // it is used rather than kept: 16 fewer VGPRs for a lane with 16 columns).  With the exact
+  // GELU, dd holds twice the gradient at the LayerNorm output; kInvD takes the factor out once
+  // per row (rstd and the row-sum coefficients) and once per block (the column partials), exactly.
+  constexpr float kInvD = GELU == 1 ? 0.5f : 1.0f;
   float xh[VPL][VEC], dd[VPL][VEC];
   P rv[VPL];
   float rs = 0.0f;
@@ -279,7 +282,14 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       for (int e = 0; e < VEC; ++e) {
         xh[i][e] = (to_f32(xn[slot][i].v[e]) - mu) * rs;
         dd[i][e] = to_f32(dn[slot][i].v[e]);
-        if constexpr (GELU == 1) dd[i][e] *= gelu_erf_grad(fmaf(xh[i][e], gam(i, e), bet(i, e)));
+        if constexpr (GELU == 1) {
+          // The GELU input comes scaled by sqrt(log2(e) / 2) (gamma and beta scaled once, out of
+          // the loop, when they sit in registers) and dd becomes 2 dy GELU'(a) in one FMA.
+          const float u = PARAMS_IN_LDS
+                              ? kGeluU * fmaf(xh[i][e], gam(i, e), bet(i, e))
+                              : fmaf(xh[i][e], kGeluU * gam(i, e), kGeluU * bet(i, e));
+          dd[i][e] = fmaf(dd[i][e], gelu_erf_grad2_sign(u), dd[i][e]);
+        }
         if constexpr (GELU == 2) dd[i][e] *= gelu_tanh_grad(fmaf(xh[i][e], gam(i, e), bet(i, e)));
       }
       if constexpr (DRES) rv[i] = rn[slot][i];
@@ -340,15 +350,16 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       s2 = combine_partials<SumOp>(slot[1], rg * wpr, wpr, lane, 0.0f);
     }
     // dx = rstd (g - sum(g)/N - xhat sum(g xhat)/N) = rstd g + cb + cx xhat.
-    const float cb = p.rms ? 0.0f : -rs * (s1 * inv_n);
-    const float cx = -rs * (s2 * inv_n);
+    const float rsd = rs * kInvD;
+    const float cb = p.rms ? 0.0f : -rsd * (s1 * inv_n);
+    const float cx = -rsd * (s2 * inv_n);
     P o[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float dxv = KEEP_G ? fmaf(rs, gd[i][e], fmaf(cx, xh[i][e], cb))
-                           : fmaf(dd[i][e], rs * gam(i, e), fmaf(cx, xh[i][e], cb));
+        float dxv = KEEP_G ? fmaf(rsd, gd[i][e], fmaf(cx, xh[i][e], cb))
+                           : fmaf(dd[i][e], rsd * gam(i, e), fmaf(cx, xh[i][e], cb));
         if constexpr (DRES) dxv += to_f32(rv[i].v[e]);
         o[i].v[e] = from_f32<T>(dxv);
         acc_g[i][e] = fmaf(dd[i][e], xh[i][e], acc_g[i][e]);
@@ -376,7 +387,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       const int v = t + i * tpr;
       float vals[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) vals[e] = a == 0 ? acc_g[i][e] : acc_b[i][e];
+      for (int e = 0; e < VEC; ++e) vals[e] = (a == 0 ? acc_g[i][e] : acc_b[i][e]) * kInvD;
       if (rgs > 1) {
         __syncthreads();
 #pragma unroll

@@ -254,16 +254,20 @@ __device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_t
 struct ErfcTerms {
   float t, e, f;  // t, exp(-v^2 / 2), F(t)
 };
-__device__ __forceinline__ ErfcTerms erfc_terms(float v) {
+// F(t) times S (1 or 2: the scaled coefficients are exact).
+template <int S> __device__ __forceinline__ float erfc_poly(float t) {
   constexpr float kF[8] = {9.873314202e-02f, 9.872655571e-02f, 9.295467287e-02f,
                            7.733605057e-02f, 8.147227019e-02f, -7.275486365e-03f,
                            1.006051227e-01f, -4.255273566e-02f};
+  float f = S * kF[7];
+#pragma unroll
+  for (int k = 6; k >= 0; --k) f = fmaf(f, t, S * kF[k]);
+  return f;
+}
+__device__ __forceinline__ ErfcTerms erfc_terms(float v) {
   const float e = exp2_fast((-0.5f * kLog2e * v) * v);
   const float t = __builtin_amdgcn_rcpf(fmaf(0.35f * 0.70710678118654752440f, fabsf(v), 1.0f));
-  float f = kF[7];
-#pragma unroll
-  for (int k = 6; k >= 0; --k) f = fmaf(f, t, kF[k]);
-  return {t, e, f};
+  return {t, e, erfc_poly<1>(t)};
 }
 // |a| * b with 0 * anything = 0 (v_mul_legacy_f32): |v| (t e) stays 0 at v = +-inf, where
 // t e = 0.  Neither operand may be the direct result of a transcendental instruction (v_rcp,
@@ -284,6 +288,20 @@ __device__ __forceinline__ float gelu_erf_grad(float v) {
   const ErfcTerms k = erfc_terms(v);
   const float w = fmaf(-kInvSqrt2Pi, fabsf(v), k.t * k.f);
   return 0.5f + __builtin_copysignf(fmaf(-k.e, w, 0.5f), v);
+}
+// The same derivative for a caller that forms u = v sqrt(log2(e) / 2) directly from its affine
+// (scaled gamma and beta), so that exp(-v^2 / 2) = 2^(-u^2) takes one multiply: returns
+// s = sign(v) (1 - 2 e w), with 2 GELU'(v) = 1 + s -- the caller's dy 2 GELU'(v) is then
+// fma(dy, s, dy), and it takes the exact factor 2 out once per row.  The doubled F and w cost
+// nothing (the coefficients are scaled at compile time).
+constexpr float kGeluU = 0.84932180028801904272f;  // sqrt(log2(e) / 2)
+__device__ __forceinline__ float gelu_erf_grad2_sign(float u) {
+  constexpr float kA = static_cast<float>(0.35 * 0.70710678118654752440 / 0.84932180028801904272);
+  constexpr float kK2 = static_cast<float>(2.0 * 0.39894228040143267794 / 0.84932180028801904272);
+  const float e = exp2_fast(-(u * u));
+  const float t = __builtin_amdgcn_rcpf(fmaf(kA, fabsf(u), 1.0f));
+  const float w2 = fmaf(-kK2, fabsf(u), t * erfc_poly<2>(t));
+  return __builtin_copysignf(fmaf(-e, w2, 1.0f), u);
 }
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const GeluTanhTerms t = gelu_tanh_terms(v);

@@ -71,10 +71,11 @@ def test_erfc_terms_constants_in_the_device_header():
     from scipy.special import erfc
     csrc = os.path.join(os.path.dirname(os.path.dirname(fl.__file__)), "csrc")
     src = open(os.path.join(csrc, "fln_device.h")).read()
+    poly = src[src.index("float erfc_poly(float t)"):]
+    coef = [np.float32(float(c)) for c in
+            re.findall(r"[-+]?\d\.\d+e[-+]\d+", poly[poly.index("kF["):poly.index("};")])]
     body = src[src.index("ErfcTerms erfc_terms(float v)"):]
     body = body[:body.index("return {")]
-    coef = [np.float32(float(c)) for c in
-            re.findall(r"[-+]?\d\.\d+e[-+]\d+", body[body.index("kF["):body.index("};")])]
     p = float(re.search(r"fmaf\(([\d.]+)f \* 0\.7071", body).group(1))
     assert len(coef) >= 6 and 0.2 < p < 0.6
     sys.path.insert(0, csrc)
@@ -97,6 +98,16 @@ def test_erfc_terms_constants_in_the_device_header():
     grad = fit_erfc.gelu_grad(coef, v, p=p)
     g_abs, d_abs, g_tail = errors(gelu, grad)
     assert g_abs <= 1e-6 and d_abs <= 2e-6 and g_tail <= 1e-4, (g_abs, d_abs, g_tail)
+    # The register backward's variant on the scaled input u = v sqrt(log2(e) / 2): same p, and
+    # sqrt(log2(e) / 2) as the scale.
+    scaled = src[src.index("float gelu_erf_grad2_sign(float u)"):]
+    scaled = scaled[:scaled.index("return ")]
+    assert float(re.search(r"kA = static_cast<float>\(([\d.]+) \* 0\.7071", scaled).group(1)) == p
+    k_u = float(re.search(r"kGeluU = ([\d.]+)f", src).group(1))
+    assert abs(k_u - np.sqrt(np.log2(np.e) / 2)) < 1e-9
+    assert float(re.search(r"/ ([\d.]+)\);\n  constexpr float kK2", scaled).group(1)) == k_u
+    grad_u = fit_erfc.gelu_grad_scaled(coef, v, p=p)
+    assert np.abs(grad_u - d_ref).max() <= 2e-6
     special = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0], np.float32)
     with np.errstate(invalid="ignore", over="ignore"):
         gs = fit_erfc.gelu(coef, special, p=p)
