@@ -31,7 +31,7 @@ ARCH = os.environ.get("FLN_OFFLOAD_ARCH", "gfx950")
 KERNEL_SOURCES = ["fln_forward.hip", "fln_forward_f32.hip", "fln_forward_bf16.hip",
                   "fln_forward_f16.hip", "fln_forward_f64.hip", "fln_backward.hip", "fln_host.hip"]
 BINDING_SOURCE = "fln_torch.cpp"
-HEADERS = ["fln_device.h", "fln_internal.h", "fln_forward_impl.h"]
+HEADERS = ["fln_device.h", "fln_internal.h", "fln_forward_impl.h", "fln_gelu_table.h"]
 
 # Packed-fp32 VALU ops are disabled for device code (the host pass warns that it does not know
 # the feature; that warning is harmless).

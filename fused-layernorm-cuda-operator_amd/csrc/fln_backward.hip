@@ -147,6 +147,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
   __shared__ float red[2][2][MAXW + 16];
   __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
+  __shared__ float4 gelu_tab[GELU == 1 ? kGeluTabN : 1];  // exact GELU: the GELU' table
   using P = Pack<T, VEC>;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -283,12 +284,13 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
         xh[i][e] = (to_f32(xn[slot][i].v[e]) - mu) * rs;
         dd[i][e] = to_f32(dn[slot][i].v[e]);
         if constexpr (GELU == 1) {
-          // The GELU input comes scaled by sqrt(log2(e) / 2) (gamma and beta scaled once, out of
-          // the loop, when they sit in registers) and dd becomes 2 dy GELU'(a) in one FMA.
+          // GELU' from the block's table: the GELU input comes as table coordinates u = a / h
+          // (gamma and beta scaled once, out of the loop, when they sit in registers), and dd
+          // becomes 2 dy GELU'(a) in one FMA.
           const float u = PARAMS_IN_LDS
-                              ? kGeluU * fmaf(xh[i][e], gam(i, e), bet(i, e))
-                              : fmaf(xh[i][e], kGeluU * gam(i, e), kGeluU * bet(i, e));
-          dd[i][e] = fmaf(dd[i][e], gelu_erf_grad2_sign(u), dd[i][e]);
+                              ? kGeluTabInvH * fmaf(xh[i][e], gam(i, e), bet(i, e))
+                              : fmaf(xh[i][e], kGeluTabInvH * gam(i, e), kGeluTabInvH * bet(i, e));
+          dd[i][e] = fmaf(dd[i][e], gelu_erf_grad2_sign_tab(gelu_tab, u), dd[i][e]);
         }
         if constexpr (GELU == 2) dd[i][e] *= gelu_tanh_grad(fmaf(xh[i][e], gam(i, e), bet(i, e)));
       }
@@ -302,6 +304,12 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // compiler's wait there covers only the slot being consumed: PD rows stay in flight through
   // the row reduction.  (Without the padding the merged wait drains the ring on every step.)
   const rsrc_t none = make_rsrc(nullptr, 0);
+  // Exact GELU: every thread loads one entry of the GELU' table (4 KiB, L2-resident after the
+  // first block), ahead of the rows.
+  float4 tab_entry;
+  if constexpr (GELU == 1)
+    tab_entry = reinterpret_cast<const float4*>(kGeluTabData)[threadIdx.x % kGeluTabN];
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int k = 0; k < PD; ++k) {
     load_row(k, k);
@@ -309,6 +317,12 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     for (int i = 0; i < VPL; ++i)  // distinct, non-adjacent: none merged away
       buf_store<P, FLN_BWD_STORE_POL>(zero_pack<T, VEC>(), none, static_cast<uint32_t>(4 * i));
     asm volatile("" ::: "memory");  // keeps the slots in issue order
+  }
+  // The GELU' table's LDS copy: its load was issued ahead of the rows, so this waits for it
+  // alone.
+  if constexpr (GELU == 1) {
+    if (threadIdx.x < kGeluTabN) gelu_tab[threadIdx.x] = tab_entry;
+    __syncthreads();
   }
   // Whole rounds of PD rows: a step past the block's last row reads zeros (its column sums add
   // nothing) and stores nothing.  An early exit from the unrolled round would make the compiler

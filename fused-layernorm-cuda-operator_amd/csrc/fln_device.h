@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fln_gelu_table.h"
+
 namespace fln {
 
 constexpr int kWave = 64;
@@ -302,6 +304,26 @@ __device__ __forceinline__ float gelu_erf_grad2_sign(float u) {
   const float t = __builtin_amdgcn_rcpf(fmaf(kA, fabsf(u), 1.0f));
   const float w2 = fmaf(-kK2, fabsf(u), t * erfc_poly<2>(t));
   return __builtin_copysignf(fmaf(-e, w2, 1.0f), u);
+}
+// The exact-GELU derivative from a table, for the backward's register kernel (where the
+// polynomial above is most of the per-element VALU work).  T(v) = 2 GELU'(v) - 1 =
+// erf(v / sqrt 2) + v sqrt(2 / pi) exp(-v^2 / 2) is odd, smooth, and within 1e-7 of its limit
+// +-1 past |v| = 6.  Interval k of kGeluTabData (fln_gelu_table.h, generated by fit_erfc.py)
+// covers |v| in [k h, (k + 1) h), h = 6 / 255, and holds the quadratic through T at its ends and
+// middle, c0 + c1 f + c2 f^2 with f in [0, 1) the position in the interval; the last interval
+// (|v| >= 6) is the constant 1.  Built in float64 and rounded to fp32, the lookup is within
+// 2.1e-7 of GELU' (the polynomial: 5.6e-7).  A lookup is one multiply-add (the caller forms
+// u = v / h from gamma / h and beta / h), fract, min, convert, shift, one ds_read_b128 from the
+// block's LDS copy, two FMAs and a copysign: no transcendental instruction.
+constexpr float kGeluTabInvH = (kGeluTabN - 1) / kGeluTabMax;  // 42.5: u = v / h
+
+// sign(v) T(|v|) for u = v / h: 2 GELU'(v) = 1 + the result (NaN propagates through fract).
+__device__ __forceinline__ float gelu_erf_grad2_sign_tab(const float4* tab, float u) {
+  const float au = fabsf(u);
+  const float f = __builtin_amdgcn_fractf(au);
+  const uint32_t k = static_cast<uint32_t>(fminf(au, static_cast<float>(kGeluTabN - 1)));
+  const float4 c = tab[k];
+  return __builtin_copysignf(fmaf(fmaf(c.z, f, c.y), f, c.x), u);
 }
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const GeluTanhTerms t = gelu_tanh_terms(v);

@@ -114,6 +114,23 @@ def test_erfc_terms_constants_in_the_device_header():
         ds = fit_erfc.gelu_grad(coef, special, p=p)
     assert gs[0] == np.inf and gs[1] == 0.0 and np.isnan(gs[2]) and gs[3] == 0.0 and gs[4] == 0.0
     assert np.isnan(ds[2]) and abs(ds[3] - 0.5) < 1e-6 and abs(ds[4] - 0.5) < 1e-6
+    # The register backward's GELU' table (fln_gelu_table.h): exactly the fp32 rounding of the
+    # float64 quadratics fit_erfc.gelu_table() builds, and its lookup within 1e-6 of GELU'.
+    hdr = open(os.path.join(csrc, "fln_gelu_table.h")).read()
+    n_tab = int(re.search(r"kGeluTabN = (\d+);", hdr).group(1))
+    v_max = float(re.search(r"kGeluTabMax = ([\d.]+)f;", hdr).group(1))
+    assert (n_tab, v_max) == (fit_erfc.TAB_N, fit_erfc.TAB_MAX)
+    body_t = hdr[hdr.index("kGeluTabData"):]
+    data = np.array([np.float32(float(c)) for c in re.findall(
+        r"([-+]?\d+\.\d+(?:e[-+]\d+)?)f", body_t[body_t.index("{"):])], np.float32)
+    tab = fit_erfc.gelu_table()
+    assert data.shape == (4 * n_tab,) and np.array_equal(data.reshape(n_tab, 4)[:, :3], tab)
+    assert not data.reshape(n_tab, 4)[:, 3].any()
+    grad_t = fit_erfc.gelu_grad_table(tab, v)
+    assert np.abs(grad_t - d_ref).max() <= 1e-6
+    with np.errstate(invalid="ignore", over="ignore"):
+        ts = fit_erfc.gelu_grad_table(tab, special)
+    assert np.isnan(ts[2]) and abs(ts[3] - 0.5) < 1e-6 and abs(ts[4] - 0.5) < 1e-6
     # Planted mistakes (in the emulation, on the CPU): each must fail the bounds above.
     bad_coef = list(coef)
     bad_coef[3] = np.float32(bad_coef[3] * (1 + 1e-4))
@@ -125,6 +142,13 @@ def test_erfc_terms_constants_in_the_device_header():
     ]
     for k, (ga, da, gt) in enumerate(planted):
         assert ga > 1e-6 or da > 2e-6 or gt > 1e-4, f"planted mistake {k} passed"
+    # ... and the table: a swapped pair of coefficients, an interval off by one, a wrong h.
+    swapped = tab.copy()
+    swapped[:, [1, 2]] = swapped[:, [2, 1]]
+    shifted = np.roll(tab, 1, axis=0)
+    for bad_grad in (fit_erfc.gelu_grad_table(swapped, v), fit_erfc.gelu_grad_table(shifted, v),
+                     fit_erfc.gelu_grad_table(tab, v, vmax=v_max * 1.01)):
+        assert np.abs(bad_grad - d_ref).max() > 1e-6
 
 
 def _gfx950_disassembly(lib_path, tmp_path):
