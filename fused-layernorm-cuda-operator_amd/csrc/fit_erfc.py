@@ -81,17 +81,23 @@ TAB_N = 256      # kGeluTabN
 TAB_MAX = 6.0    # kGeluTabMax
 
 
-def gelu_table(n=TAB_N, vmax=TAB_MAX):
-    """The GELU'-table of fln_gelu_table.h: for interval k of |v| in [k h, (k + 1) h), h = vmax /
-    (n - 1), the quadratic c0 + c1 f + c2 f^2 (f in [0, 1)) through T(v) = 2 GELU'(v) - 1 =
-    erf(v / sqrt 2) + v sqrt(2 / pi) exp(-v^2 / 2) at the interval's ends and middle, computed in
-    float64 and rounded to fp32; the last interval is the constant 1.  Returns [n, 3] fp32."""
+def gelu_table(kind="erf", n=TAB_N, vmax=TAB_MAX):
+    """A GELU'-table of fln_gelu_table.h: for interval k of |v| in [k h, (k + 1) h), h = vmax /
+    (n - 1), the quadratic c0 + c1 f + c2 f^2 (f in [0, 1)) through T(v) = 2 GELU'(v) - 1 at the
+    interval's ends and middle, computed in float64 and rounded to fp32; the last interval is the
+    constant 1.  kind "erf": T = erf(v / sqrt 2) + v sqrt(2 / pi) exp(-v^2 / 2); kind "tanh" (the
+    tanh form, u = sqrt(2 / pi) (v + 0.044715 v^3)): T = tanh(u) + v u'(v) sech^2(u).
+    Returns [n, 3] fp32."""
     from scipy.special import erf
     h = vmax / (n - 1)
     k = np.arange(n, dtype=np.float64)
 
     def t(v):
-        return erf(v / np.sqrt(2)) + v * np.sqrt(2 / np.pi) * np.exp(-v * v / 2)
+        if kind == "erf":
+            return erf(v / np.sqrt(2)) + v * np.sqrt(2 / np.pi) * np.exp(-v * v / 2)
+        k0, k1 = np.sqrt(2 / np.pi), 0.044715
+        u = k0 * (v + k1 * v ** 3)
+        return np.tanh(u) + v * k0 * (1 + 3 * k1 * v * v) / np.cosh(u) ** 2
     a, m, b = t(k * h), t((k + 0.5) * h), t((k + 1) * h)
     c = np.stack([a, 4 * m - 3 * a - b, 2 * (a + b) - 4 * m], axis=1)
     c[-1] = (1.0, 0.0, 0.0)
@@ -114,45 +120,30 @@ def gelu_grad_table(tab, v, vmax=TAB_MAX):
     return ((f32(1) + np.copysign(r, u)) * f32(0.5)).astype(f32)
 
 
-def table_header(tab, vmax=TAB_MAX):
-    """C++ source of fln_gelu_table.h."""
-    n = tab.shape[0]
-    rows = ",\n".join("    %.9ef, %.9ef, %.9ef, 0.0f" % tuple(map(float, r)) for r in tab)
+def table_header(tabs, vmax=TAB_MAX):
+    """C++ source of fln_gelu_table.h from {"erf": table, "tanh": table}."""
+    n = tabs["erf"].shape[0]
+
+    def body(tab):
+        return ",\n".join("    %.9ef, %.9ef, %.9ef, 0.0f" % tuple(map(float, r)) for r in tab)
     return ("// fln_gelu_table.h -- generated by `python3 fit_erfc.py table` (beside this file); do not\n"
             "// edit.  Interval k of |v| in [k h, (k + 1) h), h = %g / %d: the coefficients c0, c1, c2 (and\n"
             "// a zero pad) of the quadratic through T(v) = 2 GELU'(v) - 1 at the interval's ends and\n"
-            "// middle, in float64 rounded to fp32; the last interval is the constant 1.\n"
+            "// middle, in float64 rounded to fp32; the last interval is the constant 1.  kGeluTabData:\n"
+            "// the erf form, T = erf(v / sqrt 2) + v sqrt(2 / pi) exp(-v^2 / 2); kGeluTanhTabData: the\n"
+            "// tanh form, T = tanh(u) + v u'(v) sech^2(u), u = sqrt(2 / pi) (v + 0.044715 v^3).\n"
             "#pragma once\n\nnamespace fln {\n\n"
             "constexpr int kGeluTabN = %d;\n"
             "constexpr float kGeluTabMax = %.1ff;\n\n"
             "__device__ __attribute__((aligned(16))) const float kGeluTabData[kGeluTabN * 4] = {\n%s};\n\n"
-            "}  // namespace fln\n" % (vmax, n - 1, n, vmax, rows))
-
-
-K_U = np.sqrt(np.log2(np.e) / 2)  # kGeluU: u = v sqrt(log2(e) / 2), exp(-v^2 / 2) = 2^(-u^2)
-
-
-def gelu_grad_scaled(coef, v, p=P):
-    """fp32 emulation of gelu_erf_grad2_sign() on u = fp32(K_U v): the derivative it implies,
-    (1 + s) / 2 with s = copysign(1 - e (t 2F - (2 / (sqrt(2 pi) K_U)) |u|), u)."""
-    f32 = np.float32
-    u = (f32(K_U) * v.astype(f32)).astype(f32)
-    e = np.exp2(-(u * u).astype(f32)).astype(f32)
-    a = f32(p / np.sqrt(2) / K_U)
-    t = (f32(1) / _fma32(np.full_like(u, a), np.abs(u), f32(1))).astype(f32)
-    acc = np.full_like(t, f32(2) * coef[-1])
-    for ci in coef[-2::-1]:
-        acc = _fma32(acc, t, f32(2) * ci)
-    k2 = f32(2 / np.sqrt(2 * np.pi) / K_U)
-    w2 = _fma32(np.full_like(u, -k2), np.abs(u), (t * acc).astype(f32))
-    sgn = np.copysign(_fma32(-e, w2, f32(1)), u)
-    return ((f32(1) + sgn) * f32(0.5)).astype(f32)
+            "__device__ __attribute__((aligned(16))) const float kGeluTanhTabData[kGeluTabN * 4] = {\n%s};\n\n"
+            "}  // namespace fln\n" % (vmax, n - 1, n, vmax, body(tabs["erf"]), body(tabs["tanh"])))
 
 
 if __name__ == "__main__":
     import sys
     if sys.argv[1:] == ["table"]:
-        sys.stdout.write(table_header(gelu_table()))
+        sys.stdout.write(table_header({"erf": gelu_table("erf"), "tanh": gelu_table("tanh")}))
         sys.exit(0)
     coef, rel = fit()
     print("p =", P, "degree =", DEGREE, "fit max relative error %.3g" % rel)
@@ -168,7 +159,5 @@ if __name__ == "__main__":
     print("GELU max abs error %.3g, max relative error %.3g (|GELU| > 1e-30)"
           % (np.abs(g - gref).max(), (np.abs(g - gref)[big] / np.abs(gref[big])).max()))
     print("derivative max abs error %.3g" % np.abs(d - dref).max())
-    d2 = gelu_grad_scaled(coef, v)
-    print("derivative (scaled input) max abs error %.3g" % np.abs(d2 - dref).max())
     d3 = gelu_grad_table(gelu_table(), v)
     print("derivative (table) max abs error %.3g" % np.abs(d3 - dref).max())

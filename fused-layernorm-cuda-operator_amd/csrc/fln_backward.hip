@@ -147,7 +147,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
   __shared__ float red[2][2][MAXW + 16];
   __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
-  __shared__ float4 gelu_tab[GELU == 1 ? kGeluTabN : 1];  // exact GELU: the GELU' table
+  __shared__ float4 gelu_tab[GELU != 0 ? kGeluTabN : 1];  // GELU epilogue: the GELU' table
   using P = Pack<T, VEC>;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -260,10 +260,10 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   };
 
   // The row being processed, widened once: xhat and dy in fp32 (g = dy * gamma is formed where
-  // it is used rather than kept: 16 fewer VGPRs for a lane with 16 columns).  With the exact
-  // GELU, dd holds twice the gradient at the LayerNorm output; kInvD takes the factor out once
+  // it is used rather than kept: 16 fewer VGPRs for a lane with 16 columns).  With a GELU
+  // epilogue, dd holds twice the gradient at the LayerNorm output; kInvD takes the factor out once
   // per row (rstd and the row-sum coefficients) and once per block (the column partials), exactly.
-  constexpr float kInvD = GELU == 1 ? 0.5f : 1.0f;
+  constexpr float kInvD = GELU != 0 ? 0.5f : 1.0f;
   float xh[VPL][VEC], dd[VPL][VEC];
   P rv[VPL];
   float rs = 0.0f;
@@ -283,16 +283,15 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
       for (int e = 0; e < VEC; ++e) {
         xh[i][e] = (to_f32(xn[slot][i].v[e]) - mu) * rs;
         dd[i][e] = to_f32(dn[slot][i].v[e]);
-        if constexpr (GELU == 1) {
+        if constexpr (GELU != 0) {
           // GELU' from the block's table: the GELU input comes as table coordinates u = a / h
           // (gamma and beta scaled once, out of the loop, when they sit in registers), and dd
           // becomes 2 dy GELU'(a) in one FMA.
           const float u = PARAMS_IN_LDS
                               ? kGeluTabInvH * fmaf(xh[i][e], gam(i, e), bet(i, e))
                               : fmaf(xh[i][e], kGeluTabInvH * gam(i, e), kGeluTabInvH * bet(i, e));
-          dd[i][e] = fmaf(dd[i][e], gelu_erf_grad2_sign_tab(gelu_tab, u), dd[i][e]);
+          dd[i][e] = fmaf(dd[i][e], gelu_grad2_sign_tab(gelu_tab, u), dd[i][e]);
         }
-        if constexpr (GELU == 2) dd[i][e] *= gelu_tanh_grad(fmaf(xh[i][e], gam(i, e), bet(i, e)));
       }
       if constexpr (DRES) rv[i] = rn[slot][i];
     }
@@ -304,11 +303,12 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // compiler's wait there covers only the slot being consumed: PD rows stay in flight through
   // the row reduction.  (Without the padding the merged wait drains the ring on every step.)
   const rsrc_t none = make_rsrc(nullptr, 0);
-  // Exact GELU: every thread loads one entry of the GELU' table (4 KiB, L2-resident after the
-  // first block), ahead of the rows.
+  // GELU epilogue: every thread loads one entry of the GELU' table of its form (4 KiB,
+  // L2-resident after the first block), ahead of the rows.
   float4 tab_entry;
-  if constexpr (GELU == 1)
-    tab_entry = reinterpret_cast<const float4*>(kGeluTabData)[threadIdx.x % kGeluTabN];
+  if constexpr (GELU != 0)
+    tab_entry = reinterpret_cast<const float4*>(GELU == 1 ? kGeluTabData
+                                                          : kGeluTanhTabData)[threadIdx.x % kGeluTabN];
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int k = 0; k < PD; ++k) {
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   }
   // The GELU' table's LDS copy: its load was issued ahead of the rows, so this waits for it
   // alone.
-  if constexpr (GELU == 1) {
+  if constexpr (GELU != 0) {
     if (threadIdx.x < kGeluTabN) gelu_tab[threadIdx.x] = tab_entry;
     __syncthreads();
   }

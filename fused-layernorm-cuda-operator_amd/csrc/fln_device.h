@@ -291,34 +291,21 @@ __device__ __forceinline__ float gelu_erf_grad(float v) {
   const float w = fmaf(-kInvSqrt2Pi, fabsf(v), k.t * k.f);
   return 0.5f + __builtin_copysignf(fmaf(-k.e, w, 0.5f), v);
 }
-// The same derivative for a caller that forms u = v sqrt(log2(e) / 2) directly from its affine
-// (scaled gamma and beta), so that exp(-v^2 / 2) = 2^(-u^2) takes one multiply: returns
-// s = sign(v) (1 - 2 e w), with 2 GELU'(v) = 1 + s -- the caller's dy 2 GELU'(v) is then
-// fma(dy, s, dy), and it takes the exact factor 2 out once per row.  The doubled F and w cost
-// nothing (the coefficients are scaled at compile time).
-constexpr float kGeluU = 0.84932180028801904272f;  // sqrt(log2(e) / 2)
-__device__ __forceinline__ float gelu_erf_grad2_sign(float u) {
-  constexpr float kA = static_cast<float>(0.35 * 0.70710678118654752440 / 0.84932180028801904272);
-  constexpr float kK2 = static_cast<float>(2.0 * 0.39894228040143267794 / 0.84932180028801904272);
-  const float e = exp2_fast(-(u * u));
-  const float t = __builtin_amdgcn_rcpf(fmaf(kA, fabsf(u), 1.0f));
-  const float w2 = fmaf(-kK2, fabsf(u), t * erfc_poly<2>(t));
-  return __builtin_copysignf(fmaf(-e, w2, 1.0f), u);
-}
-// The exact-GELU derivative from a table, for the backward's register kernel (where the
-// polynomial above is most of the per-element VALU work).  T(v) = 2 GELU'(v) - 1 =
-// erf(v / sqrt 2) + v sqrt(2 / pi) exp(-v^2 / 2) is odd, smooth, and within 1e-7 of its limit
-// +-1 past |v| = 6.  Interval k of kGeluTabData (fln_gelu_table.h, generated by fit_erfc.py)
-// covers |v| in [k h, (k + 1) h), h = 6 / 255, and holds the quadratic through T at its ends and
-// middle, c0 + c1 f + c2 f^2 with f in [0, 1) the position in the interval; the last interval
-// (|v| >= 6) is the constant 1.  Built in float64 and rounded to fp32, the lookup is within
-// 2.1e-7 of GELU' (the polynomial: 5.6e-7).  A lookup is one multiply-add (the caller forms
-// u = v / h from gamma / h and beta / h), fract, min, convert, shift, one ds_read_b128 from the
-// block's LDS copy, two FMAs and a copysign: no transcendental instruction.
+// GELU' from a table, for the backward's register kernel (where evaluating the formulas above
+// is most of the per-element VALU work).  For either form, T(v) = 2 GELU'(v) - 1 is odd, smooth,
+// and within 1e-7 of its limit +-1 past |v| = 6 (erf form: erf(v / sqrt 2) + v sqrt(2 / pi)
+// exp(-v^2 / 2); tanh form: tanh(u) + v u'(v) sech^2(u)).  Interval k of kGeluTabData /
+// kGeluTanhTabData (fln_gelu_table.h, generated by fit_erfc.py) covers |v| in [k h, (k + 1) h),
+// h = 6 / 255, and holds the quadratic through T at its ends and middle, c0 + c1 f + c2 f^2 with
+// f in [0, 1) the position in the interval; the last interval (|v| >= 6) is the constant 1.
+// Built in float64 and rounded to fp32, the lookup is within 2.1e-7 of GELU' for both forms (the
+// erf polynomial: 5.6e-7).  A lookup is one multiply-add (the caller forms u = v / h from
+// gamma / h and beta / h), fract, min, convert, shift, one ds_read_b128 from the block's LDS
+// copy, two FMAs and a copysign: no transcendental instruction.
 constexpr float kGeluTabInvH = (kGeluTabN - 1) / kGeluTabMax;  // 42.5: u = v / h
 
 // sign(v) T(|v|) for u = v / h: 2 GELU'(v) = 1 + the result (NaN propagates through fract).
-__device__ __forceinline__ float gelu_erf_grad2_sign_tab(const float4* tab, float u) {
+__device__ __forceinline__ float gelu_grad2_sign_tab(const float4* tab, float u) {
   const float au = fabsf(u);
   const float f = __builtin_amdgcn_fractf(au);
   const uint32_t k = static_cast<uint32_t>(fminf(au, static_cast<float>(kGeluTabN - 1)));

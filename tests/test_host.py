@@ -98,39 +98,36 @@ def test_erfc_terms_constants_in_the_device_header():
     grad = fit_erfc.gelu_grad(coef, v, p=p)
     g_abs, d_abs, g_tail = errors(gelu, grad)
     assert g_abs <= 1e-6 and d_abs <= 2e-6 and g_tail <= 1e-4, (g_abs, d_abs, g_tail)
-    # The register backward's variant on the scaled input u = v sqrt(log2(e) / 2): same p, and
-    # sqrt(log2(e) / 2) as the scale.
-    scaled = src[src.index("float gelu_erf_grad2_sign(float u)"):]
-    scaled = scaled[:scaled.index("return ")]
-    assert float(re.search(r"kA = static_cast<float>\(([\d.]+) \* 0\.7071", scaled).group(1)) == p
-    k_u = float(re.search(r"kGeluU = ([\d.]+)f", src).group(1))
-    assert abs(k_u - np.sqrt(np.log2(np.e) / 2)) < 1e-9
-    assert float(re.search(r"/ ([\d.]+)\);\n  constexpr float kK2", scaled).group(1)) == k_u
-    grad_u = fit_erfc.gelu_grad_scaled(coef, v, p=p)
-    assert np.abs(grad_u - d_ref).max() <= 2e-6
     special = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0], np.float32)
     with np.errstate(invalid="ignore", over="ignore"):
         gs = fit_erfc.gelu(coef, special, p=p)
         ds = fit_erfc.gelu_grad(coef, special, p=p)
     assert gs[0] == np.inf and gs[1] == 0.0 and np.isnan(gs[2]) and gs[3] == 0.0 and gs[4] == 0.0
     assert np.isnan(ds[2]) and abs(ds[3] - 0.5) < 1e-6 and abs(ds[4] - 0.5) < 1e-6
-    # The register backward's GELU' table (fln_gelu_table.h): exactly the fp32 rounding of the
-    # float64 quadratics fit_erfc.gelu_table() builds, and its lookup within 1e-6 of GELU'.
+    # The register backward's GELU' tables (fln_gelu_table.h): exactly the fp32 rounding of the
+    # float64 quadratics fit_erfc.gelu_table() builds, and their lookup within 1e-6 of GELU'
+    # (erf form: d_ref; tanh form: its derivative in float64).
     hdr = open(os.path.join(csrc, "fln_gelu_table.h")).read()
     n_tab = int(re.search(r"kGeluTabN = (\d+);", hdr).group(1))
     v_max = float(re.search(r"kGeluTabMax = ([\d.]+)f;", hdr).group(1))
     assert (n_tab, v_max) == (fit_erfc.TAB_N, fit_erfc.TAB_MAX)
-    body_t = hdr[hdr.index("kGeluTabData"):]
-    data = np.array([np.float32(float(c)) for c in re.findall(
-        r"([-+]?\d+\.\d+(?:e[-+]\d+)?)f", body_t[body_t.index("{"):])], np.float32)
-    tab = fit_erfc.gelu_table()
-    assert data.shape == (4 * n_tab,) and np.array_equal(data.reshape(n_tab, 4)[:, :3], tab)
-    assert not data.reshape(n_tab, 4)[:, 3].any()
-    grad_t = fit_erfc.gelu_grad_table(tab, v)
-    assert np.abs(grad_t - d_ref).max() <= 1e-6
-    with np.errstate(invalid="ignore", over="ignore"):
-        ts = fit_erfc.gelu_grad_table(tab, special)
-    assert np.isnan(ts[2]) and abs(ts[3] - 0.5) < 1e-6 and abs(ts[4] - 0.5) < 1e-6
+    k0, k1 = np.sqrt(2 / np.pi), 0.044715
+    u_t = k0 * (vd + k1 * vd ** 3)
+    d_tanh = 0.5 * (1 + np.tanh(u_t)) + 0.5 * vd * k0 * (1 + 3 * k1 * vd * vd) / np.cosh(u_t) ** 2
+    tables = {}
+    for kind, name, ref in (("erf", "kGeluTabData", d_ref), ("tanh", "kGeluTanhTabData", d_tanh)):
+        body_t = hdr[hdr.index(name + "["):]
+        body_t = body_t[body_t.index("{"):body_t.index("};")]
+        data = np.array([np.float32(float(c)) for c in re.findall(
+            r"([-+]?\d+\.\d+(?:e[-+]\d+)?)f", body_t)], np.float32)
+        tab = tables[kind] = fit_erfc.gelu_table(kind)
+        assert data.shape == (4 * n_tab,) and np.array_equal(data.reshape(n_tab, 4)[:, :3], tab)
+        assert not data.reshape(n_tab, 4)[:, 3].any()
+        assert np.abs(fit_erfc.gelu_grad_table(tab, v) - ref).max() <= 1e-6, kind
+        with np.errstate(invalid="ignore", over="ignore"):
+            ts = fit_erfc.gelu_grad_table(tab, special)
+        assert np.isnan(ts[2]) and abs(ts[3] - 0.5) < 1e-6 and abs(ts[4] - 0.5) < 1e-6
+    tab = tables["erf"]
     # Planted mistakes (in the emulation, on the CPU): each must fail the bounds above.
     bad_coef = list(coef)
     bad_coef[3] = np.float32(bad_coef[3] * (1 + 1e-4))
@@ -142,12 +139,14 @@ def test_erfc_terms_constants_in_the_device_header():
     ]
     for k, (ga, da, gt) in enumerate(planted):
         assert ga > 1e-6 or da > 2e-6 or gt > 1e-4, f"planted mistake {k} passed"
-    # ... and the table: a swapped pair of coefficients, an interval off by one, a wrong h.
+    # ... and the table: a swapped pair of coefficients, an interval off by one, a wrong h, the
+    # other form's table.
     swapped = tab.copy()
     swapped[:, [1, 2]] = swapped[:, [2, 1]]
     shifted = np.roll(tab, 1, axis=0)
     for bad_grad in (fit_erfc.gelu_grad_table(swapped, v), fit_erfc.gelu_grad_table(shifted, v),
-                     fit_erfc.gelu_grad_table(tab, v, vmax=v_max * 1.01)):
+                     fit_erfc.gelu_grad_table(tab, v, vmax=v_max * 1.01),
+                     fit_erfc.gelu_grad_table(tables["tanh"], v)):
         assert np.abs(bad_grad - d_ref).max() > 1e-6
 
 
