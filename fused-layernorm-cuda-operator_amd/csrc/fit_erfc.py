@@ -120,12 +120,54 @@ def gelu_grad_table(tab, v, vmax=TAB_MAX):
     return ((f32(1) + np.copysign(r, u)) * f32(0.5)).astype(f32)
 
 
+LOG_TAB_N = 256     # kGeluLogTabN
+LOG_TAB_INV_H = 16  # kGeluLogTabInvH: interval width 1 / 16, a power of two
+
+
+def gelu_log_table(n=LOG_TAB_N, inv_h=LOG_TAB_INV_H):
+    """The forward's GELU table (kGeluLogTabData): for interval k of x = |v| in [k h, (k + 1) h),
+    h = 1 / inv_h, the quadratic c0 + c1 f + c2 f^2 through L(x) = log2(Phi(-x)) - log2(inv_h) at
+    the interval's ends and middle (float64, rounded to fp32), so that 2^L = Phi(-|v|) h and
+    GELU(v) = max(v, 0) - (|v| inv_h) 2^L; the last interval (|v| >= (n - 1) h, where Phi(-|v|)
+    is far below the fp32 range) is the constant -inf.  Returns [n, 3] fp32."""
+    from scipy.special import log_ndtr
+    h = 1.0 / inv_h
+    k = np.arange(n, dtype=np.float64)
+
+    def lg(x):
+        return log_ndtr(-x) / np.log(2) - np.log2(inv_h)
+    a, m, b = lg(k * h), lg((k + 0.5) * h), lg((k + 1) * h)
+    c = np.stack([a, 4 * m - 3 * a - b, 2 * (a + b) - 4 * m], axis=1)
+    c[-1] = (-np.inf, 0.0, 0.0)
+    return c.astype(np.float32)
+
+
+def gelu_log_tab(tab, v, inv_h=LOG_TAB_INV_H):
+    """fp32 emulation of gelu_erf_tab(): uc = min(|v| inv_h, n - 1), f = fract(uc), L from
+    interval floor(uc), GELU = fma(-uc, 2^L, maximum(v, 0)) (maximum propagates NaN)."""
+    f32 = np.float32
+    n = tab.shape[0]
+    v = v.astype(f32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        au = (np.abs(v) * f32(inv_h)).astype(f32)
+        uc = np.where(np.isnan(au), f32(n - 1), np.minimum(au, f32(n - 1))).astype(f32)
+        f = (uc - np.floor(uc)).astype(f32)
+        c = tab[uc.astype(np.int64)]
+        lg = _fma32(_fma32(c[:, 2], f, c[:, 1]), f, c[:, 0])
+        r = np.exp2(lg).astype(f32)
+        m = np.where(np.isnan(v), v, np.maximum(v, f32(0))).astype(f32)
+        return _fma32(-uc, r, m)
+
+
 def table_header(tabs, vmax=TAB_MAX):
     """C++ source of fln_gelu_table.h from {"erf": table, "tanh": table}."""
     n = tabs["erf"].shape[0]
 
+    def lit(x):
+        return "-__builtin_huge_valf()" if x == -np.inf else "%.9ef" % x
+
     def body(tab):
-        return ",\n".join("    %.9ef, %.9ef, %.9ef, 0.0f" % tuple(map(float, r)) for r in tab)
+        return ",\n".join("    %s, %s, %s, 0.0f" % tuple(lit(float(x)) for x in r) for r in tab)
     return ("// fln_gelu_table.h -- generated by `python3 fit_erfc.py table` (beside this file); do not\n"
             "// edit.  Interval k of |v| in [k h, (k + 1) h), h = %g / %d: the coefficients c0, c1, c2 (and\n"
             "// a zero pad) of the quadratic through T(v) = 2 GELU'(v) - 1 at the interval's ends and\n"
@@ -137,13 +179,22 @@ def table_header(tabs, vmax=TAB_MAX):
             "constexpr float kGeluTabMax = %.1ff;\n\n"
             "__device__ __attribute__((aligned(16))) const float kGeluTabData[kGeluTabN * 4] = {\n%s};\n\n"
             "__device__ __attribute__((aligned(16))) const float kGeluTanhTabData[kGeluTabN * 4] = {\n%s};\n\n"
-            "}  // namespace fln\n" % (vmax, n - 1, n, vmax, body(tabs["erf"]), body(tabs["tanh"])))
+            "// The forward's table (fit_erfc.gelu_log_table): interval k of |v| in [k / %d, (k + 1) / %d),\n"
+            "// the quadratic through L = log2(Phi(-|v|)) - log2(%d) (2^L = Phi(-|v|) / %d); the last\n"
+            "// interval is -inf.\n"
+            "constexpr int kGeluLogTabN = %d;\n"
+            "constexpr float kGeluLogTabInvH = %d.0f;\n\n"
+            "__device__ __attribute__((aligned(16))) const float kGeluLogTabData[kGeluLogTabN * 4] = {\n%s};\n\n"
+            "}  // namespace fln\n" % (vmax, n - 1, n, vmax, body(tabs["erf"]), body(tabs["tanh"]),
+                                        LOG_TAB_INV_H, LOG_TAB_INV_H, LOG_TAB_INV_H, LOG_TAB_INV_H,
+                                        tabs["log"].shape[0], LOG_TAB_INV_H, body(tabs["log"])))
 
 
 if __name__ == "__main__":
     import sys
     if sys.argv[1:] == ["table"]:
-        sys.stdout.write(table_header({"erf": gelu_table("erf"), "tanh": gelu_table("tanh")}))
+        sys.stdout.write(table_header({"erf": gelu_table("erf"), "tanh": gelu_table("tanh"),
+                                       "log": gelu_log_table()}))
         sys.exit(0)
     coef, rel = fit()
     print("p =", P, "degree =", DEGREE, "fit max relative error %.3g" % rel)
@@ -161,3 +212,6 @@ if __name__ == "__main__":
     print("derivative max abs error %.3g" % np.abs(d - dref).max())
     d3 = gelu_grad_table(gelu_table(), v)
     print("derivative (table) max abs error %.3g" % np.abs(d3 - dref).max())
+    g3 = gelu_log_tab(gelu_log_table(), v)
+    print("GELU (log table) max abs error %.3g, max relative error %.3g (|GELU| > 1e-30)"
+          % (np.abs(g3 - gref).max(), (np.abs(g3 - gref)[big] / np.abs(gref[big])).max()))

@@ -306,10 +306,11 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // GELU epilogue: every thread loads one entry of the GELU' table of its form (4 KiB,
   // L2-resident after the first block), ahead of the rows.
   float4 tab_entry;
-  if constexpr (GELU != 0)
+  if constexpr (GELU != 0) {
     tab_entry = reinterpret_cast<const float4*>(GELU == 1 ? kGeluTabData
                                                           : kGeluTanhTabData)[threadIdx.x % kGeluTabN];
-  asm volatile("" ::: "memory");
+    asm volatile("" ::: "memory");
+  }
 #pragma unroll
   for (int k = 0; k < PD; ++k) {
     load_row(k, k);
@@ -856,6 +857,8 @@ template <class T, bool DRES, int GELU, int VEC, int VPL, int MAXT>
 int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                     int64_t* resident) {
   auto kernel = bwd_reg_kernel<T, DRES, GELU, VEC, VPL, MAXT>;
+  // The GELU kernels fill their LDS table with one entry per thread.
+  if (GELU != 0 && threads < kGeluTabN) return FLN_ERR_INVALID;
   if (resident) {
     static std::atomic<int> per_cu[3][64];  // [threads / 512][device]
     int dev = 0;

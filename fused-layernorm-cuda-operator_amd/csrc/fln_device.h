@@ -312,6 +312,26 @@ __device__ __forceinline__ float gelu_grad2_sign_tab(const float4* tab, float u)
   const float4 c = tab[k];
   return __builtin_copysignf(fmaf(fmaf(c.z, f, c.y), f, c.x), u);
 }
+// The exact GELU from a table, for the forward's register kernel: with x = |v|,
+// GELU(v) = max(v, 0) - x Phi(-x), and L(x) = log2(Phi(-x)) is smooth, so interval k of
+// kGeluLogTabData (fln_gelu_table.h, generated by fit_erfc.py) holds the quadratic through
+// L - 4 at the ends and middle of x in [k / 16, (k + 1) / 16) (the last interval, x >= 255 / 16,
+// is -inf: Phi(-x) is far below the fp32 range there).  With uc = min(16 x, 255) (exact: the
+// interval width is a power of two), GELU = fma(-uc, 2^L, max(v, 0)).  The product keeps the
+// relative accuracy of Phi(-x) in the lower tail; under an fp32 emulation over |v| <= 13.5 it is
+// within 2.4e-7 (absolute) and 5.3e-6 (relative, |GELU| > 1e-30) of the float64 GELU, as the
+// polynomial is.  One multiply, min, fract, convert, shift, one ds_read_b128 from the block's LDS
+// copy, two FMAs, one v_exp_f32, a NaN-propagating maximum (v_maximum3_f32) and one FMA:
+// 9 VALU operations and one transcendental (the polynomial: 14 and two).  NaN propagates,
+// GELU(+inf) = +inf, GELU(-inf) = 0.
+__device__ __forceinline__ float gelu_erf_tab(const float4* tab, float v) {
+  const float uc = fminf(fabsf(v) * kGeluLogTabInvH, static_cast<float>(kGeluLogTabN - 1));
+  const float f = __builtin_amdgcn_fractf(uc);
+  const float4 c = tab[static_cast<uint32_t>(uc)];
+  const float r = exp2_fast(fmaf(fmaf(c.z, f, c.y), f, c.x));
+  return fmaf(-uc, r, __builtin_elementwise_maximum(v, 0.0f));
+}
+
 __device__ __forceinline__ float gelu_tanh_grad(float v) {
   const GeluTanhTerms t = gelu_tanh_terms(v);
   // 1 - sigmoid(2u) = e sigmoid(2u), with e kept finite: where e overflows, sigmoid(2u) = 0 and

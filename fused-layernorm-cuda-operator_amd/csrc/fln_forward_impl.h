@@ -226,6 +226,14 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
   constexpr int kStoresPerRow =
       2 + (RES ? VPL : 0) + (FP8 == 0 ? VPL : (FP8 == 2 ? 2 * VPL : VPL + 1));
   const rsrc_t none = make_rsrc(nullptr, 0);
+  // Exact GELU: every thread loads one entry of the GELU table (4 KiB, L2-resident after the
+  // first block), ahead of the rows; the LDS copy is written once they are in flight.
+  __shared__ float4 gelu_tab[GELU == 1 ? kGeluLogTabN : 1];
+  float4 tab_entry;
+  if constexpr (GELU == 1) {
+    tab_entry = reinterpret_cast<const float4*>(kGeluLogTabData)[threadIdx.x % kGeluLogTabN];
+    asm volatile("" ::: "memory");
+  }
 #pragma unroll
   for (int k = 0; k < PD; ++k) {
     load_row(rb0 + k * stride, k);
@@ -233,6 +241,10 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
     for (int j = 0; j < kStoresPerRow; ++j)  // distinct, non-adjacent: none merged away
       BufIO<4>::store(0u, none, 64u * j);
     asm volatile("" ::: "memory");  // keeps the slots in issue order
+  }
+  if constexpr (GELU == 1) {  // waits for the table's load alone (it was issued first)
+    if (threadIdx.x < kGeluLogTabN) gelu_tab[threadIdx.x] = tab_entry;
+    __syncthreads();
   }
   // Whole rounds of PD rows (the inner loop is unrolled so every slot index is static): a step
   // past the block's last row reads zeros and stores nothing.  An early exit from the unrolled
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
                  to_f32(bsh[i * MAXT + threadIdx.x].v[e]));
       else
         a = fmaf((xin(i, e) - mean) * rstd, to_f32(gv[i].v[e]), to_f32(bv[i].v[e]));
-      if constexpr (GELU == 1) a = gelu_erf(a);
+      if constexpr (GELU == 1) a = gelu_erf_tab(gelu_tab, a);
       if constexpr (GELU == 2) a = gelu_tanh(a);
       return a;
     };
@@ -1023,6 +1035,8 @@ int64_t resident_blocks(K kernel, int threads, int* cache_per_device) {
 
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
+  // The exact-GELU kernels fill their LDS table with one entry per thread.
+  if (GELU == 1 && threads < kGeluLogTabN) return FLN_ERR_INVALID;
   const int rows_per_block = threads / (kWave * p.wpr);
   const int64_t row_blocks = (p.rows + rows_per_block - 1) / rows_per_block;
   auto kernel = fwd_reg_kernel<T, FP8, RES, GELU, VEC, VPL, EXACT, MAXT>;
@@ -1277,7 +1291,11 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   p.wpr = g.wpr;
   const int vpl = g.vpl;
   const bool exact = g.exact;
-  const int threads = g.threads;
+  int threads = g.threads;
+  // The exact-GELU kernels fill their LDS table with one entry per thread: rows of three waves
+  // (192 threads) take two row groups per block.
+  if (p.gelu == 1)
+    while (threads < kGeluLogTabN) threads *= 2;
   if (vec_ok) return launch_reg_flavour<T, FP8, VV>(p, vpl, exact, threads, s);
   return launch_reg_flavour<T, FP8, 1>(p, vpl, false, threads, s);
 }

@@ -128,6 +128,24 @@ def test_erfc_terms_constants_in_the_device_header():
             ts = fit_erfc.gelu_grad_table(tab, special)
         assert np.isnan(ts[2]) and abs(ts[3] - 0.5) < 1e-6 and abs(ts[4] - 0.5) < 1e-6
     tab = tables["erf"]
+    # The forward register kernel's GELU table: L = log2(Phi(-|v|)) - log2(16) on intervals of
+    # 1 / 16, the last one -inf; its lookup keeps the bounds above, tail included.
+    n_log = int(re.search(r"kGeluLogTabN = (\d+);", hdr).group(1))
+    inv_h = float(re.search(r"kGeluLogTabInvH = ([\d.]+)f;", hdr).group(1))
+    assert (n_log, inv_h) == (fit_erfc.LOG_TAB_N, fit_erfc.LOG_TAB_INV_H)
+    body_l = hdr[hdr.index("kGeluLogTabData["):]
+    body_l = body_l[body_l.index("{"):body_l.index("};")]
+    lits = re.findall(r"(-__builtin_huge_valf\(\)|[-+]?\d+\.\d+(?:e[-+]\d+)?f)", body_l)
+    data = np.array([-np.inf if x.startswith("-__") else float(x[:-1]) for x in lits], np.float32)
+    log_tab = fit_erfc.gelu_log_table()
+    assert data.shape == (4 * n_log,) and np.array_equal(data.reshape(n_log, 4)[:, :3], log_tab)
+    gelu_l = fit_erfc.gelu_log_tab(log_tab, v)
+    gl_abs = np.abs(gelu_l - g_ref).max()
+    gl_tail = (np.abs(gelu_l[tail] - g_ref[tail]) / np.abs(g_ref[tail])).max()
+    assert gl_abs <= 1e-6 and gl_tail <= 1e-4, (gl_abs, gl_tail)
+    with np.errstate(invalid="ignore", over="ignore"):
+        gls = fit_erfc.gelu_log_tab(log_tab, special)
+    assert gls[0] == np.inf and gls[1] == 0.0 and np.isnan(gls[2]) and gls[3] == 0 and gls[4] == 0
     # Planted mistakes (in the emulation, on the CPU): each must fail the bounds above.
     bad_coef = list(coef)
     bad_coef[3] = np.float32(bad_coef[3] * (1 + 1e-4))
@@ -144,6 +162,12 @@ def test_erfc_terms_constants_in_the_device_header():
     swapped = tab.copy()
     swapped[:, [1, 2]] = swapped[:, [2, 1]]
     shifted = np.roll(tab, 1, axis=0)
+    bad_log = log_tab.copy()
+    bad_log[:, [1, 2]] = bad_log[:, [2, 1]]
+    for bad_gelu in (fit_erfc.gelu_log_tab(bad_log, v), fit_erfc.gelu_log_tab(log_tab, v, 15),
+                     fit_erfc.gelu_log_tab(np.roll(log_tab, 1, axis=0), v)):
+        bad_tail = (np.abs(bad_gelu[tail] - g_ref[tail]) / np.abs(g_ref[tail])).max()
+        assert np.abs(bad_gelu - g_ref).max() > 1e-6 or bad_tail > 1e-4
     for bad_grad in (fit_erfc.gelu_grad_table(swapped, v), fit_erfc.gelu_grad_table(shifted, v),
                      fit_erfc.gelu_grad_table(tab, v, vmax=v_max * 1.01),
                      fit_erfc.gelu_grad_table(tables["tanh"], v)):
