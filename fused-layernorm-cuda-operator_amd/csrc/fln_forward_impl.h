@@ -1047,17 +1047,23 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   // latency (loads in flight, reductions, barriers): rows dealt to the CU at once x PD rows of
   // loads ahead x the bytes each row moves >= 32 KiB for one-wave rows (no barrier), 56 KiB for
   // rows over several waves, 7/4 of that with a second dependent row reduction (fp8 row scale)
-  // or the exact GELU's VALU work.  More concurrent rows than that only cost DRAM locality.
-  // Measured on MI355X (bf16, us, HIP events; blocks per CU in brackets): 8192 x 4096 LN 26.9 [3]
-  // 24.4 [1] 23.8 [2]; LN + GELU(erf) 31.1 [2] 30.0 [4]; 32768 x 768 25.5 [1] 20.2 [2];
-  // LN -> fp8 32768 x 7168 198 [1] 147 [2] 133 [3]; residual + RMSNorm -> fp8 at that shape 283 [1]
-  // 300 [2].
+  // or the exact GELU's VALU work -- except the fp8 row scale in 256-thread blocks (one to four
+  // waves per row, no residual), which runs best at 42 KiB.  More concurrent rows than that only
+  // cost DRAM locality.  Measured on MI355X (bf16, us, HIP events; blocks per CU in brackets):
+  // 8192 x 4096 LN 26.9 [3] 24.4 [1] 23.8 [2]; LN + GELU(erf) 31.1 [2] 30.0 [4]; 32768 x 768 25.5
+  // [1] 20.2 [2]; LN -> fp8 32768 x 7168 (7 waves per row) 198 [1] 147 [2] 133 [3], 32768 x 8192
+  // 189.5 [1] 136.6 [2] 145.5 [3] 145.0 [4], 65536 x 4096 190.5 [1] 136.9 [2] 146.0 [3] 145.5
+  // [4], 262144 x 1024 198.0 [1] 146.1 [2] 153.3 [3]; residual + RMSNorm -> fp8 at 32768 x 7168
+  // 283 [1] 300 [2].
   constexpr int PD = fwd_prefetch_depth<T, RES, VEC, VPL, MAXT>();
   const int64_t es = static_cast<int64_t>(sizeof(T));
   const int64_t moved_per_row = p.cols * (es * (RES ? 3 : 1) + (FP8 ? 1 : es));
   const int64_t per_block = moved_per_row * rows_per_block * PD;
   int64_t target = p.wpr == 1 ? (32 << 10) : (56 << 10);
-  if (FP8 == 1 || GELU == 1) target = target * 7 / 4;
+  if (FP8 == 1 && !RES && threads == 256)
+    target = 42 << 10;
+  else if (FP8 == 1 || GELU == 1)
+    target = target * 7 / 4;
   int64_t per_cu = per_block > 0 ? (target + per_block - 1) / per_block : 1;
   const int forced = tuning().fwd_grid_mult;
   if (forced > 0) per_cu = forced;
@@ -1271,8 +1277,23 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   // beta alone and spill); wider fp32 rows go to the LDS-staged kernel.
   const int raw_cap = (vec_ok && VV < 8) ? wide_cap : max_cap;
   const int64_t nvec = N / vec;
-  const FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, raw_cap, vec_ok,
-                                     tun.fwd_wpr);
+  FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, raw_cap, vec_ok, tun.fwd_wpr);
+  // The fp8 row scale (no residual) takes 4 waves per row with masked tail lanes over an exact
+  // tiling of 5-7 waves when at most 1/8 of the 4-wave tile is masked (bf16, 32768 x 7168:
+  // 7 waves 134.5 us at its best grid, 4 waves 129.9 us; at 49152 x 5120, 3/8 masked, 4 waves
+  // lose: 152.2 -> 161.6 us).
+  if (FP8 == 1 && p.res == nullptr && vec_ok && !g.loop && g.exact && g.wpr >= 5 &&
+      g.wpr <= 7 && tun.fwd_wpr <= 0) {
+    const int64_t per4 = (nvec + 4 * kWave - 1) / (4 * kWave);
+    const int v4 = next_pow2(static_cast<int>(per4));
+    const int64_t slots = static_cast<int64_t>(v4) * 4 * kWave;
+    if (v4 <= cap && (slots - nvec) * 8 <= slots) {
+      g.wpr = 4;
+      g.vpl = v4;
+      g.exact = false;
+      g.threads = 256;
+    }
+  }
   // Rows past the register tiles: the LDS-staged kernel on the vector path (up to 8 vectors
   // per thread of a 1024-thread block), the streamed wide-row kernel otherwise (buffer
   // resources span at most 4 GiB: rows of 2 GiB or more keep the looped kernel).
