@@ -75,6 +75,11 @@ def parse():
     ap.add_argument("--kernel-loop", metavar="WORKLOAD", default=None,
                     help="(profiling child) launch WORKLOAD's forward and backward --iters "
                          "times each, then a device copy of known size, and exit")
+    ap.add_argument("--stream-loop", metavar="PAT:THREADS:BLOCKS_PER_CU:UNROLL:DEPTH,...",
+                    default=None,
+                    help="(profiling child) launch the streaming kernels of libfln_stream.so "
+                         "(64 MiB per stream, rotating sets) --iters times per listed pattern and "
+                         "launch shape, and exit")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--traffic-configs", action="store_true",
                     help="instead of the bench line: HBM traffic (two rocprofv3 counter passes "
@@ -307,6 +312,37 @@ def kernel_loop(args):
         b.copy_(a)
     torch.cuda.synchronize()
     print("kernel loop done", flush=True)
+
+
+def stream_loop(args):
+    """Profiling child: --iters launches of each listed streaming kernel (pattern 0 1R1W, 1 2R1W,
+    2 2R2W, 3 1R + half W) at the listed launch shape, 64 MiB per stream over rotating sets; the
+    counter passes compare the normalization kernels with these."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(PKG, "libfln_stream.so"))
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.fln_stream_run.argtypes = [i32, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32, i32, vp]
+    lib.fln_stream_run.restype = i32
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cus = lib.fln_stream_cu_count()
+    nbytes = 64 << 20
+    nsets = 8
+    sets = [[torch.empty(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(4)]
+            for _ in range(nsets)]
+    for st4 in sets:
+        for t in st4[:2]:
+            t.random_(0, 2 ** 31 - 1)
+    for spec in args.stream_loop.split(","):
+        pat, thr, bpc, u, pd = (int(v) for v in spec.split(":"))
+        for k in range(args.iters):
+            a, b, c, d = sets[k % nsets]
+            rc = lib.fln_stream_run(pat, a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(),
+                                    nbytes, thr, bpc * cus, u, pd, 2, 2, sp)
+            if rc != 0:
+                raise RuntimeError(f"fln_stream_run {spec}: {rc}")
+    torch.cuda.synchronize()
+    print("stream loop done", flush=True)
 
 
 def _counter_rows(outdir):
@@ -839,6 +875,9 @@ def main():
         sys.exit(2)
     if args.kernel_loop:
         kernel_loop(args)
+        return
+    if args.stream_loop:
+        stream_loop(args)
         return
     if args.traffic_configs:
         traffic_configs(args)
