@@ -74,6 +74,50 @@ def test_c2_layernorm_gelu_fp32(lib, name, mode):
     assert np.abs(to_np(y) - ref).max() <= 1e-5
 
 
+@pytest.mark.parametrize("mode", ["none", "tanh"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_gelu_full_range_fwd_bwd(lib, mode, dtype):
+    """LN + GELU forward and backward with the GELU input swept over [-13, 13] (beta a ramp) and a
+    random dy: the register kernels' GELU and GELU' tables (|a| < 6 interpolated, past 6 the
+    constant last interval; the forward's log table out to 16) against the oracle at both signs
+    and across every interval boundary, for both forms."""
+    rows, cols = 48, 4096
+    gen = torch.Generator().manual_seed(977 + (mode == "tanh"))
+    xc = (torch.rand(rows, cols, generator=gen) * 2 - 1).to(dtype)
+    gc = torch.ones(cols).to(dtype)
+    bc = torch.linspace(-12.0, 12.0, cols).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, b, dy = cuda(xc), cuda(gc), cuda(bc), cuda(dyc)
+    gm = capi.GELU_ERF if mode == "none" else capi.GELU_TANH
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
+                                              cols, code, 1e-5, gm, capi.stream()))
+    dx = torch.empty_like(x)
+    dg = torch.empty(cols, device="cuda")
+    db = torch.empty(cols, device="cuda")
+    ws, n = workspace(lib, rows, cols, x)
+    capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b), p(dx),
+                                               p(dg), p(db), rows, cols, code, capi.F32, gm,
+                                               p(ws), n, capi.stream()))
+    xs, gs, bs, dys = f32(xc), f32(gc), f32(bc), f32(dyc)
+    y_ref = norms.layer_norm_gelu_fwd(xs, gs, bs, 1e-5, mode)
+    dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, mode)
+    if dtype == torch.float32:
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5), kind="bf16",
+                          what="y")
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          kind="bf16", what="dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+
+
 @pytest.mark.parametrize("cols", [4096, 12288], ids=["registers", "lds"])
 def test_gelu_erf_tails_fp32(lib, cols):
     """The exact-erf GELU over a = LayerNorm(x) + beta spanning [-13.6, 13.6] (beta a ramp):
