@@ -256,20 +256,20 @@ __device__ __forceinline__ float gelu_tanh_sigmoid(float v) { return gelu_tanh_t
 struct ErfcTerms {
   float t, e, f;  // t, exp(-v^2 / 2), F(t)
 };
-// F(t) times S (1 or 2: the scaled coefficients are exact).
-template <int S> __device__ __forceinline__ float erfc_poly(float t) {
+// F(t), Horner form.
+__device__ __forceinline__ float erfc_poly(float t) {
   constexpr float kF[8] = {9.873314202e-02f, 9.872655571e-02f, 9.295467287e-02f,
                            7.733605057e-02f, 8.147227019e-02f, -7.275486365e-03f,
                            1.006051227e-01f, -4.255273566e-02f};
-  float f = S * kF[7];
+  float f = kF[7];
 #pragma unroll
-  for (int k = 6; k >= 0; --k) f = fmaf(f, t, S * kF[k]);
+  for (int k = 6; k >= 0; --k) f = fmaf(f, t, kF[k]);
   return f;
 }
 __device__ __forceinline__ ErfcTerms erfc_terms(float v) {
   const float e = exp2_fast((-0.5f * kLog2e * v) * v);
   const float t = __builtin_amdgcn_rcpf(fmaf(0.35f * 0.70710678118654752440f, fabsf(v), 1.0f));
-  return {t, e, erfc_poly<1>(t)};
+  return {t, e, erfc_poly(t)};
 }
 // |a| * b with 0 * anything = 0 (v_mul_legacy_f32): |v| (t e) stays 0 at v = +-inf, where
 // t e = 0.  Neither operand may be the direct result of a transcendental instruction (v_rcp,
@@ -304,7 +304,8 @@ __device__ __forceinline__ float gelu_erf_grad(float v) {
 // copy, two FMAs and a copysign: no transcendental instruction.
 constexpr float kGeluTabInvH = (kGeluTabN - 1) / kGeluTabMax;  // 42.5: u = v / h
 
-// sign(v) T(|v|) for u = v / h: 2 GELU'(v) = 1 + the result (NaN propagates through fract).
+// sign(v) T(|v|) for u = v / h: 2 GELU'(v) = 1 + the result (NaN propagates through fract; so
+// does an infinite u, as with the formulas above).
 __device__ __forceinline__ float gelu_grad2_sign_tab(const float4* tab, float u) {
   const float au = fabsf(u);
   const float f = __builtin_amdgcn_fractf(au);
