@@ -259,8 +259,8 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     rsn[slot] = __builtin_bit_cast(float, BufIO<4>::load(make_rsrc(p.rstd + row, sb), 0));
   };
 
-  // The row being processed, widened once: xhat and dy in fp32 (g = dy * gamma is formed where
-  // it is used rather than kept: 16 fewer VGPRs for a lane with 16 columns).  With a GELU
+  // The row being processed, widened once: xhat and dy in fp32 (g = dy * gamma is formed in the
+  // row sums and kept for dx only by lanes with 8 columns: see KEEP_G).  With a GELU
   // epilogue, dd holds twice the gradient at the LayerNorm output; kInvD takes the factor out once
   // per row (rstd and the row-sum coefficients) and once per block (the column partials), exactly.
   constexpr float kInvD = GELU != 0 ? 0.5f : 1.0f;
