@@ -153,9 +153,11 @@ struct SumOp {
 // Maximum of non-negative floats (every maximum reduced here is of |value|): their IEEE bit
 // patterns order like unsigned integers, so v_max_u32 gives the same result without the NaN
 // canonicalization fmaxf costs (one extra VALU op per step); a NaN propagates, as in amax.
+// Written as the umax builtin: the DPP operand then folds into one v_max_u32_dpp per step
+// (the equivalent `x > y ? x : y` compiles to v_mov_dpp + v_cmp + v_cndmask and a wait state).
 __device__ __forceinline__ float max_nonneg(float a, float b) {
   const uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
-  return __builtin_bit_cast(float, x > y ? x : y);
+  return __builtin_bit_cast(float, __builtin_elementwise_max(x, y));
 }
 struct MaxOp {
   __device__ __forceinline__ static float apply(float a, float b) { return max_nonneg(a, b); }
@@ -366,8 +368,12 @@ __device__ __forceinline__ float sat448(float v) {
   return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f);
 }
 
+// The first conversion writes the low 16 bits and keeps the high ones of its `old` operand,
+// which the second conversion then replaces: any register serves as `old` (the first input's
+// bits here, which saves the v_mov of a constant).
 __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
+  const float sa = sat448(a);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(sa, sat448(b), __builtin_bit_cast(int, sa), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), w, true);
   return static_cast<uint32_t>(w);
 }
@@ -375,7 +381,7 @@ __device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
 // rounds to 448 under round-to-nearest-even): a row scaled by 448 / max|row| stays within
 // 448 (1 + 2^-23).
 __device__ __forceinline__ uint32_t fp8x4_inrange(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return static_cast<uint32_t>(w);
 }
@@ -406,7 +412,9 @@ template <int G> __device__ __forceinline__ float group_max(float v) {
 }
 
 __device__ __forceinline__ uint8_t fp8x1(float a) {
-  return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), 0.0f, 0, false) & 0xFF);
+  const float sa = sat448(a);  // low byte: the code of a (the rest of the word is discarded)
+  return static_cast<uint8_t>(
+      __builtin_amdgcn_cvt_pk_fp8_f32(sa, 0.0f, __builtin_bit_cast(int, sa), false) & 0xFF);
 }
 
 }  // namespace fln
