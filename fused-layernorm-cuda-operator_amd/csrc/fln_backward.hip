@@ -174,12 +174,14 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // gamma (and, with GELU, beta) stay in registers in the I/O type and are widened at each use
   // (gamma ones when absent; zeros past the row): half the VGPRs of fp32 copies for 16-bit types.
   // The 16-bit GELU and residual-gradient flavours with two vectors per lane in 1024-thread
-  // blocks park them in LDS instead, each thread its own copy (64 KiB, no barrier): in registers
+  // blocks (three in 768-thread blocks) park them in LDS instead, each thread its own copy
+  // (64-72 KiB, no barrier): in registers
   // they made those flavours spill 84-132 B per lane (4096 x 16384 bf16: GELU tanh 132.4 ->
   // 102.6 us, erf 153.2 -> 96.5 us; with a residual gradient 97.8 us on the LDS-staged kernel
   // -> 90.8 us here).
-  constexpr bool PARAMS_IN_LDS = (GELU != 0 || DRES) && VPL == 2 && MAXT == 1024 &&
-                                 sizeof(T) == 2;
+  constexpr bool PARAMS_IN_LDS =
+      (GELU != 0 || DRES) && ((VPL == 2 && MAXT == 1024) || (VPL == 3 && MAXT == 768)) &&
+      sizeof(T) == 2;
   __shared__ P gsh[PARAMS_IN_LDS ? VPL * MAXT : 1], bsh[PARAMS_IN_LDS ? VPL * MAXT : 1];
   P gmr[PARAMS_IN_LDS ? 1 : VPL];
   P btr[GELU && !PARAMS_IN_LDS ? VPL : 1];
@@ -423,16 +425,15 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit rows of 16385..18432 columns, or up to 24576 for LayerNorm / RMSNorm without a residual
-// gradient): one NT-thread block per row at a time, thread t owning vectors t + NT i
+// 16-bit LayerNorm / RMSNorm rows of 18433..24576 columns without a residual gradient, and fp16
+// rows of 16385..18432 columns with one): one NT-thread block per row at a time, thread t owning vectors t + NT i
 // (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
 // and writes dx.  A thread reads back only the vectors it parked, so the staging needs no barrier:
 // LDS serves as per-thread spill space for the row (128 KiB at CPT 4 and 1024 threads).
-// NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168, which holds the
-// fp32 column sums and the prefetched row of a 16-bit lane with 3 vectors (gamma / beta in LDS)
-// without spilling.
+// NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168 for the fp32
+// column sums and the prefetched row of a 16-bit lane with 3-4 vectors (gamma in LDS).
 constexpr int kLdsThreads = 1024;
 constexpr int kLds16Threads = 768;
 
@@ -441,8 +442,8 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
   constexpr int kT = NT;
   constexpr int kW = kT / kWave;
   using P = Pack<T, VEC>;
-  // 768-thread blocks with 3-4 vectors per thread keep gamma (and, with GELU, beta) in LDS too,
-  // thread-private like the row: 12-32 VGPRs per lane that would otherwise spill.
+  // 768-thread blocks (16-bit rows) keep gamma in LDS too, thread-private like the row: 12-16
+  // VGPRs per lane that would otherwise spill.
   constexpr bool PARAMS_IN_LDS = NT == kLds16Threads && CPT >= 3;
   __shared__ P xs[CPT * kT], ds[CPT * kT];
   __shared__ P gs[PARAMS_IN_LDS ? CPT * kT : 1], bs[PARAMS_IN_LDS && GELU ? CPT * kT : 1];
@@ -500,28 +501,11 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
     else
       return to_f32(btr[i].v[e]);
   };
-  // GELU epilogue, 16-bit rows: the GELU' table in LDS (one entry per thread; blocks hold >= 768
-  // threads), read in both passes, so GELU' costs no transcendental either time (bf16 4096 x
-  // 18432, us: erf 159.3 -> 141.6, tanh 145.4 -> 141.6).  fp32 rows keep the formulas: their
-  // kernel is not VALU-bound and the table reads slowed it (erf 4096 x 12288 116.4 -> 120.7, tanh
-  // 2048 x 16384 101.7 -> 107.8).
-  constexpr bool TAB = GELU != 0 && sizeof(T) == 2;
-  __shared__ float4 gelu_tab[TAB ? kGeluTabN : 1];
-  if constexpr (TAB) {
-    if (t < kGeluTabN)
-      gelu_tab[t] = reinterpret_cast<const float4*>(GELU == 1 ? kGeluTabData : kGeluTanhTabData)[t];
-    __syncthreads();
-  }
-  // Upstream gradient at the LayerNorm output: dy, or dy GELU'(xhat gamma + beta) (the table's
-  // 2 GELU' taken back by an exact 1/2).
+  // Upstream gradient at the LayerNorm output: dy, or dy GELU'(xhat gamma + beta) (GELU rows
+  // reach this kernel only in fp32, which is not VALU-bound here: the GELU' formulas).
   auto dln = [&](float d, float xh, int i, int e) {
-    if constexpr (TAB) {
-      const float u = kGeluTabInvH * fmaf(xh, gam(i, e), bet(i, e));
-      d = 0.5f * fmaf(d, gelu_grad2_sign_tab(gelu_tab, u), d);
-    } else {
-      if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam(i, e), bet(i, e)));
-      if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam(i, e), bet(i, e)));
-    }
+    if constexpr (GELU == 1) d *= gelu_erf_grad(fmaf(xh, gam(i, e), bet(i, e)));
+    if constexpr (GELU == 2) d *= gelu_tanh_grad(fmaf(xh, gam(i, e), bet(i, e)));
     return d;
   };
   float acc_g[CPT][VEC], acc_b[CPT][VEC];
@@ -862,6 +846,8 @@ namespace {
 // Largest vectors per lane instantiated for the backward register path: 2 vectors (16
 // elements of a 16-bit type, 8 of fp32) on the vector path, 8 on the scalar path.
 constexpr int bwd_max_vpl(int vec, int es) { return vec == 1 ? 8 : 2; }
+// 16-bit rows of 16385..18432 columns: one row per 768-thread block, 3 vectors per lane.
+constexpr int kReg3Threads = 768;
 
 int next_pow2(int v) {
   int p = 1;
@@ -899,14 +885,17 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
 template <class T, int VEC, int VPL>
 int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                   int64_t* resident) {
+  // Three vectors per lane only in 768-thread blocks (168 VGPRs per lane).
+  constexpr int MAXT = VPL == 3 ? kReg3Threads : 1024;
+  if (VPL == 3 && threads != kReg3Threads) return FLN_ERR_INVALID;
   // GELU is never combined with a residual gradient (no entry point passes both).
   if (p.gelu == 1)
-    return launch_stage1_k<T, false, 1, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+    return launch_stage1_k<T, false, 1, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
   if (p.gelu == 2)
-    return launch_stage1_k<T, false, 2, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+    return launch_stage1_k<T, false, 2, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
   if (p.dres)
-    return launch_stage1_k<T, true, 0, VEC, VPL, 1024>(p, blocks, threads, s, resident);
-  return launch_stage1_k<T, false, 0, VEC, VPL, 1024>(p, blocks, threads, s, resident);
+    return launch_stage1_k<T, true, 0, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
+  return launch_stage1_k<T, false, 0, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
 }
 
 template <class T, int VEC>
@@ -917,6 +906,10 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
     case 1: return launch_stage1<T, VEC, 1>(p, blocks, threads, s, resident);
     case 2:
       if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, threads, s, resident);
+      return FLN_ERR_INVALID;
+    case 3:  // 16-bit rows of 16385..18432 columns (768 threads)
+      if constexpr (sizeof(T) == 2 && VEC == 8)
+        return launch_stage1<T, VEC, 3>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 4:
       if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, threads, s, resident);
@@ -984,20 +977,11 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
     } else {
       if (geo.threads == kLds16Threads) {
         const dim3 grid(static_cast<unsigned>(geo.blocks)), block(kLds16Threads);
-        if (geo.lds_cpt == 3 && !p.dres && !p.gelu)
-          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 3, kLds16Threads>), grid, block, 0,
-                             s, p);
-        else if (geo.lds_cpt == 3 && p.dres && !p.gelu)
+        if (geo.lds_cpt == 3 && p.dres && !p.gelu)
           hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VV, 3, kLds16Threads>), grid, block, 0,
                              s, p);
         else if (geo.lds_cpt == 4 && !p.dres && !p.gelu)
           hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 4, kLds16Threads>), grid, block, 0,
-                             s, p);
-        else if (geo.lds_cpt == 3 && p.gelu == 1)
-          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 1, VV, 3, kLds16Threads>), grid, block, 0,
-                             s, p);
-        else if (geo.lds_cpt == 3 && p.gelu == 2)
-          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 2, VV, 3, kLds16Threads>), grid, block, 0,
                              s, p);
         else
           return FLN_ERR_INVALID;
@@ -1106,29 +1090,44 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // The register path deals row groups out grid-stride over `blocks`; the looped fallback
   // gives each block a contiguous chunk of rows_per_block rows.
   g.blocks = g.reg_path ? blocks : (rows + g.rows_per_block - 1) / g.rows_per_block;
+  // 16-bit rows of 16385..18432 columns on the vector path: the register kernel with one row
+  // per 768-thread block and 3 vectors per lane (xhat, dy, both column sums and the next row in
+  // flight fit the 168 VGPRs a lane has at 3 waves per SIMD; the residual-gradient and GELU
+  // flavours park gamma / beta in LDS).  Against the LDS-staged kernel below, bf16 4096 x 18432
+  // backward calls, us: LN 106.1 -> 90.5, RMSNorm 93.1 -> 84.9, + residual gradient 129.2 ->
+  // 115.0, GELU erf 145.8 -> 99.3, tanh 147.9 -> 99.2; 300 x 18432 LN 42.6 -> 26.6.  fp16 with a
+  // residual gradient spills there (52 B per lane) and keeps the LDS-staged kernel (130.2
+  // against 129.3 us).
+  if (!g.reg_path && es == 2 && g.vec == 8 && nvec > 2 * 1024 && nvec <= 3 * kReg3Threads &&
+      !(dres && dtype == FLN_F16) && tun.bwd_no_lds == 0) {
+    g.reg_path = true;
+    g.vpl = 3;
+    g.threads = kReg3Threads;
+    g.wpr = kReg3Threads / kWave;
+    g.rgs = 1;
+    g.blocks = rows < device_cu_count() ? rows : device_cu_count();
+    g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
+  }
   // fp32 rows too wide for registers but within 4 vectors per thread of a 1024-thread block
   // (8193..16384 columns): the LDS-staged kernel, one block per CU, rows dealt grid-stride.
-  // (16-bit rows past 16384 columns need 48-64 VGPRs of column sums per lane on top of the
-  // prefetched row and spill in a 1024-thread block.)  16-bit rows of 8193..16384 columns with
-  // a residual gradient keep the register kernel (gamma in LDS there), measured faster than 2
-  // vectors per thread here (4096 x 16384 bf16: 90.8 against 97.8 us).  16-bit rows past
-  // 16384 columns take it with 768 threads (gamma / beta parked in LDS as well): 3 vectors per
-  // thread (up to 18432 columns) for every flavour, 4 (up to 24576) for LayerNorm / RMSNorm
-  // without a residual gradient (44 B of spill left), all measured faster than the two passes
-  // (4096 x 18432 bf16: LN 161 -> 108 us, + residual 164 -> 110 us, + GELU 206 -> 163 us;
-  // 4096 x 20480 LN 170 -> 146 us).  16-bit GELU rows of up to 16384 columns keep the register
-  // kernel (gamma / beta in LDS there), measured faster than this kernel, which evaluates GELU'
-  // in both of its passes (4096 x 12288 bf16 tanh 95.6 against 109.6 us with 2 vectors per
-  // thread in 768 threads).
+  // (16-bit rows past 18432 columns need 64 VGPRs of column sums per lane on top of the
+  // prefetched row and spill even at 768 threads.)  16-bit rows of 8193..16384 columns with a
+  // residual gradient keep the register kernel (gamma in LDS there), measured faster than 2
+  // vectors per thread here (4096 x 16384 bf16: 90.8 against 97.8 us).  16-bit LayerNorm /
+  // RMSNorm rows of 18433..24576 columns without a residual gradient take it with 768 threads
+  // and 4 vectors per thread (gamma parked in LDS as well; 44 B of spill left), and fp16 rows
+  // of 16385..18432 columns with one, 3 vectors per thread: measured faster than the two passes
+  // (4096 x 18432 bf16: LN 161 -> 108 us, + residual 164 -> 110 us; 4096 x 20480 LN 170 ->
+  // 146 us).
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
-  const bool wide16 = !g.reg_path && es == 2 && !gelu && (cpt16 == 3 || (cpt16 == 4 && !dres));
-  const bool gelu16 = gelu && es == 2 && !g.reg_path && cpt16 == 3;
-  if (g.vec > 1 && (wide_f32 || wide16 || gelu16) && tun.bwd_no_lds == 0) {
+  const bool wide16 = !g.reg_path && es == 2 && !gelu &&
+                      ((cpt16 == 3 && dres && dtype == FLN_F16) || (cpt16 == 4 && !dres));
+  if (g.vec > 1 && (wide_f32 || wide16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
-    g.lds_cpt = (wide16 || gelu16) ? static_cast<int>(cpt16) : static_cast<int>(cpt);
-    g.threads = (wide16 || gelu16) ? kLds16Threads : kLdsThreads;
+    g.lds_cpt = wide16 ? static_cast<int>(cpt16) : static_cast<int>(cpt);
+    g.threads = wide16 ? kLds16Threads : kLdsThreads;
     g.wpr = g.threads / kWave;
     g.rgs = 1;
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
