@@ -617,13 +617,17 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
 //   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
 //     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
 //     rows grid-stride, four vectors per thread in flight per array;
-//   bwd_colpass_kernel: a thread owns one vector column; over a chunk of rows (four in flight)
-//     it writes dx from the row's statistics and accumulates dgamma / dbeta in registers, then
-//     writes one partial row per chunk for col_reduce_kernel.
+//   bwd_colpass_kernel: a thread owns one vector column; over every G-th row (G = the blocks
+//     per column tile; four rows in flight) it writes dx from the row's statistics and
+//     accumulates dgamma / dbeta in registers, then writes one partial row per block row for
+//     col_reduce_kernel.
 // 5 streams (x, dy twice, dx once) instead of 3, but every access is a coalesced vector stream
 // and no thread holds more than four vectors of a row.
 constexpr int kWideThreads = 256;
 constexpr int kWideUnroll = 4;
+#ifndef FLN_COLPASS_BLOCKS_PER_CU
+#define FLN_COLPASS_BLOCKS_PER_CU 2
+#endif
 
 template <class T, int GELU, int VEC>
 __global__ __launch_bounds__(kWideThreads) void bwd_rowstat_kernel(const BwdParams p,
@@ -696,8 +700,10 @@ __global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdPara
   const int nvec = static_cast<int>(N / VEC);
   const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
   const float inv_n = 1.0f / static_cast<float>(N);
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * p.rows_per_block;
-  const int64_t r1 = r0 + p.rows_per_block < p.rows ? r0 + p.rows_per_block : p.rows;
+  // Block y takes rows y, y + G, y + 2G, ... (G = gridDim.y): all blocks stream through one
+  // window of adjacent rows at a time, which keeps DRAM page locality (contiguous row chunks
+  // per block had every block in a different part of the tensors at once).
+  const int64_t G = gridDim.y;
   const T* X = static_cast<const T*>(p.x);
   const T* DY = static_cast<const T*>(p.dy);
   const T* DR = static_cast<const T*>(p.dres);
@@ -711,13 +717,13 @@ __global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdPara
   float acc_g[VEC], acc_b[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc_g[e] = acc_b[e] = 0.0f;
-  for (int64_t row = r0; row < r1; row += kWideUnroll) {
+  for (int64_t row = blockIdx.y; row < p.rows; row += kWideUnroll * G) {
     P xv[kWideUnroll], dv[kWideUnroll], rv[DRES ? kWideUnroll : 1];
     float mu[kWideUnroll], rs[kWideUnroll], cb[kWideUnroll], cx[kWideUnroll];
 #pragma unroll
     for (int u = 0; u < kWideUnroll; ++u) {
-      const bool in = row + u < r1;  // uniform
-      const int64_t r = in ? row + u : r1 - 1;
+      const bool in = row + u * G < p.rows;  // uniform
+      const int64_t r = in ? row + u * G : row;
       const uint32_t nb = in ? row_bytes : 0u;
       xv[u] = buf_load<P, kStream>(make_rsrc(X + r * N, nb), v);
       dv[u] = buf_load<P, kStream>(make_rsrc(DY + r * N, nb), v);
@@ -730,8 +736,8 @@ __global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdPara
     }
 #pragma unroll
     for (int u = 0; u < kWideUnroll; ++u) {
-      const bool in = row + u < r1;
-      const int64_t r = in ? row + u : r1 - 1;
+      const bool in = row + u * G < p.rows;
+      const int64_t r = in ? row + u * G : row;
       P o;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
@@ -743,7 +749,7 @@ __global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdPara
         float dxv = fmaf(d, rs[u] * gam, fmaf(cx[u], xh, cb[u]));
         if constexpr (DRES) dxv += to_f32(rv[u].v[e]);
         o.v[e] = from_f32<T>(dxv);
-        if (in) {  // rows past the chunk were read as zeros: d = 0, but keep the sums exact
+        if (in) {  // rows past the tensor were read as zeros: d = 0, but keep the sums exact
           acc_g[e] = fmaf(d, xh, acc_g[e]);
           acc_b[e] += d;
         }
@@ -1134,14 +1140,19 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
     g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
   }
   // Everything else (any width) in two streaming passes, given the workspace for the row
-  // statistics; without one (dx alone, no workspace passed) the looped kernel.  Row chunks of
-  // the column pass: enough that tiles x chunks fills the device ~8 blocks per CU, at most the
-  // workspace's partial rows.
+  // statistics; without one (dx alone, no workspace passed) the looped kernel.  Block rows of
+  // the column pass (each block takes every G-th row of its column tile): enough that tiles x G
+  // gives 2 blocks per CU, at most the workspace's partial rows.  Fewer rows in progress keep
+  // DRAM locality, and the column reduction reads fewer partial rows: bf16 backward calls, us,
+  // 8 -> 2 blocks per CU: 512 x 131072 145.3 -> 134.5, 2048 x 32768 139.2 -> 124.3, 8192 x 32768
+  // -> 448.4 (540.0 with contiguous row chunks), fp32 1024 x 32768 127.4 -> 116.9; one block per
+  // CU was slower (178.0 / 165.4 / 625.4 / 155.9).
   // (Buffer resources span at most 4 GiB: rows of 2 GiB or more keep the looped kernel.)
   if (!g.reg_path && g.lds_cpt == 0 && have_workspace && cols * es < (int64_t(1) << 31) &&
       tun.bwd_no_two_pass == 0) {
     const int64_t tiles = (nvec + kWideThreads - 1) / kWideThreads;
-    int64_t chunks = (8 * static_cast<int64_t>(device_cu_count()) + tiles - 1) / tiles;
+    int64_t chunks = (FLN_COLPASS_BLOCKS_PER_CU * static_cast<int64_t>(device_cu_count()) +
+                      tiles - 1) / tiles;
     if (chunks > workspace_partial_rows(rows)) chunks = workspace_partial_rows(rows);
     if (chunks < 1) chunks = 1;
     g.two_pass = true;
