@@ -847,6 +847,41 @@ __global__ __launch_bounds__(kCrThreads) void col_reduce_kernel(const ColReduceA
   reduce_quad_block(a, blockIdx.x, kCrSlices, comb);
 }
 
+// Stage 2 for few partial rows (G <= 8: the two-pass backward's column pass over very wide rows,
+// tiny batches): every thread owns one column quad of one array and adds its G partial rows in
+// order, all loads in flight at once; no LDS, no barrier.  The sliced kernel would idle three
+// quarters of its threads at G = 8, over 8192 blocks at 131072 columns (bf16 512 x 131072
+// backward call 133.8 -> 129.5 us; at G = 16 the flat grid gets too few threads: 16 x 8192
+// 9.4 -> 10.0 us).
+constexpr int kCrFlatMaxG = 8;
+constexpr int kCrFlatThreads = 256;
+
+__host__ __device__ inline int64_t flat_blocks(const ColReduceArgs& a) {
+  const int64_t quads = ((a.N + 3) & ~int64_t(3)) >> 2;
+  return a.ny * ((quads + kCrFlatThreads - 1) / kCrFlatThreads);
+}
+
+__global__ __launch_bounds__(kCrFlatThreads) void col_reduce_flat_kernel(const ColReduceArgs a) {
+  const int64_t ld = (a.N + 3) & ~int64_t(3);
+  const int64_t per_array = ((ld >> 2) + kCrFlatThreads - 1) / kCrFlatThreads;
+  const int y = static_cast<int>(blockIdx.x / per_array);
+  const int64_t c = ((blockIdx.x - y * per_array) * kCrFlatThreads + threadIdx.x) * 4;
+  if (c >= a.N) return;
+  const float* col = a.part[y] + c;
+  float4 v[kCrFlatMaxG];
+#pragma unroll
+  for (int k = 0; k < kCrFlatMaxG; ++k)
+    if (k < a.G) v[k] = *reinterpret_cast<const float4*>(col + k * ld);
+  float4 r = v[0];
+#pragma unroll
+  for (int k = 1; k < kCrFlatMaxG; ++k)
+    if (k < a.G) add4(r, v[k]);
+  const float rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c + e < a.N) store_param(a.out[y], a.out_dtype, c + e, rr[e]);
+}
+
 namespace {
 
 // Largest vectors per lane instantiated for the backward register path: 2 vectors (16
@@ -1217,8 +1252,12 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
     default: return FLN_ERR_INVALID;
   }
   if (rc != 0 || a.ny == 0) return rc;
-  hipLaunchKernelGGL(col_reduce_kernel, dim3(static_cast<unsigned>(quad_blocks(a))),
-                     dim3(kCrThreads), 0, s, a);
+  if (a.G <= kCrFlatMaxG)
+    hipLaunchKernelGGL(col_reduce_flat_kernel, dim3(static_cast<unsigned>(flat_blocks(a))),
+                       dim3(kCrFlatThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(col_reduce_kernel, dim3(static_cast<unsigned>(quad_blocks(a))),
+                       dim3(kCrThreads), 0, s, a);
   return static_cast<int>(hipGetLastError());
 }
 
