@@ -826,8 +826,12 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
 
     // Pass 2 (per-row fp8 scale): the row maximum of the outputs.
     float inv = 0.0f, am = 0.0f;
+    // Successive passes walk the row in alternate directions, so each pass starts on the part of
+    // the row the previous one read last, which is still in L2.
+    const uint32_t steps = (nvec + kT * U - 1) / (kT * U);
     if constexpr (FP8 == 1) {
-      for (uint32_t base = 0; base < nvec; base += kT * U) {
+      for (uint32_t st = steps; st-- > 0;) {
+        const uint32_t base = st * (kT * U);
         P hv[U];
         load_step(base, hv, Keep{});
 #pragma unroll
@@ -845,8 +849,9 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
       inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // v_rcp_f32, 1 ulp
     }
 
-    // Last pass: outputs.
-    for (uint32_t base = 0; base < nvec; base += kT * U) {
+    // Last pass: outputs (backwards after the statistics pass, forwards after the fp8 maximum).
+    for (uint32_t k = 0; k < steps; ++k) {
+      const uint32_t base = (FP8 == 1 ? k : steps - 1 - k) * (kT * U);
       P hv[U];
       load_step(base, hv, Last{});
 #pragma unroll
@@ -1149,6 +1154,8 @@ int launch_wide(const FwdParams& p, hipStream_t s) {
   auto launch = [&](auto kernel) {
     static int occupancy_cache[64];  // per instantiation, per device
     int64_t grid = resident_blocks(kernel, kFwdWideThreads, occupancy_cache);
+    const int forced = tuning().fwd_grid_mult;  // FLN_FWD_GRID_MULT: blocks per CU
+    if (forced > 0 && grid > forced * device_cu_count()) grid = forced * device_cu_count();
     if (grid > p.rows) grid = p.rows;
     if (grid > kMaxGrid) grid = kMaxGrid;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kFwdWideThreads), 0, s, p);
