@@ -702,8 +702,10 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
 //     bitwise reproducible and need no E[x^2] - mean^2 cancellation.  RMSNorm sums squares;
 //   pass 2, fp8 with a per-row scale only: the row maximum of the outputs;
 //   last pass: outputs (and, with a residual, h = x + r written during pass 1).
-// x (and the residual) are read once per pass; the passes after the first find much of the row
-// in the L2 / Infinity Cache, as the block has just read it (the last pass loads non-temporal).
+// x (and the residual) are read once per pass, the passes walking the row in alternate
+// directions so that each starts on the lines the previous one read last, which are still in L2
+// (the last pass loads non-temporal).  Most of a later pass still comes from HBM: at 131072
+// bf16 columns a block's row is 256 KiB against an L2 share of 64-128 KiB per CU.
 // ---------------------------------------------------------------------------------------------
 constexpr int kFwdWideThreads = 1024;
 constexpr int kFwdWideStepBytes = 64;  // bytes of the row per thread and step (4 vectors)
