@@ -495,14 +495,14 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
 constexpr int kFwdLdsThreads = 1024;
 constexpr int kFwdLdsCpt = 8;  // vectors per thread: 128 KiB of LDS
 
-// CR > 0 (plain LayerNorm / RMSNorm only): rows of up to (8 + CR) vectors per thread, the first
+// CR > 0 (no residual, no fp8 output): rows of up to (8 + CR) vectors per thread, the first
 // 8 parked in LDS and the other CR kept in registers (cur).  The next row's LDS half is in
 // flight from the start of a row; its register half is loaded into cur once the outputs of the
 // current row's register half are written, in flight during the outputs of the LDS half.  (The
 // whole next row in flight as well spilled 205 VGPRs.)
 template <class T, int FP8, bool RES, int GELU, int VEC, int CR = 0>
 __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams p) {
-  static_assert(CR == 0 || (FP8 == 0 && !RES && GELU == 0), "register-extended rows: plain only");
+  static_assert(CR == 0 || (FP8 == 0 && !RES), "register-extended rows: no residual or fp8");
   constexpr int kT = kFwdLdsThreads;
   constexpr int CL = kFwdLdsCpt;  // vectors parked in LDS
   constexpr int CPT = CL + CR;    // vectors per thread in all
@@ -1187,18 +1187,27 @@ int launch_lds(const FwdParams& p, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-// Plain LayerNorm / RMSNorm rows of 8193..16384 vectors (16-bit 65537..131072 columns, fp32
-// 32769..65536): 8 vectors per thread parked in LDS, up to 8 in registers, so x is read from
-// HBM once.  Against the streamed wide-row kernel (which reads x twice), us: bf16 512 x 131072
+// LayerNorm / RMSNorm rows (and LN + GELU: tanh, or fp32) of 8193..16384 vectors (16-bit
+// 65537..131072 columns, fp32 32769..65536), without residual or fp8 output: 8 vectors per
+// thread parked in LDS, up to 8 in registers, so x is read from HBM once.  Against the
+// streamed wide-row kernel (which reads x twice), us: bf16 512 x 131072
 // LN 70.3 -> 58.5, RMSNorm 64.3 -> 55.1, 1024 x 65544 72.0 -> 60.2; fp16 512 x 131072 68.7 ->
-// 59.3; fp32 512 x 65536 66.8 -> 56.1, 1024 x 32772 70.1 -> 58.8.  The other flavours keep the
-// streamed kernel (their extra registers would spill).
+// 59.3; fp32 512 x 65536 66.8 -> 56.1, 1024 x 32772 70.1 -> 58.8; GELU tanh bf16 512 x 131072
+// 75.1 -> 67.9, fp32 1024 x 32772 71.7 -> 59.1; exact GELU fp32 512 x 65536 69.6 -> 59.9.  The
+// exact GELU of 16-bit rows keeps the streamed kernel (its polynomial, VALU-bound in one block
+// per CU: bf16 512 x 131072 79.0 -> 85.9 us), as do the residual and fp8 flavours (their extra
+// registers would spill: 13-42 VGPRs).
 template <class T, int VEC>
 int launch_lds_reg(const FwdParams& p, hipStream_t s) {
   int64_t grid = device_cu_count();
   if (grid > p.rows) grid = p.rows;
-  hipLaunchKernelGGL((fwd_lds_kernel<T, 0, false, 0, VEC, kFwdLdsCpt>),
-                     dim3(static_cast<unsigned>(grid)), dim3(kFwdLdsThreads), 0, s, p);
+  const dim3 g(static_cast<unsigned>(grid)), b(kFwdLdsThreads);
+  if (p.gelu == FLN_GELU_ERF)
+    hipLaunchKernelGGL((fwd_lds_kernel<T, 0, false, 1, VEC, kFwdLdsCpt>), g, b, 0, s, p);
+  else if (p.gelu == FLN_GELU_TANH)
+    hipLaunchKernelGGL((fwd_lds_kernel<T, 0, false, 2, VEC, kFwdLdsCpt>), g, b, 0, s, p);
+  else
+    hipLaunchKernelGGL((fwd_lds_kernel<T, 0, false, 0, VEC, kFwdLdsCpt>), g, b, 0, s, p);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -1368,7 +1377,7 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
             g.vpl, static_cast<int>(g.exact), g.threads);
   if (lds) return launch_lds<T, FP8, VV>(p, s);
   if constexpr (FP8 == 0) {
-    if (g.loop && vec_ok && p.res == nullptr && p.gelu == 0 &&
+    if (g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
         nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds)
       return launch_lds_reg<T, VV>(p, s);
   }

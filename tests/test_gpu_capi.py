@@ -673,10 +673,10 @@ WIDE_KINDS = ["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp
 def test_wide_rows_forward(lib, kind, dtype, rows, cols, aligned):
     """Rows past the LDS tile (16-bit > 65536 columns, fp32 > 32768) and long rows off the
     vector path (odd widths; 16-byte misaligned pointers) take the streamed wide-row kernel,
-    save plain LayerNorm / RMSNorm rows on the vector path of up to twice the tile (16-bit
-    131072, fp32 65536), which take the LDS-staged kernel with the rest of each row in
-    registers: every forward flavour against the oracle, statistics included, bitwise
-    reproducible (600 / 1100 rows: several rows per block).  MXFP8 at widths that are not a multiple of 32
+    save LayerNorm / RMSNorm / LN + GELU rows (tanh; erf in fp32) on the vector path of up to
+    twice the tile (16-bit 131072, fp32 65536), which take the LDS-staged kernel with the rest
+    of each row in registers: every forward flavour against the oracle, statistics included,
+    bitwise reproducible (600 / 1100 rows: several rows per block).  MXFP8 at widths that are not a multiple of 32
     must be refused before any launch, outputs untouched."""
     if kind.endswith("_mx") and cols % 32:
         x = torch.zeros(rows, cols, device="cuda", dtype=dtype)
