@@ -144,6 +144,11 @@ template <class T, bool DRES, int GELU, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   constexpr int PD = FLN_BWD_PREFETCH(VPL);  // rows in flight ahead of the current one
   constexpr int MAXW = MAXT / kWave;
+  // RAW: 16-bit rows of 18433..24576 columns, 3 vectors per lane in a 1024-thread block.  The
+  // row stays in the I/O type and is widened at each use: fp32 copies of x-hat and dy (48 VGPRs)
+  // would not fit the 128 a lane has there beside the column sums and the next row in flight.
+  constexpr bool RAW = VPL == 3 && MAXT == 1024;
+  static_assert(!RAW || GELU == 0, "the raw tiles have no GELU epilogue");
   // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
   __shared__ float red[2][2][MAXW + 16];
   __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
@@ -180,8 +185,8 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // 102.6 us, erf 153.2 -> 96.5 us; with a residual gradient 97.8 us on the LDS-staged kernel
   // -> 90.8 us here).
   constexpr bool PARAMS_IN_LDS =
-      (GELU != 0 || DRES) && ((VPL == 2 && MAXT == 1024) || (VPL == 3 && MAXT == 768)) &&
-      sizeof(T) == 2;
+      ((GELU != 0 || DRES) && ((VPL == 2 && MAXT == 1024) || (VPL == 3 && MAXT == 768)) &&
+       sizeof(T) == 2) || RAW;
   __shared__ P gsh[PARAMS_IN_LDS ? VPL * MAXT : 1], bsh[PARAMS_IN_LDS ? VPL * MAXT : 1];
   P gmr[PARAMS_IN_LDS ? 1 : VPL];
   P btr[GELU && !PARAMS_IN_LDS ? VPL : 1];
@@ -266,9 +271,10 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   // epilogue, dd holds twice the gradient at the LayerNorm output; kInvD takes the factor out once
   // per row (rstd and the row-sum coefficients) and once per block (the column partials), exactly.
   constexpr float kInvD = GELU != 0 ? 0.5f : 1.0f;
-  float xh[VPL][VEC], dd[VPL][VEC];
+  float xh[RAW ? 1 : VPL][VEC], dd[RAW ? 1 : VPL][VEC];
+  P xc[RAW ? VPL : 1], dc[RAW ? VPL : 1];  // RAW: the row's x and dy in the I/O type
   P rv[VPL];
-  float rs = 0.0f;
+  float rs = 0.0f, mu_c = 0.0f;
   // The statistics are the same in every lane of a wave (a wave works on one row), so they are
   // taken into scalar registers: the ring's VGPRs are free again as soon as the row is widened,
   // and the next load into the slot needs no register copy at the loop latch (such a copy would
@@ -279,6 +285,16 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   auto widen = [&](int slot) {
     rs = uniform(rsn[slot]);
     const float mu = uniform(mun[slot]);
+    if constexpr (RAW) {
+      mu_c = mu;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        xc[i] = xn[slot][i];
+        dc[i] = dn[slot][i];
+        if constexpr (DRES) rv[i] = rn[slot][i];
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
 #pragma unroll
@@ -344,16 +360,39 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     // g = dy gamma for dx below (one multiply per element serves both); with 16 the extra VGPRs
     // would spill, and dx forms dy (rstd gamma) instead.
     constexpr bool KEEP_G = VPL * VEC <= 8;
+    // x-hat and dy of element e of vector i: the widened row, or (RAW) widened from the packs
+    // at each use.
+    auto XH = [&](int i, int e) {
+      if constexpr (RAW)
+        return (to_f32(xc[i].v[e]) - mu_c) * rs;
+      else
+        return xh[i][e];
+    };
+    auto DD = [&](int i, int e) {
+      if constexpr (RAW)
+        return to_f32(dc[i].v[e]);
+      else
+        return dd[i][e];
+    };
     float s1 = 0.0f, s2 = 0.0f;
     float gd[VPL][VEC];
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        gd[i][e] = dd[i][e] * gam(i, e);
+        gd[i][e] = DD(i, e) * gam(i, e);
         s1 += gd[i][e];
-        s2 = fmaf(gd[i][e], xh[i][e], s2);
+        s2 = fmaf(gd[i][e], XH(i, e), s2);
       }
+    // RAW: the packs become opaque here, so that dx widens them again rather than the compiler
+    // keeping the fp32 values of the row sums alive across the reduction.
+    if constexpr (RAW) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        keep_packed(xc[i]);
+        keep_packed(dc[i]);
+      }
+    }
     s1 = wave_allreduce<SumOp>(s1);
     s2 = wave_allreduce<SumOp>(s2);
     if (wpr > 1) {
@@ -375,12 +414,13 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float dxv = KEEP_G ? fmaf(rsd, gd[i][e], fmaf(cx, xh[i][e], cb))
-                           : fmaf(dd[i][e], rsd * gam(i, e), fmaf(cx, xh[i][e], cb));
+        const float x_h = XH(i, e), d_d = DD(i, e);
+        float dxv = KEEP_G ? fmaf(rsd, gd[i][e], fmaf(cx, x_h, cb))
+                           : fmaf(d_d, rsd * gam(i, e), fmaf(cx, x_h, cb));
         if constexpr (DRES) dxv += to_f32(rv[i].v[e]);
         o[i].v[e] = from_f32<T>(dxv);
-        acc_g[i][e] = fmaf(dd[i][e], xh[i][e], acc_g[i][e]);
-        acc_b[i][e] += dd[i][e];
+        acc_g[i][e] = fmaf(d_d, x_h, acc_g[i][e]);
+        acc_b[i][e] += d_d;
       }
     const rsrc_t xo = make_rsrc(DX ? DX + row * N : nullptr, nb);
 #pragma unroll
@@ -425,15 +465,15 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
 }
 
 // Rows wider than the register kernel holds for their flavour (fp32 rows of 8193..16384 columns;
-// 16-bit LayerNorm / RMSNorm rows of 18433..24576 columns without a residual gradient, and fp16
-// rows of 16385..18432 columns with one): one NT-thread block per row at a time, thread t owning vectors t + NT i
+// fp16 rows of 16385..18432 columns with a residual gradient): one NT-thread block per row at a
+// time, thread t owning vectors t + NT i
 // (i < CPT) of every row.  Pass A consumes the row's raw loads (issued one row ahead, like the
 // register kernel's ring), accumulates the column sums of dy xhat and dy in registers, forms the
 // row sums and parks the raw x / dy vectors in LDS; after the row reduction, pass B reads them back
 // and writes dx.  A thread reads back only the vectors it parked, so the staging needs no barrier:
 // LDS serves as per-thread spill space for the row (128 KiB at CPT 4 and 1024 threads).
 // NT = 1024 leaves 128 VGPRs per lane; NT = 768 (12 waves, 3 per SIMD) leaves 168 for the fp32
-// column sums and the prefetched row of a 16-bit lane with 3-4 vectors (gamma in LDS).
+// column sums and the prefetched row of a 16-bit lane with 3 vectors (gamma in LDS).
 constexpr int kLdsThreads = 1024;
 constexpr int kLds16Threads = 768;
 
@@ -442,7 +482,7 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
   constexpr int kT = NT;
   constexpr int kW = kT / kWave;
   using P = Pack<T, VEC>;
-  // 768-thread blocks (16-bit rows) keep gamma in LDS too, thread-private like the row: 12-16
+  // 768-thread blocks (16-bit rows) keep gamma in LDS too, thread-private like the row: 12
   // VGPRs per lane that would otherwise spill.
   constexpr bool PARAMS_IN_LDS = NT == kLds16Threads && CPT >= 3;
   __shared__ P xs[CPT * kT], ds[CPT * kT];
@@ -612,8 +652,8 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
 }
 
 // Rows past the register and LDS tiles (16-bit rows of more than 18432 columns, save the
-// LayerNorm / RMSNorm rows of up to 24576 without a residual gradient; fp32 rows of more than
-// 16384; long rows on the scalar path), any width, in two streaming passes:
+// LayerNorm / RMSNorm rows of up to 24576 without a residual gradient (raw tiles); fp32 rows of
+// more than 16384; long rows on the scalar path), any width, in two streaming passes:
 //   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
 //     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
 //     rows grid-stride, four vectors per thread in flight per array;
@@ -926,9 +966,16 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
 template <class T, int VEC, int VPL>
 int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                   int64_t* resident) {
-  // Three vectors per lane only in 768-thread blocks (168 VGPRs per lane).
+  // Three vectors per lane: 768-thread blocks (168 VGPRs per lane), or the raw tiles of
+  // 1024-thread blocks (LayerNorm / RMSNorm without a residual gradient).
+  if constexpr (VPL == 3) {
+    if (threads == 1024) {
+      if (p.gelu != 0 || p.dres) return FLN_ERR_INVALID;
+      return launch_stage1_k<T, false, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
+    }
+    if (threads != kReg3Threads) return FLN_ERR_INVALID;
+  }
   constexpr int MAXT = VPL == 3 ? kReg3Threads : 1024;
-  if (VPL == 3 && threads != kReg3Threads) return FLN_ERR_INVALID;
   // GELU is never combined with a residual gradient (no entry point passes both).
   if (p.gelu == 1)
     return launch_stage1_k<T, false, 1, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
@@ -1020,9 +1067,6 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
         const dim3 grid(static_cast<unsigned>(geo.blocks)), block(kLds16Threads);
         if (geo.lds_cpt == 3 && p.dres && !p.gelu)
           hipLaunchKernelGGL((bwd_lds_kernel<T, true, 0, VV, 3, kLds16Threads>), grid, block, 0,
-                             s, p);
-        else if (geo.lds_cpt == 4 && !p.dres && !p.gelu)
-          hipLaunchKernelGGL((bwd_lds_kernel<T, false, 0, VV, 4, kLds16Threads>), grid, block, 0,
                              s, p);
         else
           return FLN_ERR_INVALID;
@@ -1149,22 +1193,32 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
     g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
   }
+  // 16-bit LayerNorm / RMSNorm rows of 18433..24576 columns without a residual gradient: the raw
+  // tiles (3 vectors per lane of a 1024-thread block, the row kept in the I/O type).  Against
+  // the LDS-staged kernel with 4 vectors per thread in 768 threads they replaced, bf16 backward
+  // calls, us: 4096 x 20480 LN 146.0 -> 101.4, RMSNorm 129.5 -> 95.8, 4096 x 24576 163.8 ->
+  // 118.7 (fp16 161.4 -> 117.5), 2048 x 19000 93.0 -> 63.2, 300 x 24576 56.1 -> 32.5.
+  if (!g.reg_path && es == 2 && g.vec == 8 && nvec > 3 * kReg3Threads && nvec <= 3 * 1024 &&
+      !dres && !gelu && tun.bwd_no_lds == 0) {
+    g.reg_path = true;
+    g.vpl = 3;
+    g.threads = 1024;
+    g.wpr = 1024 / kWave;
+    g.rgs = 1;
+    g.blocks = rows < device_cu_count() ? rows : device_cu_count();
+    g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
+  }
   // fp32 rows too wide for registers but within 4 vectors per thread of a 1024-thread block
   // (8193..16384 columns): the LDS-staged kernel, one block per CU, rows dealt grid-stride.
-  // (16-bit rows past 18432 columns need 64 VGPRs of column sums per lane on top of the
-  // prefetched row and spill even at 768 threads.)  16-bit rows of 8193..16384 columns with a
-  // residual gradient keep the register kernel (gamma in LDS there), measured faster than 2
-  // vectors per thread here (4096 x 16384 bf16: 90.8 against 97.8 us).  16-bit LayerNorm /
-  // RMSNorm rows of 18433..24576 columns without a residual gradient take it with 768 threads
-  // and 4 vectors per thread (gamma parked in LDS as well; 44 B of spill left), and fp16 rows
-  // of 16385..18432 columns with one, 3 vectors per thread: measured faster than the two passes
-  // (4096 x 18432 bf16: LN 161 -> 108 us, + residual 164 -> 110 us; 4096 x 20480 LN 170 ->
-  // 146 us).
+  // 16-bit rows of 8193..16384 columns with a residual gradient keep the register kernel
+  // (gamma in LDS there), measured faster than 2 vectors per thread here (4096 x 16384 bf16:
+  // 90.8 against 97.8 us).  fp16 rows of 16385..18432 columns with a residual gradient take it
+  // with 768 threads and 3 vectors per thread (gamma parked in LDS as well), measured faster
+  // than the two passes (4096 x 18432 bf16: LN 161 -> 108 us, + residual 164 -> 110 us).
   const int64_t cpt = (nvec + kLdsThreads - 1) / kLdsThreads;
   const int64_t cpt16 = (nvec + kLds16Threads - 1) / kLds16Threads;
   const bool wide_f32 = !g.reg_path && es == 4 && cpt >= 3 && cpt <= 4;
-  const bool wide16 = !g.reg_path && es == 2 && !gelu &&
-                      ((cpt16 == 3 && dres && dtype == FLN_F16) || (cpt16 == 4 && !dres));
+  const bool wide16 = !g.reg_path && es == 2 && !gelu && cpt16 == 3 && dres && dtype == FLN_F16;
   if (g.vec > 1 && (wide_f32 || wide16) && tun.bwd_no_lds == 0) {
     g.reg_path = false;
     g.lds_cpt = wide16 ? static_cast<int>(cpt16) : static_cast<int>(cpt);

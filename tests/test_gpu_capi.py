@@ -1070,7 +1070,7 @@ ROUTE_WIDTHS_32 = [4096, 4100, 8192, 8196, 16384, 16388, 32768, 32772]
 @pytest.mark.parametrize("nrows", ["few", "many"])
 def test_route_boundaries(lib, dtype, nrows, cols):
     """Widths on both sides of every kernel-route boundary (register tiles, RAW tiles, the
-    768-thread register backward with 3 vectors, the 768-thread LDS backward with 4, the LDS-staged forward, the two passes, the
+    768-thread register backward with 3 vectors, the backward raw tiles, the LDS-staged forward, the two passes, the
     streamed wide forward) at a few rows (small backward blocks) and at several rows per block:
     LayerNorm fwd + bwd with a residual gradient and RMSNorm fwd + bwd against the oracle."""
     rows = 37 if nrows == "few" else (700 if cols <= 32776 else 300)
@@ -1117,18 +1117,20 @@ def test_route_boundaries(lib, dtype, nrows, cols):
 @pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_tanh", "gelu_none"])
 @pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 18432), (torch.float16, 16392),
                                         (torch.bfloat16, 17416), (torch.bfloat16, 20480),
-                                        (torch.float16, 24576)],
+                                        (torch.bfloat16, 19000), (torch.float16, 24576)],
                          ids=["bf16-18432", "f16-16392", "bf16-17416", "bf16-20480",
-                              "f16-24576"])
+                              "bf16-19000", "f16-24576"])
 def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
     """16-bit rows of 16385..18432 columns take the register backward with one row per
     768-thread block and 3 vectors per lane (the last ones partly past the row; gamma / beta
     parked in LDS for the residual and GELU flavours; 600 rows: several per block) for every
     flavour but fp16 with a residual gradient, which takes the LDS-staged backward with
-    768-thread blocks, as do LayerNorm / RMSNorm rows of up to 24576 with 4 vectors per thread;
-    the residual and GELU flavours past 18432 keep the two passes.  Parity with the oracle,
-    bitwise reproducible, and agreement with the two-pass backward (FLN_BWD_NO_LDS, which
-    turns off both the 768-thread register and the LDS-staged kernels)."""
+    768-thread blocks; LayerNorm / RMSNorm rows of 18433..24576 take the raw tiles (3 vectors
+    per lane of a 1024-thread block, the row kept in the I/O type; 19000 columns: the last
+    vectors partly past the row); the residual and GELU flavours past 18432 keep the two
+    passes.  Parity with the oracle, bitwise reproducible, and agreement with the two-pass
+    backward (FLN_BWD_NO_LDS, which turns off the 768-thread register, raw-tile and LDS-staged
+    kernels)."""
     rows = 600
     gen = torch.Generator().manual_seed(cols + 5 * len(kind))
     xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
