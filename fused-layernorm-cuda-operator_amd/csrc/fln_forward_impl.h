@@ -579,6 +579,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       if (i >= cpt) continue;  // uniform
+      // (indices clamped so that neither arm names an element past its array)
       P v = i < CX ? xr[i < CX ? i : 0] : cur[i >= CL ? i - CL : 0];
       if constexpr (RES) {
 #pragma unroll
@@ -664,7 +665,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
         const rsrc_t br = make_rsrc(p.bscale + row * nblk, nblk);
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-      if (i >= cpt) continue;  // uniform
+          if (i >= cpt) continue;  // uniform
           const int v = t + i * kT;
           const P xv = row_vec(i);
           const P gv = buf_load<P>(g_rs, v);
@@ -687,7 +688,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
         float am = 0.0f;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-      if (i >= cpt) continue;  // uniform
+          if (i >= cpt) continue;  // uniform
           const int v = t + i * kT;
           const P xv = row_vec(i);
           const P gv = buf_load<P>(g_rs, v);
@@ -701,7 +702,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
         const float inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // 1 ulp
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-      if (i >= cpt) continue;  // uniform
+          if (i >= cpt) continue;  // uniform
           const int v = t + i * kT;
           const P xv = row_vec(i);
           const P gv = buf_load<P>(g_rs, v);
