@@ -511,6 +511,16 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
   using QW = typename BufIO<VEC>::W;  // VEC fp8 codes (VEC is 4 or 8 here)
   __shared__ P xs[CL * kT];
   __shared__ float red[2][3][kW + 16];  // [parity][sum, centred sum of squares, max][wave]
+  // Exact GELU of 16-bit rows: the log2 Phi table (4 KiB), one entry per thread, as in the
+  // register kernel; fp32 rows keep the polynomial (their kernels are not VALU-bound, and the
+  // table reads slowed them: 1024 x 24576 41.2 -> 43.0 us).
+  constexpr bool TAB = GELU == 1 && sizeof(T) == 2;
+  __shared__ float4 gelu_tab[TAB ? kGeluLogTabN : 1];
+  if constexpr (TAB) {
+    if (threadIdx.x < kGeluLogTabN)
+      gelu_tab[threadIdx.x] = reinterpret_cast<const float4*>(kGeluLogTabData)[threadIdx.x];
+    __syncthreads();
+  }
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -620,7 +630,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
       (void)i;
       float a = fmaf((to_f32(xv.v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
                      to_f32(bv.v[e]));
-      if constexpr (GELU == 1) a = gelu_erf(a);
+      if constexpr (GELU == 1) a = TAB ? gelu_erf_tab(gelu_tab, a) : gelu_erf(a);
       if constexpr (GELU == 2) a = gelu_tanh(a);
       return a;
     };
@@ -754,6 +764,16 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
   constexpr int U = kFwdWideStepBytes / (VEC * static_cast<int>(sizeof(T)));
   using P = Pack<T, VEC>;
   __shared__ float red[2][3][kW + 16];  // [parity][reduction][wave], padded
+  // Exact GELU of 16-bit rows: the log2 Phi table (4 KiB), one entry per thread, as in the
+  // register kernel; fp32 rows keep the polynomial (their kernels are not VALU-bound, and the
+  // table reads slowed them: 1024 x 24576 41.2 -> 43.0 us).
+  constexpr bool TAB = GELU == 1 && sizeof(T) == 2;
+  __shared__ float4 gelu_tab[TAB ? kGeluLogTabN : 1];
+  if constexpr (TAB) {
+    if (threadIdx.x < kGeluLogTabN)
+      gelu_tab[threadIdx.x] = reinterpret_cast<const float4*>(kGeluLogTabData)[threadIdx.x];
+    __syncthreads();
+  }
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -858,7 +878,7 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
     auto affine = [&](const P& hv, const P& gv, const P& bv, int e) -> float {
       float a = fmaf((to_f32(hv.v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
                      to_f32(bv.v[e]));
-      if constexpr (GELU == 1) a = gelu_erf(a);
+      if constexpr (GELU == 1) a = TAB ? gelu_erf_tab(gelu_tab, a) : gelu_erf(a);
       if constexpr (GELU == 2) a = gelu_tanh(a);
       return a;
     };

@@ -77,13 +77,17 @@ def test_c2_layernorm_gelu_fp32(lib, name, mode):
 @pytest.mark.parametrize("mode", ["none", "tanh"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
                          ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("cols", [4096, 7168, 18432], ids=["4096", "7168", "18432"])
+@pytest.mark.parametrize("cols", [4096, 7168, 18432, 40960, 131072],
+                         ids=["4096", "7168", "18432", "40960", "131072"])
 def test_gelu_full_range_fwd_bwd(lib, mode, dtype, cols):
     """LN + GELU forward and backward with the GELU input swept over [-13, 13] (beta a ramp) and a
     random dy: the GELU and GELU' tables (|a| < 6 interpolated, past 6 the constant last
     interval; the forward's log table out to 16) against the oracle at both signs and across
     every interval boundary, for both forms; 18432 columns take the 768-thread register backward
-    with 3 vectors per lane (16-bit) and the two-pass one (fp32)."""
+    with 3 vectors per lane (16-bit) and the two-pass one (fp32); 40960 and 131072 columns the
+    LDS-staged forward (the 16-bit exact GELU from its LDS table, fp32 from the polynomial),
+    the 16-bit exact GELU at 131072 the streamed wide-row forward (table), and the two-pass
+    backward."""
     rows = 48
     gen = torch.Generator().manual_seed(977 + (mode == "tanh") + cols)
     xc = (torch.rand(rows, cols, generator=gen) * 2 - 1).to(dtype)
