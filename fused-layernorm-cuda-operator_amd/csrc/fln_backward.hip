@@ -145,10 +145,11 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
   constexpr int PD = FLN_BWD_PREFETCH(VPL);  // rows in flight ahead of the current one
   constexpr int MAXW = MAXT / kWave;
   // RAW: 16-bit rows of 18433..24576 columns, 3 vectors per lane in a 1024-thread block.  The
-  // row stays in the I/O type and is widened at each use: fp32 copies of x-hat and dy (48 VGPRs)
-  // would not fit the 128 a lane has there beside the column sums and the next row in flight.
+  // row stays in the I/O type and is widened at each use (with GELU, GELU' is looked up at each
+  // use too): fp32 copies of x-hat and dy (48 VGPRs) would not fit the 128 a lane has there
+  // beside the column sums and the next row in flight.
   constexpr bool RAW = VPL == 3 && MAXT == 1024;
-  static_assert(!RAW || GELU == 0, "the raw tiles have no GELU epilogue");
+
   // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
   __shared__ float red[2][2][MAXW + 16];
   __shared__ float comb[MAXT * VEC];         // row-group combine, one vector slot at a time
@@ -369,10 +370,16 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
         return xh[i][e];
     };
     auto DD = [&](int i, int e) {
-      if constexpr (RAW)
-        return to_f32(dc[i].v[e]);
-      else
+      if constexpr (RAW) {
+        float d = to_f32(dc[i].v[e]);
+        if constexpr (GELU != 0) {
+          const float u = kGeluTabInvH * fmaf(XH(i, e), gam(i, e), bet(i, e));
+          d = fmaf(d, gelu_grad2_sign_tab(gelu_tab, u), d);
+        }
+        return d;
+      } else {
         return dd[i][e];
+      }
     };
     float s1 = 0.0f, s2 = 0.0f;
     float gd[VPL][VEC];
@@ -651,9 +658,9 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
   }
 }
 
-// Rows past the register and LDS tiles (16-bit rows of more than 18432 columns, save the
-// LayerNorm / RMSNorm rows of up to 24576 without a residual gradient (raw tiles); fp32 rows of
-// more than 16384; long rows on the scalar path), any width, in two streaming passes:
+// Rows past the register and LDS tiles (16-bit rows of more than 18432 columns, save the rows
+// of up to 24576 without a residual gradient (raw tiles); fp32 rows of more than 16384; long
+// rows on the scalar path), any width, in two streaming passes:
 //   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
 //     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
 //     rows grid-stride, four vectors per thread in flight per array;
@@ -967,10 +974,14 @@ template <class T, int VEC, int VPL>
 int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                   int64_t* resident) {
   // Three vectors per lane: 768-thread blocks (168 VGPRs per lane), or the raw tiles of
-  // 1024-thread blocks (LayerNorm / RMSNorm without a residual gradient).
+  // 1024-thread blocks (no residual gradient).
   if constexpr (VPL == 3) {
     if (threads == 1024) {
-      if (p.gelu != 0 || p.dres) return FLN_ERR_INVALID;
+      if (p.dres) return FLN_ERR_INVALID;
+      if (p.gelu == 1)
+        return launch_stage1_k<T, false, 1, VEC, 3, 1024>(p, blocks, threads, s, resident);
+      if (p.gelu == 2)
+        return launch_stage1_k<T, false, 2, VEC, 3, 1024>(p, blocks, threads, s, resident);
       return launch_stage1_k<T, false, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
     }
     if (threads != kReg3Threads) return FLN_ERR_INVALID;
@@ -1193,13 +1204,15 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
     g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
   }
-  // 16-bit LayerNorm / RMSNorm rows of 18433..24576 columns without a residual gradient: the raw
-  // tiles (3 vectors per lane of a 1024-thread block, the row kept in the I/O type).  Against
-  // the LDS-staged kernel with 4 vectors per thread in 768 threads they replaced, bf16 backward
-  // calls, us: 4096 x 20480 LN 146.0 -> 101.4, RMSNorm 129.5 -> 95.8, 4096 x 24576 163.8 ->
-  // 118.7 (fp16 161.4 -> 117.5), 2048 x 19000 93.0 -> 63.2, 300 x 24576 56.1 -> 32.5.
+  // 16-bit rows of 18433..24576 columns without a residual gradient: the raw tiles (3 vectors
+  // per lane of a 1024-thread block, the row kept in the I/O type).  Against the LDS-staged
+  // kernel with 4 vectors per thread in 768 threads they replaced, bf16 backward calls, us:
+  // 4096 x 20480 LN 146.0 -> 101.4, RMSNorm 129.5 -> 95.8, 4096 x 24576 163.8 -> 118.7 (fp16
+  // 161.4 -> 117.5), 2048 x 19000 93.0 -> 63.2, 300 x 24576 56.1 -> 32.5; the GELU flavours
+  // against the two passes (68 B of spill left): 4096 x 20480 erf 220.8 -> 184.3, tanh 201.1
+  // -> 184.0, 4096 x 24576 erf 243.8 -> 197.3.
   if (!g.reg_path && es == 2 && g.vec == 8 && nvec > 3 * kReg3Threads && nvec <= 3 * 1024 &&
-      !dres && !gelu && tun.bwd_no_lds == 0) {
+      !dres && tun.bwd_no_lds == 0) {
     g.reg_path = true;
     g.vpl = 3;
     g.threads = 1024;

@@ -1129,10 +1129,10 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
     768-thread block and 3 vectors per lane (the last ones partly past the row; gamma / beta
     parked in LDS for the residual and GELU flavours; 600 rows: several per block) for every
     flavour but fp16 with a residual gradient, which takes the LDS-staged backward with
-    768-thread blocks; LayerNorm / RMSNorm rows of 18433..24576 take the raw tiles (3 vectors
-    per lane of a 1024-thread block, the row kept in the I/O type; 19000 columns: the last
-    vectors partly past the row); the residual and GELU flavours past 18432 keep the two
-    passes.  Parity with the oracle, bitwise reproducible, and agreement with the two-pass
+    768-thread blocks; rows of 18433..24576 without a residual gradient take the raw tiles (3
+    vectors per lane of a 1024-thread block, the row kept in the I/O type, GELU' looked up at
+    each use; 19000 columns: the last vectors partly past the row); the residual flavour past
+    18432 keeps the two passes.  Parity with the oracle, bitwise reproducible, and agreement with the two-pass
     backward (FLN_BWD_NO_LDS, which turns off the 768-thread register, raw-tile and LDS-staged
     kernels)."""
     rows = 600
