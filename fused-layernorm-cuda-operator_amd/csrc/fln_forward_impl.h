@@ -1217,7 +1217,8 @@ int launch_lds(const FwdParams& p, hipStream_t s) {
 // 75.1 -> 67.9, fp32 1024 x 32772 71.7 -> 59.1; exact GELU fp32 512 x 65536 69.6 -> 59.9.  The
 // exact GELU of 16-bit rows keeps the streamed kernel (its polynomial, VALU-bound in one block
 // per CU: bf16 512 x 131072 79.0 -> 85.9 us), as do the residual and fp8 flavours (their extra
-// registers would spill: 13-42 VGPRs).
+// registers spill: 17-42 VGPRs; LN -> fp8 bf16 512 x 131072 72.1 -> 75.1 us, MXFP8 58.6 ->
+// 77.7 us, though 1024 x 65544 gained, 79.4 -> 72.3).
 template <class T, int VEC>
 int launch_lds_reg(const FwdParams& p, hipStream_t s) {
   int64_t grid = device_cu_count();
