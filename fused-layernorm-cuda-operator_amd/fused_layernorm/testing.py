@@ -60,9 +60,12 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
     Workload("rms_fwd_bwd_bf16_8192x4096", "rms_norm_fwd_bwd", 8192, 4096, torch.bfloat16, 3,
              1e-6, (1.0, 0.02), None),
     # Wide rows (profiled, not benchmark lines): the RAW-tile forward with the 768-thread
-    # LDS-staged backward; the streamed wide-row forward with the two-pass backward; the GELU
-    # backward with gamma / beta in LDS.
+    # register backward (3 vectors per lane), and with the backward's raw tiles at 20480; the
+    # LDS-staged forward with half of each row in registers and the two-pass backward at 131072;
+    # the GELU backward with gamma / beta in LDS.
     Workload("wide_ln_fwd_bwd_bf16_4096x18432", "layer_norm_fwd_bwd", 4096, 18432,
+             torch.bfloat16, 8, 1e-5, (1.0, 0.02), (0.0, 0.02)),
+    Workload("wide_ln_fwd_bwd_bf16_4096x20480", "layer_norm_fwd_bwd", 4096, 20480,
              torch.bfloat16, 8, 1e-5, (1.0, 0.02), (0.0, 0.02)),
     Workload("wide_ln_fwd_bwd_bf16_512x131072", "layer_norm_fwd_bwd", 512, 131072,
              torch.bfloat16, 9, 1e-5, (1.0, 0.02), (0.0, 0.02)),
