@@ -142,13 +142,18 @@ __device__ __forceinline__ void reduce_quad_block(const ColReduceArgs& a, int64_
 // of dy GELU'(a)).
 template <class T, bool DRES, int GELU, int VEC, int VPL, int MAXT>
 __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
-  constexpr int PD = FLN_BWD_PREFETCH(VPL);  // rows in flight ahead of the current one
   constexpr int MAXW = MAXT / kWave;
   // RAW: 16-bit rows of 18433..24576 columns, 3 vectors per lane in a 1024-thread block.  The
   // row stays in the I/O type and is widened at each use (with GELU, GELU' is looked up at each
   // use too): fp32 copies of x-hat and dy (48 VGPRs) would not fit the 128 a lane has there
   // beside the column sums and the next row in flight.
-  constexpr bool RAW = VPL == 3 && MAXT == 1024;
+  constexpr bool RAW = (VPL == 3 || VPL == 4) && MAXT == 1024 && VEC == 8 && sizeof(T) == 2;
+  // NOPF: 4 vectors per lane (rows of 24577..32768 columns) leave no room for the next row:
+  // each row is loaded at the top of its own step (one block per CU; the row's stores are still
+  // in flight while the next row loads).
+  constexpr bool NOPF = RAW && VPL == 4;
+  static_assert(!NOPF || (GELU == 0 && !DRES), "4-vector raw tiles: LayerNorm / RMSNorm only");
+  constexpr int PD = NOPF ? 1 : FLN_BWD_PREFETCH(VPL);  // rows in flight ahead of the current one
 
   // [double buffer][sum g, sum g*xhat][wave], padded for combine_partials
   __shared__ float red[2][2][MAXW + 16];
@@ -331,7 +336,7 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     asm volatile("" ::: "memory");
   }
 #pragma unroll
-  for (int k = 0; k < PD; ++k) {
+  for (int k = 0; k < (NOPF ? 0 : PD); ++k) {
     load_row(k, k);
 #pragma unroll
     for (int i = 0; i < VPL; ++i)  // distinct, non-adjacent: none merged away
@@ -355,8 +360,9 @@ __global__ __launch_bounds__(MAXT) void bwd_reg_kernel(const BwdParams p) {
     const int64_t row = row_of(it);
     const uint32_t nb = bytes_of(it);
     // Consume slot sl (row it) and put row it + PD in flight in its place.
+    if constexpr (NOPF) load_row(it, sl);
     widen(sl);
-    load_row(it + PD, sl);
+    if constexpr (!NOPF) load_row(it + PD, sl);
     // Row sums (elements past the row are zero in dy, hence in g).  A lane with 8 columns keeps
     // g = dy gamma for dx below (one multiply per element serves both); with 16 the extra VGPRs
     // would spill, and dx forms dy (rstd gamma) instead.
@@ -973,28 +979,35 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
 template <class T, int VEC, int VPL>
 int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                   int64_t* resident) {
-  // Three vectors per lane: 768-thread blocks (168 VGPRs per lane), or the raw tiles of
-  // 1024-thread blocks (no residual gradient).
-  if constexpr (VPL == 3) {
-    if (threads == 1024) {
-      if (p.dres) return FLN_ERR_INVALID;
-      if (p.gelu == 1)
-        return launch_stage1_k<T, false, 1, VEC, 3, 1024>(p, blocks, threads, s, resident);
-      if (p.gelu == 2)
-        return launch_stage1_k<T, false, 2, VEC, 3, 1024>(p, blocks, threads, s, resident);
-      return launch_stage1_k<T, false, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
+  // Four vectors per lane on the 16-bit vector path: the raw tiles without a prefetched row
+  // (LayerNorm / RMSNorm only).
+  if constexpr (VPL == 4 && VEC == 8 && sizeof(T) == 2) {
+    if (threads != 1024 || p.gelu != 0 || p.dres) return FLN_ERR_INVALID;
+    return launch_stage1_k<T, false, 0, VEC, 4, 1024>(p, blocks, threads, s, resident);
+  } else {
+    // Three vectors per lane: 768-thread blocks (168 VGPRs per lane), or the raw tiles of
+    // 1024-thread blocks (no residual gradient).
+    if constexpr (VPL == 3) {
+      if (threads == 1024) {
+        if (p.dres) return FLN_ERR_INVALID;
+        if (p.gelu == 1)
+          return launch_stage1_k<T, false, 1, VEC, 3, 1024>(p, blocks, threads, s, resident);
+        if (p.gelu == 2)
+          return launch_stage1_k<T, false, 2, VEC, 3, 1024>(p, blocks, threads, s, resident);
+        return launch_stage1_k<T, false, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
+      }
+      if (threads != kReg3Threads) return FLN_ERR_INVALID;
     }
-    if (threads != kReg3Threads) return FLN_ERR_INVALID;
+    constexpr int MAXT = VPL == 3 ? kReg3Threads : 1024;
+    // GELU is never combined with a residual gradient (no entry point passes both).
+    if (p.gelu == 1)
+      return launch_stage1_k<T, false, 1, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
+    if (p.gelu == 2)
+      return launch_stage1_k<T, false, 2, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
+    if (p.dres)
+      return launch_stage1_k<T, true, 0, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
+    return launch_stage1_k<T, false, 0, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
   }
-  constexpr int MAXT = VPL == 3 ? kReg3Threads : 1024;
-  // GELU is never combined with a residual gradient (no entry point passes both).
-  if (p.gelu == 1)
-    return launch_stage1_k<T, false, 1, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
-  if (p.gelu == 2)
-    return launch_stage1_k<T, false, 2, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
-  if (p.dres)
-    return launch_stage1_k<T, true, 0, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
-  return launch_stage1_k<T, false, 0, VEC, VPL, MAXT>(p, blocks, threads, s, resident);
 }
 
 template <class T, int VEC>
@@ -1011,7 +1024,8 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
         return launch_stage1<T, VEC, 3>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 4:
-      if constexpr (CAP >= 4) return launch_stage1<T, VEC, 4>(p, blocks, threads, s, resident);
+      if constexpr (CAP >= 4 || (sizeof(T) == 2 && VEC == 8))
+        return launch_stage1<T, VEC, 4>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 8:
       if constexpr (CAP >= 8) return launch_stage1<T, VEC, 8>(p, blocks, threads, s, resident);
@@ -1215,6 +1229,23 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
       !dres && tun.bwd_no_lds == 0) {
     g.reg_path = true;
     g.vpl = 3;
+    g.threads = 1024;
+    g.wpr = 1024 / kWave;
+    g.rgs = 1;
+    g.blocks = rows < device_cu_count() ? rows : device_cu_count();
+    g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
+  }
+  // 16-bit LayerNorm / RMSNorm rows of 24577..32768 columns without a residual gradient, at
+  // least 6 rows per CU: the raw tiles with 4 vectors per lane and no prefetched row (a block's
+  // row loads are exposed, so the rows of a block must be many).  Against the two passes, bf16
+  // backward calls, us: 2048 x 32768 126.4 -> 110.1, 4096 x 32768 235.1 -> 188.3, 1536 x 32768
+  // 99.9 -> 91.8, RMSNorm 2048 x 28672 121.2 -> 92.2, fp16 2048 x 32768 124.5 -> 105.9; with
+  // fewer rows the two passes win (1024 x 32768 71.6 against 74.0, 300 x 32768 37.2 against
+  // 49.0).
+  if (!g.reg_path && es == 2 && g.vec == 8 && nvec > 3 * 1024 && nvec <= 4 * 1024 && !dres &&
+      !gelu && rows >= 6 * int64_t(device_cu_count()) && tun.bwd_no_lds == 0) {
+    g.reg_path = true;
+    g.vpl = 4;
     g.threads = 1024;
     g.wpr = 1024 / kWave;
     g.rgs = 1;

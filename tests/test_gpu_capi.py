@@ -1118,6 +1118,61 @@ def test_route_boundaries(lib, dtype, nrows, cols):
     assert_close_rel(to_np(dw), dw_ref, 1e-4, "dweight")
 
 
+@pytest.mark.parametrize("kind,dtype,cols", [("ln", torch.bfloat16, 32768),
+                                              ("rms", torch.float16, 28000),
+                                              ("ln", torch.bfloat16, 24584)],
+                         ids=["ln-bf16-32768", "rms-f16-28000", "ln-bf16-24584"])
+def test_raw4_backward_many_rows(lib, monkeypatch, kind, dtype, cols):
+    """16-bit LayerNorm / RMSNorm rows of 24577..32768 columns with at least 6 rows per CU take
+    the backward raw tiles with 4 vectors per lane and no prefetched row (1600 rows: 6-7 per
+    block; 28000 / 24584 columns: the last vectors partly past the row).  dx within 1 ulp of the
+    C oracle, the parameter gradients to 1e-4, bitwise reproducible, and agreement with the two
+    passes (FLN_BWD_NO_LDS)."""
+    rows = 1600
+    gen = torch.Generator().manual_seed(cols + 3)
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, dy = cuda(xc), cuda(gc), cuda(dyc)
+    xs, gs, dys = f32(xc), f32(gc), f32(dyc)
+    ulp_kind = "bf16" if dtype == torch.bfloat16 else "f16"
+    if kind == "rms":
+        _, rstd = rms_forward(lib, x, g, 1e-6)
+
+        def run():
+            dx, dw = rms_backward(lib, dy, x, rstd, g)
+            return dx, dw, None
+        dx_ref, dg_ref = c_oracle.rmsnorm_bwd(dys, xs, gs, 1e-6)
+        db_ref = None
+    else:
+        _, mean, rstd = ln_forward(lib, x, g, None, 1e-5)
+
+        def run():
+            return ln_backward(lib, dy, x, mean, rstd, g)
+        dx_ref, dg_ref, db_ref = c_oracle.layernorm_bwd(dys, xs, gs, 1e-5)
+    dx, dg, db = run()
+    assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                      kind=ulp_kind, what="dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    if db is not None:
+        assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+    again = run()
+    for a, c in zip((dx, dg, db), again):
+        if a is not None:
+            assert torch.equal(a, c)
+    monkeypatch.setenv("FLN_BWD_NO_LDS", "1")
+    capi.reload_tuning()
+    two_pass = run()
+    monkeypatch.delenv("FLN_BWD_NO_LDS")
+    capi.reload_tuning()
+    assert_within_ulp(to_np(dx), to_np(two_pass[0]), 1.0,
+                      atol=DX_ATOL_REL * float(two_pass[0].abs().max()), kind=ulp_kind,
+                      what="dx vs two passes")
+    for a, c in zip((dg, db), two_pass[1:]):
+        if a is not None:
+            assert_close_rel(to_np(a), to_np(c), 1e-5, "parameter gradient vs two passes")
+
+
 @pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_tanh", "gelu_none"])
 @pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 18432), (torch.float16, 16392),
                                         (torch.bfloat16, 17416), (torch.bfloat16, 20480),
