@@ -979,14 +979,22 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
 template <class T, int VEC, int VPL>
 int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s,
                   int64_t* resident) {
-  // Four vectors per lane on the 16-bit vector path: the raw tiles without a prefetched row
-  // (LayerNorm / RMSNorm only).
   if constexpr (VPL == 4 && VEC == 8 && sizeof(T) == 2) {
+    // Four vectors per lane on the 16-bit vector path: the raw tiles without a prefetched row
+    // (LayerNorm / RMSNorm only).
     if (threads != 1024 || p.gelu != 0 || p.dres) return FLN_ERR_INVALID;
     return launch_stage1_k<T, false, 0, VEC, 4, 1024>(p, blocks, threads, s, resident);
+  } else if constexpr (VPL == 3 && sizeof(T) == 4) {
+    // fp32 rows of 8193..12288 columns: 1024-thread blocks (no residual gradient).
+    if (threads != 1024 || p.dres) return FLN_ERR_INVALID;
+    if (p.gelu == 1)
+      return launch_stage1_k<T, false, 1, VEC, 3, 1024>(p, blocks, threads, s, resident);
+    if (p.gelu == 2)
+      return launch_stage1_k<T, false, 2, VEC, 3, 1024>(p, blocks, threads, s, resident);
+    return launch_stage1_k<T, false, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
   } else {
-    // Three vectors per lane: 768-thread blocks (168 VGPRs per lane), or the raw tiles of
-    // 1024-thread blocks (no residual gradient).
+    // Three vectors per lane of 16-bit rows: 768-thread blocks (168 VGPRs per lane), or the raw
+    // tiles of 1024-thread blocks (no residual gradient).
     if constexpr (VPL == 3) {
       if (threads == 1024) {
         if (p.dres) return FLN_ERR_INVALID;
@@ -1019,8 +1027,8 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
     case 2:
       if constexpr (CAP >= 2) return launch_stage1<T, VEC, 2>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
-    case 3:  // 16-bit rows of 16385..18432 columns (768 threads)
-      if constexpr (sizeof(T) == 2 && VEC == 8)
+    case 3:  // 16-bit rows of 16385..24576 columns (768 / 1024 threads), fp32 8193..12288
+      if constexpr ((sizeof(T) == 2 && VEC == 8) || (sizeof(T) == 4 && VEC == 4))
         return launch_stage1<T, VEC, 3>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 4:
@@ -1227,6 +1235,20 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // -> 184.0, 4096 x 24576 erf 243.8 -> 197.3.
   if (!g.reg_path && es == 2 && g.vec == 8 && nvec > 3 * kReg3Threads && nvec <= 3 * 1024 &&
       !dres && tun.bwd_no_lds == 0) {
+    g.reg_path = true;
+    g.vpl = 3;
+    g.threads = 1024;
+    g.wpr = 1024 / kWave;
+    g.rgs = 1;
+    g.blocks = rows < device_cu_count() ? rows : device_cu_count();
+    g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
+  }
+  // fp32 rows of 8193..12288 columns without a residual gradient: the register kernel with 3
+  // vectors per lane in 1024-thread blocks (107 VGPRs; 7 spilled with GELU), against the
+  // LDS-staged kernel, backward calls, us: 4096 x 12288 LN 113.5 -> 108.6, RMSNorm 108.5 ->
+  // 105.4, GELU erf 121.4 -> 118.0, 2048 x 12288 tanh 71.2 -> 68.2, 300 x 12288 28.9 -> 24.6.
+  if (!g.reg_path && es == 4 && g.vec == 4 && nvec > 2 * 1024 && nvec <= 3 * 1024 && !dres &&
+      tun.bwd_no_lds == 0) {
     g.reg_path = true;
     g.vpl = 3;
     g.threads = 1024;
