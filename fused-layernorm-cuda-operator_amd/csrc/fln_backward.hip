@@ -984,14 +984,21 @@ int launch_stage1(const BwdParams& p, int64_t blocks, int threads, hipStream_t s
     // (LayerNorm / RMSNorm only).
     if (threads != 1024 || p.gelu != 0 || p.dres) return FLN_ERR_INVALID;
     return launch_stage1_k<T, false, 0, VEC, 4, 1024>(p, blocks, threads, s, resident);
-  } else if constexpr (VPL == 3 && sizeof(T) == 4) {
-    // fp32 rows of 8193..12288 columns: 1024-thread blocks (no residual gradient).
-    if (threads != 1024 || p.dres) return FLN_ERR_INVALID;
-    if (p.gelu == 1)
-      return launch_stage1_k<T, false, 1, VEC, 3, 1024>(p, blocks, threads, s, resident);
-    if (p.gelu == 2)
-      return launch_stage1_k<T, false, 2, VEC, 3, 1024>(p, blocks, threads, s, resident);
-    return launch_stage1_k<T, false, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
+  } else if constexpr ((VPL == 3 || VPL == 4) && sizeof(T) == 4 && VEC == 4) {
+    // fp32 rows of 8193..12288 columns (every flavour) and 12289..16384 (LayerNorm / RMSNorm):
+    // 1024-thread blocks.
+    if (threads != 1024) return FLN_ERR_INVALID;
+    if constexpr (VPL == 4) {
+      if (p.gelu != 0 || p.dres) return FLN_ERR_INVALID;
+    } else {
+      if (p.gelu == 1)
+        return launch_stage1_k<T, false, 1, VEC, 3, 1024>(p, blocks, threads, s, resident);
+      if (p.gelu == 2)
+        return launch_stage1_k<T, false, 2, VEC, 3, 1024>(p, blocks, threads, s, resident);
+      if (p.dres)
+        return launch_stage1_k<T, true, 0, VEC, 3, 1024>(p, blocks, threads, s, resident);
+    }
+    return launch_stage1_k<T, false, 0, VEC, VPL, 1024>(p, blocks, threads, s, resident);
   } else {
     // Three vectors per lane of 16-bit rows: 768-thread blocks (168 VGPRs per lane), or the raw
     // tiles of 1024-thread blocks (no residual gradient).
@@ -1032,7 +1039,7 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
         return launch_stage1<T, VEC, 3>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 4:
-      if constexpr (CAP >= 4 || (sizeof(T) == 2 && VEC == 8))
+      if constexpr (CAP >= 4 || VEC * sizeof(T) == 16)
         return launch_stage1<T, VEC, 4>(p, blocks, threads, s, resident);
       return FLN_ERR_INVALID;
     case 8:
@@ -1243,14 +1250,16 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
     g.blocks = rows < device_cu_count() ? rows : device_cu_count();
     g.rows_per_block = (rows + g.blocks - 1) / g.blocks;
   }
-  // fp32 rows of 8193..12288 columns without a residual gradient: the register kernel with 3
-  // vectors per lane in 1024-thread blocks (107 VGPRs; 7 spilled with GELU), against the
-  // LDS-staged kernel, backward calls, us: 4096 x 12288 LN 113.5 -> 108.6, RMSNorm 108.5 ->
-  // 105.4, GELU erf 121.4 -> 118.0, 2048 x 12288 tanh 71.2 -> 68.2, 300 x 12288 28.9 -> 24.6.
-  if (!g.reg_path && es == 4 && g.vec == 4 && nvec > 2 * 1024 && nvec <= 3 * 1024 && !dres &&
-      tun.bwd_no_lds == 0) {
+  // fp32 rows of 8193..12288 columns: the register kernel with 3 vectors per lane in 1024-thread
+  // blocks (107-128 VGPRs; 28 B spilled with GELU); LayerNorm / RMSNorm rows of 12289..16384: 4
+  // vectors per lane (36 B spilled).  Against the LDS-staged kernel, backward calls, us: 4096 x
+  // 12288 LN 113.5 -> 108.6, RMSNorm 108.5 -> 105.4, GELU erf 121.4 -> 118.0, + residual 149.4
+  // -> 144.3, 2048 x 12288 tanh 71.2 -> 68.2, 300 x 12288 28.9 -> 24.6; 4096 x 16384 LN 153.9
+  // -> 147.0, RMSNorm 147.1 -> 142.2, 300 x 16384 33.9 -> 31.2.
+  if (!g.reg_path && es == 4 && g.vec == 4 && nvec > 2 * 1024 &&
+      (nvec <= 3 * 1024 || (nvec <= 4 * 1024 && !dres && !gelu)) && tun.bwd_no_lds == 0) {
     g.reg_path = true;
-    g.vpl = 3;
+    g.vpl = nvec <= 3 * 1024 ? 3 : 4;
     g.threads = 1024;
     g.wpr = 1024 / kWave;
     g.rgs = 1;

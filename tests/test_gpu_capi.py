@@ -996,9 +996,9 @@ def test_residual_gradient_is_added(lib, dtype, rows, cols):
 @pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_none", "gelu_tanh"])
 @pytest.mark.parametrize("cols", [8196, 12288, 12292, 16384])
 def test_fp32_wide_row_backward(lib, monkeypatch, kind, cols):
-    """fp32 rows of 8193..12288 columns without a residual gradient take the register backward
-    with 3 vectors per lane in 1024-thread blocks, the others up to 16384 columns the
-    LDS-staged backward (one 1024-thread block per row, several rows per block here): parity
+    """fp32 rows of 8193..12288 columns take the register backward with 3 vectors per lane in
+    1024-thread blocks, LayerNorm / RMSNorm rows up to 16384 with 4, the other flavours there
+    the LDS-staged backward (one 1024-thread block per row, several rows per block here): parity
     with the oracle for every flavour, dgamma/dbeta bitwise reproducible, and agreement with
     the route those rows take without either (FLN_BWD_NO_LDS)."""
     rows = 600
