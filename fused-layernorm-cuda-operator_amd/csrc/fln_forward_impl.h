@@ -1369,12 +1369,15 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   const int raw_cap = (vec_ok && VV < 8) ? wide_cap : max_cap;
   const int64_t nvec = N / vec;
   FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, raw_cap, vec_ok, tun.fwd_wpr);
-  // The fp8 row scale (no residual) takes 4 waves per row with masked tail lanes over an exact
-  // tiling of 5-7 waves when at most 1/8 of the 4-wave tile is masked (bf16, 32768 x 7168:
-  // 7 waves 134.5 us at its best grid, 4 waves 129.9 us; at 49152 x 5120, 3/8 masked, 4 waves
-  // lose: 152.2 -> 161.6 us).
-  if (FP8 == 1 && p.res == nullptr && vec_ok && !g.loop && g.exact && g.wpr >= 5 &&
-      g.wpr <= 7 && tun.fwd_wpr <= 0) {
+  // The fp8 row scale (no residual) and 16-bit LN + GELU take 4 waves per row with masked tail
+  // lanes over an exact tiling of 5-7 waves when at most 1/8 of the 4-wave tile is masked (bf16,
+  // 32768 x 7168 LN -> fp8: 7 waves 134.5 us at its best grid, 4 waves 129.9 us; 8192 x 7168
+  // GELU tanh 57.0 -> 46.6 us, erf 57.4 -> 50.0 us, f16 32768 x 7168 tanh 197.9 -> 171.4 us; at
+  // 49152 x 5120, 3/8 masked, LN -> fp8 loses: 152.2 -> 161.6 us).  Plain LayerNorm keeps the
+  // exact tiling (32768 x 7168: 156.8 against 167.7 us), as do the residual and MX flavours and
+  // fp32 GELU (8192 x 7168 tanh 77.2 against 83.5 us).
+  if ((FP8 == 1 || (FP8 == 0 && p.gelu != 0 && sizeof(T) == 2)) && p.res == nullptr && vec_ok &&
+      !g.loop && g.exact && g.wpr >= 5 && g.wpr <= 7 && tun.fwd_wpr <= 0) {
     const int64_t per4 = (nvec + 4 * kWave - 1) / (4 * kWave);
     const int v4 = next_pow2(static_cast<int>(per4));
     const int64_t slots = static_cast<int64_t>(v4) * 4 * kWave;
