@@ -667,9 +667,11 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
 // Rows past the register and LDS tiles (16-bit rows of more than 18432 columns, save the rows
 // of up to 24576 without a residual gradient (raw tiles); fp32 rows of more than 16384; long
 // rows on the scalar path), any width, in two streaming passes:
-//   bwd_rowstat_kernel: per row, sum(g) and sum(g xhat) (g = dy' gamma, dy' = dy or
-//     dy GELU'(xhat gamma + beta)) into stats[row]; one 256-thread block per row at a time,
-//     rows grid-stride, four vectors per thread in flight per array;
+//   bwd_rowstat_kernel: per row and column split, sum(g) and sum(g xhat) (g = dy' gamma,
+//     dy' = dy or dy GELU'(xhat gamma + beta)) into stats[row, split]; one 256-thread block per
+//     (row, split) at a time, grid-stride, four vectors per thread in flight per array.  Few
+//     rows split into column chunks so that the pass still has blocks for every CU (64 x
+//     1048576 bf16: one 256-thread block per row kept 64 CUs busy);
 //   bwd_colpass_kernel: a thread owns one vector column; over every G-th row (G = the blocks
 //     per column tile; four rows in flight) it writes dx from the row's statistics and
 //     accumulates dgamma / dbeta in registers, then writes one partial row per block row for
@@ -678,6 +680,15 @@ __global__ __launch_bounds__(NT) void bwd_lds_kernel(const BwdParams p) {
 // and no thread holds more than four vectors of a row.
 constexpr int kWideThreads = 256;
 constexpr int kWideUnroll = 4;
+constexpr int kRowstatBlocksPerCu = 8;
+// Few rows: column splits per row for about kRowstatItemsPerCu (row, split) items per CU, at
+// most kMaxStatSplits (the column pass sums a row's splits across a 16-lane row).  Fewer,
+// longer streams keep DRAM locality (bf16 backward calls, us, splits 1 / 2 / 4 / 8 / 16:
+// 64 x 1048576 309.0 / 210.4 / 163.3 / 152.5 / 175.3; 256 x 262144 159.9 / 143.2 / 141.5 /
+// 146.5 / 171.6; 16 x 1048576 238.9 / 140.8 / 91.0 / 68.5 / 62.6; with 8 blocks per CU's worth
+// of splits, 64 x 1048576 took 257.9).
+constexpr int kRowstatItemsPerCu = 2;
+constexpr int kMaxStatSplits = 16;
 #ifndef FLN_COLPASS_BLOCKS_PER_CU
 #define FLN_COLPASS_BLOCKS_PER_CU 2
 #endif
@@ -699,14 +710,21 @@ __global__ __launch_bounds__(kWideThreads) void bwd_rowstat_kernel(const BwdPara
   const rsrc_t gr = make_rsrc(p.gamma, row_bytes);
   const rsrc_t br = make_rsrc(p.beta, row_bytes);  // GELU only; absent beta reads as zeros
   const bool has_g = p.gamma != nullptr;
+  const int S = p.stat_splits;
+  const int64_t items = p.rows * S;
   int parity = 0;
-  for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x, parity ^= 1) {
-    const rsrc_t xr = make_rsrc(X + row * N, row_bytes);
-    const rsrc_t dr = make_rsrc(DY + row * N, row_bytes);
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x, parity ^= 1) {
+    const int64_t row = item / S;
+    const int64_t v_lo = (item - row * S) * p.stat_chunk;
+    const int64_t v_hi = v_lo + p.stat_chunk < nvec ? v_lo + p.stat_chunk : nvec;
+    // x and dy read as zeros past the split (g = 0 there), gamma / beta over the whole row.
+    const uint32_t split_bytes = static_cast<uint32_t>(v_hi * VEC * sizeof(T));
+    const rsrc_t xr = make_rsrc(X + row * N, split_bytes);
+    const rsrc_t dr = make_rsrc(DY + row * N, split_bytes);
     const float mu = p.rms ? 0.0f : p.mean[row];
     const float rs = p.rstd[row];
     float s1 = 0.0f, s2 = 0.0f;
-    for (int v0 = t; v0 < nvec; v0 += kWideUnroll * kWideThreads) {
+    for (int v0 = static_cast<int>(v_lo) + t; v0 < v_hi; v0 += kWideUnroll * kWideThreads) {
       P xv[kWideUnroll], dv[kWideUnroll], gv[kWideUnroll], bv[GELU ? kWideUnroll : 1];
 #pragma unroll
       for (int u = 0; u < kWideUnroll; ++u) {  // vectors past the row read as zeros
@@ -740,7 +758,7 @@ __global__ __launch_bounds__(kWideThreads) void bwd_rowstat_kernel(const BwdPara
     __syncthreads();
     s1 = combine_partials<SumOp>(slot[0], 0, kW, lane, 0.0f);
     s2 = combine_partials<SumOp>(slot[1], 0, kW, lane, 0.0f);
-    if (t == 0) stats[row] = make_float2(s1, s2);
+    if (t == 0) stats[item] = make_float2(s1, s2);
   }
 }
 
@@ -770,9 +788,11 @@ __global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdPara
   float acc_g[VEC], acc_b[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc_g[e] = acc_b[e] = 0.0f;
+  const int split = threadIdx.x & 15;
   for (int64_t row = blockIdx.y; row < p.rows; row += kWideUnroll * G) {
     P xv[kWideUnroll], dv[kWideUnroll], rv[DRES ? kWideUnroll : 1];
     float mu[kWideUnroll], rs[kWideUnroll], cb[kWideUnroll], cx[kWideUnroll];
+    float2 sp[kWideUnroll];
 #pragma unroll
     for (int u = 0; u < kWideUnroll; ++u) {
       const bool in = row + u * G < p.rows;  // uniform
@@ -783,9 +803,14 @@ __global__ __launch_bounds__(kWideThreads) void bwd_colpass_kernel(const BwdPara
       if constexpr (DRES) rv[u] = buf_load<P, kStream>(make_rsrc(DR + r * N, nb), v);
       mu[u] = p.rms ? 0.0f : p.mean[r];
       rs[u] = p.rstd[r];
-      const float2 st = stats[r];
-      cb[u] = p.rms ? 0.0f : -rs[u] * (st.x * inv_n);
-      cx[u] = -rs[u] * (st.y * inv_n);
+      // The row's splits: lane k of each 16-lane row loads split k.
+      sp[u] = split < p.stat_splits ? stats[r * p.stat_splits + split] : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < kWideUnroll; ++u) {  // splits summed in a fixed order (reduce16)
+      const float s1 = reduce16<SumOp>(sp[u].x), s2 = reduce16<SumOp>(sp[u].y);
+      cb[u] = p.rms ? 0.0f : -rs[u] * (s1 * inv_n);
+      cx[u] = -rs[u] * (s2 * inv_n);
     }
 #pragma unroll
     for (int u = 0; u < kWideUnroll; ++u) {
@@ -1052,8 +1077,9 @@ int launch_stage1_vpl(const BwdParams& p, int vpl, int64_t blocks, int threads, 
 template <class T, int VEC>
 int launch_two_pass(const BwdParams& p, const BwdGeometry& geo, hipStream_t s) {
   float2* stats = reinterpret_cast<float2*>(p.rowstat);
-  const int64_t cap = 8 * static_cast<int64_t>(device_cu_count());
-  const dim3 g1(static_cast<unsigned>(p.rows < cap ? p.rows : cap)), blk(kWideThreads);
+  const int64_t cap = kRowstatBlocksPerCu * static_cast<int64_t>(device_cu_count());
+  const int64_t items = p.rows * p.stat_splits;
+  const dim3 g1(static_cast<unsigned>(items < cap ? items : cap)), blk(kWideThreads);
   const int64_t nvec = p.cols / VEC;
   const dim3 g2(static_cast<unsigned>((nvec + kWideThreads - 1) / kWideThreads),
                 static_cast<unsigned>(geo.blocks));
@@ -1352,13 +1378,38 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   const int64_t ld = (p.cols + 3) & ~int64_t(3);
   float* ws = p0.part_g;
   // Workspace layout: dgamma partials [blocks, ld] and dbeta partials [blocks, ld] when either
-  // gradient is requested, then the row statistics of the two-pass path [rows, 2] (16-byte
-  // aligned: ld is a multiple of 4).  At most fln_backward_workspace_bytes() (blocks <=
-  // workspace_partial_rows on every path).
+  // gradient is requested, then the row statistics of the two-pass path [rows, splits, 2]
+  // (16-byte aligned: ld is a multiple of 4).  At most fln_backward_workspace_bytes() (blocks <=
+  // workspace_partial_rows on every path; splits within what that bound leaves).
   const int64_t part = (dgamma || dbeta) ? 2 * geo.blocks * ld : 0;
+  // Row statistics of the two-pass path: fewer rows than the statistics pass has blocks split
+  // into column chunks of whole steps (kWideUnroll x kWideThreads vectors), as many as the
+  // workspace bound (fln_backward_workspace_bytes, not the size passed, so that the split and
+  // with it the summation order never depend on the caller's workspace) leaves after the
+  // partials.
+  int64_t splits = 1;
+  const int64_t nvec = p.cols / geo.vec;
+  p.stat_chunk = nvec;
+  if (geo.two_pass) {
+    constexpr int64_t step = int64_t(kWideUnroll) * kWideThreads;
+    const int64_t steps = (nvec + step - 1) / step;
+    const int forced = tuning().bwd_stat_splits;  // FLN_BWD_STAT_SPLITS
+    const int64_t items = kRowstatItemsPerCu * static_cast<int64_t>(device_cu_count());
+    splits = forced > 0 ? forced : (items + p.rows - 1) / p.rows;
+    if (splits > kMaxStatSplits) splits = kMaxStatSplits;
+    const int64_t bound = 2 * workspace_partial_rows(p.rows) * ld + 2 * p.rows;
+    const int64_t room = (bound - part) / (2 * p.rows);
+    if (splits > room) splits = room;
+    if (splits > steps) splits = steps;
+    if (splits < 1) splits = 1;
+    p.stat_chunk = (steps + splits - 1) / splits * step;
+    splits = (nvec + p.stat_chunk - 1) / p.stat_chunk;
+  }
+  p.stat_splits = static_cast<int>(splits);
   if (have_workspace) {
     const size_t need = (static_cast<size_t>(part) +
-                         (geo.two_pass ? 2 * static_cast<size_t>(p.rows) : 0)) * sizeof(float);
+                         (geo.two_pass ? 2 * static_cast<size_t>(p.rows * splits) : 0)) *
+                        sizeof(float);
     if (need > workspace_bytes) return FLN_ERR_TOO_LARGE;
   }
   p.part_g = dgamma ? ws : nullptr;

@@ -42,7 +42,10 @@ struct BwdParams {
   void* dx;           // or nullptr
   float* part_g;      // [blocks, cols] stage-1 partial of sum(dy * xhat), or nullptr
   float* part_b;      // [blocks, cols] stage-1 partial of sum(dy), or nullptr
-  float* rowstat;     // [rows, 2] row sums of g and g xhat (two-pass path), in the workspace
+  float* rowstat;     // [rows, stat_splits, 2] row sums of g and g xhat over each column
+                      // split (two-pass path), in the workspace
+  int64_t stat_chunk; // vectors per column split of the row statistics (two-pass path)
+  int stat_splits;    // column splits per row of the row statistics (two-pass path)
   int64_t rows;
   int64_t cols;
   int64_t rows_per_block;
@@ -71,6 +74,7 @@ struct Tuning {
   int bwd_grid_mult;   // FLN_BWD_GRID_MULT: backward blocks per CU (1-4)
   int bwd_no_lds;      // FLN_BWD_NO_LDS: never the LDS-staged backward
   int bwd_no_two_pass; // FLN_BWD_NO_TWO_PASS: never the two-pass backward
+  int bwd_stat_splits; // FLN_BWD_STAT_SPLITS: column splits per row of the two-pass statistics
 };
 const Tuning& tuning();  // read at the first call; fln_reload_tuning() reads again
 void reload_tuning();

@@ -1267,6 +1267,92 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
             assert_close_rel(to_np(a), to_np(c), 1e-5, "parameter gradient vs two passes")
 
 
+@pytest.mark.parametrize("kind,dtype,rows,cols", [
+    ("ln", torch.bfloat16, 12, 262144), ("rms", torch.float16, 8, 300000),
+    ("ln_dres", torch.float32, 16, 40000), ("gelu_tanh", torch.bfloat16, 8, 131072),
+    ("ln", torch.bfloat16, 4, 100003)],
+    ids=["ln-bf16-12x262144", "rms-f16-8x300000", "ln_dres-f32-16x40000",
+         "gelu_tanh-bf16-8x131072", "ln-bf16-4x100003-scalar"])
+def test_two_pass_backward_few_rows(lib, monkeypatch, kind, dtype, rows, cols):
+    """Few very wide rows: the two-pass backward's row statistics split each row into up to 16
+    column chunks of whole 1024-vector steps (so the statistics pass has blocks for every CU)
+    and the column pass sums a row's splits in order (300000 fp16 columns: 13 chunks of 3072
+    vectors, the last one 636; 100003 columns: the scalar path, 14 chunks).  Parity with the
+    oracle, bitwise reproducible, and agreement with one block per row
+    (FLN_BWD_STAT_SPLITS=1)."""
+    gen = torch.Generator().manual_seed(cols + rows)
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.2 * torch.randn(cols, generator=gen)).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    drc = torch.randn(rows, cols, generator=gen).to(dtype)
+    x, g, b, dy, dr = cuda(xc), cuda(gc), cuda(bc), cuda(dyc), cuda(drc)
+    xs, gs, bs, dys = f32(xc), f32(gc), f32(bc), f32(dyc)
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    if kind == "rms":
+        _, rstd = rms_forward(lib, x, g, 1e-6)
+
+        def run():
+            dx, dw = rms_backward(lib, dy, x, rstd, g)
+            return dx, dw, None
+        dx_ref, dg_ref = c_oracle.rmsnorm_bwd(dys, xs, gs, 1e-6)
+        db_ref = None
+    elif kind == "gelu_tanh":
+        mean = torch.empty(rows, device="cuda")
+        rstd = torch.empty(rows, device="cuda")
+        y = torch.empty_like(x)
+        capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd),
+                                                  rows, cols, code, 1e-5, capi.GELU_TANH,
+                                                  capi.stream()))
+
+        def run():
+            dx = torch.empty_like(x)
+            dg = torch.empty(cols, device="cuda")
+            db = torch.empty(cols, device="cuda")
+            ws, n = workspace(lib, rows, cols, x)
+            capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b),
+                                                       p(dx), p(dg), p(db), rows, cols, code,
+                                                       capi.F32, capi.GELU_TANH, p(ws), n,
+                                                       capi.stream()))
+            return dx, dg, db
+        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, "tanh")
+    else:
+        _, mean, rstd = ln_forward(lib, x, g, None, 1e-5)
+        dres = dr if kind == "ln_dres" else None
+
+        def run():
+            return ln_backward(lib, dy, x, mean, rstd, g, dres=dres)
+        dx_ref, dg_ref, db_ref = c_oracle.layernorm_bwd(dys, xs, gs, 1e-5)
+        if kind == "ln_dres":
+            dx_ref = dx_ref + f32(drc)
+    dx, dg, db = run()
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(to_np(dx), dx_ref, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within_ulp(to_np(dx), dx_ref, 1.0, atol=DX_ATOL_REL * np.abs(dx_ref).max(),
+                          kind="bf16" if dtype == torch.bfloat16 else "f16", what="dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    if db is not None:
+        assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+    again = run()
+    for a, c in zip((dx, dg, db), again):
+        if a is not None:
+            assert torch.equal(a, c)
+    monkeypatch.setenv("FLN_BWD_STAT_SPLITS", "1")
+    capi.reload_tuning()
+    one = run()
+    monkeypatch.delenv("FLN_BWD_STAT_SPLITS")
+    capi.reload_tuning()
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10 if dtype == torch.float16 else 1e-5
+    af, cf = dx.float(), one[0].float()
+    assert float((af - cf).abs().max()) <= 2 * ulp * max(1.0, float(cf.abs().max()))
+    for a, c in zip((dg, db), one[1:]):
+        if a is not None:
+            assert_close_rel(to_np(a), to_np(c), 1e-5, "parameter gradient vs one block per row")
+
+
 @pytest.mark.parametrize("kind", ["ln", "rms", "ln_dres", "gelu_none", "gelu_tanh"])
 @pytest.mark.parametrize("dtype,cols", [(torch.float32, 20480), (torch.bfloat16, 24576),
                                         (torch.float16, 40000), (torch.bfloat16, 20001)],
