@@ -1233,6 +1233,264 @@ int launch_lds_reg(const FwdParams& p, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------------------------
+// Few rows past the register tiles (vector path, bf16 / f16 / fp32 output, y overlapping no
+// input): one block per row left most CUs idle (bf16 64 x 1048576: 64 blocks, 1.9 TB/s).  Each
+// row splits into S <= 64 column chunks of whole steps, one 256-thread block per (row, chunk),
+// in three launches and without a workspace (the forward entry points take none):
+//   fwd_split_stats_kernel: the chunk's (count, sum, M2 about the chunk's mean) -- RMSNorm:
+//     (count, 0, sum of squares) -- as one float4 per chunk at the start of the row's own y
+//     (its first S x 16 bytes, the "head"); with a residual, h = x + r is written as well;
+//   fwd_split_out_kernel<HEAD = false>: every block merges its row's S triples (lane k loads
+//     triple k, wave_allreduce sums in a fixed order: the pairwise merge of Chan, Golub and
+//     LeVeque, the same bits in every block), then writes the outputs of its chunk
+//     but not the head, walking the chunk backwards from the lines the statistics pass read
+//     last;
+//   fwd_split_out_kernel<HEAD = true>: one block per row: the same statistics, the head's
+//     outputs, mean and rstd.  Stream order puts it after every read of the head.
+// x (h with a residual) is read twice, as in the streamed wide-row kernel, but by every CU.
+// ---------------------------------------------------------------------------------------------
+constexpr int kFwdSplitThreads = 256;
+constexpr int kFwdSplitU = 4;                                        // vectors per thread, step
+constexpr int kFwdSplitStep = kFwdSplitThreads * kFwdSplitU;         // vectors per step
+constexpr int kFwdSplitMax = kWave;                                  // chunks per row
+
+// The row statistics (mean, rstd) from the S <= 64 chunk triples at the row's head.  All 64
+// lanes must be active; the result is wave-uniform and identical in every block of the row.
+__device__ __forceinline__ float2 split_row_stats(const float4* head, int S, int lane,
+                                                  float fn, float inv_n, float eps, bool rms) {
+  const float4 tr = lane < S ? head[lane] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (rms) {
+    const float q = wave_allreduce<SumOp>(tr.z);
+    return make_float2(0.0f, __builtin_amdgcn_rsqf(q * inv_n + eps));  // v_rsq_f32, 1 ulp
+  }
+  const float sum = wave_allreduce<SumOp>(tr.y);
+  float mean = sum * inv_n;
+  mean = fmaf(fmaf(-mean, fn, sum), inv_n, mean);
+  const float d = (tr.x > 0.0f ? tr.y / tr.x : 0.0f) - mean;  // chunk mean - row mean
+  const float q = wave_allreduce<SumOp>(fmaf(tr.x * d, d, tr.z));
+  return make_float2(mean, __builtin_amdgcn_rsqf(q * inv_n + eps));
+}
+
+template <class T, bool RES, int VEC>
+__global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const FwdParams p) {
+  constexpr int kT = kFwdSplitThreads;
+  constexpr int kW = kT / kWave;
+  constexpr int U = kFwdSplitU;
+  using P = Pack<T, VEC>;
+  __shared__ float red[2][kW + 16];
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int64_t N = p.cols;
+  const uint32_t nvec = static_cast<uint32_t>(N / VEC);
+  const int S = p.splits;
+  const int64_t row = blockIdx.x / S;
+  const uint32_t s = static_cast<uint32_t>(blockIdx.x - row * S);
+  const uint32_t v_lo = s * static_cast<uint32_t>(p.split_chunk);
+  const uint32_t v_hi = v_lo + static_cast<uint32_t>(p.split_chunk) < nvec
+                            ? v_lo + static_cast<uint32_t>(p.split_chunk) : nvec;
+  const uint32_t hi_bytes = v_hi * static_cast<uint32_t>(sizeof(P));  // nothing past the chunk
+  const rsrc_t xq = make_rsrc(static_cast<const T*>(p.x) + row * N, hi_bytes);
+  const rsrc_t rq = make_rsrc(RES ? static_cast<const T*>(p.res) + row * N : nullptr, hi_bytes);
+  const rsrc_t hq = make_rsrc(RES && p.h ? static_cast<T*>(p.h) + row * N : nullptr, hi_bytes);
+  float cnt = 0.0f, mu = 0.0f, m2 = 0.0f;  // this thread's elements: count, mean, M2
+  for (uint32_t base = v_lo; base < v_hi; base += kFwdSplitStep) {
+    P hv[U], rv[RES ? U : 1];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      hv[u] = buf_load<P>(xq, base + t + kT * u);
+      if constexpr (RES) rv[u] = buf_load<P>(rq, base + t + kT * u);
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          hv[u].v[e] = from_f32<T>(to_f32(hv[u].v[e]) + to_f32(rv[u].v[e]));
+        buf_store<P>(hv[u], hq, base + t + kT * u);  // kept in cache for the output pass
+      }
+    }
+    if (p.rms) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) m2 = fmaf(to_f32(hv[u].v[e]), to_f32(hv[u].v[e]), m2);
+      continue;
+    }
+    float c = 0.0f, sm = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + t + kT * u < v_hi) {
+        c += static_cast<float>(VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sm += to_f32(hv[u].v[e]);
+      }
+    }
+    if (c > 0.0f) {
+      const float mg = sm / c;
+      float q = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (base + t + kT * u < v_hi) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float d = to_f32(hv[u].v[e]) - mg;
+            q = fmaf(d, d, q);
+          }
+        }
+      }
+      const float nn = cnt + c;
+      const float d = mg - mu;
+      const float w = c / nn;
+      mu = fmaf(d, w, mu);
+      m2 += fmaf(d * d, cnt * w, q);
+      cnt = nn;
+    }
+  }
+  const float nb = static_cast<float>((v_hi - v_lo) * static_cast<uint32_t>(VEC));
+  float4 out;
+  if (p.rms) {
+    out = make_float4(nb, 0.0f, row_allreduce<SumOp>(m2, red[0], kW, 0, wave, lane), 0.0f);
+  } else {
+    const float sum = row_allreduce<SumOp>(cnt * mu, red[0], kW, 0, wave, lane);
+    const float dm = mu - sum / nb;
+    out = make_float4(nb, sum,
+                      row_allreduce<SumOp>(fmaf(cnt * dm, dm, m2), red[1], kW, 0, wave, lane),
+                      0.0f);
+  }
+  if (t == 0) reinterpret_cast<float4*>(static_cast<T*>(p.y) + row * N)[s] = out;
+}
+
+template <class T, bool RES, int GELU, int VEC, bool HEAD>
+__global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_out_kernel(const FwdParams p) {
+  constexpr int kT = kFwdSplitThreads;
+  constexpr int U = kFwdSplitU;
+  using P = Pack<T, VEC>;
+  static_assert(sizeof(P) == 16, "the head holds one 16-byte triple per output vector");
+  constexpr bool TAB = GELU == 1 && sizeof(T) == 2;  // as in the register kernel
+  __shared__ float4 gelu_tab[TAB ? kGeluLogTabN : 1];
+  if constexpr (TAB) {
+    if (threadIdx.x < kGeluLogTabN)
+      gelu_tab[threadIdx.x] = reinterpret_cast<const float4*>(kGeluLogTabData)[threadIdx.x];
+    __syncthreads();
+  }
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int64_t N = p.cols;
+  const uint32_t nvec = static_cast<uint32_t>(N / VEC);
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const float fn = static_cast<float>(N);
+  const int S = p.splits;
+  const int64_t row = HEAD ? static_cast<int64_t>(blockIdx.x) : blockIdx.x / S;
+  const uint32_t s = HEAD ? 0u : static_cast<uint32_t>(blockIdx.x - row * S);
+  const uint32_t head = static_cast<uint32_t>(S);  // vectors holding the chunk triples
+  const uint32_t chunk = static_cast<uint32_t>(p.split_chunk);
+  const uint32_t v_lo = HEAD ? 0u : s * chunk;
+  const uint32_t v_hi = HEAD ? head : (v_lo + chunk < nvec ? v_lo + chunk : nvec);
+  const uint32_t v_first = HEAD ? 0u : (v_lo > head ? v_lo : head);  // first vector written
+  T* Y = static_cast<T*>(p.y) + row * N;
+  const float2 st = split_row_stats(reinterpret_cast<const float4*>(Y), S, lane, fn, 1.0f / fn,
+                                    p.eps, p.rms != 0);
+  const float mean = st.x, rstd = st.y;
+  const bool from_h = RES && p.h != nullptr;  // h was written by the statistics pass
+  const uint32_t hi_bytes = v_hi * static_cast<uint32_t>(sizeof(P));
+  const rsrc_t xq = make_rsrc(from_h ? static_cast<const T*>(p.h) + row * N
+                                     : static_cast<const T*>(p.x) + row * N, hi_bytes);
+  const rsrc_t rq = make_rsrc(RES && !from_h ? static_cast<const T*>(p.res) + row * N : nullptr,
+                              hi_bytes);
+  const rsrc_t yq = make_rsrc(Y, hi_bytes);
+  const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
+  const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
+  const bool has_g = p.gamma != nullptr;
+  constexpr uint32_t kSkip = kOutOfRange / sizeof(P);  // a store offset past every resource
+  const uint32_t steps = (v_hi - v_lo + kFwdSplitStep - 1) / kFwdSplitStep;
+  for (uint32_t k = 0; k < steps; ++k) {
+    const uint32_t base = v_lo + (steps - 1 - k) * kFwdSplitStep;
+    P hv[U], rv[RES ? U : 1];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      hv[u] = buf_load<P, kStream>(xq, base + t + kT * u);
+      if constexpr (RES) {
+        if (!from_h) rv[u] = buf_load<P, kStream>(rq, base + t + kT * u);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = base + t + kT * u;
+      if constexpr (RES) {
+        if (!from_h) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            hv[u].v[e] = from_f32<T>(to_f32(hv[u].v[e]) + to_f32(rv[u].v[e]));
+        }
+      }
+      const P gv = buf_load<P>(g_rs, v);
+      const P bv = buf_load<P>(b_rs, v);
+      P o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float a = fmaf((to_f32(hv[u].v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
+                       to_f32(bv.v[e]));
+        if constexpr (GELU == 1) a = TAB ? gelu_erf_tab(gelu_tab, a) : gelu_erf(a);
+        if constexpr (GELU == 2) a = gelu_tanh(a);
+        o.v[e] = from_f32<T>(a);
+      }
+      buf_store<P, FLN_FWD_STORE_POL>(o, yq, v >= v_first ? v : kSkip);
+    }
+  }
+  if constexpr (HEAD) {
+    const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
+    buf_store_f32(mean, make_rsrc(p.mean ? p.mean + row : nullptr, 4u), stat_off);
+    buf_store_f32(rstd, make_rsrc(p.rstd ? p.rstd + row : nullptr, 4u), stat_off);
+  }
+}
+
+// Chunks per row: kFwdSplitMax, at least one step each (FLN_FWD_SPLITS forces a count).  More
+// chunks measured faster at every row count that takes this path (bf16, us, 16 / 32 / 64
+// chunks: 64 x 1048576 81.9 / 71.0 / 67.7; 4 x 1048576 26.4 / 17.7 / 13.3; 200 x 262144 54.0 /
+// 52.1 / 51.9; residual 64 x 1048576 138.5 / 126.2 / 116.4).
+template <class T, int VEC>
+int launch_split(FwdParams p, hipStream_t s) {
+  const int64_t nvec = p.cols / VEC;
+  const int64_t steps = (nvec + kFwdSplitStep - 1) / kFwdSplitStep;
+  const int forced = tuning().fwd_splits;
+  int64_t splits = forced > 0 ? forced : kFwdSplitMax;
+  if (splits > kFwdSplitMax) splits = kFwdSplitMax;
+  if (splits > steps) splits = steps;
+  if (splits < 1) splits = 1;
+  p.split_chunk = (steps + splits - 1) / splits * kFwdSplitStep;
+  p.splits = static_cast<int>((nvec + p.split_chunk - 1) / p.split_chunk);
+  const dim3 grid(static_cast<unsigned>(p.rows * p.splits)), rows(static_cast<unsigned>(p.rows));
+  const dim3 block(kFwdSplitThreads);
+  auto three = [&](auto stats, auto body, auto head) {
+    hipLaunchKernelGGL(stats, grid, block, 0, s, p);
+    hipLaunchKernelGGL(body, grid, block, 0, s, p);
+    hipLaunchKernelGGL(head, rows, block, 0, s, p);
+    return static_cast<int>(hipGetLastError());
+  };
+  if (p.res)
+    return three(fwd_split_stats_kernel<T, true, VEC>, fwd_split_out_kernel<T, true, 0, VEC, false>,
+                 fwd_split_out_kernel<T, true, 0, VEC, true>);
+  if (p.gelu == FLN_GELU_ERF)
+    return three(fwd_split_stats_kernel<T, false, VEC>,
+                 fwd_split_out_kernel<T, false, 1, VEC, false>,
+                 fwd_split_out_kernel<T, false, 1, VEC, true>);
+  if (p.gelu == FLN_GELU_TANH)
+    return three(fwd_split_stats_kernel<T, false, VEC>,
+                 fwd_split_out_kernel<T, false, 2, VEC, false>,
+                 fwd_split_out_kernel<T, false, 2, VEC, true>);
+  return three(fwd_split_stats_kernel<T, false, VEC>, fwd_split_out_kernel<T, false, 0, VEC, false>,
+               fwd_split_out_kernel<T, false, 0, VEC, true>);
+}
+
+// Byte ranges [a, a + na) and [b, b + nb) overlap (null pointers never do).
+inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+  if (a == nullptr || b == nullptr) return false;
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + static_cast<uintptr_t>(nb) && y < x + static_cast<uintptr_t>(na);
+}
+
 template <class T, int FP8, int VEC>
 int launch_wide(const FwdParams& p, hipStream_t s) {
   auto launch = [&](auto kernel) {
@@ -1395,11 +1653,32 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
                    !tun.fwd_no_lds;
   const bool wide = g.loop && !lds && N * int64_t(sizeof(T)) < (int64_t(1) << 31) &&
                     !tun.fwd_no_wide;
+  // Fewer rows than CUs (16-bit / fp32 output): each row split over several blocks, its
+  // statistics handed over through the head of its own y row (so y may overlap no input).
+  bool split = false;
+  if constexpr (FP8 == 0) {
+    const int64_t bytes = p.rows * N * static_cast<int64_t>(sizeof(T));
+    const int64_t pbytes = N * static_cast<int64_t>(sizeof(T));
+    // Against the kernels that read x once (LDS-staged, with or without half the row in
+    // registers) the split's second read pays only with very few rows (bf16, us: 32 x 131072
+    // 19.5 -> 11.7, 64 x 131072 19.8 -> 16.2, 64 x 65536 11.0 against 11.6, 128 x 131072 21.6 /
+    // 21.6); against the streamed kernel, which reads it twice anyway, with any fewer rows than
+    // CUs (200 x 262144 64.4 -> 51.9, 64 x 1048576 157.6 -> 67.7).
+    const bool lds_reg = g.loop && vec_ok && p.res == nullptr &&
+                         (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
+                         nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
+    const int64_t max_rows = (lds || lds_reg) ? device_cu_count() / 4 - 1 : device_cu_count() - 1;
+    split = g.loop && vec_ok && p.rows <= max_rows && pbytes < (int64_t(1) << 31) &&
+            !tun.fwd_no_split && !overlaps(p.y, bytes, p.x, bytes) &&
+            !overlaps(p.y, bytes, p.res, bytes) && !overlaps(p.y, bytes, p.h, bytes) &&
+            !overlaps(p.y, bytes, p.gamma, pbytes) && !overlaps(p.y, bytes, p.beta, pbytes);
+  }
   if (tun.debug_geometry)
     fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
             "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
-            cap, wide_cap, lds ? "lds" : wide ? "wide" : g.loop ? "loop" : "registers", g.wpr,
+            cap, wide_cap, split ? "split" : lds ? "lds" : wide ? "wide" : g.loop ? "loop" : "registers", g.wpr,
             g.vpl, static_cast<int>(g.exact), g.threads);
+  if (split) return launch_split<T, VV>(p, s);
   if (lds) return launch_lds<T, FP8, VV>(p, s);
   if constexpr (FP8 == 0) {
     if (g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&

@@ -62,6 +62,8 @@ Tuning read_tuning() {
   t.debug_geometry = env_knob("FLN_DEBUG_GEOMETRY", 0);
   t.fwd_no_lds = env_knob("FLN_FWD_NO_LDS", 0);
   t.fwd_no_wide = env_knob("FLN_FWD_NO_WIDE", 0);
+  t.fwd_no_split = env_knob("FLN_FWD_NO_SPLIT", 0);
+  t.fwd_splits = env_knob("FLN_FWD_SPLITS", 0);
   t.bwd_epl = env_knob("FLN_BWD_EPL", 0);
   t.bwd_wpr = env_knob("FLN_BWD_WPR", 0);
   t.bwd_threads = env_knob("FLN_BWD_THREADS", 0);

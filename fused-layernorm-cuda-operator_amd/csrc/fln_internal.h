@@ -28,6 +28,8 @@ struct FwdParams {
   int gelu;  // FLN_GELU_*
   int mx;    // out_fp8: 0 per-row scale, 1 OCP MX blocks of 32 with E8M0 scales
   int wpr;   // waves per row (register path)
+  int splits;           // column chunks per row (few-row split forward)
+  int64_t split_chunk;  // vectors per chunk (few-row split forward)
 };
 
 // Backward launch description.
@@ -68,6 +70,8 @@ struct Tuning {
   int debug_geometry;  // FLN_DEBUG_GEOMETRY: one stderr line per forward launch
   int fwd_no_lds;      // FLN_FWD_NO_LDS: never the LDS-staged forward
   int fwd_no_wide;     // FLN_FWD_NO_WIDE: the looped forward instead of the streamed wide-row one
+  int fwd_no_split;    // FLN_FWD_NO_SPLIT: never the few-row split forward
+  int fwd_splits;      // FLN_FWD_SPLITS: column chunks per row of the split forward
   int bwd_epl;         // FLN_BWD_EPL: backward elements per lane
   int bwd_wpr;         // FLN_BWD_WPR: backward waves per row
   int bwd_threads;     // FLN_BWD_THREADS: backward block size (256, 512, 1024)

@@ -801,6 +801,105 @@ def test_wide_rows_forward(lib, kind, dtype, rows, cols, aligned):
         assert_within_ulp(to_np(got), y_ref, 1.0, atol=atol, **_tol_fwd(dtype), what=kind)
 
 
+@pytest.mark.parametrize("kind,dtype,rows,cols", [
+    ("ln", torch.bfloat16, 16, 262144), ("rms", torch.float16, 40, 70000),
+    ("gelu_none", torch.bfloat16, 8, 140000), ("gelu_tanh", torch.float32, 60, 40000),
+    ("add_ln", torch.bfloat16, 24, 100000), ("add_ln_noh", torch.float16, 12, 90000),
+    ("add_rms", torch.float16, 4, 524288), ("gelu_none", torch.float32, 6, 65536),
+    ("ln", torch.float32, 30, 32768)],
+    ids=["ln-bf16-16x262144", "rms-f16-40x70000", "gelu_none-bf16-8x140000",
+         "gelu_tanh-f32-60x40000", "add_ln-bf16-24x100000", "add_ln_noh-f16-12x90000",
+         "add_rms-f16-4x524288", "gelu_none-f32-6x65536", "ln-f32-30x32768"])
+def test_split_rows_forward(lib, monkeypatch, kind, dtype, rows, cols):
+    """Few rows past the register tiles (fewer than CUs where the streamed kernel would run, a
+    quarter of them where an LDS-staged one would): each row split into up to 64 column chunks
+    (one block each; the chunk statistics handed to the output pass through the first bytes of
+    the row's own y; 70000 fp16 columns: a last chunk of 558 vectors; a residual with and
+    without h).  Outputs and statistics against the oracle, bitwise reproducible, within 1 ulp
+    of one block per row (FLN_FWD_NO_SPLIT), and an in-place call (y = x, so no split) equal to
+    that."""
+    gen = torch.Generator().manual_seed(cols + rows)
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, r, g, b = cuda(xc), cuda(rc), cuda(gc), cuda(bc)
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    rms = "rms" in kind
+    eps = 1e-6 if rms else 1e-5
+
+    def run(src=None, inplace=False):
+        src = x if src is None else src
+        out = src if inplace else torch.empty_like(x)
+        h = torch.zeros_like(x)
+        mean = torch.zeros(rows, device="cuda")
+        rstd = torch.zeros(rows, device="cuda")
+        st = capi.stream()
+        if kind == "ln":
+            rc_ = lib.fln_layernorm_forward(p(src), p(g), p(b), p(out), p(mean), p(rstd), rows,
+                                            cols, code, eps, st)
+        elif kind == "rms":
+            rc_ = lib.fln_rmsnorm_forward(p(src), p(g), p(out), p(rstd), rows, cols, code, eps,
+                                          st)
+        elif kind.startswith("gelu"):
+            gm = capi.GELU_ERF if kind == "gelu_none" else capi.GELU_TANH
+            rc_ = lib.fln_layernorm_gelu_forward(p(src), p(g), p(b), p(out), p(mean), p(rstd),
+                                                 rows, cols, code, eps, gm, st)
+        elif kind.startswith("add_ln"):
+            rc_ = lib.fln_add_layernorm_forward(p(src), p(r), p(g), p(b),
+                                                None if kind == "add_ln_noh" else p(h), p(out),
+                                                p(mean), p(rstd), rows, cols, code, eps, st)
+        else:
+            rc_ = lib.fln_add_rmsnorm_forward(p(src), p(r), p(g), p(h), p(out), p(rstd), rows,
+                                              cols, code, eps, st)
+        capi.check(rc_)
+        torch.cuda.synchronize()
+        return out.clone(), mean, rstd, h
+
+    got, m_got, r_got, h_got = run()
+    again = run()
+    for name, a, c in zip(("out", "mean", "rstd", "h"), (got, m_got, r_got, h_got), again):
+        assert torch.equal(a, c), f"{name} bitwise reproducible"
+    xs, gs, bs = f32(xc), f32(gc), f32(bc)
+    if kind.startswith("add"):
+        h_ref = xc + rc  # torch CPU add in the I/O type
+        if kind != "add_ln_noh":
+            assert torch.equal(h_got.cpu(), h_ref), "h bit-exact"
+        hs = f32(h_ref)
+    else:
+        hs = xs
+    if rms:
+        y_ref, r_ref = norms.rms_norm_fwd(hs, gs, eps)
+        m_ref = None
+    else:
+        y_ref, m_ref, r_ref = norms.layer_norm_fwd(hs, gs, bs, eps)
+    assert np.abs(to_np(r_got) / np.asarray(r_ref).reshape(-1) - 1).max() <= 1e-5
+    if m_ref is not None:
+        m_ref = np.asarray(m_ref).reshape(-1)
+        assert np.abs(to_np(m_got) - m_ref).max() <= 1e-5 * max(1.0, np.abs(m_ref).max())
+    if kind.startswith("gelu"):
+        y_ref = norms.gelu(y_ref, kind[5:])
+    if dtype == torch.float32:
+        assert np.abs(to_np(got) - y_ref).max() <= 1e-5 * max(1, np.abs(y_ref).max())
+    else:
+        atol = affine_atol(hs, gs, None if rms else bs, eps)
+        if not rms:
+            atol = atol + 2.0 ** -21 * (np.abs(m_ref)[:, None] * np.asarray(r_ref).reshape(-1, 1)
+                                        * np.abs(gs))
+        assert_within_ulp(to_np(got), y_ref, 1.0, atol=atol, **_tol_fwd(dtype), what=kind)
+    monkeypatch.setenv("FLN_FWD_NO_SPLIT", "1")
+    capi.reload_tuning()
+    one, m_one, r_one, _ = run()
+    monkeypatch.delenv("FLN_FWD_NO_SPLIT")
+    capi.reload_tuning()
+    assert np.abs(to_np(r_got) / to_np(r_one) - 1).max() <= 1e-6
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10 if dtype == torch.float16 else 1e-5
+    assert float((got.float() - one.float()).abs().max()) <= ulp * max(1.0, float(one.float().abs().max()))
+    inplace, _, _, _ = run(src=x.clone(), inplace=True)
+    assert torch.equal(inplace, one), "in place (no split) equals one block per row"
+
+
 def test_fp8_variants_reject_bad_arguments(lib):
     x = torch.randn(4, 64, device="cuda")
     q = torch.empty(4, 64, device="cuda", dtype=torch.uint8)
