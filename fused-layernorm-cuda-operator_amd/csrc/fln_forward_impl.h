@@ -1234,21 +1234,25 @@ int launch_lds_reg(const FwdParams& p, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Few rows past the register tiles (vector path, bf16 / f16 / fp32 output, y overlapping no
-// input): one block per row left most CUs idle (bf16 64 x 1048576: 64 blocks, 1.9 TB/s).  Each
-// row splits into S <= 64 column chunks of whole steps, one 256-thread block per (row, chunk),
-// in three launches and without a workspace (the forward entry points take none):
+// Few rows past the register tiles (vector path, y overlapping no input): one block per row left
+// most CUs idle (bf16 64 x 1048576: 64 blocks, 1.9 TB/s).  Each row splits into S <= 64 column
+// chunks of whole steps, one 256-thread block per (row, chunk), in three launches (four with
+// the fp8 row scale) and without a workspace (the forward entry points take none).  The first
+// bytes of the row's own y (the "head") carry what the blocks of a row hand to each other:
 //   fwd_split_stats_kernel: the chunk's (count, sum, M2 about the chunk's mean) -- RMSNorm:
-//     (count, 0, sum of squares) -- as one float4 per chunk at the start of the row's own y
-//     (its first S x 16 bytes, the "head"); with a residual, h = x + r is written as well;
-//   fwd_split_out_kernel<HEAD = false>: every block merges its row's S triples (lane k loads
+//     (count, 0, sum of squares) -- as float4 s of the head; with a residual, h = x + r is
+//     written as well;
+//   fwd_split_max_kernel (fp8 row scale): every block merges its row's S triples (lane k loads
 //     triple k, wave_allreduce sums in a fixed order: the pairwise merge of Chan, Golub and
-//     LeVeque, the same bits in every block), then writes the outputs of its chunk
-//     but not the head, walking the chunk backwards from the lines the statistics pass read
-//     last;
+//     LeVeque, the same bits in every block) and writes its chunk's maximum |output| as float s
+//     after the triples;
+//   fwd_split_out_kernel<HEAD = false>: the same statistics (and the row maximum from the
+//     chunk maxima), then the outputs of its chunk, but not the head's vectors (for MX a whole
+//     number of 32-element blocks);
 //   fwd_split_out_kernel<HEAD = true>: one block per row: the same statistics, the head's
-//     outputs, mean and rstd.  Stream order puts it after every read of the head.
-// x (h with a residual) is read twice, as in the streamed wide-row kernel, but by every CU.
+//     outputs, mean, rstd and the row scale.  Stream order puts it after every read of the head.
+// x (h with a residual) is read twice (three times with a row scale), as in the streamed
+// wide-row kernel, but by every CU; successive passes over a chunk alternate direction.
 // ---------------------------------------------------------------------------------------------
 constexpr int kFwdSplitThreads = 256;
 constexpr int kFwdSplitU = 4;                                        // vectors per thread, step
@@ -1272,7 +1276,31 @@ __device__ __forceinline__ float2 split_row_stats(const float4* head, int S, int
   return make_float2(mean, __builtin_amdgcn_rsqf(q * inv_n + eps));
 }
 
-template <class T, bool RES, int VEC>
+// Bytes of y per row: fp8 codes or the I/O type.
+template <class T, int FP8>
+__device__ __forceinline__ char* split_y_row(const FwdParams& p, int64_t row) {
+  return static_cast<char*>(p.y) + row * p.cols * (FP8 ? 1 : static_cast<int64_t>(sizeof(T)));
+}
+
+// A block's share of its row: chunk s of S, vectors [v_lo, v_hi).
+struct SplitChunk {
+  int64_t row;
+  uint32_t s, v_lo, v_hi;
+};
+template <bool HEAD>
+__device__ __forceinline__ SplitChunk split_chunk(const FwdParams& p, uint32_t nvec,
+                                                  uint32_t head_vecs) {
+  SplitChunk c;
+  const int S = p.splits;
+  c.row = HEAD ? static_cast<int64_t>(blockIdx.x) : blockIdx.x / S;
+  c.s = HEAD ? 0u : static_cast<uint32_t>(blockIdx.x - c.row * S);
+  const uint32_t chunk = static_cast<uint32_t>(p.split_chunk);
+  c.v_lo = HEAD ? 0u : c.s * chunk;
+  c.v_hi = HEAD ? head_vecs : (c.v_lo + chunk < nvec ? c.v_lo + chunk : nvec);
+  return c;
+}
+
+template <class T, int FP8, bool RES, int VEC>
 __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const FwdParams p) {
   constexpr int kT = kFwdSplitThreads;
   constexpr int kW = kT / kWave;
@@ -1283,13 +1311,9 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const
   const int lane = t & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int64_t N = p.cols;
-  const uint32_t nvec = static_cast<uint32_t>(N / VEC);
-  const int S = p.splits;
-  const int64_t row = blockIdx.x / S;
-  const uint32_t s = static_cast<uint32_t>(blockIdx.x - row * S);
-  const uint32_t v_lo = s * static_cast<uint32_t>(p.split_chunk);
-  const uint32_t v_hi = v_lo + static_cast<uint32_t>(p.split_chunk) < nvec
-                            ? v_lo + static_cast<uint32_t>(p.split_chunk) : nvec;
+  const SplitChunk c = split_chunk<false>(p, static_cast<uint32_t>(N / VEC), 0u);
+  const int64_t row = c.row;
+  const uint32_t v_lo = c.v_lo, v_hi = c.v_hi;
   const uint32_t hi_bytes = v_hi * static_cast<uint32_t>(sizeof(P));  // nothing past the chunk
   const rsrc_t xq = make_rsrc(static_cast<const T*>(p.x) + row * N, hi_bytes);
   const rsrc_t rq = make_rsrc(RES ? static_cast<const T*>(p.res) + row * N : nullptr, hi_bytes);
@@ -1308,7 +1332,7 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
           hv[u].v[e] = from_f32<T>(to_f32(hv[u].v[e]) + to_f32(rv[u].v[e]));
-        buf_store<P>(hv[u], hq, base + t + kT * u);  // kept in cache for the output pass
+        buf_store<P>(hv[u], hq, base + t + kT * u);  // kept in cache for the later passes
       }
     }
     if (p.rms) {
@@ -1318,17 +1342,17 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const
         for (int e = 0; e < VEC; ++e) m2 = fmaf(to_f32(hv[u].v[e]), to_f32(hv[u].v[e]), m2);
       continue;
     }
-    float c = 0.0f, sm = 0.0f;
+    float cs = 0.0f, sm = 0.0f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (base + t + kT * u < v_hi) {
-        c += static_cast<float>(VEC);
+        cs += static_cast<float>(VEC);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) sm += to_f32(hv[u].v[e]);
       }
     }
-    if (c > 0.0f) {
-      const float mg = sm / c;
+    if (cs > 0.0f) {
+      const float mg = sm / cs;
       float q = 0.0f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -1340,9 +1364,9 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const
           }
         }
       }
-      const float nn = cnt + c;
+      const float nn = cnt + cs;
       const float d = mg - mu;
-      const float w = c / nn;
+      const float w = cs / nn;
       mu = fmaf(d, w, mu);
       m2 += fmaf(d * d, cnt * w, q);
       cnt = nn;
@@ -1359,15 +1383,111 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_stats_kernel(const
                       row_allreduce<SumOp>(fmaf(cnt * dm, dm, m2), red[1], kW, 0, wave, lane),
                       0.0f);
   }
-  if (t == 0) reinterpret_cast<float4*>(static_cast<T*>(p.y) + row * N)[s] = out;
+  if (t == 0) reinterpret_cast<float4*>(split_y_row<T, FP8>(p, row))[c.s] = out;
 }
 
-template <class T, bool RES, int GELU, int VEC, bool HEAD>
+// The source vectors of one step (h, or x + r rounded to T, or x) and the affine outputs.
+template <class T, bool RES, int VEC>
+struct SplitSource {
+  using P = Pack<T, VEC>;
+  rsrc_t xq, rq;
+  bool from_h;
+  __device__ __forceinline__ SplitSource(const FwdParams& p, int64_t row, uint32_t hi_bytes) {
+    const int64_t N = p.cols;
+    from_h = RES && p.h != nullptr;  // h was written by the statistics pass
+    xq = make_rsrc(from_h ? static_cast<const T*>(p.h) + row * N
+                          : static_cast<const T*>(p.x) + row * N, hi_bytes);
+    rq = make_rsrc(RES && !from_h ? static_cast<const T*>(p.res) + row * N : nullptr, hi_bytes);
+  }
+  template <int U, int POL>
+  __device__ __forceinline__ void load(uint32_t base, int t, P (&hv)[U]) const {
+    P rv[RES ? U : 1];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      hv[u] = buf_load<P, POL>(xq, base + t + kFwdSplitThreads * u);
+      if constexpr (RES) {
+        if (!from_h) rv[u] = buf_load<P, POL>(rq, base + t + kFwdSplitThreads * u);
+      }
+    }
+    if constexpr (RES) {
+      if (!from_h) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            hv[u].v[e] = from_f32<T>(to_f32(hv[u].v[e]) + to_f32(rv[u].v[e]));
+      }
+    }
+  }
+};
+
+// Head vectors: the S triples (and S chunk maxima with the fp8 row scale) in units of output
+// vectors (16 bytes of the I/O type, or VEC fp8 codes), for MX a whole number of 32-element
+// blocks.
+template <class T, int FP8, int VEC>
+__host__ __device__ inline uint32_t split_head_vecs(int S) {
+  const uint32_t bytes = static_cast<uint32_t>(S) * (FP8 == 1 ? 20u : 16u);
+  const uint32_t vb = FP8 ? static_cast<uint32_t>(VEC) : static_cast<uint32_t>(VEC * sizeof(T));
+  uint32_t v = (bytes + vb - 1) / vb;
+  if (FP8 == 2) {
+    constexpr uint32_t G = 32 / VEC;
+    v = (v + G - 1) / G * G;
+  }
+  return v;
+}
+
+template <class T, bool RES, int VEC>
+__global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_max_kernel(const FwdParams p) {
+  constexpr int kT = kFwdSplitThreads;
+  constexpr int kW = kT / kWave;
+  constexpr int U = kFwdSplitU;
+  using P = Pack<T, VEC>;
+  __shared__ float red[kW + 16];
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int64_t N = p.cols;
+  const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
+  const float fn = static_cast<float>(N);
+  const SplitChunk c = split_chunk<false>(p, static_cast<uint32_t>(N / VEC), 0u);
+  char* Y = split_y_row<T, 1>(p, c.row);
+  const float2 st = split_row_stats(reinterpret_cast<const float4*>(Y), p.splits, lane, fn,
+                                    1.0f / fn, p.eps, p.rms != 0);
+  const float mean = st.x, rstd = st.y;
+  const SplitSource<T, RES, VEC> src(p, c.row, c.v_hi * static_cast<uint32_t>(sizeof(P)));
+  const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
+  const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
+  const bool has_g = p.gamma != nullptr;
+  float am = 0.0f;
+  const uint32_t steps = (c.v_hi - c.v_lo + kFwdSplitStep - 1) / kFwdSplitStep;
+  for (uint32_t k = 0; k < steps; ++k) {  // backwards: from the lines the stats pass read last
+    const uint32_t base = c.v_lo + (steps - 1 - k) * kFwdSplitStep;
+    P hv[U];
+    src.template load<U, kDefault>(base, t, hv);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t v = base + t + kT * u;
+      const P gv = buf_load<P>(g_rs, v);
+      const P bv = buf_load<P>(b_rs, v);
+      if (v < c.v_hi) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          am = fmaxf(am, fabsf(fmaf((to_f32(hv[u].v[e]) - mean) * rstd,
+                                    has_g ? to_f32(gv.v[e]) : 1.0f, to_f32(bv.v[e]))));
+      }
+    }
+  }
+  am = row_allreduce<MaxOp>(am, red, kW, 0, wave, lane);
+  if (t == 0) reinterpret_cast<float*>(Y + p.splits * 16)[c.s] = am;
+}
+
+template <class T, int FP8, bool RES, int GELU, int VEC, bool HEAD>
 __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_out_kernel(const FwdParams p) {
   constexpr int kT = kFwdSplitThreads;
   constexpr int U = kFwdSplitU;
   using P = Pack<T, VEC>;
-  static_assert(sizeof(P) == 16, "the head holds one 16-byte triple per output vector");
+  static_assert(sizeof(P) == 16, "vector path only");
+  static_assert(FP8 == 0 || GELU == 0, "no GELU before fp8 outputs");
   constexpr bool TAB = GELU == 1 && sizeof(T) == 2;  // as in the register kernel
   __shared__ float4 gelu_tab[TAB ? kGeluLogTabN : 1];
   if constexpr (TAB) {
@@ -1378,71 +1498,91 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_out_kernel(const F
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int64_t N = p.cols;
-  const uint32_t nvec = static_cast<uint32_t>(N / VEC);
   const uint32_t row_bytes = static_cast<uint32_t>(N * sizeof(T));
   const float fn = static_cast<float>(N);
   const int S = p.splits;
-  const int64_t row = HEAD ? static_cast<int64_t>(blockIdx.x) : blockIdx.x / S;
-  const uint32_t s = HEAD ? 0u : static_cast<uint32_t>(blockIdx.x - row * S);
-  const uint32_t head = static_cast<uint32_t>(S);  // vectors holding the chunk triples
-  const uint32_t chunk = static_cast<uint32_t>(p.split_chunk);
-  const uint32_t v_lo = HEAD ? 0u : s * chunk;
-  const uint32_t v_hi = HEAD ? head : (v_lo + chunk < nvec ? v_lo + chunk : nvec);
-  const uint32_t v_first = HEAD ? 0u : (v_lo > head ? v_lo : head);  // first vector written
-  T* Y = static_cast<T*>(p.y) + row * N;
+  const uint32_t head = split_head_vecs<T, FP8, VEC>(S);
+  const SplitChunk c = split_chunk<HEAD>(p, static_cast<uint32_t>(N / VEC), head);
+  const uint32_t v_first = HEAD ? 0u : (c.v_lo > head ? c.v_lo : head);  // first vector written
+  char* Y = split_y_row<T, FP8>(p, c.row);
   const float2 st = split_row_stats(reinterpret_cast<const float4*>(Y), S, lane, fn, 1.0f / fn,
                                     p.eps, p.rms != 0);
   const float mean = st.x, rstd = st.y;
-  const bool from_h = RES && p.h != nullptr;  // h was written by the statistics pass
-  const uint32_t hi_bytes = v_hi * static_cast<uint32_t>(sizeof(P));
-  const rsrc_t xq = make_rsrc(from_h ? static_cast<const T*>(p.h) + row * N
-                                     : static_cast<const T*>(p.x) + row * N, hi_bytes);
-  const rsrc_t rq = make_rsrc(RES && !from_h ? static_cast<const T*>(p.res) + row * N : nullptr,
-                              hi_bytes);
-  const rsrc_t yq = make_rsrc(Y, hi_bytes);
+  float am = 0.0f, inv = 0.0f;
+  if constexpr (FP8 == 1) {  // the row maximum from the chunk maxima (max: any order)
+    const float* cm = reinterpret_cast<const float*>(Y + S * 16);
+    am = wave_allreduce<MaxOp>(lane < S ? cm[lane] : 0.0f);
+    inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // v_rcp_f32, 1 ulp
+  }
+  // The head block overwrites the head (several waves' worth of fp8 vectors): every wave has
+  // its statistics in registers first (the reductions above waited for the loads).
+  if constexpr (HEAD) __syncthreads();
+  const SplitSource<T, RES, VEC> src(p, c.row, c.v_hi * static_cast<uint32_t>(sizeof(P)));
+  const rsrc_t yq = make_rsrc(Y, c.v_hi * static_cast<uint32_t>(FP8 ? VEC : sizeof(P)));
   const rsrc_t g_rs = make_rsrc(p.gamma, row_bytes);
   const rsrc_t b_rs = make_rsrc(p.beta, row_bytes);  // absent beta reads as zeros
   const bool has_g = p.gamma != nullptr;
-  constexpr uint32_t kSkip = kOutOfRange / sizeof(P);  // a store offset past every resource
-  const uint32_t steps = (v_hi - v_lo + kFwdSplitStep - 1) / kFwdSplitStep;
+  const uint32_t steps = (c.v_hi - c.v_lo + kFwdSplitStep - 1) / kFwdSplitStep;
   for (uint32_t k = 0; k < steps; ++k) {
-    const uint32_t base = v_lo + (steps - 1 - k) * kFwdSplitStep;
-    P hv[U], rv[RES ? U : 1];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      hv[u] = buf_load<P, kStream>(xq, base + t + kT * u);
-      if constexpr (RES) {
-        if (!from_h) rv[u] = buf_load<P, kStream>(rq, base + t + kT * u);
-      }
-    }
+    // Opposite to the pass before: backwards after the statistics, forwards after the maximum.
+    const uint32_t base = c.v_lo + (FP8 == 1 ? k : steps - 1 - k) * kFwdSplitStep;
+    P hv[U];
+    src.template load<U, kStream>(base, t, hv);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t v = base + t + kT * u;
-      if constexpr (RES) {
-        if (!from_h) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e)
-            hv[u].v[e] = from_f32<T>(to_f32(hv[u].v[e]) + to_f32(rv[u].v[e]));
-        }
-      }
+      const bool put = v >= v_first;  // past the chunk the resource drops the store
       const P gv = buf_load<P>(g_rs, v);
       const P bv = buf_load<P>(b_rs, v);
-      P o;
+      float a[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float a = fmaf((to_f32(hv[u].v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
-                       to_f32(bv.v[e]));
-        if constexpr (GELU == 1) a = TAB ? gelu_erf_tab(gelu_tab, a) : gelu_erf(a);
-        if constexpr (GELU == 2) a = gelu_tanh(a);
-        o.v[e] = from_f32<T>(a);
+        a[e] = fmaf((to_f32(hv[u].v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
+                    to_f32(bv.v[e]));
+        if constexpr (GELU == 1) a[e] = TAB ? gelu_erf_tab(gelu_tab, a[e]) : gelu_erf(a[e]);
+        if constexpr (GELU == 2) a[e] = gelu_tanh(a[e]);
       }
-      buf_store<P, FLN_FWD_STORE_POL>(o, yq, v >= v_first ? v : kSkip);
+      if constexpr (FP8 == 0) {
+        P o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(a[e]);
+        BufIO<16, FLN_FWD_STORE_POL>::store(__builtin_bit_cast(typename BufIO<16, FLN_FWD_STORE_POL>::W, o),
+                                            yq, put ? v * 16u : kOutOfRange);
+      } else {
+        float m = inv;
+        if constexpr (FP8 == 2) {
+          // OCP MX: a 32-element block is G adjacent lanes' vectors (cols % 32 == 0, every
+          // chunk and the head a whole number of blocks).
+          constexpr int G = 32 / VEC;
+          float bm = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(a[e]));
+          const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+          m = ms.mul;  // |a * m| < 512: the saturating conversion clamps to 448
+          const uint32_t nblk = static_cast<uint32_t>(N / 32);
+          __builtin_amdgcn_raw_buffer_store_b8(
+              static_cast<uint8_t>(ms.code), make_rsrc(p.bscale + c.row * nblk, c.v_hi / G),
+              put && v % G == 0 ? v / G : kOutOfRange, 0, 0);
+        }
+        // Per-row scale: |a * inv| <= 448 (1 + 2^-22) < 464; the saturating form is kept.
+        if constexpr (VEC == 8) {
+          u32x2 w;
+          w.x = fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m);
+          w.y = fp8x4(a[4] * m, a[5] * m, a[6] * m, a[7] * m);
+          BufIO<8, FLN_FWD_STORE_POL>::store(w, yq, put ? v * 8u : kOutOfRange);
+        } else {
+          BufIO<4, FLN_FWD_STORE_POL>::store(fp8x4(a[0] * m, a[1] * m, a[2] * m, a[3] * m), yq,
+                                             put ? v * 4u : kOutOfRange);
+        }
+      }
     }
   }
   if constexpr (HEAD) {
     const uint32_t stat_off = t == 0 ? 0u : kOutOfRange;
-    buf_store_f32(mean, make_rsrc(p.mean ? p.mean + row : nullptr, 4u), stat_off);
-    buf_store_f32(rstd, make_rsrc(p.rstd ? p.rstd + row : nullptr, 4u), stat_off);
+    buf_store_f32(mean, make_rsrc(p.mean ? p.mean + c.row : nullptr, 4u), stat_off);
+    buf_store_f32(rstd, make_rsrc(p.rstd ? p.rstd + c.row : nullptr, 4u), stat_off);
+    if constexpr (FP8 == 1)
+      buf_store_f32(am * (1.0f / 448.0f), make_rsrc(p.scale + c.row, 4u), stat_off);
   }
 }
 
@@ -1450,7 +1590,7 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_out_kernel(const F
 // chunks measured faster at every row count that takes this path (bf16, us, 16 / 32 / 64
 // chunks: 64 x 1048576 81.9 / 71.0 / 67.7; 4 x 1048576 26.4 / 17.7 / 13.3; 200 x 262144 54.0 /
 // 52.1 / 51.9; residual 64 x 1048576 138.5 / 126.2 / 116.4).
-template <class T, int VEC>
+template <class T, int FP8, int VEC>
 int launch_split(FwdParams p, hipStream_t s) {
   const int64_t nvec = p.cols / VEC;
   const int64_t steps = (nvec + kFwdSplitStep - 1) / kFwdSplitStep;
@@ -1463,25 +1603,35 @@ int launch_split(FwdParams p, hipStream_t s) {
   p.splits = static_cast<int>((nvec + p.split_chunk - 1) / p.split_chunk);
   const dim3 grid(static_cast<unsigned>(p.rows * p.splits)), rows(static_cast<unsigned>(p.rows));
   const dim3 block(kFwdSplitThreads);
-  auto three = [&](auto stats, auto body, auto head) {
+  auto run = [&](auto stats, auto body, auto head) {
     hipLaunchKernelGGL(stats, grid, block, 0, s, p);
+    if constexpr (FP8 == 1) {
+      if (p.res)
+        hipLaunchKernelGGL((fwd_split_max_kernel<T, true, VEC>), grid, block, 0, s, p);
+      else
+        hipLaunchKernelGGL((fwd_split_max_kernel<T, false, VEC>), grid, block, 0, s, p);
+    }
     hipLaunchKernelGGL(body, grid, block, 0, s, p);
     hipLaunchKernelGGL(head, rows, block, 0, s, p);
     return static_cast<int>(hipGetLastError());
   };
   if (p.res)
-    return three(fwd_split_stats_kernel<T, true, VEC>, fwd_split_out_kernel<T, true, 0, VEC, false>,
-                 fwd_split_out_kernel<T, true, 0, VEC, true>);
-  if (p.gelu == FLN_GELU_ERF)
-    return three(fwd_split_stats_kernel<T, false, VEC>,
-                 fwd_split_out_kernel<T, false, 1, VEC, false>,
-                 fwd_split_out_kernel<T, false, 1, VEC, true>);
-  if (p.gelu == FLN_GELU_TANH)
-    return three(fwd_split_stats_kernel<T, false, VEC>,
-                 fwd_split_out_kernel<T, false, 2, VEC, false>,
-                 fwd_split_out_kernel<T, false, 2, VEC, true>);
-  return three(fwd_split_stats_kernel<T, false, VEC>, fwd_split_out_kernel<T, false, 0, VEC, false>,
-               fwd_split_out_kernel<T, false, 0, VEC, true>);
+    return run(fwd_split_stats_kernel<T, FP8, true, VEC>,
+               fwd_split_out_kernel<T, FP8, true, 0, VEC, false>,
+               fwd_split_out_kernel<T, FP8, true, 0, VEC, true>);
+  if constexpr (FP8 == 0) {
+    if (p.gelu == FLN_GELU_ERF)
+      return run(fwd_split_stats_kernel<T, 0, false, VEC>,
+                 fwd_split_out_kernel<T, 0, false, 1, VEC, false>,
+                 fwd_split_out_kernel<T, 0, false, 1, VEC, true>);
+    if (p.gelu == FLN_GELU_TANH)
+      return run(fwd_split_stats_kernel<T, 0, false, VEC>,
+                 fwd_split_out_kernel<T, 0, false, 2, VEC, false>,
+                 fwd_split_out_kernel<T, 0, false, 2, VEC, true>);
+  }
+  return run(fwd_split_stats_kernel<T, FP8, false, VEC>,
+             fwd_split_out_kernel<T, FP8, false, 0, VEC, false>,
+             fwd_split_out_kernel<T, FP8, false, 0, VEC, true>);
 }
 
 // Byte ranges [a, a + na) and [b, b + nb) overlap (null pointers never do).
@@ -1656,29 +1806,33 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   // Fewer rows than CUs (16-bit / fp32 output): each row split over several blocks, its
   // statistics handed over through the head of its own y row (so y may overlap no input).
   bool split = false;
-  if constexpr (FP8 == 0) {
+  {
     const int64_t bytes = p.rows * N * static_cast<int64_t>(sizeof(T));
+    const int64_t ybytes = FP8 ? p.rows * N : bytes;
     const int64_t pbytes = N * static_cast<int64_t>(sizeof(T));
     // Against the kernels that read x once (LDS-staged, with or without half the row in
     // registers) the split's second read pays only with very few rows (bf16, us: 32 x 131072
     // 19.5 -> 11.7, 64 x 131072 19.8 -> 16.2, 64 x 65536 11.0 against 11.6, 128 x 131072 21.6 /
     // 21.6); against the streamed kernel, which reads it twice anyway, with any fewer rows than
     // CUs (200 x 262144 64.4 -> 51.9, 64 x 1048576 157.6 -> 67.7).
-    const bool lds_reg = g.loop && vec_ok && p.res == nullptr &&
-                         (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
-                         nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
+    bool lds_reg = false;
+    if constexpr (FP8 == 0)
+      lds_reg = g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
+                nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
     const int64_t max_rows = (lds || lds_reg) ? device_cu_count() / 4 - 1 : device_cu_count() - 1;
-    split = g.loop && vec_ok && p.rows <= max_rows && pbytes < (int64_t(1) << 31) &&
-            !tun.fwd_no_split && !overlaps(p.y, bytes, p.x, bytes) &&
-            !overlaps(p.y, bytes, p.res, bytes) && !overlaps(p.y, bytes, p.h, bytes) &&
-            !overlaps(p.y, bytes, p.gamma, pbytes) && !overlaps(p.y, bytes, p.beta, pbytes);
+    // fp8 codes: the head's float4 triples need 16-byte aligned rows.
+    const bool y_ok = FP8 == 0 || (N % 16 == 0 && aligned16(p.y));
+    split = g.loop && vec_ok && y_ok && p.rows <= max_rows && pbytes < (int64_t(1) << 31) &&
+            !tun.fwd_no_split && !overlaps(p.y, ybytes, p.x, bytes) &&
+            !overlaps(p.y, ybytes, p.res, bytes) && !overlaps(p.y, ybytes, p.h, bytes) &&
+            !overlaps(p.y, ybytes, p.gamma, pbytes) && !overlaps(p.y, ybytes, p.beta, pbytes);
   }
   if (tun.debug_geometry)
     fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
             "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
             cap, wide_cap, split ? "split" : lds ? "lds" : wide ? "wide" : g.loop ? "loop" : "registers", g.wpr,
             g.vpl, static_cast<int>(g.exact), g.threads);
-  if (split) return launch_split<T, VV>(p, s);
+  if (split) return launch_split<T, FP8, VV>(p, s);
   if (lds) return launch_lds<T, FP8, VV>(p, s);
   if constexpr (FP8 == 0) {
     if (g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&

@@ -900,6 +900,90 @@ def test_split_rows_forward(lib, monkeypatch, kind, dtype, rows, cols):
     assert torch.equal(inplace, one), "in place (no split) equals one block per row"
 
 
+@pytest.mark.parametrize("kind,dtype,rows,cols", [
+    ("ln_fp8", torch.bfloat16, 16, 262144), ("add_rms_fp8", torch.float16, 8, 131072),
+    ("ln_fp8", torch.float32, 20, 40000), ("rms_mx", torch.bfloat16, 12, 200000),
+    ("add_rms_mx", torch.float16, 4, 524288), ("rms_fp8", torch.bfloat16, 10, 131080)],
+    ids=["ln_fp8-bf16-16x262144", "add_rms_fp8-f16-8x131072", "ln_fp8-f32-20x40000",
+         "rms_mx-bf16-12x200000", "add_rms_mx-f16-4x524288", "rms_fp8-bf16-10x131080-nosplit"])
+def test_split_rows_forward_fp8(lib, monkeypatch, kind, dtype, rows, cols):
+    """The split forward with fp8 outputs: the per-row scale takes a fourth launch (chunk
+    maxima after the chunk triples in the head, which then spans several waves' worth of code
+    vectors), MX keeps the head a whole number of 32-element blocks; 131080 columns (rows not a
+    multiple of 16 bytes of codes) keep one block per row.  Codes and scales against the
+    oracle, bitwise reproducible, and scales within 1e-6 of one block per row
+    (FLN_FWD_NO_SPLIT)."""
+    gen = torch.Generator().manual_seed(cols + rows + 3)
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, r, g, b = cuda(xc), cuda(rc), cuda(gc), cuda(bc)
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    mx = kind.endswith("_mx")
+
+    def run():
+        q = torch.zeros(rows, cols, device="cuda", dtype=torch.uint8)
+        sc = torch.zeros(rows, cols // 32 if mx else 1, device="cuda",
+                         dtype=torch.uint8 if mx else torch.float32)
+        h = torch.zeros_like(x)
+        mean = torch.zeros(rows, device="cuda")
+        rstd = torch.zeros(rows, device="cuda")
+        st = capi.stream()
+        if kind == "ln_fp8":
+            rc_ = lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(q), p(sc), p(mean), p(rstd),
+                                                rows, cols, code, 1e-5, st)
+        elif kind == "rms_fp8":
+            rc_ = lib.fln_rmsnorm_fp8_forward(p(x), p(g), p(q), p(sc), p(rstd), rows, cols, code,
+                                              1e-6, st)
+        elif kind == "add_rms_fp8":
+            rc_ = lib.fln_add_rmsnorm_fp8_forward(p(x), p(r), p(g), p(h), p(q), p(sc), p(rstd),
+                                                  rows, cols, code, 1e-6, st)
+        else:
+            rc_ = _mx_call(lib, kind[:-3], x, r, g, None, q, sc, h, rows, cols, code)
+        capi.check(rc_)
+        torch.cuda.synchronize()
+        return q, sc, mean, rstd, h
+
+    got = run()
+    again = run()
+    for name, a, c in zip(("codes", "scale", "mean", "rstd", "h"), got, again):
+        assert torch.equal(a, c), f"{name} bitwise reproducible"
+    q, sc, mean, rstd, h = got
+    xs, gs, bs = f32(xc), f32(gc), f32(bc)
+    io = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    if kind.startswith("add"):
+        h_ref = xc + rc  # torch CPU add in the I/O type
+        assert torch.equal(h.cpu(), h_ref), "h bit-exact"
+    if mx:
+        q_ref, s_ref, y_ref = _mx_ref(kind[:-3], xs, f32(rc), gs, bs, io)
+        assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, s_ref, y_ref, kind)
+    else:
+        hs = f32(xc + rc) if kind.startswith("add") else xs
+        if kind == "ln_fp8":
+            y_ref, m_ref, r_ref = norms.layer_norm_fwd(hs, gs, bs, 1e-5)
+            q_ref, s_ref = norms.layer_norm_fp8_fwd(hs, gs, bs, 1e-5)
+            m_ref = np.asarray(m_ref).reshape(-1)
+            assert np.abs(to_np(mean) - m_ref).max() <= 1e-5 * max(1.0, np.abs(m_ref).max())
+        else:
+            y_ref, r_ref = norms.rms_norm_fwd(hs, gs, 1e-6)
+            q_ref, s_ref = norms.rms_norm_fp8_fwd(hs, gs, 1e-6)
+        assert np.abs(to_np(rstd) / np.asarray(r_ref).reshape(-1) - 1).max() <= 1e-5
+        assert_fp8_close(q.cpu().numpy(), to_np(sc).reshape(-1), q_ref, s_ref, kind,
+                         t_ref=_scaled(y_ref))
+    monkeypatch.setenv("FLN_FWD_NO_SPLIT", "1")
+    capi.reload_tuning()
+    one = run()
+    monkeypatch.delenv("FLN_FWD_NO_SPLIT")
+    capi.reload_tuning()
+    if mx:
+        assert float((q.float() - one[0].float()).abs().gt(1).float().mean()) <= 1e-3
+    else:
+        assert np.abs(to_np(sc) / to_np(one[1]) - 1).max() <= 1e-6
+        assert float((q != one[0]).float().mean()) <= 1e-3
+
+
 def test_fp8_variants_reject_bad_arguments(lib):
     x = torch.randn(4, 64, device="cuda")
     q = torch.empty(4, 64, device="cuda", dtype=torch.uint8)
