@@ -1813,13 +1813,17 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     // Against the kernels that read x once (LDS-staged, with or without half the row in
     // registers) the split's second read pays only with very few rows (bf16, us: 32 x 131072
     // 19.5 -> 11.7, 64 x 131072 19.8 -> 16.2, 64 x 65536 11.0 against 11.6, 128 x 131072 21.6 /
-    // 21.6); against the streamed kernel, which reads it twice anyway, with any fewer rows than
-    // CUs (200 x 262144 64.4 -> 51.9, 64 x 1048576 157.6 -> 67.7).
+    // 21.6).  Against the streamed kernel, which reads x as often, it pays until that kernel's
+    // one or two rows per CU balance (200 x 262144 64.4 -> 51.9, 300 x 262144 106.0 -> 74.0,
+    // 512 x 262144 131.6 -> 125.4, 1024 x 262144 271.5 / 271.3, fp32 600 x 65544 93.4 -> 83.5),
+    // for fp8 outputs only below 1.5 blocks per CU (LN -> fp8 300 x 262144 118.2 -> 94.8, 512 x
+    // 140000 84.2 against 94.6; MX 400 x 262144 116.7 against 119.6).
     bool lds_reg = false;
     if constexpr (FP8 == 0)
       lds_reg = g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
                 nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
-    const int64_t max_rows = (lds || lds_reg) ? device_cu_count() / 4 - 1 : device_cu_count() - 1;
+    const int64_t cus = device_cu_count();
+    const int64_t max_rows = (lds || lds_reg) ? cus / 4 - 1 : FP8 ? cus * 3 / 2 - 1 : 4 * cus - 1;
     // fp8 codes: the head's float4 triples need 16-byte aligned rows.
     const bool y_ok = FP8 == 0 || (N % 16 == 0 && aligned16(p.y));
     split = g.loop && vec_ok && y_ok && p.rows <= max_rows && pbytes < (int64_t(1) << 31) &&

@@ -806,13 +806,14 @@ def test_wide_rows_forward(lib, kind, dtype, rows, cols, aligned):
     ("gelu_none", torch.bfloat16, 8, 140000), ("gelu_tanh", torch.float32, 60, 40000),
     ("add_ln", torch.bfloat16, 24, 100000), ("add_ln_noh", torch.float16, 12, 90000),
     ("add_rms", torch.float16, 4, 524288), ("gelu_none", torch.float32, 6, 65536),
-    ("ln", torch.float32, 30, 32768)],
+    ("ln", torch.float32, 30, 32768), ("ln", torch.bfloat16, 300, 140000)],
     ids=["ln-bf16-16x262144", "rms-f16-40x70000", "gelu_none-bf16-8x140000",
          "gelu_tanh-f32-60x40000", "add_ln-bf16-24x100000", "add_ln_noh-f16-12x90000",
-         "add_rms-f16-4x524288", "gelu_none-f32-6x65536", "ln-f32-30x32768"])
+         "add_rms-f16-4x524288", "gelu_none-f32-6x65536", "ln-f32-30x32768",
+         "ln-bf16-300x140000"])
 def test_split_rows_forward(lib, monkeypatch, kind, dtype, rows, cols):
-    """Few rows past the register tiles (fewer than CUs where the streamed kernel would run, a
-    quarter of them where an LDS-staged one would): each row split into up to 64 column chunks
+    """Few rows past the register tiles (fewer than 4 per CU where the streamed kernel would
+    run, a quarter of the CUs where an LDS-staged one would): each row split into up to 64 column chunks
     (one block each; the chunk statistics handed to the output pass through the first bytes of
     the row's own y; 70000 fp16 columns: a last chunk of 558 vectors; a residual with and
     without h).  Outputs and statistics against the oracle, bitwise reproducible, within 1 ulp
