@@ -107,9 +107,15 @@ def get_optimal_config(batch_size: int, hidden_size: int,
     loop, wpr, vpl, exact, threads = _forward_geometry(batch_size, nvec, cap, wide_cap, raw_cap,
                                                        vec_path, num_cus)
     # Rows past the register tiles: parked in LDS (vector path, <= 8 vectors per thread of a
-    # 1024-thread block), else streamed by the wide-row kernel (rows under 2 GiB).
+    # 1024-thread block; LayerNorm keeps half of the row in registers up to twice that), else
+    # streamed by the wide-row kernel (rows under 2 GiB).  Few rows split over several blocks
+    # each: fewer than a quarter of the CUs where a kernel parked in LDS would run, fewer than
+    # 4 per CU where the streamed one would.
     lds = loop and vec_path and nvec <= 8 * 1024
+    lds_reg = loop and vec_path and nvec <= 16 * 1024
     wide = loop and not lds and hidden_size * es < 2 ** 31
+    max_rows = num_cus // 4 - 1 if (lds or lds_reg) else 4 * num_cus - 1
+    split = loop and vec_path and batch_size <= max_rows and hidden_size * es < 2 ** 31
     return {
         "use_mixed_precision": dtype in (torch.float16, torch.bfloat16),
         "threads_per_block": threads,
@@ -121,9 +127,10 @@ def get_optimal_config(batch_size: int, hidden_size: int,
         "vectors_per_lane": vpl if not loop else None,
         "exact_tiling": exact,
         "register_resident": not loop,
-        "lds_staged": lds,
-        "threads_lds": 1024 if lds else None,
-        "wide_streamed": wide,
+        "lds_staged": lds and not split,
+        "threads_lds": 1024 if lds and not split else None,
+        "wide_streamed": wide and not split,
+        "split_rows": split,
     }
 
 

@@ -69,6 +69,10 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
              torch.bfloat16, 8, 1e-5, (1.0, 0.02), (0.0, 0.02)),
     Workload("wide_ln_fwd_bwd_bf16_512x131072", "layer_norm_fwd_bwd", 512, 131072,
              torch.bfloat16, 9, 1e-5, (1.0, 0.02), (0.0, 0.02)),
+    # Few very wide rows: the split forward (each row over 64 blocks) and the two-pass backward
+    # with the row statistics split into column chunks.
+    Workload("few_rows_ln_fwd_bwd_bf16_64x1048576", "layer_norm_fwd_bwd", 64, 1048576,
+             torch.bfloat16, 11, 1e-5, (1.0, 0.02), (0.0, 0.02)),
     Workload("wide_ln_gelu_erf_fwd_bwd_bf16_4096x16384", "layer_norm_gelu_fwd_bwd", 4096, 16384,
              torch.bfloat16, 10, 1e-5, (1.0, 0.02), (0.0, 0.02), approximate="none"),
     # Narrow rows (profiled, not benchmark lines): where the backward's column reduction is a

@@ -551,7 +551,8 @@ def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay(rows, cols,
     (64, 16384, torch.float16), (64, 32768, torch.bfloat16), (64, 16384, torch.float32),
     (3, 20000, torch.float32), (64, 65536, torch.bfloat16), (5, 65544, torch.bfloat16),
     (7, 32772, torch.float32), (3, 40001, torch.float16), (2, 131072, torch.bfloat16),
-    (16384, 2560, torch.bfloat16), (8192, 6656, torch.bfloat16), (16384, 3328, torch.float32)])
+    (16384, 2560, torch.bfloat16), (8192, 6656, torch.bfloat16), (16384, 3328, torch.float32),
+    (2048, 100000, torch.float32), (63, 65536, torch.bfloat16), (300, 262144, torch.bfloat16)])
 def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeypatch):
     """functional.get_optimal_config restates the forward geometry rule; the dispatcher's own
     trace (FLN_DEBUG_GEOMETRY=1, one stderr line per launch) must agree with it."""
@@ -575,6 +576,8 @@ def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeyp
         assert (int(m[1]), int(m[2]), bool(int(m[3])), int(m[4])) == (
             cfg["waves_per_row"], cfg["vectors_per_lane"], cfg["exact_tiling"],
             cfg["threads_per_block"]), line
+    elif cfg["split_rows"]:
+        assert "-> split" in line, line
     elif cfg["lds_staged"]:
         assert "-> lds" in line, line
     elif cfg["wide_streamed"]:

@@ -399,8 +399,15 @@ def test_optimal_config_reports_dispatch_geometry():
     assert wt(fl.functional.get_optimal_config(32, 768, torch.float32)) == (3, 1, True)
     assert wt(fl.functional.get_optimal_config(16384, 2560, torch.bfloat16)) == (2, 4, False)
     assert wt(fl.functional.get_optimal_config(16384, 6656, torch.bfloat16)) == (4, 4, False)
-    c2 = fl.functional.get_optimal_config(1, 100000, torch.float32)
+    c2 = fl.functional.get_optimal_config(2048, 100000, torch.float32)
     assert not c2["register_resident"] and not c2["lds_staged"] and c2["wide_streamed"]
+    # Few rows split over several blocks each: under 4 per CU past the LDS tile, under a
+    # quarter of the CUs within it.
+    c1 = fl.functional.get_optimal_config(1, 100000, torch.float32)
+    assert c1["split_rows"] and not c1["wide_streamed"] and not c1["lds_staged"]
+    assert fl.functional.get_optimal_config(1023, 262144, torch.bfloat16)["split_rows"]
+    assert not fl.functional.get_optimal_config(1024, 262144, torch.bfloat16)["split_rows"]
+    assert fl.functional.get_optimal_config(63, 65536, torch.bfloat16)["split_rows"]
     c3 = fl.functional.get_optimal_config(64, 65536, torch.bfloat16)
     assert not c3["register_resident"] and c3["lds_staged"] and not c3["wide_streamed"]
     c4 = fl.functional.get_optimal_config(64, 40001, torch.bfloat16)  # unaligned: streamed
