@@ -985,6 +985,66 @@ def test_split_rows_forward_fp8(lib, monkeypatch, kind, dtype, rows, cols):
         assert float((q != one[0]).float().mean()) <= 1e-3
 
 
+@pytest.mark.parametrize("splits", [1, 3, 7, 64])
+@pytest.mark.parametrize("kind", ["ln", "ln_fp8", "add_rms_mx"])
+def test_split_rows_forced_counts(lib, monkeypatch, kind, splits):
+    """The split forward at forced chunk counts (FLN_FWD_SPLITS: one chunk, so the head block
+    and the output block share the row; odd counts with a short last chunk; the most, whose
+    fp8 head spans several waves): outputs within 1 ulp of one block per row (fp8 / MX codes:
+    at most 0.1% differ), scales and statistics to 1e-6."""
+    rows, cols = 6, 139264  # 17408 bf16 vectors: 17 steps
+    gen = torch.Generator().manual_seed(splits + 97 * len(kind))
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(torch.bfloat16)
+    rc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16)
+    x, r, g, b = cuda(xc), cuda(rc), cuda(gc), cuda(bc)
+    code = capi.dtype_code(x)
+    p = capi.ptr
+
+    def run():
+        out = torch.zeros(rows, cols, device="cuda",
+                          dtype=torch.bfloat16 if kind == "ln" else torch.uint8)
+        sc = torch.zeros(rows, cols // 32 if kind == "add_rms_mx" else 1, device="cuda",
+                         dtype=torch.uint8 if kind == "add_rms_mx" else torch.float32)
+        h = torch.zeros_like(x)
+        mean = torch.zeros(rows, device="cuda")
+        rstd = torch.zeros(rows, device="cuda")
+        if kind == "ln":
+            rc_ = lib.fln_layernorm_forward(p(x), p(g), p(b), p(out), p(mean), p(rstd), rows,
+                                            cols, code, 1e-5, capi.stream())
+        elif kind == "ln_fp8":
+            rc_ = lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(out), p(sc), p(mean), p(rstd),
+                                                rows, cols, code, 1e-5, capi.stream())
+        else:
+            rc_ = _mx_call(lib, "add_rms", x, r, g, None, out, sc, h, rows, cols, code)
+        capi.check(rc_)
+        torch.cuda.synchronize()
+        return out, sc, mean, rstd, h
+
+    monkeypatch.setenv("FLN_FWD_SPLITS", str(splits))
+    capi.reload_tuning()
+    got = run()
+    monkeypatch.delenv("FLN_FWD_SPLITS")
+    monkeypatch.setenv("FLN_FWD_NO_SPLIT", "1")
+    capi.reload_tuning()
+    one = run()
+    monkeypatch.delenv("FLN_FWD_NO_SPLIT")
+    capi.reload_tuning()
+    if kind == "ln":
+        d = (got[0].float() - one[0].float()).abs().max()
+        assert float(d) <= 2.0 ** -7 * max(1.0, float(one[0].float().abs().max()))
+        assert np.abs(to_np(got[2]) - to_np(one[2])).max() <= 1e-6 * max(1.0, float(one[2].abs().max()))
+    else:
+        assert float((got[0] != one[0]).float().mean()) <= 1e-3
+        if kind == "ln_fp8":
+            assert np.abs(to_np(got[1]) / to_np(one[1]) - 1).max() <= 1e-6
+        else:
+            assert torch.equal(got[4], one[4]), "h"
+    if kind != "add_rms_mx":
+        assert np.abs(to_np(got[3]) / to_np(one[3]) - 1).max() <= 1e-6
+
+
 def test_fp8_variants_reject_bad_arguments(lib):
     x = torch.randn(4, 64, device="cuda")
     q = torch.empty(4, 64, device="cuda", dtype=torch.uint8)
