@@ -478,9 +478,10 @@ def test_opcheck(op, args):
     (64, 18432, torch.bfloat16),    # RAW forward tiles; 768-thread LDS-staged backward
     (48, 32768, torch.bfloat16),    # RAW forward tiles; two-pass backward (row sums, column pass)
     (40, 16384, torch.float32),     # fp32 LDS-staged backward
-    (6, 131072, torch.bfloat16),    # streamed wide-row forward; two-pass backward
+    (6, 131072, torch.bfloat16),    # split forward (3 launches); two-pass backward, split sums
+    (6, 131073, torch.bfloat16),    # streamed wide-row forward (unaligned rows); two-pass
     (0, 4096, torch.float32),       # empty batch: the backward zero-fills dgamma / dbeta
-], ids=["registers", "lds768", "two_pass", "lds_fp32", "wide", "empty"])
+], ids=["registers", "lds768", "two_pass", "lds_fp32", "split", "wide", "empty"])
 def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay(rows, cols, dtype):
     """LayerNorm forward + backward (stage 1 and column reduction) captured once per kernel
     route, replayed with new data copied into the static inputs and the outputs overwritten
