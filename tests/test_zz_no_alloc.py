@@ -42,9 +42,11 @@ def _noalloc(lib, dy, x, mean, rstd, g, dres=None, want_dbeta=True):
 
 
 @pytest.mark.parametrize("cases", [
-    # (rows, cols, dtype, residual gradient, dbeta wanted): a large call, then smaller ones.
+    # (rows, cols, dtype, residual gradient, dbeta wanted): a large call, then smaller ones
+    # (12 x 65536: the two-pass backward with its row statistics split into column chunks).
     [(16384, 8192, torch.bfloat16, False, True), (8192, 4096, torch.bfloat16, False, True),
-     (1000, 2048, torch.bfloat16, True, True), (37, 768, torch.float32, False, False)],
+     (1000, 2048, torch.bfloat16, True, True), (12, 65536, torch.bfloat16, False, True),
+     (37, 768, torch.float32, False, False)],
 ])
 def test_noalloc_backward_equals_workspace_backward(lib, cases):
     for k, (rows, cols, dtype, with_dres, want_dbeta) in enumerate(cases):
