@@ -806,11 +806,12 @@ def test_wide_rows_forward(lib, kind, dtype, rows, cols, aligned):
     ("gelu_none", torch.bfloat16, 8, 140000), ("gelu_tanh", torch.float32, 60, 40000),
     ("add_ln", torch.bfloat16, 24, 100000), ("add_ln_noh", torch.float16, 12, 90000),
     ("add_rms", torch.float16, 4, 524288), ("gelu_none", torch.float32, 6, 65536),
-    ("ln", torch.float32, 30, 32768), ("ln", torch.bfloat16, 300, 140000)],
+    ("ln", torch.float32, 30, 32768), ("ln", torch.bfloat16, 300, 140000),
+    ("gelu_tanh", torch.bfloat16, 20, 200000), ("rms", torch.float32, 50, 70000)],
     ids=["ln-bf16-16x262144", "rms-f16-40x70000", "gelu_none-bf16-8x140000",
          "gelu_tanh-f32-60x40000", "add_ln-bf16-24x100000", "add_ln_noh-f16-12x90000",
          "add_rms-f16-4x524288", "gelu_none-f32-6x65536", "ln-f32-30x32768",
-         "ln-bf16-300x140000"])
+         "ln-bf16-300x140000", "gelu_tanh-bf16-20x200000", "rms-f32-50x70000"])
 def test_split_rows_forward(lib, monkeypatch, kind, dtype, rows, cols):
     """Few rows past the register tiles (fewer than 4 per CU where the streamed kernel would
     run, a quarter of the CUs where an LDS-staged one would): each row split into up to 64 column chunks
@@ -904,9 +905,11 @@ def test_split_rows_forward(lib, monkeypatch, kind, dtype, rows, cols):
 @pytest.mark.parametrize("kind,dtype,rows,cols", [
     ("ln_fp8", torch.bfloat16, 16, 262144), ("add_rms_fp8", torch.float16, 8, 131072),
     ("ln_fp8", torch.float32, 20, 40000), ("rms_mx", torch.bfloat16, 12, 200000),
-    ("add_rms_mx", torch.float16, 4, 524288), ("rms_fp8", torch.bfloat16, 10, 131080)],
+    ("add_rms_mx", torch.float16, 4, 524288), ("rms_fp8", torch.bfloat16, 10, 131080),
+    ("add_ln_fp8", torch.bfloat16, 8, 262144), ("ln_mx", torch.float16, 6, 200000)],
     ids=["ln_fp8-bf16-16x262144", "add_rms_fp8-f16-8x131072", "ln_fp8-f32-20x40000",
-         "rms_mx-bf16-12x200000", "add_rms_mx-f16-4x524288", "rms_fp8-bf16-10x131080-nosplit"])
+         "rms_mx-bf16-12x200000", "add_rms_mx-f16-4x524288", "rms_fp8-bf16-10x131080-nosplit",
+         "add_ln_fp8-bf16-8x262144", "ln_mx-f16-6x200000"])
 def test_split_rows_forward_fp8(lib, monkeypatch, kind, dtype, rows, cols):
     """The split forward with fp8 outputs: the per-row scale takes a fourth launch (chunk
     maxima after the chunk triples in the head, which then spans several waves' worth of code
@@ -941,8 +944,12 @@ def test_split_rows_forward_fp8(lib, monkeypatch, kind, dtype, rows, cols):
         elif kind == "add_rms_fp8":
             rc_ = lib.fln_add_rmsnorm_fp8_forward(p(x), p(r), p(g), p(h), p(q), p(sc), p(rstd),
                                                   rows, cols, code, 1e-6, st)
+        elif kind == "add_ln_fp8":
+            rc_ = lib.fln_add_layernorm_fp8_forward(p(x), p(r), p(g), p(b), p(h), p(q), p(sc),
+                                                    p(mean), p(rstd), rows, cols, code, 1e-5, st)
         else:
-            rc_ = _mx_call(lib, kind[:-3], x, r, g, None, q, sc, h, rows, cols, code)
+            rc_ = _mx_call(lib, kind[:-3], x, r, g, b if kind == "ln_mx" else None, q, sc, h,
+                           rows, cols, code)
         capi.check(rc_)
         torch.cuda.synchronize()
         return q, sc, mean, rstd, h
@@ -962,7 +969,7 @@ def test_split_rows_forward_fp8(lib, monkeypatch, kind, dtype, rows, cols):
         assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, s_ref, y_ref, kind)
     else:
         hs = f32(xc + rc) if kind.startswith("add") else xs
-        if kind == "ln_fp8":
+        if kind in ("ln_fp8", "add_ln_fp8"):
             y_ref, m_ref, r_ref = norms.layer_norm_fwd(hs, gs, bs, 1e-5)
             q_ref, s_ref = norms.layer_norm_fp8_fwd(hs, gs, bs, 1e-5)
             m_ref = np.asarray(m_ref).reshape(-1)
