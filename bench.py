@@ -489,7 +489,9 @@ def torch_cpu_baseline(w, seconds):
 
     med, n = _median_time(run, seconds)
     return {"value": round(algorithmic_bytes(w)["total"] / med / 1e9, 3), "unit": "GB/s",
-            "cores": threads, "kind": "torch-cpu",
+            "cores": threads, "kind": "reference",
+            "path": ("torch-CPU F.layer_norm / F.rms_norm + autograd: what the reference module "
+                     "runs off the GPU (fused_layernorm/layernorm.py:189-193)"),
             "sample": (f"full {w.rows} x {w.cols} {str(w.dtype).replace('torch.', '')} step of "
                        f"{w.name} (the reference's CPU path: F.layer_norm + autograd backward of "
                        f"x, gamma, beta), median of {n} runs, {med * 1e3:.1f} ms per step"),
