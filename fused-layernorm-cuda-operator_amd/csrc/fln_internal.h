@@ -48,6 +48,9 @@ struct BwdParams {
                       // split (two-pass path), in the workspace
   int64_t stat_chunk; // vectors per column split of the row statistics (two-pass path)
   int stat_splits;    // column splits per row of the row statistics (two-pass path)
+  void* out_g;        // two-pass path with one block row: dgamma written by the column pass
+  void* out_b;        // ... and dbeta (no partial rows, no column reduction)
+  int out_dtype;      // their dtype
   int64_t rows;
   int64_t cols;
   int64_t rows_per_block;

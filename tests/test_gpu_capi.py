@@ -1521,16 +1521,18 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
 @pytest.mark.parametrize("kind,dtype,rows,cols", [
     ("ln", torch.bfloat16, 12, 262144), ("rms", torch.float16, 8, 300000),
     ("ln_dres", torch.float32, 16, 40000), ("gelu_tanh", torch.bfloat16, 8, 131072),
-    ("ln", torch.bfloat16, 4, 100003)],
+    ("ln", torch.bfloat16, 4, 100003), ("ln", torch.bfloat16, 4, 1048576),
+    ("rms", torch.float32, 3, 524288)],
     ids=["ln-bf16-12x262144", "rms-f16-8x300000", "ln_dres-f32-16x40000",
-         "gelu_tanh-bf16-8x131072", "ln-bf16-4x100003-scalar"])
+         "gelu_tanh-bf16-8x131072", "ln-bf16-4x100003-scalar", "ln-bf16-4x1048576-one-block-row",
+         "rms-f32-3x524288-one-block-row"])
 def test_two_pass_backward_few_rows(lib, monkeypatch, kind, dtype, rows, cols):
     """Few very wide rows: the two-pass backward's row statistics split each row into up to 16
     column chunks of whole 1024-vector steps (so the statistics pass has blocks for every CU)
     and the column pass sums a row's splits in order (300000 fp16 columns: 13 chunks of 3072
-    vectors, the last one 636; 100003 columns: the scalar path, 14 chunks).  Parity with the
-    oracle, bitwise reproducible, and agreement with one block per row
-    (FLN_BWD_STAT_SPLITS=1)."""
+    vectors, the last one 636; 100003 columns: the scalar path, 14 chunks; 131072 vectors: a
+    column pass of one block row, which writes dgamma / dbeta itself).  Parity with the oracle,
+    bitwise reproducible, and agreement with one block per row (FLN_BWD_STAT_SPLITS=1)."""
     gen = torch.Generator().manual_seed(cols + rows)
     xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
     gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
