@@ -1258,6 +1258,9 @@ constexpr int kFwdSplitThreads = 256;
 constexpr int kFwdSplitU = 4;                                        // vectors per thread, step
 constexpr int kFwdSplitStep = kFwdSplitThreads * kFwdSplitU;         // vectors per step
 constexpr int kFwdSplitMax = kWave;                                  // chunks per row
+// The head (at most 64 x 20 bytes: 320 fp8 vectors of 4 codes) lies within one step, so within
+// chunk 0 and the one step of the head launch.
+static_assert(kFwdSplitMax * 20 / 4 <= kFwdSplitStep, "split head past one step");
 
 // The row statistics (mean, rstd) from the S <= 64 chunk triples at the row's head.  All 64
 // lanes must be active; the result is wave-uniform and identical in every block of the row.
