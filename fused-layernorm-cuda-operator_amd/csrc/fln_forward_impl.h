@@ -1255,11 +1255,13 @@ int launch_lds_reg(const FwdParams& p, hipStream_t s) {
 // wide-row kernel, but by every CU; successive passes over a chunk alternate direction.
 // ---------------------------------------------------------------------------------------------
 constexpr int kFwdSplitThreads = 256;
-constexpr int kFwdSplitU = 4;                                        // vectors per thread, step
+constexpr int kFwdSplitU = 2;                                        // vectors per thread, step
 constexpr int kFwdSplitStep = kFwdSplitThreads * kFwdSplitU;         // vectors per step
 constexpr int kFwdSplitMax = kWave;                                  // chunks per row
 // The head (at most 64 x 20 bytes: 320 fp8 vectors of 4 codes) lies within one step, so within
-// chunk 0 and the one step of the head launch.
+// chunk 0 and the one step of the head launch.  Steps of 512 vectors (2 per thread) rather than
+// 1024 give shorter rows more chunks (bf16, us: 32 x 131072 10.84 -> 10.51, 60 x 131072 13.27 ->
+// 12.91, 16 x 1048576 21.03 -> 20.32; 64 x 1048576 and LN -> fp8 unchanged).
 static_assert(kFwdSplitMax * 20 / 4 <= kFwdSplitStep, "split head past one step");
 
 // The row statistics (mean, rstd) from the S <= 64 chunk triples at the row's head.  All 64

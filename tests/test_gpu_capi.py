@@ -816,7 +816,7 @@ def test_split_rows_forward(lib, monkeypatch, kind, dtype, rows, cols):
     """Few rows past the register tiles (fewer than 4 per CU where the streamed kernel would
     run, a quarter of the CUs where an LDS-staged one would): each row split into up to 64 column chunks
     (one block each; the chunk statistics handed to the output pass through the first bytes of
-    the row's own y; 70000 fp16 columns: a last chunk of 558 vectors; a residual with and
+    the row's own y; 70000 fp16 columns: a last chunk of 46 vectors; a residual with and
     without h).  Outputs and statistics against the oracle, bitwise reproducible, within 1 ulp
     of one block per row (FLN_FWD_NO_SPLIT), and an in-place call (y = x, so no split) equal to
     that."""
@@ -999,7 +999,7 @@ def test_split_rows_forced_counts(lib, monkeypatch, kind, splits):
     and the output block share the row; odd counts with a short last chunk; the most, whose
     fp8 head spans several waves): outputs within 1 ulp of one block per row (fp8 / MX codes:
     at most 0.1% differ), scales and statistics to 1e-6."""
-    rows, cols = 6, 139264  # 17408 bf16 vectors: 17 steps
+    rows, cols = 6, 139264  # 17408 bf16 vectors: 34 steps of 512
     gen = torch.Generator().manual_seed(splits + 97 * len(kind))
     xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(torch.bfloat16)
     rc = torch.randn(rows, cols, generator=gen).to(torch.bfloat16)
