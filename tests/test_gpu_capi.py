@@ -1052,6 +1052,63 @@ def test_split_rows_forced_counts(lib, monkeypatch, kind, splits):
         assert np.abs(to_np(got[3]) / to_np(one[3]) - 1).max() <= 1e-6
 
 
+@pytest.mark.parametrize("kind", ["ln", "rms", "ln_fp8"])
+def test_split_rows_forward_optional_pointers(lib, monkeypatch, kind):
+    """The split forward without gamma / beta (identity affine) and without the mean / rstd
+    outputs: the same outputs as one block per row to 1 ulp (fp8: codes differ on at most 0.1%,
+    scales to 1e-6), against the oracle with gamma = 1, beta = 0."""
+    rows, cols = 16, 262144
+    gen = torch.Generator().manual_seed(5 + len(kind))
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(torch.bfloat16)
+    x = cuda(xc)
+    code = capi.dtype_code(x)
+    p = capi.ptr
+
+    def run():
+        if kind == "ln_fp8":
+            q = torch.zeros(rows, cols, device="cuda", dtype=torch.uint8)
+            sc = torch.zeros(rows, device="cuda")
+            capi.check(lib.fln_layernorm_fp8_forward(p(x), None, None, p(q), p(sc), None, None,
+                                                     rows, cols, code, 1e-5, capi.stream()))
+            torch.cuda.synchronize()
+            return q, sc
+        y = torch.zeros_like(x)
+        if kind == "ln":
+            capi.check(lib.fln_layernorm_forward(p(x), None, None, p(y), None, None, rows, cols,
+                                                 code, 1e-5, capi.stream()))
+        else:
+            capi.check(lib.fln_rmsnorm_forward(p(x), None, p(y), None, rows, cols, code, 1e-6,
+                                               capi.stream()))
+        torch.cuda.synchronize()
+        return y, None
+
+    got = run()
+    monkeypatch.setenv("FLN_FWD_NO_SPLIT", "1")
+    capi.reload_tuning()
+    one = run()
+    monkeypatch.delenv("FLN_FWD_NO_SPLIT")
+    capi.reload_tuning()
+    xs = f32(xc)
+    if kind == "ln_fp8":
+        q_ref, s_ref = norms.layer_norm_fp8_fwd(xs, None, None, 1e-5)
+        y_ref, _, _ = norms.layer_norm_fwd(xs, None, None, 1e-5)
+        assert_fp8_close(got[0].cpu().numpy(), to_np(got[1]), q_ref, s_ref, kind,
+                         t_ref=_scaled(y_ref))
+        assert float((got[0] != one[0]).float().mean()) <= 1e-3
+        assert np.abs(to_np(got[1]) / to_np(one[1]) - 1).max() <= 1e-6
+        return
+    atol = affine_atol(xs, None, None, 1e-5)
+    if kind == "ln":
+        y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, None, None, 1e-5)
+        atol = atol + 2.0 ** -21 * (np.abs(np.asarray(m_ref)).reshape(-1, 1) *
+                                    np.asarray(r_ref).reshape(-1, 1))
+    else:
+        y_ref, _ = norms.rms_norm_fwd(xs, None, 1e-6)
+    assert_within_ulp(to_np(got[0]), y_ref, 1.0, atol=atol, kind="bf16", what=kind)
+    d = (got[0].float() - one[0].float()).abs().max()
+    assert float(d) <= 2.0 ** -7 * max(1.0, float(one[0].float().abs().max()))
+
+
 def test_fp8_variants_reject_bad_arguments(lib):
     x = torch.randn(4, 64, device="cuda")
     q = torch.empty(4, 64, device="cuda", dtype=torch.uint8)
