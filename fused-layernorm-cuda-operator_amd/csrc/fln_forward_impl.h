@@ -1822,13 +1822,19 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     // one or two rows per CU balance (200 x 262144 64.4 -> 51.9, 300 x 262144 106.0 -> 74.0,
     // 512 x 262144 131.6 -> 125.4, 1024 x 262144 271.5 / 271.3, fp32 600 x 65544 93.4 -> 83.5),
     // for fp8 outputs only below 1.5 blocks per CU (LN -> fp8 300 x 262144 118.2 -> 94.8, 512 x
-    // 140000 84.2 against 94.6; MX 400 x 262144 116.7 against 119.6).
+    // 140000 84.2 against 94.6; MX 400 x 262144 116.7 against 119.6).  Splitting rows past a
+    // quarter of the CUs on the LDS-staged routes gains nothing even where their last round runs
+    // part-empty (300 x 65536 21.0 against 23.1, 1638 x 40960 68.4 / 68.4, 682 x 98304 64.7 /
+    // 64.7: FLN_FWD_SPLIT_ROWS overrides the row limit).
     bool lds_reg = false;
     if constexpr (FP8 == 0)
       lds_reg = g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
                 nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
     const int64_t cus = device_cu_count();
-    const int64_t max_rows = (lds || lds_reg) ? cus / 4 - 1 : FP8 ? cus * 3 / 2 - 1 : 4 * cus - 1;
+    const int64_t max_rows = tun.fwd_split_rows > 0 ? tun.fwd_split_rows
+                             : (lds || lds_reg)    ? cus / 4 - 1
+                             : FP8                 ? cus * 3 / 2 - 1
+                                                   : 4 * cus - 1;
     // fp8 codes: the head's float4 triples need 16-byte aligned rows.
     const bool y_ok = FP8 == 0 || (N % 16 == 0 && aligned16(p.y));
     split = g.loop && vec_ok && y_ok && p.rows <= max_rows && pbytes < (int64_t(1) << 31) &&

@@ -64,6 +64,7 @@ Tuning read_tuning() {
   t.fwd_no_wide = env_knob("FLN_FWD_NO_WIDE", 0);
   t.fwd_no_split = env_knob("FLN_FWD_NO_SPLIT", 0);
   t.fwd_splits = env_knob("FLN_FWD_SPLITS", 0);
+  t.fwd_split_rows = env_knob("FLN_FWD_SPLIT_ROWS", 0);
   t.bwd_epl = env_knob("FLN_BWD_EPL", 0);
   t.bwd_wpr = env_knob("FLN_BWD_WPR", 0);
   t.bwd_threads = env_knob("FLN_BWD_THREADS", 0);

@@ -75,6 +75,7 @@ struct Tuning {
   int fwd_no_wide;     // FLN_FWD_NO_WIDE: the looped forward instead of the streamed wide-row one
   int fwd_no_split;    // FLN_FWD_NO_SPLIT: never the few-row split forward
   int fwd_splits;      // FLN_FWD_SPLITS: column chunks per row of the split forward
+  int fwd_split_rows;  // FLN_FWD_SPLIT_ROWS: split the forward of up to this many rows
   int bwd_epl;         // FLN_BWD_EPL: backward elements per lane
   int bwd_wpr;         // FLN_BWD_WPR: backward waves per row
   int bwd_threads;     // FLN_BWD_THREADS: backward block size (256, 512, 1024)
