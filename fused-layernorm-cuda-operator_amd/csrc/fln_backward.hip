@@ -1350,8 +1350,12 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   if (!g.reg_path && g.lds_cpt == 0 && have_workspace && cols * es < (int64_t(1) << 31) &&
       tun.bwd_no_two_pass == 0) {
     const int64_t tiles = (nvec + kWideThreads - 1) / kWideThreads;
-    int64_t chunks = (FLN_COLPASS_BLOCKS_PER_CU * static_cast<int64_t>(device_cu_count()) +
-                      tiles - 1) / tiles;
+    // FLN_BWD_COLPASS_PER_CU overrides the default; re-swept with few rows, 1 / 2 / 4 per CU,
+    // bf16 us: 128 x 131072 42.2 / 43.0 / 53.7, 256 x 131072 71.7 / 70.5 / 80.1, 300 x 65536
+    // 48.9 / 49.3 / 57.4, 1024 x 65536 129.6 / 123.8 / 129.7.
+    const int64_t per_cu =
+        tun.bwd_colpass_per_cu > 0 ? tun.bwd_colpass_per_cu : FLN_COLPASS_BLOCKS_PER_CU;
+    int64_t chunks = (per_cu * static_cast<int64_t>(device_cu_count()) + tiles - 1) / tiles;
     if (chunks > workspace_partial_rows(rows)) chunks = workspace_partial_rows(rows);
     if (chunks < 1) chunks = 1;
     g.two_pass = true;

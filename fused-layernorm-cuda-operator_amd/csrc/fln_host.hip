@@ -72,6 +72,7 @@ Tuning read_tuning() {
   t.bwd_no_lds = env_knob("FLN_BWD_NO_LDS", 0);
   t.bwd_no_two_pass = env_knob("FLN_BWD_NO_TWO_PASS", 0);
   t.bwd_stat_splits = env_knob("FLN_BWD_STAT_SPLITS", 0);
+  t.bwd_colpass_per_cu = env_knob("FLN_BWD_COLPASS_PER_CU", 0);
   return t;
 }
 

@@ -83,6 +83,7 @@ struct Tuning {
   int bwd_no_lds;      // FLN_BWD_NO_LDS: never the LDS-staged backward
   int bwd_no_two_pass; // FLN_BWD_NO_TWO_PASS: never the two-pass backward
   int bwd_stat_splits; // FLN_BWD_STAT_SPLITS: column splits per row of the two-pass statistics
+  int bwd_colpass_per_cu; // FLN_BWD_COLPASS_PER_CU: column-pass blocks per CU (two-pass path)
 };
 const Tuning& tuning();  // read at the first call; fln_reload_tuning() reads again
 void reload_tuning();
