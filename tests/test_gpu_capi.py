@@ -1585,9 +1585,9 @@ def test_16bit_rows_past_16384_backward(lib, monkeypatch, kind, dtype, cols):
          "rms-f32-3x524288-one-block-row"])
 def test_two_pass_backward_few_rows(lib, monkeypatch, kind, dtype, rows, cols):
     """Few very wide rows: the two-pass backward's row statistics split each row into up to 16
-    column chunks of whole 1024-vector steps (so the statistics pass has blocks for every CU)
-    and the column pass sums a row's splits in order (300000 fp16 columns: 13 chunks of 3072
-    vectors, the last one 636; 100003 columns: the scalar path, 14 chunks; 131072 vectors: a
+    column chunks of whole 2048-vector steps (so the statistics pass has blocks for every CU)
+    and the column pass sums a row's splits in order (300000 fp16 columns: 10 chunks of 4096
+    vectors, the last one 636; 100003 columns: the scalar path, 13 chunks; 131072 vectors: a
     column pass of one block row, which writes dgamma / dbeta itself).  Parity with the oracle,
     bitwise reproducible, and agreement with one block per row (FLN_BWD_STAT_SPLITS=1)."""
     gen = torch.Generator().manual_seed(cols + rows)
