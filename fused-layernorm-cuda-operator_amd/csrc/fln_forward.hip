@@ -34,6 +34,12 @@ int launch_forward_f32(const FwdParams& p, bool out_fp8, hipStream_t s);
 int launch_forward_bf16(const FwdParams& p, bool out_fp8, hipStream_t s);
 int launch_forward_f16(const FwdParams& p, bool out_fp8, hipStream_t s);
 int launch_forward_f64(const FwdParams& p, hipStream_t s);
+int plan_forward_f32(int64_t rows, int64_t cols, int fp8, bool res, int gelu, int64_t cus,
+                     fln_forward_plan_t* out);
+int plan_forward_bf16(int64_t rows, int64_t cols, int fp8, bool res, int gelu, int64_t cus,
+                      fln_forward_plan_t* out);
+int plan_forward_f16(int64_t rows, int64_t cols, int fp8, bool res, int gelu, int64_t cus,
+                     fln_forward_plan_t* out);
 
 int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s) {
   if (p.rows < 0 || p.cols < 0 || p.rows > INT32_MAX || p.cols > INT32_MAX) return FLN_ERR_INVALID;
@@ -57,6 +63,27 @@ int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s) {
 }  // namespace fln
 
 using fln::FwdParams;
+
+extern "C" int fln_forward_plan(int64_t rows, int64_t cols, int dtype, int fp8, int residual,
+                                int gelu_mode, int num_cus, fln_forward_plan_t* plan) {
+  if (!plan || rows < 0 || cols < 0 || rows > INT32_MAX || cols > INT32_MAX) return FLN_ERR_INVALID;
+  if (fp8 < 0 || fp8 > 2 || gelu_mode < 0 || gelu_mode > 2 || num_cus < 0) return FLN_ERR_INVALID;
+  if (fp8 && (gelu_mode != FLN_GELU_NONE || dtype == FLN_F64)) return FLN_ERR_INVALID;
+  if (fp8 == 2 && cols % 32 != 0) return FLN_ERR_INVALID;
+  if (dtype == FLN_F64 && residual) return FLN_ERR_INVALID;
+  *plan = fln_forward_plan_t{FLN_ROUTE_NONE, 0, 0, 0, 0, 0};
+  if (rows == 0 || cols == 0) return FLN_OK;  // nothing is launched
+  const int64_t cus = num_cus > 0 ? num_cus : fln::device_cu_count();
+  switch (dtype) {
+    case FLN_F32: return fln::plan_forward_f32(rows, cols, fp8, residual != 0, gelu_mode, cus, plan);
+    case FLN_BF16: return fln::plan_forward_bf16(rows, cols, fp8, residual != 0, gelu_mode, cus, plan);
+    case FLN_F16: return fln::plan_forward_f16(rows, cols, fp8, residual != 0, gelu_mode, cus, plan);
+    case FLN_F64:  // fp64 always takes the looped kernel with fp64 accumulation
+      *plan = fln_forward_plan_t{FLN_ROUTE_LOOP, 1, 0, 0, 0, cols >= 4096 ? 1024 : 256};
+      return FLN_OK;
+    default: return FLN_ERR_INVALID;
+  }
+}
 
 extern "C" int fln_layernorm(const void* x, const void* gamma, const void* beta, void* y,
                              int64_t rows, int64_t cols, int dtype, float eps, void* stream) {

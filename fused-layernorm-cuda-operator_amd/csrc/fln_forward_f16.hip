@@ -7,4 +7,8 @@ int launch_forward_f16(const FwdParams& p, bool out_fp8, hipStream_t s) {
   return p.mx ? detail::dispatch_typed<_Float16, 2>(p, s)
               : detail::dispatch_typed<_Float16, 1>(p, s);
 }
+int plan_forward_f16(int64_t rows, int64_t cols, int fp8, bool res, int gelu, int64_t cus,
+                     fln_forward_plan_t* out) {
+  return detail::plan_query<_Float16>(rows, cols, fp8, res, gelu, cus, out);
+}
 }  // namespace fln

@@ -6,4 +6,8 @@ int launch_forward_f32(const FwdParams& p, bool out_fp8, hipStream_t s) {
   if (!out_fp8) return detail::dispatch_typed<float, 0>(p, s);
   return p.mx ? detail::dispatch_typed<float, 2>(p, s) : detail::dispatch_typed<float, 1>(p, s);
 }
+int plan_forward_f32(int64_t rows, int64_t cols, int fp8, bool res, int gelu, int64_t cus,
+                     fln_forward_plan_t* out) {
+  return detail::plan_query<float>(rows, cols, fp8, res, gelu, cus, out);
+}
 }  // namespace fln

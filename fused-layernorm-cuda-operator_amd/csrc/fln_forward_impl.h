@@ -1696,7 +1696,7 @@ struct FwdGeometry {
 };
 
 inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_cap, int max_cap,
-                                bool vec_path, int forced_wpr) {
+                                bool vec_path, int forced_wpr, int64_t cus) {
   FwdGeometry g{};
   constexpr int max_wpr = 16;
   auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
@@ -1711,7 +1711,7 @@ inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_ca
   auto fits = [&](int w, int v) { return v <= (widest ? max_cap : cap_of(w)); };
   int vpl = next_pow2(static_cast<int>(per_lane(wpr)));
   bool exact = nvec == static_cast<int64_t>(vpl) * kWave * wpr;
-  const int64_t target_waves = 4 * static_cast<int64_t>(device_cu_count());
+  const int64_t target_waves = 4 * cus;
   if (vec_path && !exact) {
     const int top = widest ? max_cap : (cap > wide_cap ? cap : wide_cap);
     // One vector per lane only when rows are too few to fill the device (latency-bound calls
@@ -1754,19 +1754,33 @@ inline FwdGeometry fwd_geometry(int64_t rows, int64_t nvec, int cap, int wide_ca
   return g;
 }
 
+// The launch plan of a forward call: which kernel route runs and its tiling.  The dispatcher
+// below and the C-ABI query fln_forward_plan (what functional.get_optimal_config reports) both
+// take it from here, so there is one rule.  Inputs besides the shape: the flavour (fp8 / MX
+// outputs, residual, GELU form), whether the 16-byte vector path is open (row width and pointer
+// alignment), whether the split forward may write its hand-over into y (y overlaps no input and,
+// for fp8 codes, is 16-byte aligned), and the CU count.
+struct FwdPlan {
+  int route;  // FLN_ROUTE_*
+  int vec;    // elements per lane load (16 bytes on the vector path, 1 on the scalar path)
+  int cap, wide_cap;
+  FwdGeometry g;
+};
+
 template <class T, int FP8>
-int dispatch_typed(FwdParams p, hipStream_t s) {
+FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok, bool y_ok,
+                   int64_t cus) {
   constexpr int VV = 16 / sizeof(T);  // elements per 16-byte vector
-  const int64_t N = p.cols;
-  bool vec_ok = (N % VV == 0) && aligned16(p.x) && aligned16(p.gamma) && aligned16(p.beta) &&
-                aligned16(p.res) && aligned16(p.h);
-  if (FP8)
-    vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(p.y) % VV == 0);
-  else
-    vec_ok = vec_ok && aligned16(p.y);
   const Tuning& tun = tuning();
-  if (tun.force_loop) return launch_loop<T, float, FP8>(p, s);
-  const int vec = vec_ok ? VV : 1;
+  FwdPlan pl{};
+  pl.vec = vec_ok ? VV : 1;
+  if (tun.force_loop || sizeof(T) == 8) {
+    pl.route = FLN_ROUTE_LOOP;
+    pl.g.loop = true;
+    pl.g.threads = N >= 4096 ? 1024 : 256;  // launch_loop's block
+    return pl;
+  }
+  const int vec = pl.vec;
   // Elements per lane: at most 32 by default (measured best or equal on the 4096-8192-wide
   // benchmark rows); more waves per row beyond that.
   const int epl = tun.fwd_epl > 0 ? tun.fwd_epl : 32;
@@ -1777,11 +1791,13 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   // within the 128 VGPRs of a 1024-thread block.
   int wide_cap = vec_ok ? 16 / VV : 8;
   if (wide_cap > cap) wide_cap = cap;
+  pl.cap = cap;
+  pl.wide_cap = wide_cap;
   // The 32-element RAW tiles only for 16-bit types (fp32 ones would hold 64 VGPRs of gamma /
   // beta alone and spill); wider fp32 rows go to the LDS-staged kernel.
   const int raw_cap = (vec_ok && VV < 8) ? wide_cap : max_cap;
   const int64_t nvec = N / vec;
-  FwdGeometry g = fwd_geometry(p.rows, nvec, cap, wide_cap, raw_cap, vec_ok, tun.fwd_wpr);
+  FwdGeometry g = fwd_geometry(rows, nvec, cap, wide_cap, raw_cap, vec_ok, tun.fwd_wpr, cus);
   // The fp8 row scale (no residual) and 16-bit LN + GELU take 4 waves per row with masked tail
   // lanes over an exact tiling of 5-7 waves when at most 1/8 of the 4-wave tile is masked (bf16,
   // 32768 x 7168 LN -> fp8: 7 waves 134.5 us at its best grid, 4 waves 129.9 us; 8192 x 7168
@@ -1789,7 +1805,7 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
   // 49152 x 5120, 3/8 masked, LN -> fp8 loses: 152.2 -> 161.6 us).  Plain LayerNorm keeps the
   // exact tiling (32768 x 7168: 156.8 against 167.7 us), as do the residual and MX flavours and
   // fp32 GELU (8192 x 7168 tanh 77.2 against 83.5 us).
-  if ((FP8 == 1 || (FP8 == 0 && p.gelu != 0 && sizeof(T) == 2)) && p.res == nullptr && vec_ok &&
+  if ((FP8 == 1 || (FP8 == 0 && gelu != 0 && sizeof(T) == 2)) && !has_res && vec_ok &&
       !g.loop && g.exact && g.wpr >= 5 && g.wpr <= 7 && tun.fwd_wpr <= 0) {
     const int64_t per4 = (nvec + 4 * kWave - 1) / (4 * kWave);
     const int v4 = next_pow2(static_cast<int>(per4));
@@ -1802,70 +1818,126 @@ int dispatch_typed(FwdParams p, hipStream_t s) {
     }
   }
   // Rows past the register tiles: the LDS-staged kernel on the vector path (up to 8 vectors
-  // per thread of a 1024-thread block), the streamed wide-row kernel otherwise (buffer
-  // resources span at most 4 GiB: rows of 2 GiB or more keep the looped kernel).
+  // per thread of a 1024-thread block; LayerNorm / RMSNorm and LN + GELU -- tanh, or erf in
+  // fp32 -- with half of each row in registers up to twice that), the streamed wide-row kernel
+  // otherwise (buffer resources span at most 4 GiB: rows of 2 GiB or more keep the looped
+  // kernel).
   const bool lds = g.loop && vec_ok && nvec <= int64_t(kFwdLdsCpt) * kFwdLdsThreads &&
                    !tun.fwd_no_lds;
-  const bool wide = g.loop && !lds && N * int64_t(sizeof(T)) < (int64_t(1) << 31) &&
+  bool lds_reg = false;
+  if constexpr (FP8 == 0)
+    lds_reg = g.loop && !lds && vec_ok && !has_res && (gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
+              nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
+  const bool wide = g.loop && !lds && !lds_reg && N * int64_t(sizeof(T)) < (int64_t(1) << 31) &&
                     !tun.fwd_no_wide;
   // Fewer rows than CUs (16-bit / fp32 output): each row split over several blocks, its
   // statistics handed over through the head of its own y row (so y may overlap no input).
-  bool split = false;
-  {
-    const int64_t bytes = p.rows * N * static_cast<int64_t>(sizeof(T));
-    const int64_t ybytes = FP8 ? p.rows * N : bytes;
-    const int64_t pbytes = N * static_cast<int64_t>(sizeof(T));
-    // Against the kernels that read x once (LDS-staged, with or without half the row in
-    // registers) the split's second read pays only with very few rows (bf16, us: 32 x 131072
-    // 19.5 -> 11.7, 64 x 131072 19.8 -> 16.2, 64 x 65536 11.0 against 11.6, 128 x 131072 21.6 /
-    // 21.6).  Against the streamed kernel, which reads x as often, it pays until that kernel's
-    // one or two rows per CU balance (200 x 262144 64.4 -> 51.9, 300 x 262144 106.0 -> 74.0,
-    // 512 x 262144 131.6 -> 125.4, 1024 x 262144 271.5 / 271.3, fp32 600 x 65544 93.4 -> 83.5),
-    // for fp8 outputs only below 1.5 blocks per CU (LN -> fp8 300 x 262144 118.2 -> 94.8, 512 x
-    // 140000 84.2 against 94.6; MX 400 x 262144 116.7 against 119.6).  Splitting rows past a
-    // quarter of the CUs on the LDS-staged routes gains nothing even where their last round runs
-    // part-empty (300 x 65536 21.0 against 23.1, 1638 x 40960 68.4 / 68.4, 682 x 98304 64.7 /
-    // 64.7: FLN_FWD_SPLIT_ROWS overrides the row limit).
-    bool lds_reg = false;
-    if constexpr (FP8 == 0)
-      lds_reg = g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
-                nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds;
-    const int64_t cus = device_cu_count();
-    const int64_t max_rows = tun.fwd_split_rows > 0 ? tun.fwd_split_rows
-                             : (lds || lds_reg)    ? cus / 4 - 1
-                             : FP8                 ? cus * 3 / 2 - 1
-                                                   : 4 * cus - 1;
-    // fp8 codes: the head's float4 triples need 16-byte aligned rows.
-    const bool y_ok = FP8 == 0 || (N % 16 == 0 && aligned16(p.y));
-    split = g.loop && vec_ok && y_ok && p.rows <= max_rows && pbytes < (int64_t(1) << 31) &&
-            !tun.fwd_no_split && !overlaps(p.y, ybytes, p.x, bytes) &&
-            !overlaps(p.y, ybytes, p.res, bytes) && !overlaps(p.y, ybytes, p.h, bytes) &&
-            !overlaps(p.y, ybytes, p.gamma, pbytes) && !overlaps(p.y, ybytes, p.beta, pbytes);
+  // Against the kernels that read x once (LDS-staged, with or without half the row in
+  // registers) the split's second read pays only with very few rows (bf16, us: 32 x 131072
+  // 19.5 -> 11.7, 64 x 131072 19.8 -> 16.2, 64 x 65536 11.0 against 11.6, 128 x 131072 21.6 /
+  // 21.6).  Against the streamed kernel, which reads x as often, it pays until that kernel's
+  // one or two rows per CU balance (200 x 262144 64.4 -> 51.9, 300 x 262144 106.0 -> 74.0,
+  // 512 x 262144 131.6 -> 125.4, 1024 x 262144 271.5 / 271.3, fp32 600 x 65544 93.4 -> 83.5),
+  // for fp8 outputs only below 1.5 blocks per CU (LN -> fp8 300 x 262144 118.2 -> 94.8, 512 x
+  // 140000 84.2 against 94.6; MX 400 x 262144 116.7 against 119.6).  Splitting rows past a
+  // quarter of the CUs on the LDS-staged routes gains nothing even where their last round runs
+  // part-empty (300 x 65536 21.0 against 23.1, 1638 x 40960 68.4 / 68.4, 682 x 98304 64.7 /
+  // 64.7: FLN_FWD_SPLIT_ROWS overrides the row limit).
+  const int64_t max_rows = tun.fwd_split_rows > 0 ? tun.fwd_split_rows
+                           : (lds || lds_reg)    ? cus / 4 - 1
+                           : FP8                 ? cus * 3 / 2 - 1
+                                                 : 4 * cus - 1;
+  const int64_t pbytes = N * static_cast<int64_t>(sizeof(T));
+  const bool split = g.loop && vec_ok && y_ok && rows <= max_rows &&
+                     pbytes < (int64_t(1) << 31) && !tun.fwd_no_split;
+  pl.route = split ? FLN_ROUTE_SPLIT : lds ? FLN_ROUTE_LDS : lds_reg ? FLN_ROUTE_LDS_REG
+           : wide  ? FLN_ROUTE_WIDE  : g.loop ? FLN_ROUTE_LOOP : FLN_ROUTE_REGISTERS;
+  if (pl.route == FLN_ROUTE_REGISTERS) {
+    // The exact-GELU kernels fill their LDS table with one entry per thread: rows of three
+    // waves (192 threads) take two row groups per block.
+    if (gelu == FLN_GELU_ERF)
+      while (g.threads < kGeluLogTabN) g.threads *= 2;
+  } else {
+    g.wpr = g.vpl = 0;
+    g.exact = false;
+    g.threads = pl.route == FLN_ROUTE_SPLIT ? 256
+              : pl.route == FLN_ROUTE_LOOP  ? (N >= 4096 ? 1024 : 256)
+                                            : 1024;
   }
-  if (tun.debug_geometry)
+  pl.g = g;
+  return pl;
+}
+
+// The plan of a contiguous, 16-byte aligned call whose y overlaps no input (fln_forward_plan).
+template <class T>
+int plan_query(int64_t rows, int64_t cols, int fp8, bool res, int gelu, int64_t cus,
+               fln_forward_plan_t* out) {
+  constexpr int VV = 16 / sizeof(T);
+  const bool vec_ok = cols % VV == 0;
+  const bool y_ok = fp8 == 0 || cols % 16 == 0;
+  const FwdPlan pl = fp8 == 0 ? plan_typed<T, 0>(rows, cols, res, gelu, vec_ok, y_ok, cus)
+                   : fp8 == 1 ? plan_typed<T, 1>(rows, cols, res, gelu, vec_ok, y_ok, cus)
+                              : plan_typed<T, 2>(rows, cols, res, gelu, vec_ok, y_ok, cus);
+  out->route = pl.route;
+  out->vector_elems = pl.vec;
+  out->waves_per_row = pl.g.wpr;
+  out->vectors_per_lane = pl.g.vpl;
+  out->exact = pl.g.exact ? 1 : 0;
+  out->threads = pl.g.threads;
+  return FLN_OK;
+}
+
+inline const char* route_name(int route) {
+  switch (route) {
+    case FLN_ROUTE_REGISTERS: return "registers";
+    case FLN_ROUTE_LDS: return "lds";
+    case FLN_ROUTE_LDS_REG: return "lds+registers";
+    case FLN_ROUTE_WIDE: return "wide";
+    case FLN_ROUTE_SPLIT: return "split";
+    default: return "loop";
+  }
+}
+
+template <class T, int FP8>
+int dispatch_typed(FwdParams p, hipStream_t s) {
+  constexpr int VV = 16 / sizeof(T);  // elements per 16-byte vector
+  const int64_t N = p.cols;
+  bool vec_ok = (N % VV == 0) && aligned16(p.x) && aligned16(p.gamma) && aligned16(p.beta) &&
+                aligned16(p.res) && aligned16(p.h);
+  if (FP8)
+    vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(p.y) % VV == 0);
+  else
+    vec_ok = vec_ok && aligned16(p.y);
+  // The split forward hands each row's chunk statistics over through the head of its own y row:
+  // y may overlap no input, and fp8 codes need 16-byte aligned rows for the float4 triples.
+  const int64_t bytes = p.rows * N * static_cast<int64_t>(sizeof(T));
+  const int64_t ybytes = FP8 ? p.rows * N : bytes;
+  const int64_t pbytes = N * static_cast<int64_t>(sizeof(T));
+  const bool y_ok = (FP8 == 0 || (N % 16 == 0 && aligned16(p.y))) &&
+                    !overlaps(p.y, ybytes, p.x, bytes) && !overlaps(p.y, ybytes, p.res, bytes) &&
+                    !overlaps(p.y, ybytes, p.h, bytes) && !overlaps(p.y, ybytes, p.gamma, pbytes) &&
+                    !overlaps(p.y, ybytes, p.beta, pbytes);
+  const FwdPlan pl = plan_typed<T, FP8>(p.rows, N, p.res != nullptr, p.gelu, vec_ok, y_ok,
+                                        device_cu_count());
+  if (tuning().debug_geometry)
     fprintf(stderr, "fln forward: rows=%lld cols=%lld vec=%d cap=%d/%d -> %s wpr=%d vpl=%d "
-            "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N), vec,
-            cap, wide_cap, split ? "split" : lds ? "lds" : wide ? "wide" : g.loop ? "loop" : "registers", g.wpr,
-            g.vpl, static_cast<int>(g.exact), g.threads);
-  if (split) return launch_split<T, FP8, VV>(p, s);
-  if (lds) return launch_lds<T, FP8, VV>(p, s);
-  if constexpr (FP8 == 0) {
-    if (g.loop && vec_ok && p.res == nullptr && (p.gelu != FLN_GELU_ERF || sizeof(T) == 4) &&
-        nvec <= int64_t(2 * kFwdLdsCpt) * kFwdLdsThreads && !tun.fwd_no_lds)
-      return launch_lds_reg<T, VV>(p, s);
+            "exact=%d threads=%d\n", static_cast<long long>(p.rows), static_cast<long long>(N),
+            pl.vec, pl.cap, pl.wide_cap, route_name(pl.route), pl.g.wpr, pl.g.vpl,
+            static_cast<int>(pl.g.exact), pl.g.threads);
+  switch (pl.route) {
+    case FLN_ROUTE_SPLIT: return launch_split<T, FP8, VV>(p, s);
+    case FLN_ROUTE_LDS: return launch_lds<T, FP8, VV>(p, s);
+    case FLN_ROUTE_LDS_REG:
+      if constexpr (FP8 == 0) return launch_lds_reg<T, VV>(p, s);
+      return FLN_ERR_INVALID;  // not planned for fp8 outputs
+    case FLN_ROUTE_WIDE:
+      return vec_ok ? launch_wide<T, FP8, VV>(p, s) : launch_wide<T, FP8, 1>(p, s);
+    case FLN_ROUTE_LOOP: return launch_loop<T, float, FP8>(p, s);
+    default: break;
   }
-  if (wide) return vec_ok ? launch_wide<T, FP8, VV>(p, s) : launch_wide<T, FP8, 1>(p, s);
-  if (g.loop) return launch_loop<T, float, FP8>(p, s);
-  p.wpr = g.wpr;
-  const int vpl = g.vpl;
-  const bool exact = g.exact;
-  int threads = g.threads;
-  // The exact-GELU kernels fill their LDS table with one entry per thread: rows of three waves
-  // (192 threads) take two row groups per block.
-  if (p.gelu == 1)
-    while (threads < kGeluLogTabN) threads *= 2;
-  if (vec_ok) return launch_reg_flavour<T, FP8, VV>(p, vpl, exact, threads, s);
-  return launch_reg_flavour<T, FP8, 1>(p, vpl, false, threads, s);
+  p.wpr = pl.g.wpr;
+  if (vec_ok) return launch_reg_flavour<T, FP8, VV>(p, pl.g.vpl, pl.g.exact, pl.g.threads, s);
+  return launch_reg_flavour<T, FP8, 1>(p, pl.g.vpl, false, pl.g.threads, s);
 }
 
 }  // namespace detail

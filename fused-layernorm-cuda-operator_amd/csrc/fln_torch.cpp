@@ -546,6 +546,19 @@ std::string get_performance_hints(int batch_size, int hidden_size) {
   return s;
 }
 
+// The forward launch plan (fln_forward_plan): (route, vector_elems, waves_per_row,
+// vectors_per_lane, exact, threads) for a contiguous, aligned input; backs
+// fused_layernorm.functional.get_optimal_config (reference fused_layernorm/functional.py:47-74).
+std::tuple<int, int, int, int, bool, int> forward_plan(int64_t rows, int64_t cols, int dtype,
+                                                       int fp8, bool residual, int gelu,
+                                                       int num_cus) {
+  fln_forward_plan_t plan{};
+  check(fln_forward_plan(rows, cols, dtype, fp8, residual ? 1 : 0, gelu, num_cus, &plan),
+        "forward_plan");
+  return {plan.route, plan.vector_elems, plan.waves_per_row, plan.vectors_per_lane,
+          plan.exact != 0, plan.threads};
+}
+
 }  // namespace
 
 // Operator schemas (namespace fused_layernorm): the torch.compile-visible surface.  Fake
@@ -662,6 +675,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Residual add + RMSNorm with OCP MX fp8 output -> (codes, block scales, residual_sum)",
         py::arg("input"), py::arg("residual"), py::arg("weight") = py::none(),
         py::arg("eps") = 1e-6);
+  m.def("forward_plan", &forward_plan,
+        "Forward launch plan -> (route, vector_elems, waves_per_row, vectors_per_lane, exact, "
+        "threads); dtype / gelu are the C-ABI codes, num_cus 0 = the current device",
+        py::arg("rows"), py::arg("cols"), py::arg("dtype"), py::arg("fp8") = 0,
+        py::arg("residual") = false, py::arg("gelu") = 0, py::arg("num_cus") = 0);
   m.attr("__version__") = fln_version();
   // The reference exports the CUDA runtime version under this name; here it is HIP's.
   m.attr("__cuda_version__") = fln_hip_version();

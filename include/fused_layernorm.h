@@ -90,9 +90,10 @@ int fln_layernorm_backward(const void* dy, const void* x, const float* mean, con
 
 /* fln_layernorm_backward without a workspace argument, for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
- * counterpart in the reference.  The workspace is a fixed 32 MiB scratch array in device memory,
- * one per device that runs this entry point, held until the process ends; nothing is allocated
- * per call.  Enough for the register and LDS kernels' one partial row per CU up to 16384
+ * counterpart in the reference.  The workspace is a fixed 32 MiB scratch array in device memory
+ * (a __device__ array of the backward's code object: held on every device where libfln's
+ * backward kernels are loaded, until the process ends, whether or not this entry point is
+ * called); nothing is allocated per call.  Enough for the register and LDS kernels' one partial row per CU up to 16384
  * columns (8 MiB at 8192 x 4096); a call that needs more returns FLN_ERR_TOO_LARGE before
  * anything is launched.  Every call on a device shares that device's scratch: calls that
  * overlap on one device (other streams, other host threads) race, so serialize them.  The
@@ -195,6 +196,35 @@ int fln_add_rmsnorm_mxfp8_forward(const void* x, const void* residual, const voi
  * callers that scale themselves (and a direct check of the conversion).
  * No counterpart in the reference. */
 int fln_fp8_e4m3fn_encode(const float* x, uint8_t* q, int64_t n, void* stream);
+
+/* Forward kernel routes (fln_forward_plan). */
+#define FLN_ROUTE_NONE (-1)     /* empty call: nothing is launched */
+#define FLN_ROUTE_REGISTERS 0   /* rows held in VGPRs of one or more wave64s (fwd_reg_kernel) */
+#define FLN_ROUTE_LDS 1         /* row parked in LDS, the next row in flight (fwd_lds_kernel) */
+#define FLN_ROUTE_LDS_REG 2     /* half of each row in LDS, half in registers (fwd_lds_kernel) */
+#define FLN_ROUTE_WIDE 3        /* row streamed in passes over L2 / HBM (fwd_wide_kernel) */
+#define FLN_ROUTE_SPLIT 4       /* few rows: each split over several blocks (fwd_split_*) */
+#define FLN_ROUTE_LOOP 5        /* one block per row, scalar passes (fwd_loop_kernel) */
+
+typedef struct fln_forward_plan {
+  int route;            /* FLN_ROUTE_* */
+  int vector_elems;     /* elements per lane load: 16 bytes' worth on the vector path, else 1 */
+  int waves_per_row;    /* register route: wave64s per row (0 on the other routes) */
+  int vectors_per_lane; /* register route: vectors of the row per lane (0 on the other routes) */
+  int exact;            /* register route: 1 if no lane holds a masked slot */
+  int threads;          /* threads per block */
+} fln_forward_plan_t;
+
+/* The launch plan the forward entry points take for a contiguous, 16-byte aligned
+ * [rows, cols] input of `dtype` whose output overlaps no input: fp8 = 0 (output in dtype),
+ * 1 (fp8 e4m3fn with a per-row scale) or 2 (MXFP8); residual = 0 / 1 (residual-add flavour);
+ * gelu_mode FLN_GELU_*; num_cus the CU count to plan for (0: the current device).  It is the
+ * dispatcher's own rule (the same function decides the launches, under the same FLN_* knobs),
+ * computed on the host without touching a device when num_cus > 0.  Backs
+ * `fused_layernorm.functional.get_optimal_config`, which the reference computes from CUDA
+ * heuristics in Python (fused_layernorm/functional.py:47-74). */
+int fln_forward_plan(int64_t rows, int64_t cols, int dtype, int fp8, int residual,
+                     int gelu_mode, int num_cus, fln_forward_plan_t* plan);
 
 /* Host utilities with the reference's meaning (csrc/layernorm_cuda.cpp:144-164 and :167-195).
  * fln_get_performance_hints writes a NUL-terminated string into buf (truncated to buflen) and

@@ -58,6 +58,7 @@ SIGNATURES = {
     "fln_add_rmsnorm_mxfp8_forward": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32,
                                        _f32, _vp], _i32),
     "fln_fp8_e4m3fn_encode": ([_vp, _vp, _i64, _vp], _i32),
+    "fln_forward_plan": ([_i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "fln_get_memory_usage": ([_i32, _i32, _i32], _i64),
     "fln_get_performance_hints": ([_i32, _i32, ctypes.c_char_p, _sz], _i32),
     "fln_version": ([], ctypes.c_char_p),

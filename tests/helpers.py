@@ -42,6 +42,28 @@ def assert_within_ulp(got, ref, ulps: float = 1.0, atol: float = 0.0, kind: str 
             f"worst at {i}: got {g[i]!r} ref {r[i]!r} err {err[i]:.3g} bound {bound[i]:.3g}")
 
 
+def assert_dx(got, ref, allowance, kind: str = "bf16", what: str = "dx"):
+    """dx bar: |got - ref| <= 1 ulp_kind(ref) + allowance elementwise, where allowance is the
+    fp32 evaluation allowance of oracle.tolerance.dx_allowance (a few fp32 roundings of the
+    terms that cancel in dx, not a fraction of max|dx|).  kind: "bf16", "f16" or "f32".  The
+    share of the bound used is appended to $FLN_PARITY_REPORT when that is set."""
+    from oracle import tolerance
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    u = tolerance.ulp(r, kind)
+    err = np.abs(g - r)
+    bound = u + allowance
+    bad = err > bound
+    tolerance.report(what, tolerance.within_stats(g, r, allowance, kind))
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        al = np.broadcast_to(allowance, err.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {bad.size} elements exceed 1 {kind} ulp + the fp32 "
+            f"allowance; worst at {i}: got {g[i]!r} ref {r[i]!r} err {err[i]:.3g} ulp "
+            f"{u[i]:.3g} allowance {al[i]:.3g}")
+
+
 def assert_close_rel(got, ref, rtol: float, what: str = ""):
     """Max-norm relative check: max|got - ref| <= rtol * max|ref| (for column sums)."""
     g = np.asarray(got, np.float64)

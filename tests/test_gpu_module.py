@@ -553,10 +553,14 @@ def test_forward_backward_in_a_hip_graph_match_eager_on_every_replay(rows, cols,
     (3, 20000, torch.float32), (64, 65536, torch.bfloat16), (5, 65544, torch.bfloat16),
     (7, 32772, torch.float32), (3, 40001, torch.float16), (2, 131072, torch.bfloat16),
     (16384, 2560, torch.bfloat16), (8192, 6656, torch.bfloat16), (16384, 3328, torch.float32),
-    (2048, 100000, torch.float32), (63, 65536, torch.bfloat16), (300, 262144, torch.bfloat16)])
+    (2048, 100000, torch.float32), (63, 65536, torch.bfloat16), (300, 262144, torch.bfloat16),
+    (64, 98304, torch.bfloat16), (512, 131072, torch.bfloat16), (64, 40960, torch.float32),
+    (64, 65536, torch.float32)])
 def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeypatch):
-    """functional.get_optimal_config restates the forward geometry rule; the dispatcher's own
-    trace (FLN_DEBUG_GEOMETRY=1, one stderr line per launch) must agree with it."""
+    """functional.get_optimal_config reports the plan of the C-ABI query fln_forward_plan; the
+    dispatcher's own trace of the launch it made (FLN_DEBUG_GEOMETRY=1, one stderr line per
+    launch) must name the same route and geometry (register route: waves per row, vectors per
+    lane, exact tiling; every route: threads per block)."""
     import re
     import capi
     x = torch.randn(rows, cols, device=DEV, dtype=dtype)
@@ -569,22 +573,14 @@ def test_optimal_config_matches_the_dispatcher(rows, cols, dtype, capfd, monkeyp
     monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
     capi.reload_tuning()
     line = capfd.readouterr().err.strip().splitlines()[-1]
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    cfg = fl.functional.get_optimal_config(rows, cols, dtype, num_cus=cus)
+    cfg = fl.functional.get_optimal_config(rows, cols, dtype)
+    m = re.search(r"-> (\S+) wpr=(\d+) vpl=(\d+) exact=(\d) threads=(\d+)", line)
+    assert m, line
+    assert m[1] == cfg["route"], line
+    assert int(m[5]) == cfg["threads_per_block"], line
     if cfg["register_resident"]:
-        m = re.search(r"registers wpr=(\d+) vpl=(\d+) exact=(\d) threads=(\d+)", line)
-        assert m, line
-        assert (int(m[1]), int(m[2]), bool(int(m[3])), int(m[4])) == (
-            cfg["waves_per_row"], cfg["vectors_per_lane"], cfg["exact_tiling"],
-            cfg["threads_per_block"]), line
-    elif cfg["split_rows"]:
-        assert "-> split" in line, line
-    elif cfg["lds_staged"]:
-        assert "-> lds" in line, line
-    elif cfg["wide_streamed"]:
-        assert "-> wide" in line, line
-    else:
-        assert "-> loop" in line, line
+        assert (int(m[2]), int(m[3]), bool(int(m[4]))) == (
+            cfg["waves_per_row"], cfg["vectors_per_lane"], cfg["exact_tiling"]), line
 
 
 # ------------------------------------------------------------------------------------------------

@@ -424,6 +424,41 @@ def test_optimal_config_reports_dispatch_geometry():
     assert geo(fl.functional.get_optimal_config(4096, 16384, torch.float32)) == (16, 4, True, 1024)
     assert geo(fl.functional.get_optimal_config(8192, 8192, torch.bfloat16)) == (4, 4, True, 256)
     assert geo(fl.functional.get_optimal_config(4096, 8192, torch.float32)) == (4, 8, True, 256)
+    # Rows of 65537..131072 16-bit columns: half of each row in LDS, half in registers, for
+    # LayerNorm and the tanh GELU; the exact GELU and the residual / fp8 flavours stream them
+    # (split over several blocks each below 4 rows per CU, 1.5 with fp8 outputs).
+    route = lambda *a, **k: fl.functional.get_optimal_config(*a, **k)["route"]  # noqa: E731
+    assert route(512, 131072, torch.bfloat16) == "lds+registers"
+    assert route(512, 131072, torch.bfloat16, approximate="tanh") == "lds+registers"
+    assert route(2048, 131072, torch.bfloat16, approximate="none") == "wide"
+    assert route(512, 131072, torch.bfloat16, approximate="none") == "split"
+    assert route(2048, 131072, torch.bfloat16, residual=True) == "wide"
+    assert route(512, 131072, torch.bfloat16, fp8=1) == "wide"
+    assert route(256, 131072, torch.bfloat16, fp8=1) == "split"
+    assert route(512, 65536, torch.float32, approximate="none") == "lds+registers"
+    assert route(512, 65536, torch.bfloat16) == "lds"
+    assert route(16, 65536, torch.bfloat16) == "split"
+    assert route(4, 8, torch.float64) == "loop"
+    assert route(0, 4096, torch.bfloat16) == "none"
+    # The plan is the dispatcher's rule for the CU count asked for (the split limits scale).
+    assert route(63, 65536, torch.bfloat16, num_cus=256) == "split"
+    assert route(63, 65536, torch.bfloat16, num_cus=128) == "lds"
+
+
+def test_forward_plan_rejects_bad_arguments():
+    import capi
+    lib = capi.load()
+    plan = (ctypes.c_int * 6)()
+    assert lib.fln_forward_plan(8, 4096, capi.BF16, 0, 0, 0, 256, plan) == 0
+    assert list(plan)[:2] == [0, 8]
+    bad = [(-1, 4096, capi.BF16, 0, 0, 0, 256), (8, 4096, 9, 0, 0, 0, 256),
+           (8, 4096, capi.BF16, 3, 0, 0, 256), (8, 4096, capi.BF16, 0, 0, 3, 256),
+           (8, 4096, capi.BF16, 1, 0, capi.GELU_TANH, 256), (8, 4112, capi.BF16, 2, 0, 0, 256),
+           (8, 4096, capi.F64, 1, 0, 0, 256), (8, 4096, capi.F64, 0, 1, 0, 256),
+           (8, 4096, capi.BF16, 0, 0, 0, -1)]
+    for args in bad:
+        assert lib.fln_forward_plan(*args, plan) == capi.ERR_INVALID, args
+    assert lib.fln_forward_plan(8, 4096, capi.BF16, 0, 0, 0, 256, None) == capi.ERR_INVALID
 
 
 def test_byte_model_matches_baseline_figures():

@@ -344,3 +344,98 @@ def test_c_fp8_encoder_matches_numpy_on_a_sweep(rng):
                         [(1 + m / 16) * 2.0 ** e for e in range(-11, 10) for m in range(16)]])
     ours = norms.fp8_e4m3fn_encode(v)
     assert [c_oracle.fp8_encode_scalar(a) for a in v] == [int(c) for c in ours]
+
+
+# ------------------------------------------------------------------------------------------------
+# The dx error model (oracle/tolerance.py) used by the GPU parity bar.
+# ------------------------------------------------------------------------------------------------
+def _fp32_dx(x, dy, gamma, eps, rms, order="pairwise", round_g=False, round_xh=False,
+             out="bf16"):
+    """An fp32 evaluation of dx = rstd (g - c1 - xhat c2), rounded once to the output type:
+    statistics and row sums in fp32 (numpy's pairwise sums, or sequential running sums), with
+    optional planted bf16 roundings of g = dy gamma or of xhat."""
+    f = np.float32
+    x32, dy32, g32 = x.astype(f), dy.astype(f), gamma.astype(f)
+    n = x.shape[-1]
+
+    def rowsum(a):
+        if order == "pairwise":
+            return a.sum(axis=1, keepdims=True, dtype=f)
+        if order == "lanes":
+            # running sums over 64 elements per lane, then a tree over the lanes (the kernels'
+            # shape: per-lane partials, then cross-lane and cross-wave reductions)
+            k = min(64, a.shape[1])
+            part = np.cumsum(a.reshape(a.shape[0], -1, k), axis=2, dtype=f)[:, :, -1]
+            return part.sum(axis=1, keepdims=True, dtype=f)
+        return np.cumsum(a, axis=1, dtype=f)[:, -1:]
+
+    if rms:
+        mu = np.zeros((x.shape[0], 1), f)
+        rs = (f(1) / np.sqrt(rowsum(x32 * x32) / f(n) + f(eps))).astype(f)
+    else:
+        mu = (rowsum(x32) / f(n)).astype(f)
+        rs = (f(1) / np.sqrt(rowsum((x32 - mu) ** 2) / f(n) + f(eps))).astype(f)
+    xh = ((x32 - mu) * rs).astype(f)
+    gd = (dy32 * g32).astype(f)
+    if round_g:
+        gd = norms.round_to_bf16(gd).astype(f)
+    if round_xh:
+        xh = norms.round_to_bf16(xh).astype(f)
+    cb = f(0) if rms else (-rs * (rowsum(gd) / f(n))).astype(f)
+    cx = (-rs * (rowsum(gd * xh) / f(n))).astype(f)
+    dx = (rs * gd + (cx * xh + cb)).astype(f)
+    return norms.round_to_bf16(dx) if out == "bf16" else dx.astype(np.float64)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (16, 8192), (4, 65536)])
+@pytest.mark.parametrize("rms", [False, True], ids=["ln", "rms"])
+def test_dx_allowance_covers_fp32_and_rejects_bf16_intermediates(rows, cols, rms):
+    """The dx bar (1 ulp + oracle.tolerance.dx_allowance) holds for an fp32 evaluation of the
+    formula, with pairwise or sequential row sums, in bf16 and fp32 outputs, on data with an
+    offset mean; and it rejects the same evaluation with g = dy gamma or xhat rounded to bf16
+    (what the previous bar, 2^-12 max|dx|, could let through).  Row sums: pairwise, running
+    sums of 64 elements per lane then a tree (the kernels' order), and fully sequential running
+    sums up to 1024 columns (longer sequential sums grow past a log2 N model; no kernel sums more
+    than 64 elements of a row in one running sum)."""
+    from oracle import tolerance
+    rng = np.random.RandomState(rows + cols + rms)
+    to_bf16 = norms.round_to_bf16
+    x = to_bf16(rng.standard_normal((rows, cols)) * 1.5 + 0.25)
+    dy = to_bf16(rng.standard_normal((rows, cols)))
+    g = to_bf16(1 + 0.1 * rng.standard_normal(cols))
+    eps = 1e-6 if rms else 1e-5
+    if rms:
+        ref, _ = norms.rms_norm_bwd(dy, x, g, eps)
+    else:
+        ref, _, _ = norms.layer_norm_bwd(dy, x, g, eps)
+    al = tolerance.dx_allowance(x, dy, g, eps, rms=rms)
+    for order in ("pairwise", "lanes") + (("sequential",) if cols <= 1024 else ()):
+        for out in ("bf16", "f32"):
+            got = _fp32_dx(x, dy, g, eps, rms, order=order, out=out)
+            err = np.abs(got - ref)
+            assert (err <= tolerance.ulp(ref, out) + al).all(), (order, out)
+    for plant in ("round_g", "round_xh"):
+        got = _fp32_dx(x, dy, g, eps, rms, **{plant: True})
+        assert (np.abs(got - ref) > tolerance.ulp(ref, "bf16") + al).any(), plant
+    # For a typical element the bar is one bf16 ulp: the allowance is a small fraction of it.
+    assert np.median(al / tolerance.ulp(ref, "bf16")) < 0.125
+
+
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_dx_allowance_gelu_covers_an_approximate_derivative(approximate):
+    """With the GELU epilogue the allowance also covers GELU' evaluated within 2.1e-7 (the
+    tables' bound): an fp32 evaluation that perturbs GELU' by +-2.1e-7 stays inside."""
+    from oracle import tolerance
+    rng = np.random.RandomState(4096 + len(approximate))
+    rows, cols = 32, 4096
+    to_bf16 = norms.round_to_bf16
+    x = to_bf16(rng.standard_normal((rows, cols)))
+    dy = to_bf16(rng.standard_normal((rows, cols)))
+    g = to_bf16(1 + 0.1 * rng.standard_normal(cols))
+    b = to_bf16(0.2 * rng.standard_normal(cols))
+    ref, _, _ = norms.layer_norm_gelu_bwd(dy, x, g, b, 1e-5, approximate)
+    a, _, _ = norms.layer_norm_fwd(x, g, b, 1e-5)
+    d = norms.gelu_grad(a, approximate) + 2.1e-7 * np.sign(rng.standard_normal(a.shape))
+    got = _fp32_dx(x, (dy * d).astype(np.float32), g, 1e-5, False)
+    al = tolerance.dx_allowance(x, dy, g, 1e-5, beta=b, approximate=approximate)
+    assert (np.abs(got - ref) <= tolerance.ulp(ref, "bf16") + al).all()
