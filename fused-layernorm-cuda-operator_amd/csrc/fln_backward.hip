@@ -997,8 +997,7 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
   if (GELU != 0 && threads < kGeluTabN) return FLN_ERR_INVALID;
   if (resident) {
     static std::atomic<int> per_cu[3][64];  // [threads / 512][device]
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    const int dev = current_device();
     std::atomic<int>& slot = per_cu[threads / 512][dev];
     int v = slot.load(std::memory_order_relaxed);
     if (v == 0) {
@@ -1010,8 +1009,8 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
     *resident = static_cast<int64_t>(v) * device_cu_count();
     return 0;
   }
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), 0, s, p);
-  return static_cast<int>(hipGetLastError());
+  static std::atomic<void*> fn_cache[64];
+  return launch_cached(kernel, fn_cache, dim3(blocks), dim3(threads), s, p);
 }
 
 template <class T, int VEC, int VPL>
@@ -1462,9 +1461,11 @@ int launch_backward(const BwdParams& p0, int dtype, void* dgamma, void* dbeta, i
   if (a.G <= kCrFlatMaxG)
     hipLaunchKernelGGL(col_reduce_flat_kernel, dim3(static_cast<unsigned>(flat_blocks(a))),
                        dim3(kCrFlatThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(col_reduce_kernel, dim3(static_cast<unsigned>(quad_blocks(a))),
-                       dim3(kCrThreads), 0, s, a);
+  else {
+    static std::atomic<void*> fn_cache[64];
+    return launch_cached(col_reduce_kernel, fn_cache, dim3(static_cast<unsigned>(quad_blocks(a))),
+                         dim3(kCrThreads), s, a);
+  }
   return static_cast<int>(hipGetLastError());
 }
 
@@ -1509,6 +1510,7 @@ int backward_common(fln::BwdParams p, int dtype, void* dgamma, void* dbeta, int 
       (scratch || workspace_bytes >= fln_backward_workspace_bytes(p.rows, p.cols, dtype));
   if ((dgamma || dbeta) && !have_workspace) return FLN_ERR_INVALID;
   p.part_g = have_workspace ? static_cast<float*>(workspace) : nullptr;
+  const fln::CallDevice device_scope;
   return fln::launch_backward(p, dtype, dgamma, dbeta, dparam_dtype, have_workspace,
                               workspace_bytes, static_cast<hipStream_t>(stream));
 }

@@ -50,6 +50,7 @@ int launch_forward(const FwdParams& p, int dtype, bool out_fp8, hipStream_t s) {
   if (out_fp8 && !p.mx && !p.scale) return FLN_ERR_INVALID;
   if (out_fp8 && p.mx && (!p.bscale || p.cols % 32 != 0)) return FLN_ERR_INVALID;
   if (p.rms && p.beta) return FLN_ERR_INVALID;
+  const CallDevice device_scope;
   switch (dtype) {
     case FLN_F32: return launch_forward_f32(p, out_fp8, s);
     case FLN_BF16: return launch_forward_bf16(p, out_fp8, s);

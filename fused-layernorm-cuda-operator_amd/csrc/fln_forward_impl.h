@@ -1085,8 +1085,7 @@ inline int next_pow2(int v) {
 // Blocks of `kernel` that fit on the current device at once.
 template <class K>
 int64_t resident_blocks(K kernel, int threads, int* cache_per_device) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  const int dev = current_device();
   if (cache_per_device[dev] == 0) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
@@ -1135,8 +1134,8 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   if (grid > resident) grid = resident;
   if (grid > row_blocks) grid = row_blocks;
   if (grid > kMaxGrid) grid = kMaxGrid;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, s, p, row_blocks);
-  return static_cast<int>(hipGetLastError());
+  static std::atomic<void*> fn_cache[64];
+  return launch_cached(kernel, fn_cache, dim3(grid), dim3(threads), s, p, row_blocks);
 }
 
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT>

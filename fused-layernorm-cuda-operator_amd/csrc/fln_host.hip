@@ -27,12 +27,11 @@ int element_size(int dtype) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// CU count of the current device, cached per device index (lock-free after the first query;
-// two threads racing on the first query store the same value).
-int device_cu_count() {
+// CU count of device `dev`, cached per device index (lock-free after the first query; two
+// threads racing on the first query store the same value).
+namespace {
+int cus_of(int dev) {
   static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
   int cus = cache[dev].load(std::memory_order_relaxed);
   if (cus == 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -41,6 +40,39 @@ int device_cu_count() {
     cache[dev].store(cus, std::memory_order_relaxed);
   }
   return cus;
+}
+
+// The current device while an entry point runs (CallDevice): its launch path asks for the
+// device and its CU count a dozen times, and each hipGetDevice costs ~0.05 us.
+thread_local int tl_call_dev = -1;
+thread_local int tl_call_cus = 0;
+}  // namespace
+
+CallDevice::CallDevice() : prev_dev_(tl_call_dev), prev_cus_(tl_call_cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    tl_call_dev = dev;
+    tl_call_cus = cus_of(dev);
+  }
+}
+
+CallDevice::~CallDevice() {
+  tl_call_dev = prev_dev_;
+  tl_call_cus = prev_cus_;
+}
+
+int current_device() {
+  if (tl_call_dev >= 0) return tl_call_dev;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  return dev;
+}
+
+int device_cu_count() {
+  if (tl_call_dev >= 0) return tl_call_cus;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  return cus_of(dev);
 }
 
 // Tuning and debugging knobs: getenv scans the whole environment (~0.1 us each with ~100

@@ -11,8 +11,12 @@
 
 #include <c10/hip/HIPGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <torch/csrc/autograd/function.h>
+#include <torch/csrc/autograd/functions/utils.h>
+#include <torch/csrc/autograd/saved_variable.h>
 
 #include <array>
+#include <mutex>
 #include <optional>
 #include <string>
 #include <tuple>
@@ -546,6 +550,82 @@ std::string get_performance_hints(int batch_size, int hidden_size) {
   return s;
 }
 
+// ------------------------------------------------------------------------------------------
+// LayerNorm with autograd in C++: the eager path of FusedLayerNorm / fused_layer_norm.  A
+// Python torch.autograd.Function plus an operator call cost ~10 us per forward on the host (the
+// GPU work at BERT shapes is ~3 us).  Here the output gets a graph node of its own, built the way
+// PyTorch's generated autograd code builds one (edges to the inputs that require grad, saved
+// variables, no type-erased context), and the kernels are called directly.  It saves what the
+// reference's FusedLayerNormFunction saves (input, weight, bias, mean, rstd:
+// fused_layernorm/layernorm.py:76; mean and rstd here as the two rows of one fp32 tensor).
+// torch.compile keeps the fused_layernorm::layer_norm_fwd / layer_norm_bwd operators (the
+// Python side chooses).
+// ------------------------------------------------------------------------------------------
+struct FusedLayerNormBackward : public torch::autograd::Node {
+  torch::autograd::SavedVariable x_, w_, b_, stats_;
+  bool has_w = false, has_b = false;
+
+  torch::autograd::variable_list apply(torch::autograd::variable_list&& grads) override {
+    std::lock_guard<std::mutex> lock(mutex_);
+    const Tensor x = x_.unpack(), stats = stats_.unpack();
+    const OptT w = has_w ? OptT(w_.unpack()) : std::nullopt;
+    const OptT b = has_b ? OptT(b_.unpack()) : std::nullopt;
+    const std::array<bool, 3> mask{task_should_compute_output(0),
+                                   has_w && task_should_compute_output(1),
+                                   has_b && task_should_compute_output(2)};
+    if (!grads[0].defined() || !(mask[0] || mask[1] || mask[2])) return {Tensor(), Tensor(), Tensor()};
+    const Tensor dy = grads[0].is_contiguous() ? grads[0] : grads[0].contiguous();
+    auto r = layer_norm_bwd(dy, x, stats[0], stats[1], w, b, mask, std::nullopt);
+    return {mask[0] ? std::get<0>(r) : Tensor(), mask[1] ? std::get<1>(r) : Tensor(),
+            mask[2] ? std::get<2>(r) : Tensor()};
+  }
+  std::string name() const override { return "FusedLayerNormBackward"; }
+  void release_variables() override {
+    std::lock_guard<std::mutex> lock(mutex_);
+    x_.reset_data();
+    w_.reset_data();
+    b_.reset_data();
+    stats_.reset_data();
+  }
+};
+
+// FusedLayerNorm.forward's eager call: LayerNorm over the last dimension, which must equal
+// `normalized` (torch.nn.functional.layer_norm's error otherwise), with autograd.
+Tensor layer_norm_autograd(const Tensor& input, int64_t normalized, const OptT& weight,
+                           const OptT& bias, double eps) {
+  TORCH_CHECK(input.dim() >= 1 && input.size(-1) == normalized,
+              "Given normalized_shape=[", normalized, "], expected input with shape [*, ",
+              normalized, "], but got input of size", input.sizes());
+  const Tensor x = input.is_contiguous() ? input : input.contiguous();
+  const Shape s = check_input(x, "input", true);
+  check_param(weight, x, s.cols, "weight");
+  check_param(bias, x, s.cols, "bias");
+  c10::hip::HIPGuard guard(x.device().index());
+  Tensor y = at::empty_like(x);
+  Tensor stats = at::empty({2, s.rows}, x.options().dtype(at::kFloat));  // mean, rstd
+  float* st = stats.data_ptr<float>();
+  check(fln_layernorm_forward(x.data_ptr(), ptr_or_null(weight), ptr_or_null(bias),
+                              y.data_ptr(), st, st + s.rows, s.rows, s.cols, dtype_code(x),
+                              static_cast<float>(eps), stream_of(x)),
+        "layer_norm forward");
+  const bool wg = has(weight) && weight->requires_grad();
+  const bool bg = has(bias) && bias->requires_grad();
+  if (c10::GradMode::is_enabled() && (x.requires_grad() || wg || bg)) {
+    std::shared_ptr<FusedLayerNormBackward> node(new FusedLayerNormBackward(),
+                                                 torch::autograd::deleteNode);
+    node->set_next_edges(torch::autograd::collect_next_edges(
+        x, has(weight) ? *weight : Tensor(), has(bias) ? *bias : Tensor()));
+    node->x_ = torch::autograd::SavedVariable(x, false);
+    node->stats_ = torch::autograd::SavedVariable(stats, false);
+    node->has_w = has(weight);
+    node->has_b = has(bias);
+    if (node->has_w) node->w_ = torch::autograd::SavedVariable(*weight, false);
+    if (node->has_b) node->b_ = torch::autograd::SavedVariable(*bias, false);
+    torch::autograd::set_history(y, node);
+  }
+  return y;
+}
+
 // The forward launch plan (fln_forward_plan): (route, vector_elems, waves_per_row,
 // vectors_per_lane, exact, threads) for a contiguous, aligned input; backs
 // fused_layernorm.functional.get_optimal_config (reference fused_layernorm/functional.py:47-74).
@@ -675,6 +755,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Residual add + RMSNorm with OCP MX fp8 output -> (codes, block scales, residual_sum)",
         py::arg("input"), py::arg("residual"), py::arg("weight") = py::none(),
         py::arg("eps") = 1e-6);
+  m.def("layer_norm_autograd", &layer_norm_autograd,
+        "LayerNorm over the last dimension with autograd in C++ (FusedLayerNorm's eager path)",
+        py::arg("input"), py::arg("normalized"), py::arg("weight") = py::none(),
+        py::arg("bias") = py::none(), py::arg("eps") = 1e-5);
   m.def("forward_plan", &forward_plan,
         "Forward launch plan -> (route, vector_elems, waves_per_row, vectors_per_lane, exact, "
         "threads); dtype / gelu are the C-ABI codes, num_cus 0 = the current device",

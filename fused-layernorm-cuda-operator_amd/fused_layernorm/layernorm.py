@@ -30,6 +30,8 @@ from ._ext import load as _load_ext
 
 fused_layernorm_cuda = _load_ext()
 _ops = torch.ops.fused_layernorm
+_layer_norm_autograd = fused_layernorm_cuda.layer_norm_autograd
+_compiling = torch.compiler.is_compiling
 
 
 class FusedLayerNormFunction(Function):
@@ -131,6 +133,10 @@ class FusedLayerNorm(nn.Module):
                 nn.init.zeros_(self.bias)
 
     def forward(self, input: torch.Tensor) -> torch.Tensor:
+        if len(self.normalized_shape) == 1 and not _compiling():
+            # Eager: autograd in C++ around the kernels (host cost close to nn.LayerNorm's).
+            return _layer_norm_autograd(input, self.normalized_shape[0], self.weight, self.bias,
+                                        self.eps)
         if input.dim() == 2 and len(self.normalized_shape) == 1:
             return FusedLayerNormFunction.apply(input, self.normalized_shape, self.weight,
                                                 self.bias, self.eps)
@@ -165,6 +171,8 @@ def fused_layer_norm(input: torch.Tensor, normalized_shape: Tuple[int, ...],
                      eps: float = 1e-5) -> torch.Tensor:
     """Functional LayerNorm with F.layer_norm's signature (reference layernorm.py:234-266)."""
     ns = _as_shape(normalized_shape)
+    if len(ns) == 1 and not _compiling():
+        return _layer_norm_autograd(input, ns[0], weight, bias, eps)
     if input.dim() == 2 and len(ns) == 1 and ns[0] == input.size(1):
         return FusedLayerNormFunction.apply(input, ns, weight, bias, eps)
     return _apply_rows(input, ns, weight, bias, eps)

@@ -118,6 +118,59 @@ def test_backward_correctness(batch, hidden):
         torch.testing.assert_close(got.double().cpu(), ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("shape,dtype,affine,bias", [
+    ((32, 768), torch.float32, True, True), ((4, 9, 1024), torch.bfloat16, True, True),
+    ((2, 3, 5, 2048), torch.float16, True, False), ((4096,), torch.float32, False, False),
+    ((64, 4096), torch.bfloat16, True, True)],
+    ids=["2d-f32", "3d-bf16", "4d-f16-nobias", "1d-f32-noaffine", "2d-bf16"])
+@pytest.mark.parametrize("grads", ["all", "params", "input"])
+def test_module_eager_path_matches_the_autograd_function(shape, dtype, affine, bias, grads):
+    """FusedLayerNorm's eager forward runs autograd in C++ (fused_layernorm_cuda.
+    layer_norm_autograd) instead of the Python FusedLayerNormFunction + operator call: the same
+    kernels, so output and every gradient are bitwise identical to the Python path
+    (FusedLayerNormFunction on the rows), for any rank, with or without affine parameters,
+    for each combination of tensors requiring grad, and on a non-contiguous input."""
+    hidden = shape[-1]
+    ln = make_ln(hidden, dtype, affine=affine, bias=bias)
+    base = torch.randn(*shape[:-1], 2 * hidden, device=DEV).to(dtype)
+    x = base[..., ::2]  # non-contiguous
+    dy = torch.randn(shape, device=DEV).to(dtype)
+    need_x = grads in ("all", "input")
+    for p in ln.parameters():
+        p.requires_grad_(grads in ("all", "params"))
+    xa = x.detach().clone().requires_grad_(need_x)
+    ya = ln(xa)
+    assert ya.requires_grad == (need_x or (affine and grads in ("all", "params")))
+    if ya.requires_grad:
+        ya.backward(dy)
+    ga = [t.grad.clone() if t is not None and t.grad is not None else None
+          for t in (xa, ln.weight, ln.bias)]
+    for p in ln.parameters():
+        p.grad = None
+    xb = x.detach().contiguous().reshape(-1, hidden).requires_grad_(need_x)
+    yb = fl.FusedLayerNormFunction.apply(xb, (hidden,), ln.weight, ln.bias, ln.eps)
+    if yb.requires_grad:
+        yb.backward(dy.reshape(-1, hidden))
+    gb = [xb.grad.reshape(shape) if xb.grad is not None else None,
+          ln.weight.grad if ln.weight is not None else None,
+          ln.bias.grad if ln.bias is not None else None]
+    assert torch.equal(ya.detach(), yb.detach().reshape(shape))
+    for name, a, b in zip(("dx", "dweight", "dbias"), ga, gb):
+        assert (a is None) == (b is None), name
+        if a is not None:
+            assert torch.equal(a, b), name
+    check_out(ya, ref_ln(x, (hidden,), ln.weight, ln.bias), dtype, x, ln.weight, ln.bias,
+              shape=(hidden,))
+
+
+def test_module_eager_path_rejects_mismatched_shapes():
+    ln = make_ln(768)
+    with pytest.raises(RuntimeError, match="normalized_shape"):
+        ln(torch.randn(4, 1024, device=DEV))
+    with pytest.raises(RuntimeError):
+        fl.fused_layer_norm(torch.randn(4, 768, device=DEV), (768,), torch.ones(512, device=DEV))
+
+
 def test_gradient_accumulation():
     x = torch.randn(32, 1024, device=DEV, requires_grad=True)
     ln = make_ln(1024)

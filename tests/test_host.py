@@ -294,6 +294,18 @@ def _cpu(*shape, dtype=torch.float32):
     return torch.randn(*shape).to(dtype)
 
 
+def test_module_eager_path_checks_arguments_on_the_host():
+    """FusedLayerNorm's C++ autograd path validates before anything is launched: a last
+    dimension other than normalized_shape raises torch's F.layer_norm message, a CPU tensor the
+    binding's device error."""
+    with pytest.raises(RuntimeError, match="normalized_shape"):
+        ext.layer_norm_autograd(_cpu(2, 4), 5, None, None, 1e-5)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ext.layer_norm_autograd(_cpu(2, 4), 4, None, None, 1e-5)
+    with pytest.raises(RuntimeError, match="GPU"):
+        fl.FusedLayerNorm(4)(_cpu(2, 4))
+
+
 @pytest.mark.parametrize("call", [
     lambda: ext.layernorm(_cpu(4, 8), _cpu(8), _cpu(8), 1e-5),
     lambda: ext.layernorm_gelu(_cpu(4, 8), _cpu(8), _cpu(8)),
