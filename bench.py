@@ -20,7 +20,11 @@ reduction), the larger of the two, timed with HIP events on its launch stream; i
 comes from two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over a child run of this
 script (--kernel-loop), each scaled by what the counter reads for a device copy of known size.
 `stream_ceilings` times hand-written streaming kernels (libfln_stream.so) of each access
-pattern as the HBM ceiling the kernels are judged against.  `cpu_baseline` times the reference's
+pattern as the HBM ceiling the kernels are judged against (and, per bandwidth-bound config, at
+that config's own tensor size: `configs[*].stream_ceiling`).  `reference_paths` times the
+reference's own call paths with its own methods: the binding `fused_layernorm_cuda.layernorm`
+at the shapes of its published latencies, and the `FusedLayerNorm` module against nn.LayerNorm
+at the shapes of its performance-regression test.  `cpu_baseline` times the reference's
 CPU path (torch-CPU F.layer_norm + autograd backward, which the reference's module falls back to
 off the GPU) on the full headline workload with the process's host threads; the C oracle
 (oracle/fln_oracle.c, the "port") on a row sample is nested beside it.
@@ -544,13 +548,14 @@ STREAM_NAMES = {0: "1r1w", 1: "2r1w", 2: "2r2w", 3: "1r_half_w"}
 STREAM_MOVED = {0: 2.0, 1: 3.0, 2: 4.0, 3: 1.5}  # bytes moved per input-stream byte
 
 
-def stream_ceilings(torch, nbytes, fwd_bytes, bwd_bytes, n=100):
+def stream_ceilings(torch, nbytes, fwd_bytes=None, bwd_bytes=None, n=100, patterns=None):
     """HBM ceiling of each access pattern on this device: the streaming reference kernels of
     libfln_stream.so (include/fln_stream.h; raw buffer loads / stores, persistent grid, a ring of
     loads in flight: the normalization kernels' own idioms with nothing computed) over streams of
     `nbytes` each, rotating over >= 2 GiB, best launch shape of STREAM_SHAPES, HIP events on the
     launch stream.  The step ceiling is the headline step's algorithmic bytes with the forward's
-    at the 1R1W rate and the backward's at the 2R1W rate."""
+    at the 1R1W rate and the backward's at the 2R1W rate.  `patterns`: the pattern numbers to
+    time (default: all four)."""
     import ctypes
     lib = ctypes.CDLL(os.path.join(PKG, "libfln_stream.so"))
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
@@ -567,6 +572,8 @@ def stream_ceilings(torch, nbytes, fwd_bytes, bwd_bytes, n=100):
             t.random_(0, 2 ** 31 - 1)
     res = {}
     for pat, shapes in STREAM_SHAPES.items():
+        if patterns is not None and pat not in patterns:
+            continue
         best = None
         for thr, bpc, u, pd in shapes:
             k = [0]
@@ -598,12 +605,161 @@ def stream_ceilings(torch, nbytes, fwd_bytes, bwd_bytes, n=100):
                                              "us_per_call": round(best[1], 2)}
     del sets
     torch.cuda.empty_cache()
-    step_s = fwd_bytes / (res["1r1w_gbs"] * 1e9) + bwd_bytes / (res["2r1w_gbs"] * 1e9)
-    res["step_ceiling_gbs"] = round((fwd_bytes + bwd_bytes) / step_s / 1e9, 1)
-    res["what"] = (f"libfln_stream.so kernels, {nbytes >> 20} MiB per stream (the headline's "
-                   "tensor size), rotating >= 2 GiB, best of STREAM_SHAPES; step ceiling = the "
-                   "step's algorithmic bytes at the 1R1W (forward) and 2R1W (backward) rates")
+    if fwd_bytes is not None and "1r1w_gbs" in res and "2r1w_gbs" in res:
+        step_s = fwd_bytes / (res["1r1w_gbs"] * 1e9) + bwd_bytes / (res["2r1w_gbs"] * 1e9)
+        res["step_ceiling_gbs"] = round((fwd_bytes + bwd_bytes) / step_s / 1e9, 1)
+        res["what"] = (f"libfln_stream.so kernels, {nbytes >> 20} MiB per stream (the headline's "
+                       "tensor size), rotating >= 2 GiB, best of STREAM_SHAPES; step ceiling = "
+                       "the step's algorithmic bytes at the 1R1W (forward) and 2R1W (backward) "
+                       "rates")
     return res
+
+
+# Access pattern of each bandwidth-bound config's calls and its per-stream size (the size of its
+# largest input), for ceilings measured at the config's own size: (forward pattern, backward
+# pattern or None, bytes per stream).  C6 / C7 (two reads, a full and a half-width write) have
+# no stream kernel of their own pattern.
+CONFIG_PATTERNS = {
+    "c3_add_ln_fwd_bf16_8192x4096": (2, None, 8192 * 4096 * 2),
+    "c4_rms_fwd_bwd_bf16_16384x8192": (0, 1, 16384 * 8192 * 2),
+    "c5_ln_fp8_bf16_32768x7168": (3, None, 32768 * 7168 * 2),
+    "ln_gelu_fwd_bwd_bf16_8192x4096": (0, 1, 8192 * 4096 * 2),
+    "ln_gelu_erf_fwd_bwd_bf16_8192x4096": (0, 1, 8192 * 4096 * 2),
+}
+
+
+def config_ceiling(torch, name, fwd_bytes, bwd_bytes, cache):
+    """Streaming ceiling (GB/s) of config `name`'s call pattern at its own tensor size: the
+    forward's pattern rate, or for a forward + backward step the step's algorithmic bytes at the
+    forward's and backward's pattern rates.  `cache` maps (pattern, bytes) -> GB/s."""
+    fpat, bpat, nbytes = CONFIG_PATTERNS[name]
+    want = [p for p in (fpat, bpat) if p is not None and (p, nbytes) not in cache]
+    if want:
+        r = stream_ceilings(torch, nbytes, patterns=want)
+        for p in want:
+            cache[(p, nbytes)] = r[STREAM_NAMES[p] + "_gbs"]
+    if bpat is None:
+        return cache[(fpat, nbytes)], STREAM_NAMES[fpat], nbytes
+    t = fwd_bytes / (cache[(fpat, nbytes)] * 1e9) + bwd_bytes / (cache[(bpat, nbytes)] * 1e9)
+    return ((fwd_bytes + bwd_bytes) / t / 1e9,
+            f"{STREAM_NAMES[fpat]} + {STREAM_NAMES[bpat]}", nbytes)
+
+
+# The reference's published small-shape latencies ("optimal": 500 back-to-back calls on one
+# tensor, HIP/CUDA events; publication_validation_results.json:91-172, A100, ms per call).
+PUBLICATION_OPTIMAL = (
+    ("Tiny Batch", 1, 768, 0.021110784530639647, 0.01005568027496338),
+    ("Small Batch", 8, 768, 0.021123071670532227, 0.010141695976257324),
+    ("BERT", 32, 768, 0.021166080474853514, 0.010106880187988282),
+    ("GPT-2 Small", 32, 1024, 0.021170175552368165, 0.01003110408782959),
+    ("GPT-2 Medium", 32, 2048, 0.02207744026184082, 0.01009663963317871),
+    ("GPT-3", 32, 4096, 0.02109235191345215, 0.009992192268371582),
+    ("Large Batch", 64, 4096, 0.02105548858642578, 0.010108927726745605),
+    ("XL Batch", 128, 4096, 0.021360639572143555, 0.010102784156799317),
+    ("Odd Dims", 17, 1023, 0.024211456298828125, 0.010010623931884765),
+    ("GPT-3 Large", 32, 12288, 0.024375295639038085, 0.01245798397064209),
+)
+# The reference's performance regression test: FusedLayerNorm >= 1.2x nn.LayerNorm
+# (tests/test_layernorm.py:361-413).
+GATE_SHAPES = ((32, 768), (32, 1024), (16, 2048), (8, 4096))
+
+
+def reference_paths(torch):
+    """Latency of the reference's own call paths on this GPU, with the reference's own methods:
+      * publication_optimal: fused_layernorm_cuda.layernorm(x, ln.weight, ln.bias, 1e-5) and
+        nn.LayerNorm(x), 500 back-to-back calls each on one tensor between HIP events after 100
+        warm-ups (tests/publication_validation.py:181-205), at the published shapes, beside the
+        published A100 figures;
+      * module_gate: FusedLayerNorm(h) and nn.LayerNorm(h) (weights requiring grad), 100
+        back-to-back forwards timed by wall clock after 50 warm-ups
+        (tests/test_layernorm.py:376-413; >= 1.2x required there), median of 7 repetitions;
+      * c1_binding: the binding call at 32 x 768 fp32 back to back (host-bound: per-call host
+        cost) and 32 calls captured in one HIP graph (GPU-side latency per call).
+    fp32 throughout, torch.randn inputs, nn.LayerNorm's default affine parameters."""
+    import torch.nn as nn
+    import fused_layernorm as fl
+    import fused_layernorm_cuda as ext
+    out = {"publication_optimal": [], "module_gate": []}
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    for name, b, h, pt_a100, ours_a100 in PUBLICATION_OPTIMAL:
+        x = torch.randn(b, h, device="cuda")
+        ln = nn.LayerNorm(h).cuda()
+        for _ in range(100):
+            ln(x)
+            ext.layernorm(x, ln.weight, ln.bias, 1e-5)
+        torch.cuda.synchronize()
+        res = {}
+        for key, fn in (("pytorch_us", lambda: ln(x)),
+                        ("ours_us", lambda: ext.layernorm(x, ln.weight, ln.bias, 1e-5))):
+            e0, e1 = ev(), ev()
+            e0.record()
+            for _ in range(500):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            res[key] = round(e0.elapsed_time(e1) / 500 * 1e3, 2)
+        out["publication_optimal"].append({
+            "config": name, "batch": b, "hidden": h, **res,
+            "speedup": round(res["pytorch_us"] / res["ours_us"], 3),
+            "reference_a100_ours_us": round(ours_a100 * 1e3, 2),
+            "reference_a100_pytorch_us": round(pt_a100 * 1e3, 2)})
+    for b, h in GATE_SHAPES:
+        x = torch.randn(b, h, device="cuda")
+        pt = nn.LayerNorm(h).cuda()
+        fu = fl.FusedLayerNorm(h).cuda()
+        for _ in range(50):
+            pt(x)
+            fu(x)
+        torch.cuda.synchronize()
+        tp, tf = [], []
+        for _ in range(7):
+            for lst, mod in ((tp, pt), (tf, fu)):
+                t0 = time.time()
+                for _ in range(100):
+                    mod(x)
+                torch.cuda.synchronize()
+                lst.append((time.time() - t0) / 100 * 1e6)
+        sp = [a / c for a, c in zip(tp, tf)]
+        out["module_gate"].append({"batch": b, "hidden": h,
+                                   "nn_layernorm_us": round(statistics.median(tp), 2),
+                                   "fused_layernorm_us": round(statistics.median(tf), 2),
+                                   "speedup": round(statistics.median(sp), 3),
+                                   "speedup_min": round(min(sp), 3), "required": 1.2})
+    x = torch.randn(32, 768, device="cuda")
+    ln = nn.LayerNorm(768).cuda()
+    w, bb = ln.weight.detach(), ln.bias.detach()
+    for _ in range(200):
+        ext.layernorm(x, w, bb, 1e-5)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(2000):
+        ext.layernorm(x, w, bb, 1e-5)
+    torch.cuda.synchronize()
+    eager = (time.perf_counter() - t0) / 2000 * 1e6
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            ext.layernorm(x, w, bb, 1e-5)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for _ in range(32):
+            ext.layernorm(x, w, bb, 1e-5)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = ev(), ev()
+    e0.record()
+    for _ in range(20):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    out["c1_binding"] = {"call": "fused_layernorm_cuda.layernorm(x, w, b, 1e-5), 32 x 768 fp32",
+                         "eager_us_per_call": round(eager, 2),
+                         "graph_us_per_call": round(e0.elapsed_time(e1) / (20 * 32) * 1e3, 2),
+                         "target_us": 5.0}
+    return out
 
 
 def torch_gpu_compare(torch, ours, warmup=10, n=50):
@@ -967,6 +1123,8 @@ def main():
 
     if not args.no_configs and not args.headline_only:
         cfg = {}
+        ceiling_cache = {(p, 8192 * 4096 * 2): ceil[STREAM_NAMES[p] + "_gbs"]
+                         for p in STREAM_NAMES if STREAM_NAMES[p] + "_gbs" in ceil}
         for name in CONFIGS:
             w = WORKLOADS[name]
             small = w.op in ("layer_norm", "layer_norm_gelu")
@@ -982,8 +1140,16 @@ def main():
                 entry["gbs"] = round(gbs(res["bytes"]["total"], res["ms"]), 1)
             else:
                 entry["gbs"] = round(gbs(res["bytes"]["fwd"], res["ms_fwd"]), 1)
+            if name in CONFIG_PATTERNS:
+                ceil_gbs, pattern, nbytes = config_ceiling(
+                    torch, name, res["bytes"]["fwd"], res["bytes"].get("bwd"), ceiling_cache)
+                entry["pct_of_hbm_peak"] = round(100 * entry["gbs"] / HBM_PEAK_GBS, 1)
+                entry["stream_ceiling"] = {"pattern": pattern, "bytes_per_stream": nbytes,
+                                           "gbs": round(ceil_gbs, 1),
+                                           "frac": round(entry["gbs"] / ceil_gbs, 3)}
             cfg[name] = entry
         out["configs"] = cfg
+        out["reference_paths"] = reference_paths(torch)
 
     if not args.no_configs and not args.headline_only:
         ours = {HEADLINE: head["ms"], "c1_ln_fwd_fp32_32x768": None,
