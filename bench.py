@@ -85,6 +85,8 @@ def parse():
                          "(64 MiB per stream, rotating sets) --iters times per listed pattern and "
                          "launch shape, and exit")
     ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--stream-bytes", type=int, default=64 << 20,
+                    help="bytes per stream of --stream-loop (default 64 MiB)")
     ap.add_argument("--traffic-configs", action="store_true",
                     help="instead of the bench line: HBM traffic (two rocprofv3 counter passes "
                          "each) and call times of every bandwidth-bound config (C3..C7, LN+GELU)")
@@ -320,8 +322,9 @@ def kernel_loop(args):
 
 def stream_loop(args):
     """Profiling child: --iters launches of each listed streaming kernel (pattern 0 1R1W, 1 2R1W,
-    2 2R2W, 3 1R + half W) at the listed launch shape, 64 MiB per stream over rotating sets; the
-    counter passes compare the normalization kernels with these."""
+    2 2R2W, 3 1R + half W) at the listed launch shape, --stream-bytes per stream (64 MiB by
+    default) over rotating sets; the counter passes compare the normalization kernels with
+    these."""
     import ctypes
     import torch
     lib = ctypes.CDLL(os.path.join(PKG, "libfln_stream.so"))
@@ -330,8 +333,8 @@ def stream_loop(args):
     lib.fln_stream_run.restype = i32
     sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     cus = lib.fln_stream_cu_count()
-    nbytes = 64 << 20
-    nsets = 8
+    nbytes = args.stream_bytes
+    nsets = max(2, min(8, -(-ROTATE_BYTES // (4 * nbytes))))
     sets = [[torch.empty(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(4)]
             for _ in range(nsets)]
     for st4 in sets:

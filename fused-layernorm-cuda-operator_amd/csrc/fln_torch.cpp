@@ -626,6 +626,55 @@ Tensor layer_norm_autograd(const Tensor& input, int64_t normalized, const OptT& 
   return y;
 }
 
+// RMSNorm with autograd in C++: the eager path of FusedRMSNorm / fused_rms_norm, built like
+// layer_norm_autograd (saves input, weight, rstd).
+struct FusedRMSNormBackward : public torch::autograd::Node {
+  torch::autograd::SavedVariable x_, w_, rstd_;
+  bool has_w = false;
+
+  torch::autograd::variable_list apply(torch::autograd::variable_list&& grads) override {
+    std::lock_guard<std::mutex> lock(mutex_);
+    const Tensor x = x_.unpack(), rstd = rstd_.unpack();
+    const OptT w = has_w ? OptT(w_.unpack()) : std::nullopt;
+    const std::array<bool, 2> mask{task_should_compute_output(0),
+                                   has_w && task_should_compute_output(1)};
+    if (!grads[0].defined() || !(mask[0] || mask[1])) return {Tensor(), Tensor()};
+    const Tensor dy = grads[0].is_contiguous() ? grads[0] : grads[0].contiguous();
+    auto r = rms_norm_bwd(dy, x, rstd, w, mask, std::nullopt);
+    return {mask[0] ? std::get<0>(r) : Tensor(), mask[1] ? std::get<1>(r) : Tensor()};
+  }
+  std::string name() const override { return "FusedRMSNormBackward"; }
+  void release_variables() override {
+    std::lock_guard<std::mutex> lock(mutex_);
+    x_.reset_data();
+    w_.reset_data();
+    rstd_.reset_data();
+  }
+};
+
+Tensor rms_norm_autograd(const Tensor& input, int64_t normalized, const OptT& weight,
+                         double eps) {
+  TORCH_CHECK(input.dim() >= 1 && input.size(-1) == normalized,
+              "Given normalized_shape=[", normalized, "], expected input with shape [*, ",
+              normalized, "], but got input of size", input.sizes());
+  const Tensor x = input.is_contiguous() ? input : input.contiguous();
+  auto r = rms_norm_fwd(x, weight, eps);
+  Tensor y = std::get<0>(r);
+  const bool wg = has(weight) && weight->requires_grad();
+  if (c10::GradMode::is_enabled() && (x.requires_grad() || wg)) {
+    std::shared_ptr<FusedRMSNormBackward> node(new FusedRMSNormBackward(),
+                                               torch::autograd::deleteNode);
+    node->set_next_edges(
+        torch::autograd::collect_next_edges(x, has(weight) ? *weight : Tensor()));
+    node->x_ = torch::autograd::SavedVariable(x, false);
+    node->rstd_ = torch::autograd::SavedVariable(std::get<1>(r), false);
+    node->has_w = has(weight);
+    if (node->has_w) node->w_ = torch::autograd::SavedVariable(*weight, false);
+    torch::autograd::set_history(y, node);
+  }
+  return y;
+}
+
 // The forward launch plan (fln_forward_plan): (route, vector_elems, waves_per_row,
 // vectors_per_lane, exact, threads) for a contiguous, aligned input; backs
 // fused_layernorm.functional.get_optimal_config (reference fused_layernorm/functional.py:47-74).
@@ -759,6 +808,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "LayerNorm over the last dimension with autograd in C++ (FusedLayerNorm's eager path)",
         py::arg("input"), py::arg("normalized"), py::arg("weight") = py::none(),
         py::arg("bias") = py::none(), py::arg("eps") = 1e-5);
+  m.def("rms_norm_autograd", &rms_norm_autograd,
+        "RMSNorm over the last dimension with autograd in C++ (FusedRMSNorm's eager path)",
+        py::arg("input"), py::arg("normalized"), py::arg("weight") = py::none(),
+        py::arg("eps") = 1e-6);
   m.def("forward_plan", &forward_plan,
         "Forward launch plan -> (route, vector_elems, waves_per_row, vectors_per_lane, exact, "
         "threads); dtype / gelu are the C-ABI codes, num_cus 0 = the current device",

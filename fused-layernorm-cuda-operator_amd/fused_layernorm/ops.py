@@ -321,6 +321,10 @@ def rms_norm(input: torch.Tensor, normalized_shape: ShapeLike,
     """RMSNorm with torch.nn.functional.rms_norm semantics (eps=None -> finfo(dtype).eps)."""
     if eps is None:
         eps = torch.finfo(input.dtype).eps
+    ns = _norm_shape(normalized_shape)
+    if len(ns) == 1 and not torch.compiler.is_compiling():
+        # Eager: autograd in C++ around the kernels (FusedRMSNorm's hot path).
+        return _ext.rms_norm_autograd(input, ns[0], weight, eps)
     x, _ = _flatten(input, normalized_shape)
     y, _ = _ops.rms_norm_fwd(x, _flat_param(weight), eps)
     return y.view(input.shape)

@@ -163,6 +163,35 @@ def test_module_eager_path_matches_the_autograd_function(shape, dtype, affine, b
               shape=(hidden,))
 
 
+@pytest.mark.parametrize("shape,dtype,affine", [
+    ((32, 768), torch.float32, True), ((4, 9, 4096), torch.bfloat16, True),
+    ((2, 3, 2048), torch.float16, False)], ids=["2d-f32", "3d-bf16", "3d-f16-noaffine"])
+def test_rms_module_eager_path_matches_the_operator(shape, dtype, affine):
+    """FusedRMSNorm's eager forward runs autograd in C++ (fused_layernorm_cuda.
+    rms_norm_autograd): output and gradients bitwise identical to the torch.compile-visible
+    operator path (fused_layernorm::rms_norm_fwd with its registered autograd)."""
+    hidden = shape[-1]
+    m = fl.FusedRMSNorm(hidden, eps=1e-6, elementwise_affine=affine).to(DEV, dtype)
+    if affine:
+        with torch.no_grad():
+            m.weight.copy_(1 + 0.1 * torch.randn(hidden))
+    x = torch.randn(shape, device=DEV).to(dtype)
+    dy = torch.randn(shape, device=DEV).to(dtype)
+    xa = x.clone().requires_grad_(True)
+    ya = m(xa)
+    ya.backward(dy)
+    ga = (xa.grad.clone(), m.weight.grad.clone() if affine else None)
+    if affine:
+        m.weight.grad = None
+    xb = x.clone().reshape(-1, hidden).requires_grad_(True)
+    yb, _ = torch.ops.fused_layernorm.rms_norm_fwd(xb, m.weight, 1e-6)
+    yb.backward(dy.reshape(-1, hidden))
+    assert torch.equal(ya.detach(), yb.detach().reshape(shape))
+    assert torch.equal(ga[0], xb.grad.reshape(shape))
+    if affine:
+        assert torch.equal(ga[1], m.weight.grad)
+
+
 def test_module_eager_path_rejects_mismatched_shapes():
     ln = make_ln(768)
     with pytest.raises(RuntimeError, match="normalized_shape"):

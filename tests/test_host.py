@@ -304,6 +304,10 @@ def test_module_eager_path_checks_arguments_on_the_host():
         ext.layer_norm_autograd(_cpu(2, 4), 4, None, None, 1e-5)
     with pytest.raises(RuntimeError, match="GPU"):
         fl.FusedLayerNorm(4)(_cpu(2, 4))
+    with pytest.raises(RuntimeError, match="normalized_shape"):
+        ext.rms_norm_autograd(_cpu(2, 4), 5, None, 1e-6)
+    with pytest.raises(RuntimeError, match="GPU"):
+        fl.FusedRMSNorm(4)(_cpu(2, 4))
 
 
 @pytest.mark.parametrize("call", [
