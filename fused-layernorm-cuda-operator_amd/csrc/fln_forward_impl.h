@@ -1164,6 +1164,13 @@ int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStre
     case 1: return launch_reg_exact<T, FP8, RES, GELU, VEC, 1>(p, exact, threads, s);
     case 2: return launch_reg_exact<T, FP8, RES, GELU, VEC, 2>(p, exact, threads, s);
     case 4: return launch_reg_exact<T, FP8, RES, GELU, VEC, 4>(p, exact, threads, s);
+    case 7:
+      // Seven 16-byte vectors per lane, exact tilings only, 256-thread blocks (219-224 VGPRs):
+      // planned for 16-bit LN / RMSNorm rows of 448 vectors and the fp8 row scale of 896.
+      if constexpr (VEC == 8 && !RES && GELU == 0 && FP8 != 2)
+        if (exact && threads <= 256)
+          return launch_reg_t<T, FP8, RES, GELU, VEC, 7, true, 256>(p, threads, s);
+      return FLN_ERR_INVALID;
     case 8:
       if constexpr (CAP >= 8)
         return launch_reg_exact<T, FP8, RES, GELU, VEC, 8>(p, exact, threads, s);
@@ -1813,6 +1820,23 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.wpr = 4;
       g.vpl = v4;
       g.exact = false;
+      g.threads = 256;
+    }
+  }
+  // Seven vectors per lane tile two 16-bit widths exactly where the power-of-two tiles mask 1/8
+  // of their slots: the fp8 row scale at 7168 columns over 2 waves (bf16 32768 x 7168, us: 4
+  // masked waves 125.1 -> 120.7, one 256-thread block per CU; 2 blocks 125.3, 128-thread blocks
+  // 126.5-152.5) and LN / RMSNorm at 3584 over 1 wave (65536 x 3584: 2 masked waves 169.0 ->
+  // 161.8).  Not for 16-bit output at 7168 (the 7-wave tiling: 157.4 against 167.8), the
+  // residual flavours (their 7-vector tiles spill into AGPRs at one wave per SIMD: residual +
+  // RMSNorm -> fp8 283.1 -> 289.9, MX 274.7 -> 281.5) or GELU; only with enough rows to fill the
+  // device (fewer rows keep the latency tiling above).
+  if (VV == 8 && vec_ok && !g.loop && !has_res && gelu == 0 && tun.fwd_wpr <= 0) {
+    const int w7 = FP8 == 1 && nvec == 2 * kWave * 7 ? 2 : FP8 == 0 && nvec == kWave * 7 ? 1 : 0;
+    if (w7 > 0 && rows * w7 >= 4 * cus) {
+      g.wpr = w7;
+      g.vpl = 7;
+      g.exact = true;
       g.threads = 256;
     }
   }

@@ -709,7 +709,75 @@ def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
                      t_ref=_scaled(norms.rms_norm_fwd(h_o, f32(gc), 1e-6)[0]))
 
 
-WIDE_KINDS = ["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp8", "rms_fp8",
+@pytest.mark.parametrize("op,dtype,rows,cols", [
+    ("ln", torch.bfloat16, 1024, 3584), ("rms", torch.float16, 1100, 3584),
+    ("ln_fp8", torch.bfloat16, 600, 7168), ("rms_fp8", torch.float16, 512, 7168)],
+    ids=["ln-bf16-1024x3584", "rms-f16-1100x3584", "ln_fp8-bf16-600x7168",
+         "rms_fp8-f16-512x7168"])
+def test_seven_vectors_per_lane(lib, capfd, monkeypatch, op, dtype, rows, cols):
+    """The 7-vectors-per-lane register tiles (exact, 256-thread blocks): 16-bit LayerNorm /
+    RMSNorm at 3584 columns over one wave per row, LN / RMSNorm -> fp8 with the row scale at
+    7168 over two, with rows enough to fill the device; the dispatcher's trace must show the
+    tiling fln_forward_plan reports, and the outputs must meet the oracle's bar."""
+    import re
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if rows * (cols // 3584) < 4 * cus:
+        pytest.skip(f"{cus} CUs: the tiling needs more rows to be planned")
+    plan = fl_functional().get_optimal_config(rows, cols, dtype, fp8=int(op.endswith("fp8")))
+    assert (plan["waves_per_row"], plan["vectors_per_lane"], plan["exact_tiling"]) == (
+        cols // 512 // 7, 7, True), plan
+    gen = torch.Generator().manual_seed(rows + cols)
+    xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, g, b = cuda(xc), cuda(gc), cuda(bc)
+    xs, gs, bs = f32(xc), f32(gc), f32(bc)
+    kind = "bf16" if dtype == torch.bfloat16 else "f16"
+    code = capi.dtype_code(x)
+    p = capi.ptr
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
+    if op == "ln":
+        y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+    elif op == "rms":
+        y, rstd = rms_forward(lib, x, g, 1e-6)
+    else:
+        q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+        s = torch.empty(rows, device="cuda")
+        if op == "ln_fp8":
+            capi.check(lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(q), p(s), None, None,
+                                                     rows, cols, code, 1e-5, capi.stream()))
+        else:
+            capi.check(lib.fln_rmsnorm_fp8_forward(p(x), p(g), p(q), p(s), None, rows, cols,
+                                                   code, 1e-6, capi.stream()))
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
+    trace = re.findall(r"-> (\S+) wpr=(\d+) vpl=(\d+) exact=(\d+) threads=(\d+)",
+                       capfd.readouterr().err)
+    assert trace == [("registers", str(cols // 3584), "7", "1", "256")], trace
+    if op == "ln":
+        y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5), kind=kind,
+                          what="y")
+        assert np.abs(to_np(mean) - m_ref).max() <= 1e-5 * np.abs(xs).max()
+        assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+    elif op == "rms":
+        y_ref, r_ref = norms.rms_norm_fwd(xs, gs, 1e-6)
+        assert_within_ulp(to_np(y), y_ref, 1.0, kind=kind, what="y")
+        assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+    elif op == "ln_fp8":
+        q_ref, s_ref = c_oracle.layernorm_fp8(xs, gs, bs, 1e-5)
+        assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "ln fp8",
+                         t_ref=_scaled(norms.layer_norm_fwd(xs, gs, bs, 1e-5)[0]))
+    else:
+        q_ref, s_ref = c_oracle.rmsnorm_fp8(xs, gs, 1e-6)
+        assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "rms fp8",
+                         t_ref=_scaled(norms.rms_norm_fwd(xs, gs, 1e-6)[0]))
+
+
+WIDE_KINDS =["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp8", "rms_fp8",
               "add_rms_fp8", "ln_mx", "rms_mx", "add_rms_mx"]
 
 

@@ -409,6 +409,26 @@ def test_optimal_config_reports_dispatch_geometry():
     assert c["waves_per_row"] * 64 * c["vectors_per_lane"] * c["vector_elems"] == 4096
     c7 = fl.functional.get_optimal_config(32768, 7168, torch.bfloat16)
     assert (c7["waves_per_row"], c7["vectors_per_lane"], c7["threads_per_block"]) == (7, 2, 448)
+    # Seven vectors per lane: LN -> fp8 (row scale) at 7168 columns over 2 waves and LN /
+    # RMSNorm at 3584 over 1 wave, 16-bit only, with enough rows to fill the device (4 waves
+    # per CU); the residual, MX and GELU flavours and fp32 keep their tilings.
+    w7 = lambda *a, **k: (lambda c: (c["waves_per_row"], c["vectors_per_lane"],  # noqa: E731
+                                     c["exact_tiling"], c["threads_per_block"]))(
+        fl.functional.get_optimal_config(*a, **k))
+    assert w7(32768, 7168, torch.bfloat16, fp8=1) == (2, 7, True, 256)
+    assert w7(512, 7168, torch.float16, fp8=1) == (2, 7, True, 256)
+    assert w7(511, 7168, torch.bfloat16, fp8=1)[1] != 7
+    assert w7(65536, 3584, torch.bfloat16) == (1, 7, True, 256)
+    assert w7(1024, 3584, torch.float16) == (1, 7, True, 256)
+    assert w7(1023, 3584, torch.bfloat16)[1] != 7
+    assert w7(128, 7168, torch.bfloat16, fp8=1, num_cus=64) == (2, 7, True, 256)
+    for k in (dict(fp8=1, residual=True), dict(fp8=2), dict(approximate="tanh"),
+              dict(approximate="none"), dict(fp8=1, residual=False, dtype=torch.float32)):
+        dt = k.pop("dtype", torch.bfloat16)
+        assert w7(32768, 7168, dt, **k)[1] != 7, k
+        assert w7(65536, 3584, dt, **k)[1] != 7, k
+    assert w7(65536, 3584, torch.bfloat16, fp8=1)[1] != 7
+    assert w7(32768, 7168, torch.bfloat16)[1] != 7
     # Exact tilings of one vector per lane only for rows too few to fill the device (C1);
     # with many rows the power-of-two tiling with masked slots is taken instead.
     wt = lambda c: (c["waves_per_row"], c["vectors_per_lane"], c["exact_tiling"])  # noqa: E731
