@@ -1157,6 +1157,14 @@ int launch_reg_exact(const FwdParams& p, bool exact, int threads, hipStream_t s)
   return launch_reg<T, FP8, RES, GELU, VEC, VPL, false>(p, threads, s);
 }
 
+template <class T, int FP8, bool RES, int GELU, int VEC, int VPL>
+int launch_reg_odd(const FwdParams& p, bool exact, int threads, hipStream_t s) {
+  if constexpr (VEC == 8 && !RES && GELU == 0 && FP8 != 2 && (VPL != 6 || FP8 == 1))
+    if (exact && threads <= 256)
+      return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, true, 256>(p, threads, s);
+  return FLN_ERR_INVALID;
+}
+
 template <class T, int FP8, bool RES, int GELU, int VEC>
 int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStream_t s) {
   constexpr int CAP = max_vpl<VEC>();
@@ -1164,13 +1172,13 @@ int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStre
     case 1: return launch_reg_exact<T, FP8, RES, GELU, VEC, 1>(p, exact, threads, s);
     case 2: return launch_reg_exact<T, FP8, RES, GELU, VEC, 2>(p, exact, threads, s);
     case 4: return launch_reg_exact<T, FP8, RES, GELU, VEC, 4>(p, exact, threads, s);
-    case 7:
-      // Seven 16-byte vectors per lane, exact tilings only, 256-thread blocks (219-224 VGPRs):
-      // planned for 16-bit LN / RMSNorm rows of 448 vectors and the fp8 row scale of 896.
-      if constexpr (VEC == 8 && !RES && GELU == 0 && FP8 != 2)
-        if (exact && threads <= 256)
-          return launch_reg_t<T, FP8, RES, GELU, VEC, 7, true, 256>(p, threads, s);
-      return FLN_ERR_INVALID;
+    // Odd and six-vector tiles (3, 5, 6, 7 vectors per lane): exact tilings only, in blocks of at
+    // most 256 threads, for the 16-bit LayerNorm / RMSNorm and fp8-row-scale flavours that the
+    // plan gives them.
+    case 3: return launch_reg_odd<T, FP8, RES, GELU, VEC, 3>(p, exact, threads, s);
+    case 5: return launch_reg_odd<T, FP8, RES, GELU, VEC, 5>(p, exact, threads, s);
+    case 6: return launch_reg_odd<T, FP8, RES, GELU, VEC, 6>(p, exact, threads, s);
+    case 7: return launch_reg_odd<T, FP8, RES, GELU, VEC, 7>(p, exact, threads, s);
     case 8:
       if constexpr (CAP >= 8)
         return launch_reg_exact<T, FP8, RES, GELU, VEC, 8>(p, exact, threads, s);
@@ -1823,21 +1831,42 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.threads = 256;
     }
   }
-  // Seven vectors per lane tile two 16-bit widths exactly where the power-of-two tiles mask 1/8
-  // of their slots: the fp8 row scale at 7168 columns over 2 waves (bf16 32768 x 7168, us: 4
-  // masked waves 125.1 -> 120.7, one 256-thread block per CU; 2 blocks 125.3, 128-thread blocks
-  // 126.5-152.5) and LN / RMSNorm at 3584 over 1 wave (65536 x 3584: 2 masked waves 169.0 ->
-  // 161.8).  Not for 16-bit output at 7168 (the 7-wave tiling: 157.4 against 167.8), the
-  // residual flavours (their 7-vector tiles spill into AGPRs at one wave per SIMD: residual +
-  // RMSNorm -> fp8 283.1 -> 289.9, MX 274.7 -> 281.5) or GELU; only with enough rows to fill the
-  // device (fewer rows keep the latency tiling above).
-  if (VV == 8 && vec_ok && !g.loop && !has_res && gelu == 0 && tun.fwd_wpr <= 0) {
-    const int w7 = FP8 == 1 && nvec == 2 * kWave * 7 ? 2 : FP8 == 0 && nvec == kWave * 7 ? 1 : 0;
-    if (w7 > 0 && rows * w7 >= 4 * cus) {
-      g.wpr = w7;
-      g.vpl = 7;
+  // 16-bit LayerNorm / RMSNorm and the fp8 row scale, rows enough to fill the device: an exact
+  // tiling of 3, 5, 6 or 7 vectors per lane over 1-4 waves (the fewest waves that tile the row)
+  // replaces a power-of-two tiling that masks more than 1/16 of its slots or spreads the row
+  // over more waves.  Measured on MI355X, bf16, us (waves x vectors per lane; "m": masked):
+  //   LN / RMSNorm: 1536 (1x3) 69.7 -> 65.6 against 1x4m; 2560 (1x5) 62.0 -> 56.1 against 2x4m;
+  //     3072 (2x3) 157.4 -> 140.0 against 3x2 (1x6: 145.4); 3584 (1x7) 169.0 -> 160.8 against
+  //     2x4m; 4608 (3x3) 57.4 -> 55.0 against 4x4m; 5120 (2x5) 60.0 -> 58.5 against 5x2; 6144
+  //     (4x3) 70.7 -> 69.1 against 3x4 (2x6: 71.2).  Kept: 7168 (7x2 157.3, 2x7 167.4), 10240
+  //     (10x2 56.7, 4x5 58.5), 7680 (4x4m with 1/16 masked: 86.4, 3x5 85.7).
+  //   LN -> fp8: 1536 (1x3) 56.8 -> 54.0; 2560 (1x5) 104.6 -> 88.8; 3072 (1x6) 126.6 -> 105.5
+  //     (2x3 107.4); 3584 (1x7) 64.4 -> 58.1; 4608 (3x3) 102.5 -> 88.4; 5120 (2x5) 101.2 ->
+  //     88.0; 6144 (2x6) 112.6 -> 107.4; 7168 (2x7, C5) 125.1 -> 120.2 against the masked 4-wave
+  //     tiling (one 256-thread block per CU; 2 blocks 125.3, 128-thread blocks 126.5-152.5);
+  //     10240 (4x5) 97.5 -> 86.9 against 10x2.  Kept: 7680 (4x4m 128.8, 3x5 139.8).
+  // Not for the residual flavours (their 7-vector tiles need AGPRs at one wave per SIMD:
+  // residual + RMSNorm -> fp8 at 7168 283.1 -> 289.9, MX 274.7 -> 281.5), MX outputs or GELU.
+  if (VV == 8 && vec_ok && !g.loop && !has_res && gelu == 0 && FP8 != 2 && tun.fwd_wpr <= 0) {
+    const int64_t slots = static_cast<int64_t>(g.wpr) * kWave * g.vpl;
+    const bool well_tiled = !g.exact && (slots - nvec) * 16 <= slots;
+    int w_odd = 0, v_odd = 0;
+    for (int w = 1; w <= 4 && w_odd == 0 && !well_tiled; ++w) {
+      for (const int v : {3, 5, 6, 7}) {
+        const bool ok = FP8 == 1 ? (w <= 2 || v <= 5)
+                                 : (v == 3 || (v == 5 && w <= 3) || (v == 7 && w == 1));
+        if (ok && nvec == static_cast<int64_t>(w) * kWave * v) {
+          w_odd = w;
+          v_odd = v;
+          break;
+        }
+      }
+    }
+    if (w_odd > 0 && rows * w_odd >= 4 * cus) {
+      g.wpr = w_odd;
+      g.vpl = v_odd;
       g.exact = true;
-      g.threads = 256;
+      g.threads = (4 % w_odd == 0) ? 256 : kWave * w_odd;
     }
   }
   // Rows past the register tiles: the LDS-staged kernel on the vector path (up to 8 vectors

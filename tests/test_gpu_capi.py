@@ -709,23 +709,35 @@ def test_fp8_variants_dtype_shape_matrix(lib, dtype, rows, cols):
                      t_ref=_scaled(norms.rms_norm_fwd(h_o, f32(gc), 1e-6)[0]))
 
 
-@pytest.mark.parametrize("op,dtype,rows,cols", [
-    ("ln", torch.bfloat16, 1024, 3584), ("rms", torch.float16, 1100, 3584),
-    ("ln_fp8", torch.bfloat16, 600, 7168), ("rms_fp8", torch.float16, 512, 7168)],
-    ids=["ln-bf16-1024x3584", "rms-f16-1100x3584", "ln_fp8-bf16-600x7168",
-         "rms_fp8-f16-512x7168"])
-def test_seven_vectors_per_lane(lib, capfd, monkeypatch, op, dtype, rows, cols):
-    """The 7-vectors-per-lane register tiles (exact, 256-thread blocks): 16-bit LayerNorm /
-    RMSNorm at 3584 columns over one wave per row, LN / RMSNorm -> fp8 with the row scale at
-    7168 over two, with rows enough to fill the device; the dispatcher's trace must show the
-    tiling fln_forward_plan reports, and the outputs must meet the oracle's bar."""
+ODD_TILES = [  # op, dtype, rows, cols, (waves per row, vectors per lane, threads)
+    ("ln", torch.bfloat16, 1024, 1536, (1, 3, 256)), ("rms", torch.float16, 1024, 2560, (1, 5, 256)),
+    ("ln", torch.bfloat16, 512, 3072, (2, 3, 256)), ("ln", torch.bfloat16, 1024, 3584, (1, 7, 256)),
+    ("rms", torch.float16, 1100, 3584, (1, 7, 256)), ("rms", torch.bfloat16, 342, 4608, (3, 3, 192)),
+    ("ln", torch.float16, 512, 5120, (2, 5, 256)), ("ln", torch.bfloat16, 256, 6144, (4, 3, 256)),
+    ("ln_fp8", torch.bfloat16, 1024, 2560, (1, 5, 256)),
+    ("ln_fp8", torch.bfloat16, 1024, 3072, (1, 6, 256)),
+    ("rms_fp8", torch.bfloat16, 342, 4608, (3, 3, 192)),
+    ("rms_fp8", torch.float16, 512, 6144, (2, 6, 256)),
+    ("ln_fp8", torch.bfloat16, 600, 7168, (2, 7, 256)),
+    ("rms_fp8", torch.float16, 512, 7168, (2, 7, 256)),
+    ("ln_fp8", torch.bfloat16, 256, 10240, (4, 5, 256))]
+
+
+@pytest.mark.parametrize("op,dtype,rows,cols,tile", ODD_TILES,
+                         ids=[f"{o}-{str(d)[6:]}-{r}x{c}" for o, d, r, c, _ in ODD_TILES])
+def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
+    """The exact register tilings of 3, 5, 6 or 7 vectors per lane (16-bit LayerNorm / RMSNorm
+    and the fp8 row scale, blocks of at most 256 threads), with rows enough to fill the device:
+    the dispatcher's trace must show the tiling fln_forward_plan reports, and the outputs must
+    meet the oracle's bar."""
     import re
+    w_exp, v_exp, t_exp = tile
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if rows * (cols // 3584) < 4 * cus:
+    if rows * w_exp < 4 * cus:
         pytest.skip(f"{cus} CUs: the tiling needs more rows to be planned")
     plan = fl_functional().get_optimal_config(rows, cols, dtype, fp8=int(op.endswith("fp8")))
-    assert (plan["waves_per_row"], plan["vectors_per_lane"], plan["exact_tiling"]) == (
-        cols // 512 // 7, 7, True), plan
+    assert (plan["waves_per_row"], plan["vectors_per_lane"], plan["exact_tiling"],
+            plan["threads_per_block"]) == (w_exp, v_exp, True, t_exp), plan
     gen = torch.Generator().manual_seed(rows + cols)
     xc = (torch.randn(rows, cols, generator=gen) * 2 + 0.5).to(dtype)
     gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
@@ -756,7 +768,7 @@ def test_seven_vectors_per_lane(lib, capfd, monkeypatch, op, dtype, rows, cols):
     capi.reload_tuning()
     trace = re.findall(r"-> (\S+) wpr=(\d+) vpl=(\d+) exact=(\d+) threads=(\d+)",
                        capfd.readouterr().err)
-    assert trace == [("registers", str(cols // 3584), "7", "1", "256")], trace
+    assert trace == [("registers", str(w_exp), str(v_exp), "1", str(t_exp))], trace
     if op == "ln":
         y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
         assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5), kind=kind,

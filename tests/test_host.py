@@ -409,31 +409,43 @@ def test_optimal_config_reports_dispatch_geometry():
     assert c["waves_per_row"] * 64 * c["vectors_per_lane"] * c["vector_elems"] == 4096
     c7 = fl.functional.get_optimal_config(32768, 7168, torch.bfloat16)
     assert (c7["waves_per_row"], c7["vectors_per_lane"], c7["threads_per_block"]) == (7, 2, 448)
-    # Seven vectors per lane: LN -> fp8 (row scale) at 7168 columns over 2 waves and LN /
-    # RMSNorm at 3584 over 1 wave, 16-bit only, with enough rows to fill the device (4 waves
-    # per CU); the residual, MX and GELU flavours and fp32 keep their tilings.
+    # Exact tilings of 3, 5, 6 or 7 vectors per lane over 1-4 waves for 16-bit LayerNorm /
+    # RMSNorm and the fp8 row scale, with rows enough to fill the device (4 waves per CU), where
+    # the power-of-two tiles mask more than 1/16 of their slots or use more waves; the residual,
+    # MX and GELU flavours and fp32 keep their tilings.
     w7 = lambda *a, **k: (lambda c: (c["waves_per_row"], c["vectors_per_lane"],  # noqa: E731
                                      c["exact_tiling"], c["threads_per_block"]))(
         fl.functional.get_optimal_config(*a, **k))
-    assert w7(32768, 7168, torch.bfloat16, fp8=1) == (2, 7, True, 256)
+    plain = {1536: (1, 3, True, 256), 2560: (1, 5, True, 256), 3072: (2, 3, True, 256),
+             3584: (1, 7, True, 256), 4608: (3, 3, True, 192), 5120: (2, 5, True, 256),
+             6144: (4, 3, True, 256), 7168: (7, 2, True, 448), 7680: (4, 4, False, 256),
+             10240: (10, 2, True, 640), 4096: (2, 4, True, 256), 8192: (4, 4, True, 256)}
+    fp8 = {1536: (1, 3, True, 256), 2560: (1, 5, True, 256), 3072: (1, 6, True, 256),
+           3584: (1, 7, True, 256), 4608: (3, 3, True, 192), 5120: (2, 5, True, 256),
+           6144: (2, 6, True, 256), 7168: (2, 7, True, 256), 7680: (4, 4, False, 256),
+           10240: (4, 5, True, 256), 4096: (2, 4, True, 256)}
+    for cols, want in plain.items():
+        assert w7(65536, cols, torch.bfloat16) == want, cols
+        assert w7(65536, cols, torch.float16, num_cus=128) == want, cols
+    for cols, want in fp8.items():
+        assert w7(65536, cols, torch.bfloat16, fp8=1) == want, cols
     assert w7(512, 7168, torch.float16, fp8=1) == (2, 7, True, 256)
     assert w7(511, 7168, torch.bfloat16, fp8=1)[1] != 7
-    assert w7(65536, 3584, torch.bfloat16) == (1, 7, True, 256)
     assert w7(1024, 3584, torch.float16) == (1, 7, True, 256)
     assert w7(1023, 3584, torch.bfloat16)[1] != 7
     assert w7(128, 7168, torch.bfloat16, fp8=1, num_cus=64) == (2, 7, True, 256)
     for k in (dict(fp8=1, residual=True), dict(fp8=2), dict(approximate="tanh"),
-              dict(approximate="none"), dict(fp8=1, residual=False, dtype=torch.float32)):
+              dict(approximate="none"), dict(residual=True), dict(dtype=torch.float32)):
         dt = k.pop("dtype", torch.bfloat16)
-        assert w7(32768, 7168, dt, **k)[1] != 7, k
-        assert w7(65536, 3584, dt, **k)[1] != 7, k
-    assert w7(65536, 3584, torch.bfloat16, fp8=1)[1] != 7
-    assert w7(32768, 7168, torch.bfloat16)[1] != 7
+        for cols in (1536, 2560, 3584, 5120, 7168):
+            assert w7(65536, cols, dt, **k)[1] not in (3, 5, 6, 7), (k, cols)
     # Exact tilings of one vector per lane only for rows too few to fill the device (C1);
-    # with many rows the power-of-two tiling with masked slots is taken instead.
+    # with many rows a power-of-two tiling with masked slots is taken instead, unless 3-7
+    # vectors per lane tile the row exactly (2560: 1 x 5; 6656 = 13 x 512 has none).
     wt = lambda c: (c["waves_per_row"], c["vectors_per_lane"], c["exact_tiling"])  # noqa: E731
     assert wt(fl.functional.get_optimal_config(32, 768, torch.float32)) == (3, 1, True)
-    assert wt(fl.functional.get_optimal_config(16384, 2560, torch.bfloat16)) == (2, 4, False)
+    assert wt(fl.functional.get_optimal_config(16384, 2560, torch.bfloat16)) == (1, 5, True)
+    assert wt(fl.functional.get_optimal_config(16384, 2560, torch.float32)) == (5, 2, True)
     assert wt(fl.functional.get_optimal_config(16384, 6656, torch.bfloat16)) == (4, 4, False)
     c2 = fl.functional.get_optimal_config(2048, 100000, torch.float32)
     assert not c2["register_resident"] and not c2["lds_staged"] and c2["wide_streamed"]
