@@ -17,6 +17,7 @@
 // many small blocks (32 columns each).  Nothing uses atomics, so dgamma/dbeta are bitwise
 // reproducible run to run.  (Fusing stage 2 into stage 1 behind a cooperative grid barrier was
 // measured at 2x the time of the two launches on gfx950 and is not used.)
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <atomic>
@@ -1132,6 +1133,12 @@ int dispatch_backward(BwdParams p, const BwdGeometry& geo, hipStream_t s,
   p.rgs = geo.rgs;
   p.rows_per_block = geo.rows_per_block;
   constexpr int VV = 16 / sizeof(T);
+  if (!resident && tuning().debug_geometry)
+    fprintf(stderr, "fln backward: rows=%lld cols=%lld vec=%d -> %s wpr=%d vpl=%d threads=%d "
+            "blocks=%lld\n", static_cast<long long>(p.rows), static_cast<long long>(p.cols),
+            geo.vec, geo.lds_cpt > 0 ? "lds" : geo.two_pass ? "two-pass"
+                     : !geo.reg_path ? "loop" : "registers",
+            geo.wpr, geo.vpl, geo.threads, static_cast<long long>(geo.blocks));
   if (geo.lds_cpt > 0) {
     if (resident) {
       *resident = geo.blocks;  // one block per CU (the staged row fills most of the LDS)
@@ -1203,6 +1210,15 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   const int forced = tun.bwd_wpr;
   if (forced >= 1 && forced <= 16 && (forced & (forced - 1)) == 0 && per_lane(forced) <= cap)
     wpr = forced;
+  // 16-bit rows of 9-12 whole waves of vectors (4608-6144 columns) take a row group of exactly
+  // that many waves instead of 16 with 4-7 of them idle.  bf16 backward calls, us, 8192 rows:
+  // 4608 49.4 -> 44.8, 5120 50.6 -> 49.0, 5632 56.7 -> 53.4, 6144 59.6 -> 57.1 (16384 rows:
+  // 5120 87.9 / 88.1, 6144 105.8 -> 104.1).  Fewer waves than 9 in a power-of-two group lost
+  // (16384 x 2560, 5 of 8 waves: 47.8 -> 48.8; 32768 x 1536, 3 of 4: 55.3 -> 55.9), 14 of 16
+  // tied (8192 x 7168 66.5 / 66.6).
+  if (es == 2 && g.vec == 8 && wpr == 16 && cap == 1 && nvec % kWave == 0 &&
+      nvec / kWave >= 9 && nvec / kWave <= 12 && forced <= 0)
+    wpr = static_cast<int>(nvec / kWave);
   g.reg_path = per_lane(wpr) <= cap;
   g.wpr = g.reg_path ? wpr : 16;
   g.vpl = g.reg_path ? next_pow2(static_cast<int>(per_lane(wpr))) : 0;
@@ -1241,6 +1257,7 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   }
   if (!g.reg_path) threads = 1024;
   if (threads < kWave * g.wpr) threads = kWave * g.wpr;
+  if (g.reg_path) threads = threads / (kWave * g.wpr) * (kWave * g.wpr);  // whole row groups
   g.threads = threads;
   g.rgs = g.reg_path ? threads / (kWave * g.wpr) : 1;
   if (few_rows || tun.bwd_threads > 0) per_cu = 1024 / threads;  // 16 waves per CU in total

@@ -789,7 +789,84 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
                          t_ref=_scaled(norms.rms_norm_fwd(xs, gs, 1e-6)[0]))
 
 
-WIDE_KINDS =["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp8", "rms_fp8",
+BWD_EXACT_GROUPS = [("ln", torch.bfloat16, 4608), ("rms", torch.bfloat16, 5120),
+                    ("ln_dres", torch.float16, 5632), ("gelu_tanh", torch.bfloat16, 6144),
+                    ("gelu_none", torch.float16, 4608), ("ln", torch.float16, 6144)]
+
+
+@pytest.mark.parametrize("kind,dtype,cols", BWD_EXACT_GROUPS,
+                         ids=[f"{k}-{str(d)[6:]}-{c}" for k, d, c in BWD_EXACT_GROUPS])
+@pytest.mark.parametrize("rows", [300, 2048])
+def test_backward_exact_row_groups(lib, capfd, monkeypatch, kind, dtype, rows, cols):
+    """16-bit backward rows of 9-12 whole waves of vectors (4608-6144 columns) take a row group
+    of exactly cols / 512 waves (one per block) instead of 16: the backward's trace must show it,
+    and dx, dgamma, dbeta must meet the oracle's bar for every flavour."""
+    import re
+    gen = torch.Generator().manual_seed(rows + 3 * cols)
+    xc = (torch.randn(rows, cols, generator=gen) + 0.3).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    drc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = torch.linspace(-3.0, 3.0, cols).to(dtype)
+    x, dy, dr, g, b = cuda(xc), cuda(dyc), cuda(drc), cuda(gc), cuda(bc)
+    xs, dys, drs, gs, bs = f32(xc), f32(dyc), f32(drc), f32(gc), f32(bc)
+    p = capi.ptr
+    code = capi.dtype_code(x)
+    eps = 1e-6 if kind == "rms" else 1e-5
+    if kind == "rms":
+        _, rstd = rms_forward(lib, x, g, eps)
+    elif kind.startswith("gelu"):
+        gm = capi.GELU_ERF if kind == "gelu_none" else capi.GELU_TANH
+        y = torch.empty_like(x)
+        mean = torch.empty(rows, device="cuda")
+        rstd = torch.empty(rows, device="cuda")
+        capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
+                                                  cols, code, eps, gm, capi.stream()))
+    else:
+        _, mean, rstd = ln_forward(lib, x, g, b, eps)
+    torch.cuda.synchronize()
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
+    if kind == "rms":
+        dx, dg = rms_backward(lib, dy, x, rstd, g)
+        db = None
+    elif kind.startswith("gelu"):
+        dx = torch.empty_like(x)
+        dg = torch.empty(cols, device="cuda")
+        db = torch.empty(cols, device="cuda")
+        ws, n = workspace(lib, rows, cols, x)
+        capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b),
+                                                   p(dx), p(dg), p(db), rows, cols, code,
+                                                   capi.F32, gm, p(ws), n, capi.stream()))
+    else:
+        dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g,
+                                 dres=dr if kind == "ln_dres" else None)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
+    trace = re.findall(r"fln backward: .* -> (\S+) wpr=(\d+) vpl=(\d+) threads=(\d+)",
+                       capfd.readouterr().err)
+    w = cols // 512
+    assert trace == [("registers", str(w), "1", str(64 * w))], trace
+    if kind == "rms":
+        dx_ref, dg_ref = norms.rms_norm_bwd(dys, xs, gs, eps)
+        db_ref = None
+    elif kind.startswith("gelu"):
+        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, eps, kind[5:])
+    else:
+        dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, eps)
+        if kind == "ln_dres":
+            dx_ref = dx_ref + drs
+    k = "bf16" if dtype == torch.bfloat16 else "f16"
+    assert_dx(to_np(dx), dx_ref, _flavour_allowance(kind, xs, dys, gs, bs, drs), k,
+              f"{kind} {cols} dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+    if db_ref is not None:
+        assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+
+
+WIDE_KINDS = ["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp8", "rms_fp8",
               "add_rms_fp8", "ln_mx", "rms_mx", "add_rms_mx"]
 
 
