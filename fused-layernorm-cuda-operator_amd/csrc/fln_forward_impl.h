@@ -1159,7 +1159,8 @@ int launch_reg_exact(const FwdParams& p, bool exact, int threads, hipStream_t s)
 
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL>
 int launch_reg_odd(const FwdParams& p, bool exact, int threads, hipStream_t s) {
-  if constexpr (VEC == 8 && !RES && GELU == 0 && FP8 != 2 && (VPL != 6 || FP8 == 1))
+  if constexpr (VEC == 8 && !RES && FP8 != 2 && (GELU == 0 || FP8 == 0) &&
+                (VPL != 6 || FP8 == 1 || GELU != 0))
     if (exact && threads <= 256)
       return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, true, 256>(p, threads, s);
   return FLN_ERR_INVALID;
@@ -1173,8 +1174,8 @@ int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStre
     case 2: return launch_reg_exact<T, FP8, RES, GELU, VEC, 2>(p, exact, threads, s);
     case 4: return launch_reg_exact<T, FP8, RES, GELU, VEC, 4>(p, exact, threads, s);
     // Odd and six-vector tiles (3, 5, 6, 7 vectors per lane): exact tilings only, in blocks of at
-    // most 256 threads, for the 16-bit LayerNorm / RMSNorm and fp8-row-scale flavours that the
-    // plan gives them.
+    // most 256 threads, for the 16-bit LayerNorm / RMSNorm, LN + GELU and fp8-row-scale flavours
+    // that the plan gives them.
     case 3: return launch_reg_odd<T, FP8, RES, GELU, VEC, 3>(p, exact, threads, s);
     case 5: return launch_reg_odd<T, FP8, RES, GELU, VEC, 5>(p, exact, threads, s);
     case 6: return launch_reg_odd<T, FP8, RES, GELU, VEC, 6>(p, exact, threads, s);
@@ -1831,10 +1832,11 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.threads = 256;
     }
   }
-  // 16-bit LayerNorm / RMSNorm and the fp8 row scale, rows enough to fill the device: an exact
-  // tiling of 3, 5, 6 or 7 vectors per lane over 1-4 waves (the fewest waves that tile the row)
-  // replaces a power-of-two tiling that masks more than 1/16 of its slots or spreads the row
-  // over more waves.  Measured on MI355X, bf16, us (waves x vectors per lane; "m": masked):
+  // 16-bit LayerNorm / RMSNorm, LN + GELU and the fp8 row scale, rows enough to fill the device:
+  // an exact tiling of 3, 5, 6 or 7 vectors per lane over 1-4 waves (the fewest waves that tile
+  // the row, among the shapes each flavour measured faster with) replaces a power-of-two tiling
+  // that masks more than 1/16 of its slots or spreads the row over more waves.  Measured on
+  // MI355X, bf16, us (waves x vectors per lane; "m": masked):
   //   LN / RMSNorm: 1536 (1x3) 69.7 -> 65.6 against 1x4m; 2560 (1x5) 62.0 -> 56.1 against 2x4m;
   //     3072 (2x3) 157.4 -> 140.0 against 3x2 (1x6: 145.4); 3584 (1x7) 169.0 -> 160.8 against
   //     2x4m; 4608 (3x3) 57.4 -> 55.0 against 4x4m; 5120 (2x5) 60.0 -> 58.5 against 5x2; 6144
@@ -1845,17 +1847,31 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
   //     88.0; 6144 (2x6) 112.6 -> 107.4; 7168 (2x7, C5) 125.1 -> 120.2 against the masked 4-wave
   //     tiling (one 256-thread block per CU; 2 blocks 125.3, 128-thread blocks 126.5-152.5);
   //     10240 (4x5) 97.5 -> 86.9 against 10x2.  Kept: 7680 (4x4m 128.8, 3x5 139.8).
+  //   LN + GELU tanh / erf: 1536 (1x3) 75.1 -> 72.7 / 84.2 -> 74.5; 2560 (1x5) 75.5 -> 57.1 /
+  //     84.1 -> 60.9; 3072 (1x6) 161.9 -> 132.8 / 166.5 -> 146.3 (2x3 145.6 / 151.7); 3584 tanh
+  //     (1x7) 44.0 -> 42.4 (erf 46.3 -> 54.9: kept); 4608 tanh (3x3) 74.5 -> 61.0 (the erf
+  //     table needs 256 threads); 5120 (2x5) 76.4 -> 59.8 / 72.6 -> 62.7; 6144 (4x3) 74.4 ->
+  //     72.5 / 101.9 -> 77.0 (2x6 75.0 / 79.2); 7168 (2x7) 85.9 -> 82.8 / 93.0 -> 89.4 against
+  //     the masked 4-wave tiling.
   // Not for the residual flavours (their 7-vector tiles need AGPRs at one wave per SIMD:
-  // residual + RMSNorm -> fp8 at 7168 283.1 -> 289.9, MX 274.7 -> 281.5), MX outputs or GELU.
-  if (VV == 8 && vec_ok && !g.loop && !has_res && gelu == 0 && FP8 != 2 && tun.fwd_wpr <= 0) {
+  // residual + RMSNorm -> fp8 at 7168 283.1 -> 289.9, MX 274.7 -> 281.5) or MX outputs.
+  if (VV == 8 && vec_ok && !g.loop && !has_res && FP8 != 2 && (gelu == 0 || FP8 == 0) &&
+      tun.fwd_wpr <= 0) {
     const int64_t slots = static_cast<int64_t>(g.wpr) * kWave * g.vpl;
     const bool well_tiled = !g.exact && (slots - nvec) * 16 <= slots;
+    auto shape_ok = [&](int w, int v) {
+      if (gelu != 0)
+        return v == 3 ? (gelu == FLN_GELU_TANH || w != 3)
+             : v == 5 ? w <= 2
+             : v == 6 ? w == 1
+                      : (w == 2 || (w == 1 && gelu == FLN_GELU_TANH));
+      if (FP8 == 1) return w <= 2 || v <= 5;
+      return v == 3 || (v == 5 && w <= 3) || (v == 7 && w == 1);
+    };
     int w_odd = 0, v_odd = 0;
     for (int w = 1; w <= 4 && w_odd == 0 && !well_tiled; ++w) {
       for (const int v : {3, 5, 6, 7}) {
-        const bool ok = FP8 == 1 ? (w <= 2 || v <= 5)
-                                 : (v == 3 || (v == 5 && w <= 3) || (v == 7 && w == 1));
-        if (ok && nvec == static_cast<int64_t>(w) * kWave * v) {
+        if (shape_ok(w, v) && nvec == static_cast<int64_t>(w) * kWave * v) {
           w_odd = w;
           v_odd = v;
           break;

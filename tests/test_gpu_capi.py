@@ -720,7 +720,12 @@ ODD_TILES = [  # op, dtype, rows, cols, (waves per row, vectors per lane, thread
     ("rms_fp8", torch.float16, 512, 6144, (2, 6, 256)),
     ("ln_fp8", torch.bfloat16, 600, 7168, (2, 7, 256)),
     ("rms_fp8", torch.float16, 512, 7168, (2, 7, 256)),
-    ("ln_fp8", torch.bfloat16, 256, 10240, (4, 5, 256))]
+    ("ln_fp8", torch.bfloat16, 256, 10240, (4, 5, 256)),
+    ("gelu_tanh", torch.bfloat16, 1024, 2560, (1, 5, 256)),
+    ("gelu_none", torch.float16, 1024, 3072, (1, 6, 256)),
+    ("gelu_tanh", torch.bfloat16, 342, 4608, (3, 3, 192)),
+    ("gelu_none", torch.bfloat16, 512, 7168, (2, 7, 256)),
+    ("gelu_tanh", torch.float16, 256, 6144, (4, 3, 256))]
 
 
 @pytest.mark.parametrize("op,dtype,rows,cols,tile", ODD_TILES,
@@ -735,7 +740,9 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if rows * w_exp < 4 * cus:
         pytest.skip(f"{cus} CUs: the tiling needs more rows to be planned")
-    plan = fl_functional().get_optimal_config(rows, cols, dtype, fp8=int(op.endswith("fp8")))
+    form = op[5:] if op.startswith("gelu") else None
+    plan = fl_functional().get_optimal_config(rows, cols, dtype, fp8=int(op.endswith("fp8")),
+                                              approximate=form)
     assert (plan["waves_per_row"], plan["vectors_per_lane"], plan["exact_tiling"],
             plan["threads_per_block"]) == (w_exp, v_exp, True, t_exp), plan
     gen = torch.Generator().manual_seed(rows + cols)
@@ -754,6 +761,11 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
         y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
     elif op == "rms":
         y, rstd = rms_forward(lib, x, g, 1e-6)
+    elif form is not None:
+        y = torch.empty_like(x)
+        capi.check(lib.fln_layernorm_gelu(p(x), p(g), p(b), p(y), rows, cols, code, 1e-5,
+                                          capi.GELU_TANH if form == "tanh" else capi.GELU_ERF,
+                                          capi.stream()))
     else:
         q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
         s = torch.empty(rows, device="cuda")
@@ -779,6 +791,10 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
         y_ref, r_ref = norms.rms_norm_fwd(xs, gs, 1e-6)
         assert_within_ulp(to_np(y), y_ref, 1.0, kind=kind, what="y")
         assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+    elif form is not None:
+        y_ref = norms.layer_norm_gelu_fwd(xs, gs, bs, 1e-5, form)
+        assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5), kind=kind,
+                          what="gelu y")
     elif op == "ln_fp8":
         q_ref, s_ref = c_oracle.layernorm_fp8(xs, gs, bs, 1e-5)
         assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "ln fp8",

@@ -434,8 +434,17 @@ def test_optimal_config_reports_dispatch_geometry():
     assert w7(1024, 3584, torch.float16) == (1, 7, True, 256)
     assert w7(1023, 3584, torch.bfloat16)[1] != 7
     assert w7(128, 7168, torch.bfloat16, fp8=1, num_cus=64) == (2, 7, True, 256)
-    for k in (dict(fp8=1, residual=True), dict(fp8=2), dict(approximate="tanh"),
-              dict(approximate="none"), dict(residual=True), dict(dtype=torch.float32)):
+    gelu = {1536: (1, 3), 2560: (1, 5), 3072: (1, 6), 5120: (2, 5), 6144: (4, 3), 7168: (2, 7)}
+    for cols, (w, v) in gelu.items():
+        for form in ("tanh", "none"):
+            assert w7(65536, cols, torch.bfloat16, approximate=form) == (w, v, True, 256), cols
+    assert w7(65536, 3584, torch.bfloat16, approximate="tanh") == (1, 7, True, 256)
+    assert w7(65536, 4608, torch.bfloat16, approximate="tanh") == (3, 3, True, 192)
+    # erf: the 1-wave 7-vector tile measured slower, and its table needs 256-thread blocks
+    assert w7(65536, 3584, torch.bfloat16, approximate="none")[1] not in (3, 5, 6, 7)
+    assert w7(65536, 4608, torch.bfloat16, approximate="none")[1] not in (3, 5, 6, 7)
+    for k in (dict(fp8=1, residual=True), dict(fp8=2), dict(residual=True),
+              dict(dtype=torch.float32), dict(dtype=torch.float32, approximate="tanh")):
         dt = k.pop("dtype", torch.bfloat16)
         for cols in (1536, 2560, 3584, 5120, 7168):
             assert w7(65536, cols, dt, **k)[1] not in (3, 5, 6, 7), (k, cols)
