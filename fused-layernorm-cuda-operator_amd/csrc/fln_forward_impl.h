@@ -1159,8 +1159,13 @@ int launch_reg_exact(const FwdParams& p, bool exact, int threads, hipStream_t s)
 
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL>
 int launch_reg_odd(const FwdParams& p, bool exact, int threads, hipStream_t s) {
-  if constexpr (VEC == 8 && !RES && FP8 != 2 && (GELU == 0 || FP8 == 0) &&
-                (VPL != 6 || FP8 == 1 || GELU != 0))
+  // The flavours the plan gives these tiles: GELU only as LN + GELU; with a residual 3 or 5
+  // vectors per lane (6 and 7 need AGPRs there); MX outputs only with a residual; 6 vectors for
+  // the fp8 row scale and GELU.
+  constexpr bool kPlanned =
+      VEC == 8 && (GELU == 0 || (FP8 == 0 && !RES)) && (!RES || VPL == 3 || VPL == 5) &&
+      (FP8 != 2 || RES) && (VPL != 6 || (FP8 == 1 && !RES) || GELU != 0);
+  if constexpr (kPlanned)
     if (exact && threads <= 256)
       return launch_reg_t<T, FP8, RES, GELU, VEC, VPL, true, 256>(p, threads, s);
   return FLN_ERR_INVALID;
@@ -1174,8 +1179,7 @@ int launch_reg_vpl(const FwdParams& p, int vpl, bool exact, int threads, hipStre
     case 2: return launch_reg_exact<T, FP8, RES, GELU, VEC, 2>(p, exact, threads, s);
     case 4: return launch_reg_exact<T, FP8, RES, GELU, VEC, 4>(p, exact, threads, s);
     // Odd and six-vector tiles (3, 5, 6, 7 vectors per lane): exact tilings only, in blocks of at
-    // most 256 threads, for the 16-bit LayerNorm / RMSNorm, LN + GELU and fp8-row-scale flavours
-    // that the plan gives them.
+    // most 256 threads, for the 16-bit flavours that the plan gives them.
     case 3: return launch_reg_odd<T, FP8, RES, GELU, VEC, 3>(p, exact, threads, s);
     case 5: return launch_reg_odd<T, FP8, RES, GELU, VEC, 5>(p, exact, threads, s);
     case 6: return launch_reg_odd<T, FP8, RES, GELU, VEC, 6>(p, exact, threads, s);
@@ -1832,7 +1836,7 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.threads = 256;
     }
   }
-  // 16-bit LayerNorm / RMSNorm, LN + GELU and the fp8 row scale, rows enough to fill the device:
+  // 16-bit rows (every flavour but MX outputs without a residual), rows enough to fill the device:
   // an exact tiling of 3, 5, 6 or 7 vectors per lane over 1-4 waves (the fewest waves that tile
   // the row, among the shapes each flavour measured faster with) replaces a power-of-two tiling
   // that masks more than 1/16 of its slots or spreads the row over more waves.  Measured on
@@ -1853,13 +1857,22 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
   //     table needs 256 threads); 5120 (2x5) 76.4 -> 59.8 / 72.6 -> 62.7; 6144 (4x3) 74.4 ->
   //     72.5 / 101.9 -> 77.0 (2x6 75.0 / 79.2); 7168 (2x7) 85.9 -> 82.8 / 93.0 -> 89.4 against
   //     the masked 4-wave tiling.
-  // Not for the residual flavours (their 7-vector tiles need AGPRs at one wave per SIMD:
-  // residual + RMSNorm -> fp8 at 7168 283.1 -> 289.9, MX 274.7 -> 281.5) or MX outputs.
-  if (VV == 8 && vec_ok && !g.loop && !has_res && FP8 != 2 && (gelu == 0 || FP8 == 0) &&
+  //   Residual + LN / residual + RMSNorm -> fp8 / -> MXFP8, 3 and 5 vectors per lane only
+  //     (6 and 7 need AGPRs at one wave per SIMD: residual + RMSNorm -> fp8 at 7168 (2x7) 283.1
+  //     -> 289.9, MXFP8 274.7 -> 281.5): 1536 (1x3) 143.7 -> 133.6 / 124.9 -> 116.9; 2560 (1x5)
+  //     121.3 -> 115.7 / 109.2 -> 97.6 / 104.9 -> 98.5; 3072 (2x3) 140.3 -> 139.0 / 133.9 ->
+  //     125.1 / 125.7 -> 118.1; 4608 (3x3) 110.1 -> 100.1 / 97.1 -> 95.4; 5120 (2x5) residual +
+  //     RMSNorm -> fp8 106.9 -> 104.1 (kept: residual + LN 113.7 / 114.5, MX 94.3 / 96.7); 6144
+  //     (4x3) 144.2 -> 139.0 / MX 122.8 -> 117.9 (kept: -> fp8 123.5 / 124.6).
+  // MX outputs without a residual keep the power-of-two tiles.
+  if (VV == 8 && vec_ok && !g.loop && (FP8 != 2 || has_res) && (gelu == 0 || FP8 == 0) &&
       tun.fwd_wpr <= 0) {
     const int64_t slots = static_cast<int64_t>(g.wpr) * kWave * g.vpl;
     const bool well_tiled = !g.exact && (slots - nvec) * 16 <= slots;
     auto shape_ok = [&](int w, int v) {
+      if (has_res)
+        return FP8 == 1 ? ((v == 3 && w <= 3) || (v == 5 && w <= 2))
+                        : (v == 3 || (v == 5 && w == 1));
       if (gelu != 0)
         return v == 3 ? (gelu == FLN_GELU_TANH || w != 3)
              : v == 5 ? w <= 2

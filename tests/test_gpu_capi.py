@@ -725,7 +725,13 @@ ODD_TILES = [  # op, dtype, rows, cols, (waves per row, vectors per lane, thread
     ("gelu_none", torch.float16, 1024, 3072, (1, 6, 256)),
     ("gelu_tanh", torch.bfloat16, 342, 4608, (3, 3, 192)),
     ("gelu_none", torch.bfloat16, 512, 7168, (2, 7, 256)),
-    ("gelu_tanh", torch.float16, 256, 6144, (4, 3, 256))]
+    ("gelu_tanh", torch.float16, 256, 6144, (4, 3, 256)),
+    ("add_ln", torch.bfloat16, 1024, 1536, (1, 3, 256)),
+    ("add_ln", torch.float16, 342, 4608, (3, 3, 192)),
+    ("add_rms_fp8", torch.bfloat16, 1024, 2560, (1, 5, 256)),
+    ("add_rms_fp8", torch.float16, 512, 5120, (2, 5, 256)),
+    ("add_rms_mx", torch.bfloat16, 512, 3072, (2, 3, 256)),
+    ("add_rms_mx", torch.bfloat16, 256, 6144, (4, 3, 256))]
 
 
 @pytest.mark.parametrize("op,dtype,rows,cols,tile", ODD_TILES,
@@ -741,8 +747,9 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
     if rows * w_exp < 4 * cus:
         pytest.skip(f"{cus} CUs: the tiling needs more rows to be planned")
     form = op[5:] if op.startswith("gelu") else None
-    plan = fl_functional().get_optimal_config(rows, cols, dtype, fp8=int(op.endswith("fp8")),
-                                              approximate=form)
+    fp8 = 1 if op.endswith("fp8") else 2 if op.endswith("mx") else 0
+    plan = fl_functional().get_optimal_config(rows, cols, dtype, fp8=fp8, approximate=form,
+                                              residual=op.startswith("add"))
     assert (plan["waves_per_row"], plan["vectors_per_lane"], plan["exact_tiling"],
             plan["threads_per_block"]) == (w_exp, v_exp, True, t_exp), plan
     gen = torch.Generator().manual_seed(rows + cols)
@@ -761,6 +768,28 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
         y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
     elif op == "rms":
         y, rstd = rms_forward(lib, x, g, 1e-6)
+    elif op.startswith("add"):
+        rc = torch.randn(rows, cols, generator=gen).to(dtype)
+        r = cuda(rc)
+        h = torch.empty_like(x)
+        if op == "add_ln":
+            y = torch.empty_like(x)
+            mean = torch.empty(rows, device="cuda")
+            rstd = torch.empty(rows, device="cuda")
+            capi.check(lib.fln_add_layernorm_forward(p(x), p(r), p(g), p(b), p(h), p(y), p(mean),
+                                                     p(rstd), rows, cols, code, 1e-5,
+                                                     capi.stream()))
+        elif op == "add_rms_fp8":
+            q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+            s = torch.empty(rows, device="cuda")
+            capi.check(lib.fln_add_rmsnorm_fp8_forward(p(x), p(r), p(g), p(h), p(q), p(s), None,
+                                                       rows, cols, code, 1e-6, capi.stream()))
+        else:
+            q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+            sc = torch.empty(rows, cols // 32, device="cuda", dtype=torch.uint8)
+            capi.check(lib.fln_add_rmsnorm_mxfp8_forward(p(x), p(r), p(g), p(h), p(q), p(sc),
+                                                         None, rows, cols, code, 1e-6,
+                                                         capi.stream()))
     elif form is not None:
         y = torch.empty_like(x)
         capi.check(lib.fln_layernorm_gelu(p(x), p(g), p(b), p(y), rows, cols, code, 1e-5,
@@ -791,6 +820,21 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
         y_ref, r_ref = norms.rms_norm_fwd(xs, gs, 1e-6)
         assert_within_ulp(to_np(y), y_ref, 1.0, kind=kind, what="y")
         assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+    elif op.startswith("add"):
+        rs = f32(rc)
+        assert np.array_equal(to_np(h), to_np(xc + rc)), "h bit-exact"
+        if op == "add_ln":
+            y_ref, h_ref, m_ref, r_ref = norms.add_layer_norm_fwd(xs, rs, gs, bs, 1e-5, kind)
+            assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(h_ref, gs, bs, 1e-5),
+                              kind=kind, what="add ln y")
+            assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+        elif op == "add_rms_fp8":
+            q_ref, s_ref, h_o = norms.add_rms_norm_fp8_fwd(xs, rs, gs, 1e-6, kind)
+            assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, "add rms fp8",
+                             t_ref=_scaled(norms.rms_norm_fwd(h_o, gs, 1e-6)[0]))
+        else:
+            q_ref, sc_ref, y_ref = _mx_ref("add_rms", xs, rs, gs, bs, kind)
+            assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, sc_ref, y_ref, "mx add_rms")
     elif form is not None:
         y_ref = norms.layer_norm_gelu_fwd(xs, gs, bs, 1e-5, form)
         assert_within_ulp(to_np(y), y_ref, 1.0, atol=affine_atol(xs, gs, bs, 1e-5), kind=kind,

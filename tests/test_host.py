@@ -443,11 +443,23 @@ def test_optimal_config_reports_dispatch_geometry():
     # erf: the 1-wave 7-vector tile measured slower, and its table needs 256-thread blocks
     assert w7(65536, 3584, torch.bfloat16, approximate="none")[1] not in (3, 5, 6, 7)
     assert w7(65536, 4608, torch.bfloat16, approximate="none")[1] not in (3, 5, 6, 7)
-    for k in (dict(fp8=1, residual=True), dict(fp8=2), dict(residual=True),
-              dict(dtype=torch.float32), dict(dtype=torch.float32, approximate="tanh")):
+    # Residual flavours: 3 or 5 vectors per lane only, at the shapes each measured faster with.
+    odd = lambda c: c[1] in (3, 5, 6, 7)  # noqa: E731
+    res = {"": {1536: (1, 3), 2560: (1, 5), 3072: (2, 3), 4608: (3, 3), 6144: (4, 3)},
+           "fp8": {1536: (1, 3), 2560: (1, 5), 3072: (2, 3), 4608: (3, 3), 5120: (2, 5)},
+           "mx": {1536: (1, 3), 2560: (1, 5), 3072: (2, 3), 4608: (3, 3), 6144: (4, 3)}}
+    for name, fp in (("", 0), ("fp8", 1), ("mx", 2)):
+        for cols in (1536, 2560, 3072, 3584, 4608, 5120, 6144, 7168):
+            got = w7(65536, cols, torch.bfloat16, fp8=fp, residual=True)
+            if cols in res[name]:
+                w, v = res[name][cols]
+                assert got == (w, v, True, 256 if w != 3 else 192), (name, cols, got)
+            else:
+                assert not odd(got), (name, cols, got)
+    for k in (dict(fp8=2), dict(dtype=torch.float32), dict(dtype=torch.float32, approximate="tanh")):
         dt = k.pop("dtype", torch.bfloat16)
         for cols in (1536, 2560, 3584, 5120, 7168):
-            assert w7(65536, cols, dt, **k)[1] not in (3, 5, 6, 7), (k, cols)
+            assert not odd(w7(65536, cols, dt, **k)), (k, cols)
     # Exact tilings of one vector per lane only for rows too few to fill the device (C1);
     # with many rows a power-of-two tiling with masked slots is taken instead, unless 3-7
     # vectors per lane tile the row exactly (2560: 1 x 5; 6656 = 13 x 512 has none).
