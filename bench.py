@@ -23,8 +23,9 @@ script (--kernel-loop), each scaled by what the counter reads for a device copy 
 pattern as the HBM ceiling the kernels are judged against (and, per bandwidth-bound config, at
 that config's own tensor size: `configs[*].stream_ceiling`).  `reference_paths` times the
 reference's own call paths with its own methods: the binding `fused_layernorm_cuda.layernorm`
-at the shapes of its published latencies, and the `FusedLayerNorm` module against nn.LayerNorm
-at the shapes of its performance-regression test.  `cpu_baseline` times the reference's
+at the shapes of its published latencies, the `FusedLayerNorm` module against nn.LayerNorm
+at the shapes of its performance-regression test, and the binding at the shapes of its
+large-row bandwidth table (fp32, with the 1R1W stream of the same size).  `cpu_baseline` times the reference's
 CPU path (torch-CPU F.layer_norm + autograd backward, which the reference's module falls back to
 off the GPU) on the full headline workload with the process's host threads; the C oracle
 (oracle/fln_oracle.c, the "port") on a row sample is nested beside it.
@@ -662,6 +663,14 @@ PUBLICATION_OPTIMAL = (
     ("Odd Dims", 17, 1023, 0.024211456298828125, 0.010010623931884765),
     ("GPT-3 Large", 32, 12288, 0.024375295639038085, 0.01245798397064209),
 )
+# The reference's large-row forward table (benchmarks/results/final_benchmark_results.csv:2-7;
+# rows = batch x seq_len, fp32, ms per call on its A100; no script in the reference produces it).
+LARGE_ROWS = (
+    ("GPT-3 Medium", 2048, 4096, 0.07, 0.049), ("GPT-3 Large", 2048, 4096, 0.07, 0.049),
+    ("Custom-4K", 2048, 4096, 0.07, 0.049), ("GPT-3 XL", 2048, 5120, 0.087, 0.058),
+    ("Custom-6K", 2048, 6144, 0.102, 0.069), ("Large Model", 1024, 8192, 0.069, 0.049),
+)
+A100_HBM_GBS = 1555.0  # A100 40 GB
 # The reference's performance regression test: FusedLayerNorm >= 1.2x nn.LayerNorm
 # (tests/test_layernorm.py:361-413).
 GATE_SHAPES = ((32, 768), (32, 1024), (16, 2048), (8, 4096))
@@ -762,7 +771,60 @@ def reference_paths(torch):
                          "eager_us_per_call": round(eager, 2),
                          "graph_us_per_call": round(e0.elapsed_time(e1) / (20 * 32) * 1e3, 2),
                          "target_us": 5.0}
+    out["large_rows_fp32"] = large_rows(torch)
     return out
+
+
+def large_rows(torch, n=200):
+    """The reference's large-row forward table (LARGE_ROWS) on this GPU: the binding call
+    fused_layernorm_cuda.layernorm and nn.LayerNorm, fp32, each timed over n calls between HIP
+    events on rotating inputs of at least 1 GiB (no call reads what an earlier one left in the
+    256 MB last-level cache), beside the published A100 figures, the fraction of each GPU's HBM
+    peak that the algorithmic bytes (x read, y written) give, and the hand-written 1R1W stream's
+    rate at the same tensor size (a 32 MiB stream takes ~12 us, of which ramp and drain are a
+    large share)."""
+    import torch.nn as nn
+    import fused_layernorm_cuda as ext
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    rows_out = []
+    ceilings = {}
+    for name, rows, cols, pt_ms, ref_ms in LARGE_ROWS:
+        nbytes = rows * cols * 4
+        k = max(4, -(-(1 << 30) // nbytes))
+        xs = [torch.randn(rows, cols, device="cuda") for _ in range(k)]
+        ln = nn.LayerNorm(cols).cuda()
+        w, b = ln.weight.detach(), ln.bias.detach()
+        res = {}
+        with torch.no_grad():
+            for key, fn in (("pytorch_us", lambda x: ln(x)),
+                            ("ours_us", lambda x: ext.layernorm(x, w, b, 1e-5))):
+                for i in range(2 * k):
+                    fn(xs[i % k])
+                torch.cuda.synchronize()
+                e0, e1 = ev(), ev()
+                e0.record()
+                for i in range(n):
+                    fn(xs[i % k])
+                e1.record()
+                torch.cuda.synchronize()
+                res[key] = round(e0.elapsed_time(e1) / n * 1e3, 2)
+        moved = 2 * nbytes
+        if nbytes not in ceilings:  # 1R1W stream of the same tensor size
+            ceilings[nbytes] = stream_ceilings(torch, nbytes, patterns=[0])["1r1w_gbs"]
+        rows_out.append({
+            "config": name, "rows": rows, "hidden": cols, **res,
+            "speedup": round(res["pytorch_us"] / res["ours_us"], 3),
+            "ours_gbs": round(moved / res["ours_us"] / 1e3, 1),
+            "ours_pct_of_hbm_peak": round(100 * moved / res["ours_us"] / 1e3 / HBM_PEAK_GBS, 1),
+            "stream_1r1w_gbs": round(ceilings[nbytes], 1),
+            "ours_over_stream": round(moved / res["ours_us"] / 1e3 / ceilings[nbytes], 3),
+            "reference_a100_pytorch_us": round(pt_ms * 1e3, 1),
+            "reference_a100_ours_us": round(ref_ms * 1e3, 1),
+            "reference_a100_pct_of_hbm_peak": round(
+                100 * moved / (ref_ms * 1e3) / 1e3 / A100_HBM_GBS, 1)})
+        del xs
+        torch.cuda.empty_cache()
+    return rows_out
 
 
 def torch_gpu_compare(torch, ours, warmup=10, n=50):
