@@ -731,7 +731,11 @@ ODD_TILES = [  # op, dtype, rows, cols, (waves per row, vectors per lane, thread
     ("add_rms_fp8", torch.bfloat16, 1024, 2560, (1, 5, 256)),
     ("add_rms_fp8", torch.float16, 512, 5120, (2, 5, 256)),
     ("add_rms_mx", torch.bfloat16, 512, 3072, (2, 3, 256)),
-    ("add_rms_mx", torch.bfloat16, 256, 6144, (4, 3, 256))]
+    ("add_rms_mx", torch.bfloat16, 256, 6144, (4, 3, 256)),
+    # rows that leave the last block part-empty (4 / 2 row groups per 256-thread block)
+    ("ln", torch.bfloat16, 1027, 2560, (1, 5, 256)),
+    ("rms_fp8", torch.float16, 1026, 3072, (1, 6, 256)),
+    ("gelu_none", torch.bfloat16, 513, 5120, (2, 5, 256))]
 
 
 @pytest.mark.parametrize("op,dtype,rows,cols,tile", ODD_TILES,
