@@ -75,13 +75,22 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 #define FLN_FWD_STORE_POL kStream
 #endif
 // Rows of raw loads in flight ahead of the current one, per instantiation (the rule above; the
-// 16-bit RAW tiles without a residual keep two: their gamma / beta live in LDS).
-template <class T, bool RES, int VEC, int VPL, int MAXT> constexpr int fwd_prefetch_depth() {
+// 16-bit RAW tiles without a residual keep two: their gamma / beta live in LDS; so do the odd
+// tiles of LayerNorm / RMSNorm with 5 or 7 vectors per lane, which have the registers for it
+// (178-248 VGPRs).  bf16, us, one row ahead -> two: 65536 x 3584 (1 x 7) 160.3 -> 157.3, 16384
+// x 5120 (2 x 5) 58.3 -> 56.2, 32768 x 2560 (1 x 5) 55.9 / 55.9.  The fp8 row scale keeps one:
+// two gained on one-wave rows (65536 x 3072, 1 x 6: 105.5 -> 97.2; 32768 x 2560, 1 x 5: 44.7 ->
+// 41.4) and lost on two-wave rows with the same tile (16384 x 6144, 2 x 6: 53.1 -> 57.0; 16384
+// x 5120, 2 x 5: 44.4 -> 51.6; C5, 2 x 7: 121.1 / 121.5), and the depth is fixed per tile.
+template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, int MAXT>
+constexpr int fwd_prefetch_depth() {
   constexpr bool raw = MAXT > 256 && VPL * VEC >= 32;
   constexpr bool params_in_lds =
       MAXT == 1024 && ((raw && VEC > 1 && sizeof(T) == 2) || (VEC == 1 && VPL == 16 &&
                                                                sizeof(T) <= 4));
-  return params_in_lds && raw && !RES
+  constexpr bool odd_two =
+      VEC == 8 && MAXT == 256 && !RES && GELU == 0 && FP8 == 0 && (VPL == 5 || VPL == 7);
+  return (params_in_lds && raw && !RES) || odd_two
              ? 2
              : FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT);
 }
@@ -100,11 +109,8 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
                                                                 sizeof(T) <= 4));
   // rows in flight ahead of the current one (the residual flavour's second input leaves room for
   // one only)
-  constexpr int PD = fwd_prefetch_depth<T, RES, VEC, VPL, MAXT>();
-  static_assert(PD == (PARAMS_IN_LDS && RAW && !RES
-                           ? 2
-                           : FLN_FWD_PREFETCH(VPL * VEC * static_cast<int>(sizeof(T)), MAXT)),
-                "fwd_prefetch_depth must match the kernel's ring");
+  constexpr int PD = fwd_prefetch_depth<T, FP8, RES, GELU, VEC, VPL, MAXT>();
+  static_assert(PD == 1 || PD == 2, "the ring holds one or two rows ahead");
   constexpr int MAXW = MAXT / kWave;
   __shared__ float red[2][3][MAXW + 16];  // padded: combine_partials reads 16 past the base
   using P = Pack<T, VEC>;
@@ -1118,7 +1124,7 @@ int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   // 189.5 [1] 136.6 [2] 145.5 [3] 145.0 [4], 65536 x 4096 190.5 [1] 136.9 [2] 146.0 [3] 145.5
   // [4], 262144 x 1024 198.0 [1] 146.1 [2] 153.3 [3]; residual + RMSNorm -> fp8 at 32768 x 7168
   // 283 [1] 300 [2].
-  constexpr int PD = fwd_prefetch_depth<T, RES, VEC, VPL, MAXT>();
+  constexpr int PD = fwd_prefetch_depth<T, FP8, RES, GELU, VEC, VPL, MAXT>();
   const int64_t es = static_cast<int64_t>(sizeof(T));
   const int64_t moved_per_row = p.cols * (es * (RES ? 3 : 1) + (FP8 ? 1 : es));
   const int64_t per_block = moved_per_row * rows_per_block * PD;
