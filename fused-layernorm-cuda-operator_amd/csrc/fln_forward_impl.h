@@ -1904,6 +1904,19 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.threads = (4 % w_odd == 0) ? 256 : kWave * w_odd;
     }
   }
+  // fp32 LayerNorm / RMSNorm rows of 8192 columns with 2-8 rows per CU (the reference's
+  // large-row table has 1024 x 8192): 16 waves x 2 vectors per lane in a 1024-thread block, two
+  // rows of loads ahead, instead of 4 waves x 8 vectors with one.  us: 512 rows 7.54 -> 7.27,
+  // 1024 rows 14.12 -> 12.31, 1536 rows 19.39 -> 18.22, 2048 rows 24.7 -> 24.1; 4096 rows
+  // 45.5 / 45.6.  Other fp32 widths gained less or lost (1024 x 6144 11.57 -> 11.39, 1024 x
+  // 4096 7.44 -> 8.56, 1024 x 12288 18.16 -> 19.56).
+  if (VV == 4 && vec_ok && !g.loop && !has_res && gelu == 0 && FP8 == 0 && tun.fwd_wpr <= 0 &&
+      nvec == 16 * kWave * 2 && rows >= 2 * cus && rows <= 8 * cus) {
+    g.wpr = 16;
+    g.vpl = 2;
+    g.exact = true;
+    g.threads = 16 * kWave;
+  }
   // Rows past the register tiles: the LDS-staged kernel on the vector path (up to 8 vectors
   // per thread of a 1024-thread block; LayerNorm / RMSNorm and LN + GELU -- tanh, or erf in
   // fp32 -- with half of each row in registers up to twice that), the streamed wide-row kernel

@@ -853,6 +853,46 @@ def test_odd_vector_tiles(lib, capfd, monkeypatch, op, dtype, rows, cols, tile):
                          t_ref=_scaled(norms.rms_norm_fwd(xs, gs, 1e-6)[0]))
 
 
+@pytest.mark.parametrize("rms", [False, True], ids=["ln", "rms"])
+@pytest.mark.parametrize("rows", [512, 1024, 1500])
+def test_fp32_8192_wide_row_groups(lib, capfd, monkeypatch, rms, rows):
+    """fp32 rows of 8192 columns with 2-8 rows per CU take 16 waves x 2 vectors per lane in a
+    1024-thread block: the trace must show it and the outputs must match the oracle (1500 rows
+    leave the grid's last round part-empty)."""
+    import re
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if not 2 * cus <= rows <= 8 * cus:
+        pytest.skip(f"{cus} CUs: {rows} rows are outside the planned range")
+    cols = 8192
+    gen = torch.Generator().manual_seed(rows * 3 + rms)
+    xc = torch.randn(rows, cols, generator=gen) * 3 + 1
+    gc = 1 + 0.1 * torch.randn(cols, generator=gen)
+    bc = 0.1 * torch.randn(cols, generator=gen)
+    x, g, b = cuda(xc), cuda(gc), cuda(bc)
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
+    if rms:
+        y, rstd = rms_forward(lib, x, g, 1e-6)
+    else:
+        y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
+    trace = re.findall(r"-> (\S+) wpr=(\d+) vpl=(\d+) exact=(\d+) threads=(\d+)",
+                       capfd.readouterr().err)
+    assert trace == [("registers", "16", "2", "1", "1024")], trace
+    xs, gs, bs = f32(xc), f32(gc), f32(bc)
+    if rms:
+        y_ref, r_ref = norms.rms_norm_fwd(xs, gs, 1e-6)
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1.0, np.abs(y_ref).max())
+    else:
+        y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
+        assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1.0, np.abs(y_ref).max())
+        assert np.abs(to_np(mean) - m_ref).max() <= 1e-6 * np.abs(xs).max()
+    assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+
+
 BWD_EXACT_GROUPS = [("ln", torch.bfloat16, 4608), ("rms", torch.bfloat16, 5120),
                     ("ln_dres", torch.float16, 5632), ("gelu_tanh", torch.bfloat16, 6144),
                     ("gelu_none", torch.float16, 4608), ("ln", torch.float16, 6144)]

@@ -443,6 +443,15 @@ def test_optimal_config_reports_dispatch_geometry():
     # erf: the 1-wave 7-vector tile measured slower, and its table needs 256-thread blocks
     assert w7(65536, 3584, torch.bfloat16, approximate="none")[1] not in (3, 5, 6, 7)
     assert w7(65536, 4608, torch.bfloat16, approximate="none")[1] not in (3, 5, 6, 7)
+    # fp32 rows of 8192 columns with 2-8 rows per CU: 16 waves x 2 vectors per lane.
+    for rows in (512, 1024, 2048):
+        assert w7(rows, 8192, torch.float32) == (16, 2, True, 1024), rows
+    for rows in (511, 2049, 65536):
+        assert w7(rows, 8192, torch.float32) != (16, 2, True, 1024), rows
+    assert w7(1024, 8192, torch.float32, approximate="tanh") != (16, 2, True, 1024)
+    assert w7(1024, 8192, torch.float32, fp8=1) != (16, 2, True, 1024)
+    assert w7(1024, 8192, torch.float32, residual=True) != (16, 2, True, 1024)
+    assert w7(1024, 8192, torch.bfloat16) != (16, 2, True, 1024)
     # Residual flavours: 3 or 5 vectors per lane only, at the shapes each measured faster with.
     odd = lambda c: c[1] in (3, 5, 6, 7)  # noqa: E731
     res = {"": {1536: (1, 3), 2560: (1, 5), 3072: (2, 3), 4608: (3, 3), 6144: (4, 3)},
