@@ -1807,7 +1807,8 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
   }
   const int vec = pl.vec;
   // Elements per lane: at most 32 by default (measured best or equal on the 4096-8192-wide
-  // benchmark rows); more waves per row beyond that.
+  // benchmark rows); more waves per row beyond that.  The exact odd tiles chosen further down
+  // take up to 7 vectors (56 16-bit elements) per lane where they fill every lane.
   const int epl = tun.fwd_epl > 0 ? tun.fwd_epl : 32;
   int cap = (epl >= vec ? epl : vec) / vec;
   const int max_cap = vec_ok ? max_vpl<VV>() : max_vpl<1>();
