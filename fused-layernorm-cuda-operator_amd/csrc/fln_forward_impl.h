@@ -82,6 +82,10 @@ __device__ __forceinline__ float row_allreduce(float v, float* slot, int wpr, in
 // two gained on one-wave rows (65536 x 3072, 1 x 6: 105.5 -> 97.2; 32768 x 2560, 1 x 5: 44.7 ->
 // 41.4) and lost on two-wave rows with the same tile (16384 x 6144, 2 x 6: 53.1 -> 57.0; 16384
 // x 5120, 2 x 5: 44.4 -> 51.6; C5, 2 x 7: 121.1 / 121.5), and the depth is fixed per tile.
+// Two rows ahead on the 4-vector tiles lost or tied in every flavour (LN 8192 x 4096, 2 x 4:
+// 23.9 -> 24.6; 65536 x 2048, 1 x 4: 86.4 -> 87.5; C4's RMSNorm, 4 x 4: 86.8 / 86.8; residual +
+// LN 16384 x 8192: 181.8 -> 185.0; LN -> fp8 16384 x 4096: 35.6 -> 47.4) and tied on the
+// 3-vector LayerNorm tiles (1536-6144 columns).
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, int MAXT>
 constexpr int fwd_prefetch_depth() {
   constexpr bool raw = MAXT > 256 && VPL * VEC >= 32;
