@@ -2221,3 +2221,131 @@ def test_reference_epsilon_1e12(lib, scenario, dtype):
         assert np.abs(to_np(y) - ref).max() <= 1e-5
     else:
         assert_within_ulp(to_np(y), ref, 1.0, what=f"{scenario} eps=1e-12 y")
+
+
+def _random_cases(n=120, seed=20261202):
+    """Seeded shapes for test_random_shapes_against_the_oracle: the flavour cycles, the dtype is
+    drawn, rows are log-uniform in 1..16384 and columns log-uniform in 1..70000; a third of the
+    widths are rounded down to whole 16-byte vectors (of the 16-bit types), a third to 32-element
+    blocks, the rest stay as drawn (the scalar path); at most 4 M elements per case."""
+    rng = np.random.default_rng(seed)
+    kinds = ["ln", "rms", "gelu_tanh", "gelu_none", "add_ln", "ln_fp8", "add_rms_mx"]
+    cases = []
+    for i in range(n):
+        kind = kinds[i % len(kinds)]
+        dtype = DTYPES[int(rng.integers(3))]
+        rows = int(np.exp(rng.uniform(0.0, np.log(16384.0))))
+        cols = int(np.exp(rng.uniform(0.0, np.log(70000.0))))
+        shape = int(rng.integers(3))
+        if kind == "add_rms_mx" or shape == 1:
+            cols = max(32, cols // 32 * 32)
+        elif shape == 0:
+            cols = max(8, cols // 8 * 8)
+        rows = max(1, min(rows, 4_000_000 // cols))
+        cases.append((kind, dtype, rows, cols))
+    return cases
+
+
+RANDOM_CASES = _random_cases()
+
+
+@pytest.mark.parametrize("kind,dtype,rows,cols", RANDOM_CASES,
+                         ids=[f"{i}-{k}-{str(d)[6:]}-{r}x{c}"
+                              for i, (k, d, r, c) in enumerate(RANDOM_CASES)])
+def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
+    """Seeded random shapes through whatever route the dispatcher picks for them (register
+    tiles, odd tiles, LDS-staged, split, streamed, scalar path; the register, LDS and two-pass
+    backwards): LayerNorm, RMSNorm and LN + GELU (both forms) forward and backward, residual +
+    LayerNorm, LN -> fp8 and residual + RMSNorm -> MXFP8 forwards, each against the oracle's
+    bar for its dtype."""
+    gen = torch.Generator().manual_seed(rows * 65537 + cols)
+    xc = (torch.randn(rows, cols, generator=gen) * 1.5 + 0.25).to(dtype)
+    rc = torch.randn(rows, cols, generator=gen).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, r, dy, g, b = cuda(xc), cuda(rc), cuda(dyc), cuda(gc), cuda(bc)
+    xs, rs, dys, gs, bs = f32(xc), f32(rc), f32(dyc), f32(gc), f32(bc)
+    io = _kind(dtype)
+    p = capi.ptr
+    code = capi.dtype_code(x)
+    what = f"{kind} {io} {rows}x{cols}"
+
+    def check_y(y, y_ref, xin, bias=True):
+        if dtype == torch.float32:
+            assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1.0, np.abs(y_ref).max()), what
+        else:
+            assert_within_ulp(to_np(y), y_ref, 1.0,
+                              atol=affine_atol(xin, gs, bs, 1e-5) if bias else 0.0, kind=io,
+                              what=what + " y")
+
+    def check_h(h):
+        assert np.array_equal(to_np(h), to_np(xc + rc)), what + " h bit-exact"
+
+    if kind == "ln":
+        y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+        dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+        y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
+        check_y(y, y_ref, xs)
+        assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5, what + " rstd"
+        dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
+    elif kind == "rms":
+        y, rstd = rms_forward(lib, x, g, 1e-6)
+        dx, dg = rms_backward(lib, dy, x, rstd, g)
+        db = None
+        y_ref, r_ref = norms.rms_norm_fwd(xs, gs, 1e-6)
+        check_y(y, y_ref, xs, bias=False)
+        assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5, what + " rstd"
+        dx_ref, dg_ref = norms.rms_norm_bwd(dys, xs, gs, 1e-6)
+        db_ref = None
+    elif kind.startswith("gelu"):
+        form = kind[5:]
+        gm = capi.GELU_ERF if form == "none" else capi.GELU_TANH
+        y = torch.empty_like(x)
+        mean = torch.empty(rows, device="cuda")
+        rstd = torch.empty(rows, device="cuda")
+        capi.check(lib.fln_layernorm_gelu_forward(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows,
+                                                  cols, code, 1e-5, gm, capi.stream()))
+        dx = torch.empty_like(x)
+        dg = torch.empty(cols, device="cuda")
+        db = torch.empty(cols, device="cuda")
+        ws, n = workspace(lib, rows, cols, x)
+        capi.check(lib.fln_layernorm_gelu_backward(p(dy), p(x), p(mean), p(rstd), p(g), p(b),
+                                                   p(dx), p(dg), p(db), rows, cols, code,
+                                                   capi.F32, gm, p(ws), n, capi.stream()))
+        check_y(y, norms.layer_norm_gelu_fwd(xs, gs, bs, 1e-5, form), xs)
+        dx_ref, dg_ref, db_ref = norms.layer_norm_gelu_bwd(dys, xs, gs, bs, 1e-5, form)
+    elif kind == "add_ln":
+        h = torch.empty_like(x)
+        y = torch.empty_like(x)
+        mean = torch.empty(rows, device="cuda")
+        rstd = torch.empty(rows, device="cuda")
+        capi.check(lib.fln_add_layernorm_forward(p(x), p(r), p(g), p(b), p(h), p(y), p(mean),
+                                                 p(rstd), rows, cols, code, 1e-5, capi.stream()))
+        check_h(h)
+        y_ref, h_ref, _, r_ref = norms.add_layer_norm_fwd(xs, rs, gs, bs, 1e-5, io)
+        check_y(y, y_ref, h_ref)
+        assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5, what + " rstd"
+        return
+    elif kind == "ln_fp8":
+        q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+        s = torch.empty(rows, device="cuda")
+        capi.check(lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(q), p(s), None, None, rows,
+                                                 cols, code, 1e-5, capi.stream()))
+        q_ref, s_ref = c_oracle.layernorm_fp8(xs, gs, bs, 1e-5)
+        assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, what,
+                         t_ref=_scaled(norms.layer_norm_fwd(xs, gs, bs, 1e-5)[0]))
+        return
+    else:
+        h = torch.empty_like(x)
+        q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+        sc = torch.empty(rows, cols // 32, device="cuda", dtype=torch.uint8)
+        capi.check(_mx_call(lib, "add_rms", x, r, g, b, q, sc, h, rows, cols, code))
+        check_h(h)
+        q_ref, sc_ref, y_ref = _mx_ref("add_rms", xs, rs, gs, bs, io)
+        assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, sc_ref, y_ref, what)
+        return
+    assert_dx(to_np(dx), dx_ref, _flavour_allowance(kind, xs, dys, gs, bs), io, what + " dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, what + " dgamma")
+    if db_ref is not None:
+        assert_close_rel(to_np(db), db_ref, 1e-4, what + " dbeta")
