@@ -1909,6 +1909,25 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.threads = (4 % w_odd == 0) ? 256 : kWave * w_odd;
     }
   }
+  // fp32 LayerNorm / RMSNorm tiles of 8 vectors (32 floats) per lane -- rows of 2048, 4096,
+  // 6144 or 8192 columns over 1-4 waves -- with rows enough for 32 waves per CU at half the
+  // vectors: twice the waves, 4 vectors per lane (for 8192 columns only from 64 rows per CU).
+  // LayerNorm, us, rows: 8 -> 4 vectors per lane.
+  //   2048 columns: 4096 14.06 -> 13.27, 8192 24.48 -> 23.87, 16384 46.15 -> 44.54 (kept:
+  //     1024 5.13 / 5.41, 2048 7.22 / 7.76);
+  //   4096: 2048 14.08 -> 13.68, 4096 24.53 -> 24.14, 8192 45.28 -> 44.77, 16384 89.89 ->
+  //     87.45 (kept: 1024 7.42 / 7.94);
+  //   6144: 2048 19.78 -> 19.36, 4096 36.07 -> 35.63, 8192 69.80 -> 68.79, 16384 140.56 ->
+  //     138.10 (1024: 11.57 / 11.59);
+  //   8192 (8 waves, a 512-thread block): 16384 186.03 -> 179.87 (kept: 4096 45.41 / 45.72,
+  //     8192 89.74 / 89.84).
+  if (VV == 4 && vec_ok && !g.loop && !has_res && gelu == 0 && FP8 == 0 && tun.fwd_wpr <= 0 &&
+      tun.fwd_epl <= 0 && g.exact && g.vpl == 8 && g.wpr <= 4 &&
+      rows * 2 * g.wpr >= 32 * cus && (g.wpr <= 3 || rows >= 64 * cus)) {
+    g.wpr *= 2;
+    g.vpl = 4;
+    g.threads = (4 % g.wpr == 0) ? 256 : kWave * g.wpr;
+  }
   // fp32 LayerNorm / RMSNorm rows of 8192 columns with 2-8 rows per CU (the reference's
   // large-row table has 1024 x 8192): 16 waves x 2 vectors per lane in a 1024-thread block, two
   // rows of loads ahead, instead of 4 waves x 8 vectors with one.  us: 512 rows 7.54 -> 7.27,

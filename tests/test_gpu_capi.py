@@ -893,6 +893,53 @@ def test_fp32_8192_wide_row_groups(lib, capfd, monkeypatch, rms, rows):
     assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
 
 
+FP32_HALVED = [(4096, 2048, (2, 4, 256)), (2048, 4096, (4, 4, 256)), (3001, 4096, (4, 4, 256)),
+               (2048, 6144, (6, 4, 384)), (2500, 6144, (6, 4, 384)), (16384, 8192, (8, 4, 512))]
+
+
+@pytest.mark.parametrize("rms", [False, True], ids=["ln", "rms"])
+@pytest.mark.parametrize("rows,cols,tile", FP32_HALVED,
+                         ids=[f"{r}x{c}" for r, c, _ in FP32_HALVED])
+def test_fp32_halved_vector_tiles(lib, capfd, monkeypatch, rms, rows, cols, tile):
+    """fp32 LayerNorm / RMSNorm rows that would take 8 vectors per lane over 1-4 waves, with
+    rows enough for 32 waves per CU, take twice the waves at 4 vectors per lane (6 and 8 waves
+    in the 1024-thread instantiation; 3001 and 2500 rows leave the last round part-empty): the
+    trace must show the tiling fln_forward_plan reports, and the outputs must match the oracle
+    (the C oracle: up to 134 M elements)."""
+    import re
+    w, v, t = tile
+    plan = fl_functional().get_optimal_config(rows, cols, torch.float32)
+    if (plan["waves_per_row"], plan["vectors_per_lane"]) != (w, v):
+        assert torch.cuda.get_device_properties(0).multi_processor_count != 256, plan
+        pytest.skip("the tiling is planned for another CU count")
+    gen = torch.Generator().manual_seed(rows * 5 + cols + rms)
+    xc = torch.randn(rows, cols, generator=gen) * 2 - 0.5
+    gc = 1 + 0.1 * torch.randn(cols, generator=gen)
+    bc = 0.1 * torch.randn(cols, generator=gen)
+    x, g, b = cuda(xc), cuda(gc), cuda(bc)
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
+    if rms:
+        y, rstd = rms_forward(lib, x, g, 1e-6)
+    else:
+        y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
+    trace = re.findall(r"-> (\S+) wpr=(\d+) vpl=(\d+) exact=(\d+) threads=(\d+)",
+                       capfd.readouterr().err)
+    assert trace == [("registers", str(w), str(v), "1", str(t))], trace
+    xs, gs, bs = f32(xc), f32(gc), f32(bc)
+    if rms:
+        y_ref, r_ref = c_oracle.rmsnorm_fwd(xs, gs, 1e-6)
+    else:
+        y_ref, m_ref, r_ref = c_oracle.layernorm_fwd(xs, gs, bs, 1e-5)
+        assert np.abs(to_np(mean) - m_ref).max() <= 1e-6 * np.abs(xs).max()
+    assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1.0, np.abs(y_ref).max())
+    assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+
+
 BWD_EXACT_GROUPS = [("ln", torch.bfloat16, 4608), ("rms", torch.bfloat16, 5120),
                     ("ln_dres", torch.float16, 5632), ("gelu_tanh", torch.bfloat16, 6144),
                     ("gelu_none", torch.float16, 4608), ("ln", torch.float16, 6144)]

@@ -452,6 +452,22 @@ def test_optimal_config_reports_dispatch_geometry():
     assert w7(1024, 8192, torch.float32, fp8=1) != (16, 2, True, 1024)
     assert w7(1024, 8192, torch.float32, residual=True) != (16, 2, True, 1024)
     assert w7(1024, 8192, torch.bfloat16) != (16, 2, True, 1024)
+    # fp32 LayerNorm / RMSNorm 8-vector tiles with rows enough for 32 waves per CU at half the
+    # vectors: twice the waves, 4 vectors per lane (8192 columns from 64 rows per CU).
+    halved = {(4096, 2048): (2, 4, True, 256), (2048, 4096): (4, 4, True, 256),
+              (16384, 4096): (4, 4, True, 256), (2048, 6144): (6, 4, True, 384),
+              (16384, 8192): (8, 4, True, 512)}
+    for (rows, cols), tile in halved.items():
+        assert w7(rows, cols, torch.float32) == tile, (rows, cols)
+    kept = {(2048, 2048): (1, 8, True, 256), (1024, 4096): (2, 8, True, 256),
+            (1024, 6144): (3, 8, True, 192), (4096, 8192): (4, 8, True, 256),
+            (8192, 8192): (4, 8, True, 256)}
+    for (rows, cols), tile in kept.items():
+        assert w7(rows, cols, torch.float32) == tile, (rows, cols)
+    assert w7(2048, 4096, torch.float32, residual=True)[:2] == (2, 8)
+    assert w7(2048, 4096, torch.float32, approximate="tanh")[:2] == (2, 8)
+    assert w7(2048, 4096, torch.float32, fp8=1)[:2] == (2, 8)
+    assert w7(4096, 2048, torch.float32, num_cus=512) == (1, 8, True, 256)
     # Residual flavours: 3 or 5 vectors per lane only, at the shapes each measured faster with.
     odd = lambda c: c[1] in (3, 5, 6, 7)  # noqa: E731
     res = {"": {1536: (1, 3), 2560: (1, 5), 3072: (2, 3), 4608: (3, 3), 6144: (4, 3)},
