@@ -1921,6 +1921,9 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
   //     138.10 (1024: 11.57 / 11.59);
   //   8192 (8 waves, a 512-thread block): 16384 186.03 -> 179.87 (kept: 4096 45.41 / 45.72,
   //     8192 89.74 / 89.84).
+  // The halved tiles hold 64 bytes of the row per lane, as the 16-bit 4-vector tiles do; those
+  // lose when halved (bf16 65536 x 2048 86.7 -> 98.4, 32768 x 4096 87.6 -> 99.2; LN -> fp8
+  // 32768 x 4096 68.3 -> 80.2).
   if (VV == 4 && vec_ok && !g.loop && !has_res && gelu == 0 && FP8 == 0 && tun.fwd_wpr <= 0 &&
       tun.fwd_epl <= 0 && g.exact && g.vpl == 8 && g.wpr <= 4 &&
       rows * 2 * g.wpr >= 32 * cus && (g.wpr <= 3 || rows >= 64 * cus)) {
