@@ -1909,27 +1909,39 @@ FwdPlan plan_typed(int64_t rows, int64_t N, bool has_res, int gelu, bool vec_ok,
       g.threads = (4 % w_odd == 0) ? 256 : kWave * w_odd;
     }
   }
-  // fp32 LayerNorm / RMSNorm tiles of 8 vectors (32 floats) per lane -- rows of 2048, 4096,
-  // 6144 or 8192 columns over 1-4 waves -- with rows enough for 32 waves per CU at half the
-  // vectors: twice the waves, 4 vectors per lane (for 8192 columns only from 64 rows per CU).
-  // LayerNorm, us, rows: 8 -> 4 vectors per lane.
-  //   2048 columns: 4096 14.06 -> 13.27, 8192 24.48 -> 23.87, 16384 46.15 -> 44.54 (kept:
-  //     1024 5.13 / 5.41, 2048 7.22 / 7.76);
-  //   4096: 2048 14.08 -> 13.68, 4096 24.53 -> 24.14, 8192 45.28 -> 44.77, 16384 89.89 ->
-  //     87.45 (kept: 1024 7.42 / 7.94);
-  //   6144: 2048 19.78 -> 19.36, 4096 36.07 -> 35.63, 8192 69.80 -> 68.79, 16384 140.56 ->
-  //     138.10 (1024: 11.57 / 11.59);
-  //   8192 (8 waves, a 512-thread block): 16384 186.03 -> 179.87 (kept: 4096 45.41 / 45.72,
-  //     8192 89.74 / 89.84).
+  // fp32 tiles of 8 vectors (32 floats) per lane -- rows of 2048, 4096, 6144 or 8192 columns
+  // over 1-4 waves -- with rows enough for 32 waves per CU at half the vectors: twice the waves,
+  // 4 vectors per lane.  LayerNorm / RMSNorm from 64 rows per CU at 8192 columns, LN + GELU from
+  // 32; residual + LayerNorm / RMSNorm up to 6144 columns and from 64 waves per CU; not the fp8
+  // outputs (tied: LN -> fp8 8192 x 4096 31.2 / 30.9, 16384 x 2048 30.8 / 30.8).  us, rows x
+  // columns, 8 -> 4 vectors per lane:
+  //   LayerNorm: 4096 x 2048 14.06 -> 13.27, 8192 x 2048 24.48 -> 23.87, 16384 x 2048 46.15 ->
+  //     44.54; 2048 x 4096 14.08 -> 13.68, 4096 x 4096 24.53 -> 24.14, 8192 x 4096 45.28 ->
+  //     44.77, 16384 x 4096 89.89 -> 87.45; 2048 x 6144 19.78 -> 19.36, 4096 x 6144 36.07 ->
+  //     35.63, 8192 x 6144 69.80 -> 68.79, 16384 x 6144 140.56 -> 138.10; 16384 x 8192 (8
+  //     waves, a 512-thread block) 186.03 -> 179.87.  Kept: 1024 x 2048 5.13 / 5.41, 2048 x
+  //     2048 7.22 / 7.76, 1024 x 4096 7.42 / 7.94, 1024 x 6144 11.57 / 11.59, 4096 x 8192
+  //     45.41 / 45.72, 8192 x 8192 89.74 / 89.84.
+  //   LN + GELU tanh / erf: 2048 x 4096 14.94 -> 13.78 / 14.70 / 14.77, 8192 x 4096 46.25 ->
+  //     45.10 / 50.93 -> 47.13, 4096 x 2048 erf 15.99 -> 14.69, 2048 x 6144 tanh 20.01 ->
+  //     19.82, 8192 x 8192 erf 98.00 -> 91.22, 16384 x 8192 tanh 186.83 -> 179.58.
+  //   Residual + LayerNorm: 8192 x 4096 94.99 -> 88.68, 16384 x 2048 94.67 -> 90.28.  Kept:
+  //     2048 x 4096 25.11 / 24.36 and 2048 x 6144 36.02 / 35.28 (gains below 64 waves per CU),
+  //     4096 x 2048 23.75 / 24.22, 16384 x 8192 406.3 / 443.6 (8 waves).
   // The halved tiles hold 64 bytes of the row per lane, as the 16-bit 4-vector tiles do; those
   // lose when halved (bf16 65536 x 2048 86.7 -> 98.4, 32768 x 4096 87.6 -> 99.2; LN -> fp8
   // 32768 x 4096 68.3 -> 80.2).
-  if (VV == 4 && vec_ok && !g.loop && !has_res && gelu == 0 && FP8 == 0 && tun.fwd_wpr <= 0 &&
-      tun.fwd_epl <= 0 && g.exact && g.vpl == 8 && g.wpr <= 4 &&
-      rows * 2 * g.wpr >= 32 * cus && (g.wpr <= 3 || rows >= 64 * cus)) {
-    g.wpr *= 2;
-    g.vpl = 4;
-    g.threads = (4 % g.wpr == 0) ? 256 : kWave * g.wpr;
+  if (VV == 4 && vec_ok && !g.loop && FP8 == 0 && tun.fwd_wpr <= 0 && tun.fwd_epl <= 0 &&
+      g.exact && g.vpl == 8 && g.wpr <= 4) {
+    const int64_t halved_waves = rows * 2 * g.wpr;
+    const bool take = has_res ? g.wpr <= 3 && halved_waves >= 64 * cus
+                              : halved_waves >= 32 * cus &&
+                                    (g.wpr <= 3 || rows >= (gelu != 0 ? 32 : 64) * cus);
+    if (take) {
+      g.wpr *= 2;
+      g.vpl = 4;
+      g.threads = (4 % g.wpr == 0) ? 256 : kWave * g.wpr;
+    }
   }
   // fp32 LayerNorm / RMSNorm rows of 8192 columns with 2-8 rows per CU (the reference's
   // large-row table has 1024 x 8192): 16 waves x 2 vectors per lane in a 1024-thread block, two

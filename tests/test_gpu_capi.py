@@ -940,6 +940,68 @@ def test_fp32_halved_vector_tiles(lib, capfd, monkeypatch, rms, rows, cols, tile
     assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
 
 
+FP32_HALVED_FLAVOURS = [("add_ln", 8192, 4096, (4, 4, 256)), ("add_ln", 16384, 2048, (2, 4, 256)),
+                        ("add_ln", 9001, 4096, (4, 4, 256)),
+                        ("gelu_tanh", 2048, 4096, (4, 4, 256)),
+                        ("gelu_none", 3001, 4096, (4, 4, 256)),
+                        ("gelu_tanh", 2048, 6144, (6, 4, 384)),
+                        ("gelu_none", 8192, 8192, (8, 4, 512))]
+
+
+@pytest.mark.parametrize("kind,rows,cols,tile", FP32_HALVED_FLAVOURS,
+                         ids=[f"{k}-{r}x{c}" for k, r, c, _ in FP32_HALVED_FLAVOURS])
+def test_fp32_halved_vector_tiles_residual_and_gelu(lib, capfd, monkeypatch, kind, rows, cols,
+                                                     tile):
+    """The halved fp32 tiles (twice the waves at 4 vectors per lane) in the residual + LayerNorm
+    and LN + GELU flavours: the trace must show the tiling fln_forward_plan reports; h must be
+    bit-exact and y must match the oracle (max-abs 1e-5 of max(1, |y|))."""
+    import re
+    w, v, t = tile
+    form = kind[5:] if kind.startswith("gelu") else None
+    plan = fl_functional().get_optimal_config(rows, cols, torch.float32, approximate=form,
+                                              residual=kind == "add_ln")
+    if (plan["waves_per_row"], plan["vectors_per_lane"]) != (w, v):
+        assert torch.cuda.get_device_properties(0).multi_processor_count != 256, plan
+        pytest.skip("the tiling is planned for another CU count")
+    gen = torch.Generator().manual_seed(rows * 7 + cols)
+    xc = torch.randn(rows, cols, generator=gen) * 1.5 + 0.25
+    rc = torch.randn(rows, cols, generator=gen)
+    gc = 1 + 0.1 * torch.randn(cols, generator=gen)
+    bc = 0.1 * torch.randn(cols, generator=gen)
+    x, r, g, b = cuda(xc), cuda(rc), cuda(gc), cuda(bc)
+    p = capi.ptr
+    y = torch.empty_like(x)
+    h = torch.empty_like(x)
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
+    if kind == "add_ln":
+        capi.check(lib.fln_add_layernorm_forward(p(x), p(r), p(g), p(b), p(h), p(y), p(mean),
+                                                 p(rstd), rows, cols, capi.F32, 1e-5,
+                                                 capi.stream()))
+    else:
+        capi.check(lib.fln_layernorm_gelu_forward(
+            p(x), p(g), p(b), p(y), p(mean), p(rstd), rows, cols, capi.F32, 1e-5,
+            capi.GELU_TANH if form == "tanh" else capi.GELU_ERF, capi.stream()))
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
+    trace = re.findall(r"-> (\S+) wpr=(\d+) vpl=(\d+) exact=(\d+) threads=(\d+)",
+                       capfd.readouterr().err)
+    assert trace == [("registers", str(w), str(v), "1", str(t))], trace
+    xs, rs, gs, bs = f32(xc), f32(rc), f32(gc), f32(bc)
+    if kind == "add_ln":
+        assert torch.equal(h.cpu(), xc + rc), "h bit-exact"
+        y_ref, _, _, r_ref = norms.add_layer_norm_fwd(xs, rs, gs, bs, 1e-5, "f32")
+    else:
+        y_ref = norms.layer_norm_gelu_fwd(xs, gs, bs, 1e-5, form)
+        _, _, r_ref = norms.layer_norm_fwd(xs, None, None, 1e-5)
+    assert np.abs(to_np(y) - y_ref).max() <= 1e-5 * max(1.0, np.abs(y_ref).max())
+    assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5
+
+
 BWD_EXACT_GROUPS = [("ln", torch.bfloat16, 4608), ("rms", torch.bfloat16, 5120),
                     ("ln_dres", torch.float16, 5632), ("gelu_tanh", torch.bfloat16, 6144),
                     ("gelu_none", torch.float16, 4608), ("ln", torch.float16, 6144)]

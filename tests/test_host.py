@@ -464,9 +464,19 @@ def test_optimal_config_reports_dispatch_geometry():
             (8192, 8192): (4, 8, True, 256)}
     for (rows, cols), tile in kept.items():
         assert w7(rows, cols, torch.float32) == tile, (rows, cols)
-    assert w7(2048, 4096, torch.float32, residual=True)[:2] == (2, 8)
-    assert w7(2048, 4096, torch.float32, approximate="tanh")[:2] == (2, 8)
+    # Residual flavours from 64 waves per CU at half the vectors and up to 6144 columns; LN +
+    # GELU like LayerNorm but from 32 rows per CU at 8192 columns; fp8 outputs keep 8 vectors.
+    res = {(8192, 4096): (4, 4), (16384, 2048): (2, 4), (2048, 4096): (2, 8),
+           (4096, 2048): (1, 8), (16384, 8192): (4, 8)}
+    for (rows, cols), wv in res.items():
+        assert w7(rows, cols, torch.float32, residual=True)[:2] == wv, (rows, cols)
+    for form in ("tanh", "none"):
+        assert w7(2048, 4096, torch.float32, approximate=form) == (4, 4, True, 256)
+        assert w7(8192, 8192, torch.float32, approximate=form) == (8, 4, True, 512)
+        assert w7(4096, 8192, torch.float32, approximate=form)[:2] == (4, 8)
+        assert w7(1024, 4096, torch.float32, approximate=form)[:2] == (2, 8)
     assert w7(2048, 4096, torch.float32, fp8=1)[:2] == (2, 8)
+    assert w7(16384, 2048, torch.float32, fp8=1)[:2] == (1, 8)
     assert w7(4096, 2048, torch.float32, num_cus=512) == (1, 8, True, 256)
     # Residual flavours: 3 or 5 vectors per lane only, at the shapes each measured faster with.
     odd = lambda c: c[1] in (3, 5, 6, 7)  # noqa: E731
