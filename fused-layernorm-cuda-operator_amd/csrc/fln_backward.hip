@@ -1196,12 +1196,16 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   g.vec = (vec_ok && cols % vv == 0) ? vv : 1;
   const int64_t nvec = cols / g.vec;
   auto per_lane = [&](int w) { return (nvec + kWave * w - 1) / (kWave * w); };
-  // Elements per lane: 8 by default for 16-bit types, 4 for fp32 (x-hat, dy, g, gamma, both
-  // column accumulators and the prefetched raw rows of a lane's columns stay in registers;
-  // fp32 rows with 8 per lane exceed the 128-VGPR budget of a 1024-thread block and spill);
-  // more only for rows too wide for 16 waves.
+  // Elements per lane: 8 by default (x-hat, dy, g, gamma, both column accumulators and the
+  // prefetched raw rows of a lane's columns stay in registers: 84-98 VGPRs for fp32 rows at 2
+  // vectors per lane, one row in flight); more only for rows too wide for 16 waves.  fp32
+  // backward calls, us, 4 -> 8 elements per lane: 300 x 768 9.31 -> 8.81, 4096 x 768 13.79 ->
+  // 13.19, 16384 x 768 31.46 -> 30.26, 16384 x 1024 38.12 -> 37.68, 8192 x 2048 38.60 ->
+  // 38.13, 4096 x 3072 32.62 -> 31.06, 1024 x 4096 17.74 -> 17.14, 8192 x 4096 70.54 -> 69.36
+  // (RMSNorm 69.02 -> 67.77); 32 x 768 and 1024 x 1024 tied.  The fp32 scalar path (rows not
+  // whole 16-byte vectors) keeps 4.
   const Tuning& tun = tuning();
-  const int epl = tun.bwd_epl > 0 ? tun.bwd_epl : (es == 4 ? 4 : 8);
+  const int epl = tun.bwd_epl > 0 ? tun.bwd_epl : (es == 4 && g.vec == 1 ? 4 : 8);
   int cap = (epl >= g.vec ? epl : g.vec) / g.vec;
   if (cap > bwd_max_vpl(g.vec, es)) cap = bwd_max_vpl(g.vec, es);
   int wpr = 1;
