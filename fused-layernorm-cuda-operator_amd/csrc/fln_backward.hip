@@ -1223,6 +1223,20 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   if (es == 2 && g.vec == 8 && wpr == 16 && cap == 1 && nvec % kWave == 0 &&
       nvec / kWave >= 9 && nvec / kWave <= 12 && forced <= 0)
     wpr = static_cast<int>(nvec / kWave);
+  // 16-bit LayerNorm / RMSNorm rows whose one-vector tile leaves lanes masked (768, 1280, 1536,
+  // 2560, 3072, 3584, 7168 columns, ...), with at least 16 rows per CU: 2 vectors per lane over
+  // half the waves (one row in flight instead of two).  bf16 backward calls, us: 16384 x 768
+  // 20.31 -> 19.79 (RMSNorm 19.59 -> 18.70), 65536 x 768 54.83 -> 54.24, 16384 x 1280 28.12 ->
+  // 27.97, 16384 x 1536 31.91 -> 31.37 (fp16 32.20 -> 31.42), 4096 x 2560 20.03 -> 19.43, 8192
+  // x 2560 29.28 -> 28.67, 16384 x 3072 55.92 -> 54.63, 16384 x 3584 64.17 -> 63.19, 8192 x
+  // 7168 66.31 -> 65.93.  Whole power-of-two tiles keep one vector (16384 x 1024 23.07 / 23.74,
+  // 16384 x 2048 38.44 / 38.65, 8192 x 4096 39.84 / 40.50).
+  if (es == 2 && g.vec == 8 && cap == 1 && forced <= 0 && tun.bwd_epl <= 0 && !gelu && !dres &&
+      nvec % (static_cast<int64_t>(kWave) * wpr) != 0 && rows >= 16 * device_cu_count()) {
+    cap = 2;
+    wpr = 1;
+    while (per_lane(wpr) > cap && wpr < 16) wpr *= 2;
+  }
   g.reg_path = per_lane(wpr) <= cap;
   g.wpr = g.reg_path ? wpr : 16;
   g.vpl = g.reg_path ? next_pow2(static_cast<int>(per_lane(wpr))) : 0;

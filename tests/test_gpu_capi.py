@@ -1079,6 +1079,64 @@ def test_backward_exact_row_groups(lib, capfd, monkeypatch, kind, dtype, rows, c
         assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
 
 
+BWD_TWO_VECTORS = [("ln", torch.bfloat16, 4096, 768, (1, 2)),
+                   ("rms", torch.float16, 4096, 1536, (2, 2)),
+                   ("ln", torch.bfloat16, 8193, 1280, (2, 2)),
+                   ("rms", torch.bfloat16, 4100, 2560, (4, 2)),
+                   ("ln", torch.float16, 4096, 7168, (8, 2)),
+                   ("ln", torch.bfloat16, 4096, 1024, (2, 1)),
+                   ("ln", torch.bfloat16, 1000, 768, (2, 1))]
+
+
+@pytest.mark.parametrize("kind,dtype,rows,cols,tile", BWD_TWO_VECTORS,
+                         ids=[f"{k}-{str(d)[6:]}-{r}x{c}" for k, d, r, c, _ in BWD_TWO_VECTORS])
+def test_backward_two_vectors_on_masked_widths(lib, capfd, monkeypatch, kind, dtype, rows, cols,
+                                               tile):
+    """16-bit LayerNorm / RMSNorm backwards whose one-vector tile would leave lanes masked take 2
+    vectors per lane over half the waves once there are 16 rows per CU; whole power-of-two
+    tiles (1024 columns) and fewer rows (1000) keep one vector: the backward's trace must show
+    the tiling, and dx, dgamma, dbeta must meet the oracle's bar."""
+    import re
+    w, v = tile
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip(f"{cus} CUs: the row thresholds are for 256")
+    gen = torch.Generator().manual_seed(rows + 11 * cols)
+    xc = (torch.randn(rows, cols, generator=gen) + 0.2).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    x, dy, g, b = cuda(xc), cuda(dyc), cuda(gc), cuda(bc)
+    xs, dys, gs = f32(xc), f32(dyc), f32(gc)
+    eps = 1e-6 if kind == "rms" else 1e-5
+    if kind == "rms":
+        _, rstd = rms_forward(lib, x, g, eps)
+    else:
+        _, mean, rstd = ln_forward(lib, x, g, b, eps)
+    torch.cuda.synchronize()
+    capfd.readouterr()
+    monkeypatch.setenv("FLN_DEBUG_GEOMETRY", "1")
+    capi.reload_tuning()
+    if kind == "rms":
+        dx, dg = rms_backward(lib, dy, x, rstd, g)
+    else:
+        dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("FLN_DEBUG_GEOMETRY")
+    capi.reload_tuning()
+    trace = re.findall(r"fln backward: .* -> (\S+) wpr=(\d+) vpl=(\d+) threads=(\d+)",
+                       capfd.readouterr().err)
+    assert [t[:3] for t in trace] == [("registers", str(w), str(v))], trace
+    io = "bf16" if dtype == torch.bfloat16 else "f16"
+    if kind == "rms":
+        dx_ref, dg_ref = norms.rms_norm_bwd(dys, xs, gs, eps)
+    else:
+        dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, eps)
+        assert_close_rel(to_np(db), db_ref, 1e-4, "dbeta")
+    assert_dx(to_np(dx), dx_ref, _flavour_allowance(kind, xs, dys, gs), io, f"{kind} {cols} dx")
+    assert_close_rel(to_np(dg), dg_ref, 1e-4, "dgamma")
+
+
 WIDE_KINDS = ["ln", "rms", "add_ln", "add_rms", "gelu_none", "gelu_tanh", "ln_fp8", "rms_fp8",
               "add_rms_fp8", "ln_mx", "rms_mx", "add_rms_mx"]
 
