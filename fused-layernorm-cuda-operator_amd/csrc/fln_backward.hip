@@ -1230,7 +1230,9 @@ BwdGeometry backward_geometry(int64_t rows, int64_t cols, int dtype, bool vec_ok
   // 27.97, 16384 x 1536 31.91 -> 31.37 (fp16 32.20 -> 31.42), 4096 x 2560 20.03 -> 19.43, 8192
   // x 2560 29.28 -> 28.67, 16384 x 3072 55.92 -> 54.63, 16384 x 3584 64.17 -> 63.19, 8192 x
   // 7168 66.31 -> 65.93.  Whole power-of-two tiles keep one vector (16384 x 1024 23.07 / 23.74,
-  // 16384 x 2048 38.44 / 38.65, 8192 x 4096 39.84 / 40.50).
+  // 16384 x 2048 38.44 / 38.65, 8192 x 4096 39.84 / 40.50), and so do the GELU flavours, whose
+  // 2-vector tiles keep gamma / beta in LDS (16384 x 768 tanh 22.4 -> 25.1, 16384 x 3072 erf
+  // 63.4 -> 68.8).
   if (es == 2 && g.vec == 8 && cap == 1 && forced <= 0 && tun.bwd_epl <= 0 && !gelu && !dres &&
       nvec % (static_cast<int64_t>(kWave) * wpr) != 0 && rows >= 16 * device_cu_count()) {
     cap = 2;
