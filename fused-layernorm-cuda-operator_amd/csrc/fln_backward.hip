@@ -997,9 +997,10 @@ int launch_stage1_k(const BwdParams& p, int64_t blocks, int threads, hipStream_t
   // The GELU kernels fill their LDS table with one entry per thread.
   if (GELU != 0 && threads < kGeluTabN) return FLN_ERR_INVALID;
   if (resident) {
-    static std::atomic<int> per_cu[3][64];  // [threads / 512][device]
+    if (threads < kWave || threads > MAXT || threads % kWave != 0) return FLN_ERR_INVALID;
+    static std::atomic<int> per_cu[MAXT / kWave + 1][64];  // [waves per block][device]
     const int dev = current_device();
-    std::atomic<int>& slot = per_cu[threads / 512][dev];
+    std::atomic<int>& slot = per_cu[threads / kWave][dev];
     int v = slot.load(std::memory_order_relaxed);
     if (v == 0) {
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, threads, 0) != hipSuccess ||

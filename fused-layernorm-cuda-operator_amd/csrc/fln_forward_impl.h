@@ -1092,30 +1092,36 @@ inline int next_pow2(int v) {
   return p;
 }
 
-// Blocks of `kernel` that fit on the current device at once.
+// Blocks of `kernel` in `threads`-thread blocks that fit on the current device at once; the
+// per-CU count is cached per device in `cache_per_device` (threads may race to fill a slot: they
+// store the same value).
 template <class K>
-int64_t resident_blocks(K kernel, int threads, int* cache_per_device) {
+int64_t resident_blocks(K kernel, int threads, std::atomic<int>* cache_per_device) {
   const int dev = current_device();
-  if (cache_per_device[dev] == 0) {
-    int per_cu = 0;
+  int per_cu = cache_per_device[dev].load(std::memory_order_relaxed);
+  if (per_cu == 0) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
         per_cu < 1)
       per_cu = 1;
-    cache_per_device[dev] = per_cu;
+    cache_per_device[dev].store(per_cu, std::memory_order_relaxed);
   }
-  return static_cast<int64_t>(cache_per_device[dev]) * device_cu_count();
+  return static_cast<int64_t>(per_cu) * device_cu_count();
 }
 
 template <class T, int FP8, bool RES, int GELU, int VEC, int VPL, bool EXACT, int MAXT>
 int launch_reg_t(const FwdParams& p, int threads, hipStream_t s) {
   // The exact-GELU kernels fill their LDS table with one entry per thread.
   if (GELU == 1 && threads < kGeluLogTabN) return FLN_ERR_INVALID;
+  if (p.wpr < 1 || threads < kWave * p.wpr || threads > MAXT || threads % kWave != 0)
+    return FLN_ERR_INVALID;
   const int rows_per_block = threads / (kWave * p.wpr);
   const int64_t row_blocks = (p.rows + rows_per_block - 1) / rows_per_block;
   auto kernel = fwd_reg_kernel<T, FP8, RES, GELU, VEC, VPL, EXACT, MAXT>;
-  static int occupancy_cache[2][64];  // per instantiation; [threads == MAXT][device]
+  // Per instantiation, [waves per block][device]: one instantiation runs with several block
+  // sizes (a 1024-thread one with 5-16 waves per row, one row per block).
+  static std::atomic<int> occupancy_cache[MAXT / kWave + 1][64];
   const int64_t cus = device_cu_count();
-  const int64_t resident = resident_blocks(kernel, threads, occupancy_cache[threads == MAXT]);
+  const int64_t resident = resident_blocks(kernel, threads, occupancy_cache[threads / kWave]);
   // Blocks per CU: the fewest whose rows in flight move enough bytes per CU to cover the per-row
   // latency (loads in flight, reductions, barriers): rows dealt to the CU at once x PD rows of
   // loads ahead x the bytes each row moves >= 32 KiB for one-wave rows (no barrier), 56 KiB for
@@ -1678,7 +1684,7 @@ inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
 template <class T, int FP8, int VEC>
 int launch_wide(const FwdParams& p, hipStream_t s) {
   auto launch = [&](auto kernel) {
-    static int occupancy_cache[64];  // per instantiation, per device
+    static std::atomic<int> occupancy_cache[64];  // per instantiation, per device
     int64_t grid = resident_blocks(kernel, kFwdWideThreads, occupancy_cache);
     const int forced = tuning().fwd_grid_mult;  // FLN_FWD_GRID_MULT: blocks per CU
     if (forced > 0 && grid > forced * device_cu_count()) grid = forced * device_cu_count();
