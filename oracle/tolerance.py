@@ -1,4 +1,4 @@
-"""Error model of an fp32 evaluation of the normalization backward (test infrastructure only).
+"""Error model of fp32 evaluations of the normalizations, forward and backward (tests only).
 
 The parity bar for dx is "within one ulp of the output type of the float64 reference" plus, per
 element, what an fp32 evaluation of the same formula cannot avoid.  dx cancels:
@@ -17,8 +17,10 @@ than itself.  `dx_allowance` bounds that rounding element by element, from the f
              + 2^-21 log2 N (mean|g| + |xhat| mean|g xhat|)            the row sums c1, c2
              + (|c2| + |xhat| mean|g|) e_x                              xhat's centring, e_x =
                                                                           2^-23 log2 N rstd mean|x|
-             + 2^-21 (|dy gamma| + mean|dy gamma| + |xhat| mean|dy gamma xhat|)   GELU' (tables
-                                                                          within 2.1e-7) ]
+             + (2^-21 + 0.8 max|gamma| e_x)                                     GELU' (tables
+                 (|dy gamma| + mean|dy gamma| + |xhat| mean|dy gamma xhat|)     within 2.1e-7;
+                                                                          |GELU''| <= 0.8 times
+                                                                          a's centring error) ]
     + 2^-23 |dres|                                                     the residual gradient add
 
 Every coefficient is an fp32 rounding count, not a fraction of max|dx|: an evaluation that rounds
@@ -26,6 +28,18 @@ g = dy gamma, xhat or dx to bf16 before the last step (relative error 2^-9) exce
 orders of magnitude.  tests/test_oracle.py checks the model on the CPU against an fp32 evaluation
 of the formula (it must cover that) and against planted bf16 roundings of g and xhat (it must
 reject them).
+
+The forward output y = xhat gamma + beta cancels too, where xhat gamma and beta nearly cancel,
+and there it also carries the rounding of the fp32 row mean, which shifts every xhat of the row:
+`y_allowance` is
+
+    2^-21 (|xhat gamma| + |beta|)          the affine step's own roundings (8 fp32 ulps)
+    + |gamma| e_x                          LayerNorm: xhat's centring, e_x as above
+
+times 1.13 (the largest |GELU'|) for LN + GELU.  torch's own fp32 layer_norm on the CPU needs
+this term as much as the kernels do (bf16 h = x + r, 416 columns: an element at -4.6e-9 comes
+out 9.6e-9 off from torch, 6.1e-9 from the kernel); tests/test_oracle.py checks that fp32
+evaluations stay within it and that a mean rounded to bf16 does not.
 """
 from __future__ import annotations
 
@@ -88,13 +102,44 @@ def dx_allowance(x, dy, gamma=None, eps=1e-5, rms=False, beta=None, approximate=
         a_ = (2.0 ** -20 + 2.0 ** -23 * lg) * terms + 2.0 ** -21 * lg * sums + \
             (np.abs(c2) + np.abs(xh) * np.abs(g).mean(axis=1, keepdims=True)) * e_x
         if approximate is not None:
-            a_ = a_ + 2.0 ** -21 * (np.abs(dg) + np.abs(dg).mean(axis=1, keepdims=True) +
-                                    np.abs(xh) * np.abs(dg * xh).mean(axis=1, keepdims=True))
+            # GELU'(a) off by the tables' error and by GELU'' (at most 0.8) times the centring
+            # error of a = xhat gamma + beta.
+            dgp = 2.0 ** -21 + 0.8 * np.abs(g64).max() * e_x
+            a_ = a_ + dgp * (np.abs(dg) + np.abs(dg).mean(axis=1, keepdims=True) +
+                             np.abs(xh) * np.abs(dg * xh).mean(axis=1, keepdims=True))
         out[r0:r0 + chunk] = rstd * a_
     out = out.reshape(x.shape)
     if dres is not None:
         out = out + 2.0 ** -23 * np.abs(_f64(dres))
     return out
+
+
+def y_allowance(x, gamma=None, beta=None, eps=1e-5, rms=False, approximate=None,
+                chunk=2048) -> np.ndarray:
+    """Elementwise fp32 evaluation allowance of the forward output y (module docstring), float64,
+    x's shape: 2^-21 (|xhat gamma| + |beta|) + |gamma| e_x (LayerNorm), times 1.13 with a GELU
+    epilogue (`approximate` "none" / "tanh")."""
+    x = np.asarray(x)
+    n = x.shape[-1]
+    x2 = x.reshape(-1, n)
+    out = np.empty(x2.shape, np.float64)
+    g64 = np.ones(n) if gamma is None else _f64(gamma).reshape(n)
+    b64 = np.zeros(n) if beta is None else _f64(beta).reshape(n)
+    lg = np.log2(max(n, 2))
+    for r0 in range(0, x2.shape[0], chunk):
+        xs = x2[r0:r0 + chunk].astype(np.float64)
+        if rms:
+            rstd = 1.0 / np.sqrt((xs * xs).mean(axis=1, keepdims=True) + eps)
+            xh = xs * rstd
+            e_x = 0.0
+        else:
+            mu = xs.mean(axis=1, keepdims=True)
+            rstd = 1.0 / np.sqrt(((xs - mu) ** 2).mean(axis=1, keepdims=True) + eps)
+            xh = (xs - mu) * rstd
+            e_x = 2.0 ** -23 * lg * rstd * np.abs(xs).mean(axis=1, keepdims=True)
+        al = 2.0 ** -21 * (np.abs(xh * g64) + np.abs(b64)) + np.abs(g64) * e_x
+        out[r0:r0 + chunk] = al * (1.13 if approximate is not None else 1.0)
+    return out.reshape(x.shape)
 
 
 def within_stats(got, ref, allowance, kind: str) -> dict:

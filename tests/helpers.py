@@ -91,14 +91,16 @@ def fp8_ambiguous(t, rel=2.0 ** -20):
     return norms.fp8_e4m3fn_encode(t * (1 - rel)) != norms.fp8_e4m3fn_encode(t * (1 + rel))
 
 
-def assert_fp8_close(q_got, s_got, q_ref, s_ref, what="", t_ref=None):
-    """fp8 output bar: per-row scales within 1e-6 relative; codes identical except +-1 code on
-    at most 0.1% of the elements.  With t_ref (the reference's unquantized scaled values), a
-    +-1 code at an element within fp32 noise of a rounding midpoint (fp8_ambiguous) does not
-    count against the 0.1%."""
+def assert_fp8_close(q_got, s_got, q_ref, s_ref, what="", t_ref=None, s_atol=None):
+    """fp8 output bar: per-row scales within 1e-6 relative (plus s_atol per row where given: the
+    fp32 evaluation allowance of the row maximum over 448, for rows whose statistics are
+    ill-conditioned); codes identical except +-1 code on at most 0.1% of the elements.  With
+    t_ref (the reference's unquantized scaled values), a +-1 code at an element within fp32 noise
+    of a rounding midpoint (fp8_ambiguous) does not count against the 0.1%."""
     s_got = np.asarray(s_got, np.float64)
     s_ref = np.asarray(s_ref, np.float64)
-    rel = np.abs(s_got - s_ref) / np.where(s_ref > 0, s_ref, 1.0)
+    err = np.abs(s_got - s_ref) - (0.0 if s_atol is None else np.asarray(s_atol, np.float64))
+    rel = np.maximum(err, 0.0) / np.where(s_ref > 0, s_ref, 1.0)
     assert rel.max() <= 1e-6, f"{what}: scale rel err {rel.max():.3g}"
     diff = np.abs(fp8_ordinal(q_got) - fp8_ordinal(q_ref))
     assert int(diff.max()) <= 1, f"{what}: a code differs by {int(diff.max())} steps"

@@ -439,3 +439,101 @@ def test_dx_allowance_gelu_covers_an_approximate_derivative(approximate):
     got = _fp32_dx(x, (dy * d).astype(np.float32), g, 1e-5, False)
     al = tolerance.dx_allowance(x, dy, g, 1e-5, beta=b, approximate=approximate)
     assert (np.abs(got - ref) <= tolerance.ulp(ref, "bf16") + al).all()
+    # Rows with ill-conditioned statistics (fp32 pairs with small spreads around large means):
+    # GELU' taken at the GELU input of an fp32 forward, whose xhat carries the fp32 mean's
+    # centring error, amplified by rstd in dx.  Without the allowance's GELU'' term this fails.
+    m = rng.uniform(-3, 3, (512, 1))
+    dd = 10.0 ** rng.uniform(-4, -1, (512, 1))
+    x2 = np.concatenate([m + dd, m - dd], axis=1).astype(np.float32)
+    dy2 = rng.standard_normal((512, 2)).astype(np.float32)
+    g2 = (1 + 0.1 * rng.standard_normal(2)).astype(np.float32)
+    b2 = (0.2 * rng.standard_normal(2)).astype(np.float32)
+    ref2, _, _ = norms.layer_norm_gelu_bwd(dy2, x2, g2, b2, 1e-5, approximate)
+    a32 = _fp32_y(x2, g2, b2, 1e-5)
+    got2 = _fp32_dx(x2, (dy2 * norms.gelu_grad(a32, approximate)).astype(np.float32), g2, 1e-5,
+                    False, out="f32")
+    al2 = tolerance.dx_allowance(x2, dy2, g2, 1e-5, beta=b2, approximate=approximate)
+    assert (np.abs(got2 - ref2) <= tolerance.ulp(ref2, "f32") + al2).all()
+
+
+# ------------------------------------------------------------------------------------------------
+# The forward error model (oracle.tolerance.y_allowance) used by the GPU parity bar for y.
+# ------------------------------------------------------------------------------------------------
+def _fp32_y(x, gamma, beta, eps, order="pairwise", round_mean=False, approximate=None):
+    """An fp32 two-pass LayerNorm (+ GELU) evaluation, y in fp32: row sums pairwise (numpy) or
+    as running sums of 64 elements per lane then a tree (the kernels' shape); optionally the
+    mean rounded to bf16 (a planted loss of precision)."""
+    f = np.float32
+    x32, g32, b32 = x.astype(f), gamma.astype(f), beta.astype(f)
+    n = x.shape[-1]
+
+    def rowsum(a):
+        if order == "pairwise" or a.shape[1] % 64:
+            return a.sum(axis=1, keepdims=True, dtype=f)
+        part = np.cumsum(a.reshape(a.shape[0], -1, 64), axis=2, dtype=f)[:, :, -1]
+        return part.sum(axis=1, keepdims=True, dtype=f)
+
+    mu = (rowsum(x32) / f(n)).astype(f)
+    if round_mean:
+        mu = norms.round_to_bf16(mu).astype(f)
+    rs = (f(1) / np.sqrt(rowsum((x32 - mu) ** 2) / f(n) + f(eps))).astype(f)
+    a = (((x32 - mu) * rs).astype(f) * g32 + b32).astype(f)
+    if approximate is None:
+        return a.astype(np.float64)
+    return torch.nn.functional.gelu(torch.from_numpy(a), approximate=approximate).double().numpy()
+
+
+def _y_cases():
+    """Rows where y cancels or the statistics are ill-conditioned: bf16 h = x + r with an offset
+    mean at 416 and 22784 columns (the widths where an extended GPU sweep met the old bar's
+    limit), fp32 pairs and f16 triples with small spreads around large means."""
+    rng = np.random.RandomState(17)
+    to_bf16, to_f16 = norms.round_to_bf16, norms.round_to_f16
+    out = []
+    for rows, cols in ((512, 416), (8, 22784)):
+        h = to_bf16(to_bf16(rng.standard_normal((rows, cols)) * 1.5 + 0.25) +
+                    to_bf16(rng.standard_normal((rows, cols))))
+        out.append(("bf16 h", h, to_bf16(1 + 0.1 * rng.standard_normal(cols)),
+                    to_bf16(0.1 * rng.standard_normal(cols))))
+    m = rng.uniform(-3, 3, (512, 1))
+    d = 10.0 ** rng.uniform(-4, -1, (512, 1))
+    out.append(("f32 pairs", np.concatenate([m + d, m - d], axis=1).astype(np.float32),
+                (1 + 0.1 * rng.standard_normal(2)).astype(np.float32),
+                (0.1 * rng.standard_normal(2)).astype(np.float32)))
+    x3 = to_f16(rng.uniform(-3, 3, (512, 1)) + 1e-3 * rng.standard_normal((512, 3)))
+    out.append(("f16 triples", x3, to_f16(1 + 0.1 * rng.standard_normal(3)),
+                to_f16(0.1 * rng.standard_normal(3))))
+    return out
+
+
+@pytest.mark.parametrize("approximate", [None, "none", "tanh"], ids=["ln", "gelu-erf", "gelu-tanh"])
+def test_y_allowance_covers_fp32_evaluations_and_rejects_a_bf16_mean(approximate):
+    """The forward bar (1 ulp + oracle.tolerance.y_allowance) holds for fp32 two-pass
+    evaluations -- numpy with pairwise or per-lane-then-tree row sums, and torch's own fp32
+    F.layer_norm on the CPU -- on rows where y cancels and rows with ill-conditioned statistics
+    (fp32 pairs, f16 triples with small spreads); and it rejects the evaluation whose mean is
+    rounded to bf16."""
+    from oracle import tolerance
+    for what, x, g, b in _y_cases():
+        eps = 1e-5
+        ref = norms.layer_norm_fwd(x, g, b, eps)[0]
+        if approximate is not None:
+            ref = norms.gelu(ref, approximate)
+        al = tolerance.y_allowance(x, g, b, eps, approximate=approximate)
+        bound = tolerance.ulp(ref, "f32") + al
+        for order in ("pairwise", "lanes"):
+            got = _fp32_y(x, g, b, eps, order=order, approximate=approximate)
+            assert (np.abs(got - ref) <= bound).all(), (what, order)
+        t = torch.nn.functional.layer_norm(torch.from_numpy(x.astype(np.float32)),
+                                           (x.shape[-1],), torch.from_numpy(g.astype(np.float32)),
+                                           torch.from_numpy(b.astype(np.float32)), eps)
+        if approximate is not None:
+            t = torch.nn.functional.gelu(t, approximate=approximate)
+        assert (np.abs(t.double().numpy() - ref) <= bound).all(), (what, "torch")
+        planted = _fp32_y(x, g, b, eps, round_mean=True, approximate=approximate)
+        assert (np.abs(planted - ref) > bound).any(), (what, "bf16 mean")
+    # Away from cancellation the allowance is a small fraction of a bf16 ulp.
+    x, g, b = _y_cases()[0][1:]
+    ref = norms.layer_norm_fwd(x, g, b, 1e-5)[0]
+    al = tolerance.y_allowance(x, g, b, 1e-5)
+    assert np.median(al / tolerance.ulp(ref, "bf16")) < 0.01
