@@ -2390,13 +2390,14 @@ def test_reference_epsilon_1e12(lib, scenario, dtype):
         assert_within_ulp(to_np(y), ref, 1.0, what=f"{scenario} eps=1e-12 y")
 
 
-def _random_cases(n=120, seed=20261202):
+def _random_cases(n=240, seed=20261202):
     """Seeded shapes for test_random_shapes_against_the_oracle: the flavour cycles, the dtype is
     drawn, rows are log-uniform in 1..16384 and columns log-uniform in 1..70000; a third of the
     widths are rounded down to whole 16-byte vectors (of the 16-bit types), a third to 32-element
     blocks, the rest stay as drawn (the scalar path); at most 4 M elements per case."""
     rng = np.random.default_rng(seed)
-    kinds = ["ln", "rms", "gelu_tanh", "gelu_none", "add_ln", "ln_fp8", "add_rms_mx"]
+    kinds = ["ln", "rms", "gelu_tanh", "gelu_none", "add_ln", "ln_fp8", "add_rms_mx", "ln_dres",
+             "add_rms", "rms_fp8", "add_ln_fp8", "ln_mx"]
     cases = []
     for i in range(n):
         kind = kinds[i % len(kinds)]
@@ -2404,7 +2405,7 @@ def _random_cases(n=120, seed=20261202):
         rows = int(np.exp(rng.uniform(0.0, np.log(16384.0))))
         cols = int(np.exp(rng.uniform(0.0, np.log(70000.0))))
         shape = int(rng.integers(3))
-        if kind == "add_rms_mx" or shape == 1:
+        if kind in ("add_rms_mx", "ln_mx") or shape == 1:
             cols = max(32, cols // 32 * 32)
         elif shape == 0:
             cols = max(8, cols // 8 * 8)
@@ -2422,9 +2423,10 @@ RANDOM_CASES = _random_cases()
 def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
     """Seeded random shapes through whatever route the dispatcher picks for them (register
     tiles, odd tiles, LDS-staged, split, streamed, scalar path; the register, LDS and two-pass
-    backwards): LayerNorm, RMSNorm and LN + GELU (both forms) forward and backward, residual +
-    LayerNorm, LN -> fp8 and residual + RMSNorm -> MXFP8 forwards, each against the oracle's
-    bar for its dtype."""
+    backwards): LayerNorm, RMSNorm and LN + GELU (both forms) forward and backward, the
+    LayerNorm backward with a residual gradient, residual + LayerNorm / RMSNorm, LN -> fp8,
+    RMSNorm -> fp8, residual + LN -> fp8, LN -> MXFP8 and residual + RMSNorm -> MXFP8 forwards,
+    each against the oracle's bar for its dtype."""
     gen = torch.Generator().manual_seed(rows * 65537 + cols)
     xc = (torch.randn(rows, cols, generator=gen) * 1.5 + 0.25).to(dtype)
     rc = torch.randn(rows, cols, generator=gen).to(dtype)
@@ -2449,13 +2451,15 @@ def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
     def check_h(h):
         assert np.array_equal(to_np(h), to_np(xc + rc)), what + " h bit-exact"
 
-    if kind == "ln":
+    if kind in ("ln", "ln_dres"):
         y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
-        dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+        dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g, dres=r if kind == "ln_dres" else None)
         y_ref, m_ref, r_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)
         check_y(y, y_ref, xs)
         assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5, what + " rstd"
         dx_ref, dg_ref, db_ref = norms.layer_norm_bwd(dys, xs, gs, 1e-5)
+        if kind == "ln_dres":
+            dx_ref = dx_ref + rs
     elif kind == "rms":
         y, rstd = rms_forward(lib, x, g, 1e-6)
         dx, dg = rms_backward(lib, dy, x, rstd, g)
@@ -2494,6 +2498,44 @@ def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
         check_y(y, y_ref, h_ref)
         assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5, what + " rstd"
         return
+    elif kind == "add_rms":
+        h = torch.empty_like(x)
+        y = torch.empty_like(x)
+        rstd = torch.empty(rows, device="cuda")
+        capi.check(lib.fln_add_rmsnorm_forward(p(x), p(r), p(g), p(h), p(y), p(rstd), rows, cols,
+                                               code, 1e-6, capi.stream()))
+        check_h(h)
+        y_ref, h_ref, r_ref = norms.add_rms_norm_fwd(xs, rs, gs, 1e-6, io)
+        check_y(y, y_ref, h_ref, bias=False)
+        assert np.abs(to_np(rstd) / r_ref - 1).max() <= 1e-5, what + " rstd"
+        return
+    elif kind in ("rms_fp8", "add_ln_fp8"):
+        q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+        s = torch.empty(rows, device="cuda")
+        if kind == "rms_fp8":
+            capi.check(lib.fln_rmsnorm_fp8_forward(p(x), p(g), p(q), p(s), None, rows, cols, code,
+                                                   1e-6, capi.stream()))
+            q_ref, s_ref = c_oracle.rmsnorm_fp8(xs, gs, 1e-6)
+            t_ref = _scaled(norms.rms_norm_fwd(xs, gs, 1e-6)[0])
+            s_atol = None
+        else:
+            h = torch.empty_like(x)
+            capi.check(lib.fln_add_layernorm_fp8_forward(p(x), p(r), p(g), p(b), p(h), p(q), p(s),
+                                                         None, None, rows, cols, code, 1e-5,
+                                                         capi.stream()))
+            check_h(h)
+            q_ref, s_ref, h_ref = norms.add_layer_norm_fp8_fwd(xs, rs, gs, bs, 1e-5, io)
+            t_ref = _scaled(norms.layer_norm_fwd(h_ref, gs, bs, 1e-5)[0])
+            s_atol = affine_atol(h_ref, gs, bs, 1e-5).max(axis=1) / 448.0
+        assert_fp8_close(q.cpu().numpy(), to_np(s), q_ref, s_ref, what, t_ref=t_ref, s_atol=s_atol)
+        return
+    elif kind == "ln_mx":
+        q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+        sc = torch.empty(rows, cols // 32, device="cuda", dtype=torch.uint8)
+        capi.check(_mx_call(lib, "ln", x, r, g, b, q, sc, None, rows, cols, code))
+        q_ref, sc_ref, y_ref = _mx_ref("ln", xs, rs, gs, bs, io)
+        assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, sc_ref, y_ref, what)
+        return
     elif kind == "ln_fp8":
         q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
         s = torch.empty(rows, device="cuda")
@@ -2513,7 +2555,7 @@ def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
         q_ref, sc_ref, y_ref = _mx_ref("add_rms", xs, rs, gs, bs, io)
         assert_mx_close(q.cpu().numpy(), sc.cpu().numpy(), q_ref, sc_ref, y_ref, what)
         return
-    assert_dx(to_np(dx), dx_ref, _flavour_allowance(kind, xs, dys, gs, bs), io, what + " dx")
+    assert_dx(to_np(dx), dx_ref, _flavour_allowance(kind, xs, dys, gs, bs, rs), io, what + " dx")
     assert_close_rel(to_np(dg), dg_ref, 1e-4, what + " dgamma")
     if db_ref is not None:
         assert_close_rel(to_np(db), db_ref, 1e-4, what + " dbeta")
