@@ -91,6 +91,10 @@ def parse():
     ap.add_argument("--traffic-configs", action="store_true",
                     help="instead of the bench line: HBM traffic (two rocprofv3 counter passes "
                          "each) and call times of every bandwidth-bound config (C3..C7, LN+GELU)")
+    ap.add_argument("--large-rows-only", action="store_true",
+                    help="instead of the bench line: only the reference's large-row table "
+                         "(reference_paths.large_rows_fp32), one JSON line; used for its "
+                         "kernel profile")
     return ap.parse_args()
 
 
@@ -1104,6 +1108,11 @@ def main():
         return
     if args.traffic_configs:
         traffic_configs(args)
+        return
+    if args.large_rows_only:
+        import torch
+        assert torch.cuda.is_available(), "bench.py needs a GPU"
+        print(json.dumps({"large_rows_fp32": large_rows(torch)}), flush=True)
         return
 
     # Counter passes first, in child processes, before this process touches the GPU.
