@@ -27,13 +27,17 @@ def f16_ulp(ref: np.ndarray) -> np.ndarray:
 
 def assert_within_ulp(got, ref, ulps: float = 1.0, atol: float = 0.0, kind: str = "bf16",
                       what: str = ""):
-    """|got - ref| <= ulps * ulp_kind(ref) + atol, elementwise."""
+    """|got - ref| <= ulps * ulp_kind(ref) + atol, elementwise.  For the 1-ulp bar the share of
+    the bound used is appended to $FLN_PARITY_REPORT when that is set."""
     g = np.asarray(got, np.float64)
     r = np.asarray(ref, np.float64)
     ulp = bf16_ulp(r) if kind == "bf16" else f16_ulp(r)
     err = np.abs(g - r)
     bound = ulps * ulp + atol
     bad = err > bound
+    if ulps == 1.0:
+        from oracle import tolerance
+        tolerance.report(what, tolerance.within_stats(g, r, atol, kind))
     if bad.any():
         i = np.unravel_index(np.argmax(err - bound), err.shape)
         extra = f"{atol:g}" if np.ndim(atol) == 0 else "elementwise atol"
