@@ -2394,7 +2394,8 @@ def _random_cases(n=240, seed=20261202):
     """Seeded shapes for test_random_shapes_against_the_oracle: the flavour cycles, the dtype is
     drawn, rows are log-uniform in 1..16384 and columns log-uniform in 1..70000; a third of the
     widths are rounded down to whole 16-byte vectors (of the 16-bit types), a third to 32-element
-    blocks, the rest stay as drawn (the scalar path); at most 4 M elements per case."""
+    blocks, the rest stay as drawn (the scalar path); at most 4 M elements per case.  Every fifth
+    case passes x one element past a 16-byte boundary (the scalar path at any width)."""
     rng = np.random.default_rng(seed)
     kinds = ["ln", "rms", "gelu_tanh", "gelu_none", "add_ln", "ln_fp8", "add_rms_mx", "ln_dres",
              "add_rms", "rms_fp8", "add_ln_fp8", "ln_mx"]
@@ -2410,17 +2411,17 @@ def _random_cases(n=240, seed=20261202):
         elif shape == 0:
             cols = max(8, cols // 8 * 8)
         rows = max(1, min(rows, 4_000_000 // cols))
-        cases.append((kind, dtype, rows, cols))
+        cases.append((kind, dtype, rows, cols, i % 5 == 4))
     return cases
 
 
 RANDOM_CASES = _random_cases()
 
 
-@pytest.mark.parametrize("kind,dtype,rows,cols", RANDOM_CASES,
-                         ids=[f"{i}-{k}-{str(d)[6:]}-{r}x{c}"
-                              for i, (k, d, r, c) in enumerate(RANDOM_CASES)])
-def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
+@pytest.mark.parametrize("kind,dtype,rows,cols,shifted", RANDOM_CASES,
+                         ids=[f"{i}-{k}-{str(d)[6:]}-{r}x{c}{'-shifted' if sh else ''}"
+                              for i, (k, d, r, c, sh) in enumerate(RANDOM_CASES)])
+def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols, shifted):
     """Seeded random shapes through whatever route the dispatcher picks for them (register
     tiles, odd tiles, LDS-staged, split, streamed, scalar path; the register, LDS and two-pass
     backwards): LayerNorm, RMSNorm and LN + GELU (both forms) forward and backward, the
@@ -2434,11 +2435,15 @@ def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols):
     gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
     bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
     x, r, dy, g, b = cuda(xc), cuda(rc), cuda(dyc), cuda(gc), cuda(bc)
+    if shifted:  # x one element past a 16-byte boundary
+        xbuf = torch.empty(rows * cols + 1, dtype=dtype, device="cuda")
+        xbuf[1:] = x.flatten()
+        x = xbuf[1:].view(rows, cols)
     xs, rs, dys, gs, bs = f32(xc), f32(rc), f32(dyc), f32(gc), f32(bc)
     io = _kind(dtype)
     p = capi.ptr
     code = capi.dtype_code(x)
-    what = f"{kind} {io} {rows}x{cols}"
+    what = f"{kind} {io} {rows}x{cols}{' shifted' if shifted else ''}"
 
     def check_y(y, y_ref, xin, bias=True, approximate=None):
         al = affine_atol(xin, gs, bs, 1e-5, approximate) if bias else 0.0
