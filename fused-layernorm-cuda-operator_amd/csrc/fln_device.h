@@ -387,16 +387,38 @@ __device__ __forceinline__ uint32_t fp8x4_inrange(float a, float b, float c, flo
 }
 // OCP MX (Microscaling v1.0) block scale for E4M3 elements: for a block maximum m, the shared
 // exponent is floor(log2 m) - 8 (8 = emax of E4M3), clamped to [-127, 127]; the E8M0 code is
-// exponent + 127 (2^(code - 127)); elements are v * 2^-exponent, saturated to +-448.  A zero
-// (or subnormal) maximum gives code 0.
+// exponent + 127 (2^(code - 127)), i.e. the maximum's biased exponent field minus 8, at least
+// `floor`; elements are v * 2^-exponent, saturated to +-448.  A zero (or subnormal) maximum gives
+// code 0.  floor is 0, or 0xFF (E8M0's NaN) for a row whose every block is to read as NaN
+// (mx_poison): the clamp the code needs anyway then yields 0xFF at no cost, and the block's codes,
+// scaled by the meaningless mul that goes with it, carry no value.
 struct MxScale {
   int code;     // E8M0 byte
   float mul;    // 2^-exponent (exact)
 };
-__device__ __forceinline__ MxScale mx_scale_e4m3(float block_max) {
-  const int e_max = static_cast<int>((__builtin_bit_cast(uint32_t, block_max) >> 23) & 0xFF) - 127;
-  const int e = e_max - 8 < -127 ? -127 : e_max - 8;  // e <= 119 for finite maxima
-  return {e + 127, __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23)};
+__device__ __forceinline__ MxScale mx_scale_e4m3(float block_max, int floor = 0) {
+  const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, block_max) >> 23) & 0xFF);
+  const int code = eb - 8 < floor ? floor : eb - 8;  // <= 247 for finite maxima
+  return {code, __builtin_bit_cast(float, (254u - static_cast<uint32_t>(code)) << 23)};
+}
+
+// fp8 outputs of a row whose statistics are not usable: a mean that is not finite, or an rstd
+// outside (0, inf), which is what a NaN or an infinity in the row, an fp32 sum of squares that
+// overflows, or a constant row with eps = 0 leave.  Every output of such a row is meaningless, so
+// its row scale is NaN and each of its MX block scales 0xFF, and a reader sees NaN throughout.
+// row_poison is +0 for a usable row and NaN otherwise (x - x is NaN exactly for x infinite or
+// NaN; 0 * (1 / rstd) is NaN for rstd = 0): added to the row maximum, it leaves a usable row's
+// unchanged.  mx_poison is its exponent field, 0 or 0xFF: the floor of each E8M0 block code.
+// Tested on the statistics, which stay live through the epilogue anyway, rather than per element:
+// the row maximum keeps its two-elements-per-instruction chain (v_max3_f32), whose maxNum
+// semantics would drop a NaN.  Every lane of a wave works on one row, so the value is
+// wave-uniform: read from the first lane, it lives in an SGPR and costs the epilogue no VGPR.
+__device__ __forceinline__ float row_poison(float mean, float rstd) {
+  const float p = ((mean - mean) + (rstd - rstd)) + 0.0f * __builtin_amdgcn_rcpf(rstd);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, p)));
+}
+__device__ __forceinline__ int mx_poison(float poison) {
+  return static_cast<int>((__builtin_bit_cast(uint32_t, poison) >> 23) & 0xFF);
 }
 
 // Max over aligned groups of G adjacent lanes (G = 2 ... 32) of non-negative values, result in

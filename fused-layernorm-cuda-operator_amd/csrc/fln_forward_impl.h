@@ -348,6 +348,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
       }
     }
     const float rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);  // v_rsq_f32, 1 ulp
+    const float poison = FP8 != 0 ? row_poison(mean, rstd) : 0.0f;  // fp8 scales: NaN
 
     //    Normalize + affine + epilogue, packed to the output format.
     auto affine = [&](int i, int e) -> float {
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
         float bm = 0.0f;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(out(i, e)));
-        const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+        const MxScale ms = mx_scale_e4m3(group_max<G>(bm), mx_poison(poison));
         float a[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) a[e] = out(i, e);
@@ -422,6 +423,7 @@ __global__ __launch_bounds__(MAXT) void fwd_reg_kernel(const FwdParams p, int64_
         }
       }
       am = row_allreduce<MaxOp>(am, slots[2], wpr, rg, wave, lane);
+      am += poison;
       const float inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // 1 ulp
       scale = am * (1.0f / 448.0f);
 #pragma unroll
@@ -634,6 +636,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
     }
     q = row_allreduce<SumOp>(q, slots[1], kW, 0, wave, lane);
     const float rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);  // v_rsq_f32, 1 ulp
+    const float poison = FP8 != 0 ? row_poison(mean, rstd) : 0.0f;  // fp8 scales: NaN
 
     // Output element e of vector i of the row.
     auto affine = [&](int i, int e, const P& xv, const P& gv, const P& bv) -> float {
@@ -697,7 +700,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
             a[e] = affine(i, e, xv, gv, bv);
             bm = fmaxf(bm, fabsf(a[e]));
           }
-          const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+          const MxScale ms = mx_scale_e4m3(group_max<G>(bm), mx_poison(poison));
           BufIO<VEC, FLN_FWD_STORE_POL>::store(codes(a, ms.mul, false), qr,
                                                static_cast<uint32_t>(v) * VEC);
           __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(ms.code), br,
@@ -719,6 +722,7 @@ __global__ __launch_bounds__(kFwdLdsThreads) void fwd_lds_kernel(const FwdParams
           }
         }
         am = row_allreduce<MaxOp>(am, slots[2], kW, 0, wave, lane);
+        am += poison;
         const float inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // 1 ulp
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
@@ -884,6 +888,7 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
       const float q = row_allreduce<SumOp>(fmaf(cnt * dm, dm, m2), slots[1], kW, 0, wave, lane);
       rstd = __builtin_amdgcn_rsqf(q * inv_n + p.eps);
     }
+    const float poison = FP8 != 0 ? row_poison(mean, rstd) : 0.0f;  // fp8 scales: NaN
 
     auto affine = [&](const P& hv, const P& gv, const P& bv, int e) -> float {
       float a = fmaf((to_f32(hv.v[e]) - mean) * rstd, has_g ? to_f32(gv.v[e]) : 1.0f,
@@ -915,6 +920,7 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
         }
       }
       am = row_allreduce<MaxOp>(am, slots[2], kW, 0, wave, lane);
+      am += poison;
       inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // v_rcp_f32, 1 ulp
     }
 
@@ -946,7 +952,7 @@ __global__ __launch_bounds__(kFwdWideThreads) void fwd_wide_kernel(const FwdPara
             float bm = 0.0f;
 #pragma unroll
             for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(a[e]));
-            const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+            const MxScale ms = mx_scale_e4m3(group_max<G>(bm), mx_poison(poison));
             m = ms.mul;  // |a * m| < 512: the saturating conversion clamps to 448
             const uint32_t nblk = static_cast<uint32_t>(N / 32);
             __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(ms.code),
@@ -1034,6 +1040,8 @@ __global__ __launch_bounds__(1024) void fwd_loop_kernel(const FwdParams p) {
     }
     q = block_allreduce<A, false>(q, red[1]);
     const A rstd = static_cast<A>(1) / sqrt(q / static_cast<A>(N) + static_cast<A>(p.eps));
+    // fp8 scales of a row with unusable statistics (as row_poison): NaN, 0xFF for MX blocks
+    const bool bad = !__builtin_isfinite(mean) || !(rstd > 0 && rstd < __builtin_huge_val());
     if (threadIdx.x == 0) {
       if (p.mean) p.mean[row] = static_cast<float>(mean);
       if (p.rstd) p.rstd[row] = static_cast<float>(rstd);
@@ -1054,9 +1062,10 @@ __global__ __launch_bounds__(1024) void fwd_loop_kernel(const FwdParams p) {
         uint8_t* q8 = static_cast<uint8_t*>(p.y);
         for (int64_t j = threadIdx.x; j < N; j += blockDim.x) {
           const float a = static_cast<float>(outv(j));
-          const MxScale ms = mx_scale_e4m3(group_max<32>(fabsf(a)));
+          const MxScale ms = mx_scale_e4m3(group_max<32>(fabsf(a)), bad ? 0xFF : 0);
           q8[base + j] = fp8x1(a * ms.mul);
-          if ((j & 31) == 0) p.bscale[row * (N / 32) + j / 32] = static_cast<uint8_t>(ms.code);
+          if ((j & 31) == 0)
+            p.bscale[row * (N / 32) + j / 32] = static_cast<uint8_t>(ms.code);
         }
         __syncthreads();
         continue;
@@ -1068,7 +1077,7 @@ __global__ __launch_bounds__(1024) void fwd_loop_kernel(const FwdParams p) {
         am = m > am ? m : am;
       }
       am = block_allreduce<A, true>(am, red[2]);
-      const float amf = static_cast<float>(am);
+      const float amf = bad ? __builtin_nanf("") : static_cast<float>(am);
       const float inv = amf > 0.0f ? 448.0f / amf : 0.0f;
       if (threadIdx.x == 0) p.scale[row] = amf / 448.0f;
       uint8_t* q8 = static_cast<uint8_t*>(p.y);
@@ -1548,10 +1557,11 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_out_kernel(const F
   const float2 st = split_row_stats(reinterpret_cast<const float4*>(Y), S, lane, fn, 1.0f / fn,
                                     p.eps, p.rms != 0);
   const float mean = st.x, rstd = st.y;
+  const float poison = FP8 != 0 ? row_poison(mean, rstd) : 0.0f;  // fp8 scales: NaN
   float am = 0.0f, inv = 0.0f;
   if constexpr (FP8 == 1) {  // the row maximum from the chunk maxima (max: any order)
     const float* cm = reinterpret_cast<const float*>(Y + S * 16);
-    am = wave_allreduce<MaxOp>(lane < S ? cm[lane] : 0.0f);
+    am = wave_allreduce<MaxOp>(lane < S ? cm[lane] : 0.0f) + poison;
     inv = am > 0.0f ? 448.0f * __builtin_amdgcn_rcpf(am) : 0.0f;  // v_rcp_f32, 1 ulp
   }
   // The head block overwrites the head (several waves' worth of fp8 vectors): every wave has
@@ -1597,7 +1607,7 @@ __global__ __launch_bounds__(kFwdSplitThreads) void fwd_split_out_kernel(const F
           float bm = 0.0f;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) bm = fmaxf(bm, fabsf(a[e]));
-          const MxScale ms = mx_scale_e4m3(group_max<G>(bm));
+          const MxScale ms = mx_scale_e4m3(group_max<G>(bm), mx_poison(poison));
           m = ms.mul;  // |a * m| < 512: the saturating conversion clamps to 448
           const uint32_t nblk = static_cast<uint32_t>(N / 32);
           __builtin_amdgcn_raw_buffer_store_b8(

@@ -143,7 +143,11 @@ int fln_add_rmsnorm_forward(const void* x, const void* residual, const void* wei
 
 /* LayerNorm with OCP fp8 e4m3fn output: v = LN(x) [* gamma + beta] in fp32,
  * scale[r] = max_j |v_rj| / 448, q = sat_rne_e4m3fn(v / scale[r]) (one byte per element);
- * a row whose max is 0 gets scale 0 and all-zero codes.  mean and rstd may be NULL.
+ * a row whose max is 0 gets scale 0 and all-zero codes.  A row whose statistics are not usable
+ * (a NaN or an infinity in it, an fp32 sum over it that overflows, or a constant row with
+ * eps = 0: mean not finite or rstd outside (0, inf)) gets scale NaN, so its codes read as NaN;
+ * gamma and beta are taken to be finite.  The fp8 and MXFP8 entry points below share this rule
+ * (MXFP8: every block scale of such a row is 0xFF, E8M0's NaN).  mean and rstd may be NULL.
  * No counterpart in the reference. */
 int fln_layernorm_fp8_forward(const void* x, const void* gamma, const void* beta, uint8_t* q,
                               float* scale, float* mean, float* rstd, int64_t rows, int64_t cols,

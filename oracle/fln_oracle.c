@@ -155,7 +155,7 @@ void orc_layernorm_fp8(const float* x, const float* gamma, const float* beta, in
       double v = (xr[j] - mu) * rs;
       if (gamma) v *= gamma[j];
       if (beta) v += beta[j];
-      if (fabs(v) > amax) amax = fabs(v);
+      if (fabs(v) > amax || v != v) amax = fabs(v); /* a NaN propagates, as in amax */
     }
     const double sc = amax / 448.0;
     scale[r] = (float)sc;
@@ -178,7 +178,7 @@ void orc_rmsnorm_fp8(const float* x, const float* weight, int64_t rows, int64_t 
     for (int64_t j = 0; j < cols; ++j) {
       double v = xr[j] * rs;
       if (weight) v *= weight[j];
-      if (fabs(v) > amax) amax = fabs(v);
+      if (fabs(v) > amax || v != v) amax = fabs(v); /* a NaN propagates, as in amax */
     }
     const double sc = amax / 448.0;
     scale[r] = (float)sc;

@@ -224,14 +224,28 @@ def fp8_e4m3fn_decode(codes):
 def layer_norm_fp8_fwd(x, gamma=None, beta=None, eps=1e-5):
     """LayerNorm with fp8 output -> (codes uint8, scale float32 per row).
     v = LayerNorm(x) (affine), scale = max|v| / 448 per row, codes = sat_rne_e4m3fn(v / scale);
-    a row with max|v| == 0 gets scale 0 and all-zero codes.  No reference code."""
-    y, _, _ = layer_norm_fwd(x, gamma, beta, eps)
-    return _row_fp8(y)
+    a row with max|v| == 0 gets scale 0 and all-zero codes.  A row whose statistics are not usable
+    (see unusable_rows: a NaN or an infinity in the row) gets a NaN scale, and the codes under a
+    NaN scale carry no value; for such rows this is torch's amax of v as well.  gamma and beta are
+    taken to be finite.  No reference code."""
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        y, mean, rstd = layer_norm_fwd(x, gamma, beta, eps)
+    return _row_fp8(y, unusable_rows(mean, rstd))
 
 
-def _row_fp8(y):
-    amax = np.abs(y).max(axis=-1, keepdims=True)
-    scale = amax / FP8_E4M3FN_MAX
+def unusable_rows(mean, rstd):
+    """Rows whose statistics leave every output meaningless: a mean that is not finite, or an rstd
+    outside (0, inf) -- a NaN or an infinity in the row (in float64; fp32 statistics also flag a
+    sum of squares past 3.4e38), or a constant row with eps = 0.  Their fp8 row scale is NaN and
+    every MX block scale 0xFF (E8M0's NaN), so a reader sees NaN throughout."""
+    mean, rstd = np.asarray(mean), np.asarray(rstd)
+    return ~np.isfinite(mean) | ~((rstd > 0) & (rstd < np.inf))
+
+
+def _row_fp8(y, bad):
+    with np.errstate(invalid="ignore"):
+        amax = np.abs(y).max(axis=-1, keepdims=True)
+    scale = np.where(bad[..., None], np.nan, amax / FP8_E4M3FN_MAX)
     with np.errstate(divide="ignore", invalid="ignore"):
         q = np.where(amax > 0, y / np.where(amax > 0, scale, 1.0), 0.0)
     return fp8_e4m3fn_encode(q), scale[..., 0].astype(np.float32)
@@ -240,22 +254,23 @@ def _row_fp8(y):
 def rms_norm_fp8_fwd(x, weight=None, eps=1e-6):
     """RMSNorm with fp8 output -> (codes, scale): the row rule of layer_norm_fp8_fwd applied to
     rms_norm_fwd's output.  No reference code."""
-    y, _ = rms_norm_fwd(x, weight, eps)
-    return _row_fp8(y)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        y, rstd = rms_norm_fwd(x, weight, eps)
+    return _row_fp8(y, unusable_rows(np.zeros_like(rstd), rstd))
 
 
 def add_layer_norm_fp8_fwd(x, residual, gamma=None, beta=None, eps=1e-5, io_dtype="bf16"):
     """Residual add + LayerNorm -> fp8: (codes, scale, h); h rounded as in add_layer_norm_fwd.
     No reference code."""
-    y, h, _, _ = add_layer_norm_fwd(x, residual, gamma, beta, eps, io_dtype)
-    q, scale = _row_fp8(y)
+    y, h, mean, rstd = add_layer_norm_fwd(x, residual, gamma, beta, eps, io_dtype)
+    q, scale = _row_fp8(y, unusable_rows(mean, rstd))
     return q, scale, h
 
 
 def add_rms_norm_fp8_fwd(x, residual, weight=None, eps=1e-6, io_dtype="bf16"):
     """Residual add + RMSNorm -> fp8: (codes, scale, h).  No reference code."""
-    y, h, _ = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
-    q, scale = _row_fp8(y)
+    y, h, rstd = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
+    q, scale = _row_fp8(y, unusable_rows(np.zeros_like(rstd), rstd))
     return q, scale, h
 
 
@@ -263,35 +278,51 @@ def mx_e4m3_quantize(y, block=MX_BLOCK):
     """OCP Microscaling (MX v1.0) MXFP8 E4M3 of the last axis -> (codes uint8, E8M0 scales uint8
     [..., n / block]).  Per block of `block` consecutive elements: shared exponent
     e = floor(log2(max|y|)) - 8 (8 = emax of E4M3), clamped to [-127, 127] (a zero maximum gives
-    -127); scale byte e + 127; codes = sat_rne_e4m3fn(y 2^-e).  Written from the format
-    definition (no reference code)."""
+    -127); scale byte e + 127; codes = sat_rne_e4m3fn(y 2^-e).  A block whose maximum is not
+    finite (an infinity, or a NaN, which the maximum propagates) gets the scale byte 0xFF, E8M0's
+    NaN (torch's float8_e8m0fnu cast of 2^(floor(log2 max) - 8) gives the same byte), under which
+    every element of the block reads as NaN: its codes carry no value (here those of e = 120).
+    Written from the format definition (no reference code)."""
     y = _f64(y)
     n = y.shape[-1]
     if n % block:
         raise ValueError("the row length must be a multiple of the block")
     yb = y.reshape(*y.shape[:-1], n // block, block)
     amax = np.abs(yb).max(axis=-1)
-    _, k = np.frexp(amax)                    # amax = f 2^k, f in [0.5, 1): floor(log2) = k - 1
-    e = np.where(amax > 0, k - 1 - 8, -127)
+    finite = np.isfinite(amax)
+    _, k = np.frexp(np.where(finite, amax, 1.0))  # amax = f 2^k, f in [0.5, 1): floor(log2) = k - 1
+    e = np.where(finite, np.where(amax > 0, k - 1 - 8, -127), 120)
     e = np.clip(e, -127, 127).astype(np.int64)
-    codes = fp8_e4m3fn_encode(yb * np.exp2(-e.astype(np.float64))[..., None])
-    return codes.reshape(y.shape), (e + 127).astype(np.uint8)
+    with np.errstate(invalid="ignore"):
+        codes = fp8_e4m3fn_encode(yb * np.exp2(-e.astype(np.float64))[..., None])
+    return codes.reshape(y.shape), np.where(finite, e + 127, 0xFF).astype(np.uint8)
+
+
+def _mx_rows(y, bad):
+    q, sc = mx_e4m3_quantize(y)
+    sc[np.asarray(bad)] = 0xFF  # every block of a row with unusable statistics reads as NaN
+    return q, sc
 
 
 def layer_norm_mxfp8_fwd(x, gamma=None, beta=None, eps=1e-5):
-    """LayerNorm -> MXFP8 E4M3 (codes, E8M0 block scales).  No reference code."""
-    y, _, _ = layer_norm_fwd(x, gamma, beta, eps)
-    return mx_e4m3_quantize(y)
+    """LayerNorm -> MXFP8 E4M3 (codes, E8M0 block scales); rows with unusable statistics
+    (unusable_rows) get 0xFF in every block.  No reference code."""
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        y, mean, rstd = layer_norm_fwd(x, gamma, beta, eps)
+    return _mx_rows(y, unusable_rows(mean, rstd))
 
 
 def rms_norm_mxfp8_fwd(x, weight=None, eps=1e-6):
-    """RMSNorm -> MXFP8 E4M3.  No reference code."""
-    y, _ = rms_norm_fwd(x, weight, eps)
-    return mx_e4m3_quantize(y)
+    """RMSNorm -> MXFP8 E4M3; rows with unusable statistics get 0xFF in every block (an infinity
+    makes rstd 0: torch's composition would give only the block holding it 0xFF, the others the
+    scale and codes of zeros).  No reference code."""
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        y, rstd = rms_norm_fwd(x, weight, eps)
+    return _mx_rows(y, unusable_rows(np.zeros_like(rstd), rstd))
 
 
 def add_rms_norm_mxfp8_fwd(x, residual, weight=None, eps=1e-6, io_dtype="bf16"):
     """Residual add + RMSNorm -> MXFP8 E4M3: (codes, block scales, h).  No reference code."""
-    y, h, _ = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
-    q, sc = mx_e4m3_quantize(y)
+    y, h, rstd = add_rms_norm_fwd(x, residual, weight, eps, io_dtype)
+    q, sc = _mx_rows(y, unusable_rows(np.zeros_like(rstd), rstd))
     return q, sc, h

@@ -2564,3 +2564,90 @@ def test_random_shapes_against_the_oracle(lib, kind, dtype, rows, cols, shifted)
     assert_close_rel(to_np(dg), dg_ref, 1e-4, what + " dgamma")
     if db_ref is not None:
         assert_close_rel(to_np(db), db_ref, 1e-4, what + " dbeta")
+
+
+NONFINITE_CASES = [(4096, 4096, torch.bfloat16), (1024, 3072, torch.bfloat16),
+                   (64, 40960, torch.bfloat16), (8, 65536, torch.float32), (100, 1023, torch.float16),
+                   (300, 768, torch.float32), (400, 131072, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("rows,cols,dtype", NONFINITE_CASES,
+                         ids=[f"{r}x{c}-{str(d)[6:]}" for r, c, d in NONFINITE_CASES])
+@pytest.mark.parametrize("op", ["ln", "rms", "ln_fp8", "rms_mx"])
+def test_non_finite_inputs_stay_in_their_rows(lib, op, rows, cols, dtype):
+    """A NaN in row 3 and an infinity in row 5 (register tiles, odd tiles, the LDS-staged,
+    streamed and split forwards, the scalar path): every other row's outputs are bitwise those of
+    the same call without them, the call reports no error, and rows 3 and 5 are what the float64
+    oracle makes of them.  LayerNorm: an infinity makes the mean infinite and every centred value
+    NaN or infinite, so y is NaN throughout.  RMSNorm: an infinity makes rstd 0, so y is zero but
+    NaN (inf * 0) at the infinity.  Both rows' statistics are unusable (oracle.norms.unusable_rows),
+    so their fp8 row scale is NaN (torch's amax of y gives the same) and every MX block scale of
+    theirs 0xFF, E8M0's NaN."""
+    if op == "rms_mx" and cols % 32:
+        pytest.skip("MX blocks need a multiple of 32 columns")
+    gen = torch.Generator().manual_seed(rows + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bad = xc.clone()
+    r5 = min(5, rows - 1)
+    bad[3, cols // 3] = float("nan")
+    bad[r5, cols - 1] = float("inf")
+    g, b = cuda(gc), cuda(bc)
+    p = capi.ptr
+    code = capi.dtype_code(g)
+
+    def run(xh):
+        x = cuda(xh)
+        if op == "ln":
+            y, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+            return [y.float().cpu(), torch.stack([mean, rstd], 1).cpu()]
+        if op == "rms":
+            y, rstd = rms_forward(lib, x, g, 1e-6)
+            return [y.float().cpu(), rstd[:, None].cpu()]
+        q = torch.empty(rows, cols, device="cuda", dtype=torch.uint8)
+        if op == "ln_fp8":
+            s = torch.empty(rows, device="cuda")
+            capi.check(lib.fln_layernorm_fp8_forward(p(x), p(g), p(b), p(q), p(s), None, None,
+                                                     rows, cols, code, 1e-5, capi.stream()))
+            return [q.cpu(), s[:, None].cpu()]
+        sc = torch.empty(rows, cols // 32, device="cuda", dtype=torch.uint8)
+        capi.check(lib.fln_rmsnorm_mxfp8_forward(p(x), p(g), p(q), p(sc), None, rows, cols,
+                                                 code, 1e-6, capi.stream()))
+        return [q.cpu(), sc.cpu()]
+
+    clean, dirty = run(xc), run(bad)
+    torch.cuda.synchronize()
+    keep = torch.ones(rows, dtype=torch.bool)
+    keep[3] = keep[r5] = False
+    for c_out, d_out in zip(clean, dirty):
+        assert torch.equal(c_out[keep], d_out[keep]), f"{op}: a clean row changed"
+    rr = [3, r5]
+    xs, gs, bs = bad[rr].double().numpy(), gc.double().numpy(), bc.double().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        if op == "ln":
+            y_ref = norms.layer_norm_fwd(xs, gs, bs, 1e-5)[0]
+        elif op == "rms":
+            y_ref = norms.rms_norm_fwd(xs, gs, 1e-6)[0]
+        elif op == "ln_fp8":
+            s_ref = norms.layer_norm_fp8_fwd(xs, gs, bs, 1e-5)[1]
+        else:
+            q_ref, sc_ref = norms.rms_norm_mxfp8_fwd(xs, gs, 1e-6)
+    if op in ("ln", "rms"):
+        y = dirty[0][rr]
+        assert torch.equal(y.isnan(), torch.from_numpy(np.isnan(y_ref))), op
+        assert torch.equal(y[~y.isnan()].double(), torch.from_numpy(y_ref[~np.isnan(y_ref)])), op
+        if op == "ln":  # rstd NaN for both rows; the mean NaN or infinite
+            assert torch.isnan(dirty[1][rr][:, 1]).all(), (op, dirty[1][rr])
+            assert not torch.isfinite(dirty[1][rr][:, 0]).any(), (op, dirty[1][rr])
+        else:           # rstd NaN for the NaN row, 1 / sqrt(inf) = 0 for the infinity's
+            assert torch.isnan(dirty[1][3, 0]) and dirty[1][r5, 0] == 0, (op, dirty[1][rr])
+    elif op == "ln_fp8":
+        assert np.isnan(s_ref).all() and torch.isnan(dirty[1][rr]).all(), (op, dirty[1][rr])
+    else:
+        assert np.array_equal(dirty[1][rr].numpy(), sc_ref), (dirty[1][rr], sc_ref)
+        live = np.repeat(sc_ref != 0xFF, 32, axis=1)  # blocks under a NaN scale are NaN anyway
+        got, want = dirty[0][rr].numpy()[live], q_ref[live]
+        # the zeros of the infinity's row: +0 or -0 codes (0x00 / 0x80) read as the same zero
+        assert np.array_equal(norms.fp8_e4m3fn_decode(got), norms.fp8_e4m3fn_decode(want)), \
+            (op, np.unique(got), np.unique(want))

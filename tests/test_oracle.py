@@ -310,6 +310,70 @@ def test_mx_e4m3_matches_torch_casts(rng):
     assert np.array_equal(deq[sat], np.sign(yb[sat]) * 448 * np.broadcast_to(x, yb.shape)[sat])
 
 
+def test_mx_e4m3_non_finite_blocks_take_the_e8m0_nan(rng):
+    """A block holding a NaN or an infinity: torch's amax propagates the NaN, and its
+    float8_e8m0fnu cast of 2^(floor(log2 max) - 8) gives 0xFF (E8M0's NaN) for both; the other
+    blocks keep the scales and codes they have without the non-finite values."""
+    y = rng.randn(3, 128) * 3
+    bad = y.copy()
+    bad[0, 5], bad[1, 70], bad[2, 127] = np.nan, np.inf, -np.inf
+    q, sc = norms.mx_e4m3_quantize(bad)
+    amax = t64(bad).reshape(3, 4, 32).abs().amax(-1)
+    e8 = torch.exp2(torch.floor(torch.log2(amax)) - 8).to(torch.float8_e8m0fnu)
+    assert np.array_equal(sc, e8.view(torch.uint8).numpy())
+    assert sc[0, 0] == sc[1, 2] == sc[2, 3] == 0xFF and (sc == 0xFF).sum() == 3
+    q0, sc0 = norms.mx_e4m3_quantize(y)
+    keep = sc != 0xFF
+    assert np.array_equal(sc[keep], sc0[keep])
+    blocks = np.repeat(keep, 32, axis=1)
+    assert np.array_equal(q[blocks], q0[blocks])
+
+
+def test_row_fp8_scale_of_a_non_finite_row_is_nan(rng):
+    """torch's amax of a row's LayerNorm / RMSNorm outputs is NaN as soon as one is NaN (a NaN
+    input, or an infinity, which makes the mean infinite and every centred value NaN or
+    infinite); both oracles give that NaN scale and leave the other rows alone."""
+    x = rng.randn(4, 96).astype(np.float32)
+    bad = x.copy()
+    bad[1, 7], bad[2, 95] = np.nan, np.inf
+    with np.errstate(invalid="ignore", over="ignore"):
+        for q, s in [norms.layer_norm_fp8_fwd(bad), c_oracle.layernorm_fp8(bad)]:
+            yt = F.layer_norm(t64(bad), (96,), eps=1e-5)
+            assert np.isnan(s[1:3]).all() and yt.abs().amax(-1)[1:3].isnan().all()
+            q0, s0 = norms.layer_norm_fp8_fwd(x)
+            assert np.array_equal(q[[0, 3]], q0[[0, 3]])
+            np.testing.assert_allclose(s[[0, 3]], s0[[0, 3]], rtol=1e-7)
+        for q, s in [norms.rms_norm_fp8_fwd(bad), c_oracle.rmsnorm_fp8(bad)]:
+            assert np.isnan(s[1]), s      # a NaN row: NaN
+            assert np.isnan(s[2]), s      # rstd = 0: zeros and inf * 0 = NaN
+
+
+def test_mx_rows_with_unusable_statistics_read_as_nan(rng):
+    """MXFP8 of a row whose statistics are not usable: every block scale 0xFF, whatever the
+    block holds (LayerNorm: all of y is NaN there, as in torch's composition; RMSNorm with an
+    infinity: rstd = 0 leaves zeros beside one NaN, where torch's composition would mark only the
+    NaN's block); the other rows are those of the clean input, and eps = 0 on a constant row
+    flags that row (rstd infinite)."""
+    x = rng.randn(5, 96)
+    bad = x.copy()
+    bad[1, 7], bad[3, 95] = np.nan, np.inf
+    for fn in (norms.layer_norm_mxfp8_fwd, norms.rms_norm_mxfp8_fwd):
+        q, sc = fn(bad)
+        q0, sc0 = fn(x)
+        assert (sc[[1, 3]] == 0xFF).all() and (sc0 != 0xFF).all(), fn
+        keep = [0, 2, 4]
+        assert np.array_equal(sc[keep], sc0[keep]) and np.array_equal(q[keep], q0[keep]), fn
+    with np.errstate(invalid="ignore"):
+        y = norms.rms_norm_fwd(bad[3:4])[0]
+    assert np.isnan(y[0, 95]) and (y[0, :95] == 0).all()   # what the flag stands in for
+    const = np.ones((2, 64))
+    const[1] = rng.randn(64)
+    _, s = norms.layer_norm_fp8_fwd(const, eps=0.0)
+    assert np.isnan(s[0]) and np.isfinite(s[1]) and s[1] > 0
+    _, sc = norms.layer_norm_mxfp8_fwd(const, eps=0.0)
+    assert (sc[0] == 0xFF).all() and (sc[1] != 0xFF).all()
+
+
 # ---------------------------------------------------------------- C oracle vs numpy oracle
 def test_c_oracle_matches_numpy_oracle(rng):
     x = rng.randn(9, 1023).astype(np.float32)
