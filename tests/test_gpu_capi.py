@@ -2651,3 +2651,56 @@ def test_non_finite_inputs_stay_in_their_rows(lib, op, rows, cols, dtype):
         # the zeros of the infinity's row: +0 or -0 codes (0x00 / 0x80) read as the same zero
         assert np.array_equal(norms.fp8_e4m3fn_decode(got), norms.fp8_e4m3fn_decode(want)), \
             (op, np.unique(got), np.unique(want))
+
+NONFINITE_BWD_CASES = [(4096, 4096, torch.bfloat16), (64, 40960, torch.bfloat16),
+                       (100, 1023, torch.float16), (300, 768, torch.float32)]
+
+
+@pytest.mark.parametrize("rows,cols,dtype", NONFINITE_BWD_CASES,
+                         ids=[f"{r}x{c}-{str(d)[6:]}" for r, c, d in NONFINITE_BWD_CASES])
+@pytest.mark.parametrize("op", ["ln", "rms"])
+def test_non_finite_rows_in_the_backward(lib, op, rows, cols, dtype):
+    """The backward of a batch with a NaN in row 3 and an infinity in row 5, fed the forward's
+    own statistics: dx of every other row is bitwise that of the clean batch; dx of rows 3 and 5
+    is NaN wherever the float64 oracle's is; dγ / dw is NaN in every column (row 3's x̂ is NaN
+    throughout) while dβ, a plain sum of dy, is bitwise the clean batch's (the non-finite rows
+    leak into no other reduction)."""
+    gen = torch.Generator().manual_seed(3 * rows + cols)
+    xc = torch.randn(rows, cols, generator=gen).to(dtype)
+    dyc = torch.randn(rows, cols, generator=gen).to(dtype)
+    gc = (1 + 0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bc = (0.1 * torch.randn(cols, generator=gen)).to(dtype)
+    bad = xc.clone()
+    r5 = min(5, rows - 1)
+    bad[3, cols // 3] = float("nan")
+    bad[r5, cols - 1] = float("inf")
+    g, b, dy = cuda(gc), cuda(bc), cuda(dyc)
+    print(f"[non-finite bwd] {op} {rows}x{cols} {dtype}", flush=True)
+
+    def run(xh):
+        x = cuda(xh)
+        if op == "ln":
+            _, mean, rstd = ln_forward(lib, x, g, b, 1e-5)
+            dx, dg, db = ln_backward(lib, dy, x, mean, rstd, g)
+            return dx.float().cpu(), dg.cpu(), db.cpu()
+        _, rstd = rms_forward(lib, x, g, 1e-6)
+        dx, dw = rms_backward(lib, dy, x, rstd, g)
+        return dx.float().cpu(), dw.cpu(), None
+
+    (dxc, dgc, dbc), (dxd, dgd, dbd) = run(xc), run(bad)
+    torch.cuda.synchronize()
+    keep = torch.ones(rows, dtype=torch.bool)
+    keep[3] = keep[r5] = False
+    assert torch.equal(dxc[keep], dxd[keep]), f"{op}: dx of a clean row changed"
+    rr = [3, r5]
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        if op == "ln":
+            dx_ref = norms.layer_norm_bwd(dyc[rr].double().numpy(), bad[rr].double().numpy(),
+                                          gc.double().numpy(), 1e-5)[0]
+        else:
+            dx_ref = norms.rms_norm_bwd(dyc[rr].double().numpy(), bad[rr].double().numpy(),
+                                        gc.double().numpy(), 1e-6)[0]
+    assert torch.equal(dxd[rr].isnan(), torch.from_numpy(np.isnan(dx_ref))), op
+    assert torch.isnan(dgd).all(), (op, dgd)
+    if op == "ln":
+        assert torch.equal(dbc, dbd), "dβ changed"
