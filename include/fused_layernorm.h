@@ -93,8 +93,9 @@ int fln_layernorm_backward(const void* dy, const void* x, const float* mean, con
  * counterpart in the reference.  The workspace is a fixed 32 MiB scratch array in device memory
  * (a __device__ array of the backward's code object: held on every device where libfln's
  * backward kernels are loaded, until the process ends, whether or not this entry point is
- * called); nothing is allocated per call.  Enough for the register and LDS kernels' one partial row per CU up to 16384
- * columns (8 MiB at 8192 x 4096); a call that needs more returns FLN_ERR_TOO_LARGE before
+ * called); nothing is allocated per call.  Enough for the register and LDS kernels' one
+ * partial row per CU up to 16384 columns (8 MiB at 8192 x 4096); a call that needs more
+ * returns FLN_ERR_TOO_LARGE before
  * anything is launched.  Every call on a device shares that device's scratch: calls that
  * overlap on one device (other streams, other host threads) race, so serialize them.  The
  * stream must belong to the current device (FLN_ERR_INVALID otherwise).  Results equal
